@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""Benchmark: one GPU's share of a live-state reshard on MI355X.
+
+Default workload: Llama2-7B-shaped state (bf16 param + f32 master / exp_avg /
+exp_avg_sq), TP4,PP2 -> TP2,PP2, destination (pp0, tp0) = layers 0-15 plus the
+vocabulary-parallel embedding, from two source TP shards resident in HBM.
+A step is one full reshard: pack (sources -> per-peer buffers) + unpack
+(buffers -> destination shards), each a single kernel launch.
+
+Prints ONE JSON line.  ``value`` is the whole-job algorithmic throughput
+B_alg / t in GB/s with B_alg = 3P + D (pack reads and writes P, unpack reads P
+and writes D); ``roofline`` is for the slower of the two kernels, timed with
+HIP events on the stream the kernels run on; ``cpu_baseline`` times the
+reference-style torch-CPU reshard (chunk/contiguous/cat) on a bounded sample
+of the same workload on this host's cores, scaled to the same unit.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from dataclasses import replace
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "reshard ms and achieved HBM GB/s (% of peak) per GPU share; speedup vs CPU ref"
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default=None, help="workload key (default: the Llama2-7B share)")
+    ap.add_argument("--tile-bytes", type=int, default=0)
+    ap.add_argument("--max-blocks", type=int, default=0)
+    ap.add_argument("--nontemporal", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=8,
+                    help="decoder layers on the destination stage in the CPU sample")
+    ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
+                    help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
+    ap.add_argument("--json-out", default=None)
+    return ap.parse_args(argv)
+
+
+def to_ometa(m):
+    from oracle import reshard_oracle as O
+    return O.OMeta(name=m.name, itemsize=m.dtype.itemsize, shape=tuple(int(s) for s in m.shape),
+                   tp=None if m.tp_meta is None else tuple(m.tp_meta), kind=m.kind,
+                   kind_args=tuple(m.kind_args), rows=m.rows)
+
+
+def cpu_baseline(w, layers: int, threads: int):
+    """Time the torch-CPU restatement of the reference's CPU reshard on a
+    sample of ``w`` whose destination stage holds ``layers`` decoder layers."""
+    import torch
+    from oracle import reshard_oracle as O
+    from oracle.torch_ref import execute_torch_cpu
+
+    pp = w.dst.pp if w.dst.pp > 1 else 1
+    # sample: same plan change, fewer layers (destination stage = ``layers``)
+    n_layer = max(w.src.pp, pp) * layers
+    ws = replace(w, model=replace(w.model, n_layer=n_layer))
+    spl, tpl = ws.layouts()
+    osrc = {r: {n: to_ometa(m) for n, m in metas.items()} for r, metas in spl.layout.items()}
+    odst = {r: {n: to_ometa(m) for n, m in metas.items()} for r, metas in tpl.layout.items()}
+    ops = [op for op in O.schedule(osrc, odst) if op.dst == ws.dst_rank]
+    dt = ws.dtypes
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        srcs = {}
+        P = 0
+        for op in ops:
+            for f in ws.src_fields:
+                key = (op.src, op.name, f)
+                ent = srcs.setdefault(op.src, {}).setdefault(op.name, {})
+                if f not in ent:
+                    t = torch.empty(O.actual_shape(op.src_meta), dtype=dt[f])
+                    t.fill_(0.5)
+                    ent[f] = t
+        out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)  # warm
+        del out
+        t0 = time.perf_counter()
+        out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)
+        dt_s = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(prev)
+    # algorithmic bytes of the sample, same definition as the GPU figure
+    from suika_amd.plan import ReshardPlan, SlotSpec
+    ops_p = ws.ops()
+    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
+             for op in ops_p for f in ws.src_fields}
+    plan = ReshardPlan(ops_p, specs, list(ws.src_fields), recast=ws.recast_map)
+    b_alg = plan.pack_bytes + plan.unpack_bytes
+    plan.close()
+    return dt_s, b_alg, n_layer
+
+
+def cpu_model() -> str:
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return "unknown"
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's share of the reshard; --gpus {args.gpus} is not "
+              "supported by this build (the cross-GPU exchange is not implemented).", file=sys.stderr)
+        return 2
+
+    import torch
+    from suika_amd.plan import PlanOptions, ReshardPlan, SlotSpec
+    from suika_amd.workloads import BENCH_CONFIG, CONFIGS, make_source_state
+
+    key = args.config or BENCH_CONFIG
+    w = CONFIGS[key]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    print(f"[bench] workload {key}: planning", file=sys.stderr, flush=True)
+    ops = w.ops()
+    dt = w.dtypes
+    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
+             for op in ops for f in w.src_fields}
+    opts = PlanOptions(tile_bytes=args.tile_bytes, max_blocks=args.max_blocks,
+                       nontemporal=args.nontemporal)
+    plan = ReshardPlan(ops, specs, list(w.src_fields), recast=w.recast_map, options=opts)
+    info = plan.info
+    P = int(info.pack_bytes_read)
+    D = int(info.unpack_bytes_written)
+    b_pack = plan.pack_bytes
+    b_unpack = plan.unpack_bytes
+    b_alg = b_pack + b_unpack
+    b_min = P + D
+
+    print(f"[bench] generating {P / 1e9:.2f} GB of source shards on {dev}", file=sys.stderr, flush=True)
+    sources = make_source_state(w, plan.peers, dev)
+    bufs = plan.alloc_buffers(dev)
+    dst = plan.alloc_dst(dev)
+    sp = plan.src_pointers(sources)
+    bp = plan.buf_pointers(bufs)
+    dp = plan.dst_pointers(dst)
+    stream = torch.cuda.current_stream()
+
+    for _ in range(args.warmup):
+        plan.pack_ptrs(sp, bp, stream)
+        plan.unpack_ptrs(bp, dp, stream)
+    torch.cuda.synchronize()
+
+    K = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record(stream)
+    for k in range(K):
+        ev[k][0].record(stream)
+        plan.pack_ptrs(sp, bp, stream)
+        ev[k][1].record(stream)
+        plan.unpack_ptrs(bp, dp, stream)
+        ev[k][2].record(stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - wall0
+    total_ms = start.elapsed_time(end) / K
+    pack_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
+    unpack_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
+    print(f"[bench] pack {pack_ms:.3f} ms  unpack {unpack_ms:.3f} ms  step {total_ms:.3f} ms  "
+          f"wall {wall_s * 1e3 / K:.3f} ms/step", file=sys.stderr, flush=True)
+
+    value = b_alg / (total_ms * 1e-3) / 1e9
+    pack_gbps = b_pack / (pack_ms * 1e-3) / 1e9
+    unpack_gbps = b_unpack / (unpack_ms * 1e-3) / 1e9
+    dom = "sr_unpack_kernel" if unpack_ms >= pack_ms else "sr_pack_kernel"
+    dom_ms = max(pack_ms, unpack_ms)
+    dom_bytes = b_unpack if unpack_ms >= pack_ms else b_pack
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+
+    traffic = None
+    tf = Path(args.traffic_file)
+    if tf.exists():
+        try:
+            tdata = json.loads(tf.read_text())
+            ent = tdata.get(key, {}).get(dom)
+            if ent is not None and ent.get("tile_bytes", 0) == args.tile_bytes \
+                    and bool(ent.get("nontemporal", False)) == args.nontemporal:
+                traffic = ent["bytes_per_launch"]
+        except Exception as e:  # a malformed file must not hide the measurement
+            print(f"[bench] ignoring {tf}: {e}", file=sys.stderr)
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic",
+        "config": {
+            "workload": w.description or key,
+            "key": key,
+            "fields": list(w.src_fields) + [t for t, _ in w.recast],
+            "pieces": plan.n_pieces,
+            "P_bytes": P,
+            "D_bytes": D,
+            "B_alg_bytes": b_alg,
+            "B_min_bytes": b_min,
+            "tile_bytes": args.tile_bytes or 262144,
+            "nontemporal": args.nontemporal,
+        },
+        "reshard_ms": round(total_ms, 4),
+        "pack_ms": round(pack_ms, 4),
+        "unpack_ms": round(unpack_ms, 4),
+        "pct_of_peak": round(100.0 * value / PEAK_HBM_GBPS, 2),
+        "B_min_GBps": round(b_min / (total_ms * 1e-3) / 1e9, 1),
+        "pack_GBps": round(pack_gbps, 1),
+        "unpack_GBps": round(unpack_gbps, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": None,
+    }
+
+    del sources, bufs, dst
+    torch.cuda.empty_cache()
+
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        print(f"[bench] CPU baseline: torch-CPU reshard sample, {threads} threads", file=sys.stderr,
+              flush=True)
+        t_n, b_n, nl = cpu_baseline(w, args.cpu_layers, threads)
+        t_1, b_1, nl1 = cpu_baseline(w, max(1, args.cpu_layers // 4), 1)
+        rate_n = b_n / t_n / 1e9
+        rate_1 = b_1 / t_1 / 1e9
+        full_ms = b_alg / (rate_n * 1e9) * 1e3
+        result["cpu_baseline"] = {
+            "value": round(rate_n, 2),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"torch-CPU chunk/contiguous/cat reshard of the same plan change with "
+                       f"{nl} layers ({b_n / 1e9:.2f} GB algorithmic), {t_n:.2f} s"),
+            "full_share_ms_estimate": round(full_ms, 1),
+            "one_thread_GBps": round(rate_1, 2),
+            "one_thread_sample": f"{nl1} layers, {b_1 / 1e9:.2f} GB, {t_1:.2f} s",
+            "cpu_model": cpu_model(),
+            "speedup_gpu_vs_cpu": round(full_ms / total_ms, 1),
+        }
+        print(f"[bench] CPU {rate_n:.2f} GB/s ({threads} thr), 1 thr {rate_1:.2f} GB/s", file=sys.stderr,
+              flush=True)
+
+    plan.close()
+    line = json.dumps(result)
+    print(line, flush=True)
+    if args.json_out:
+        Path(args.json_out).write_text(line + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,187 @@
+/*
+ * suika_reshard.h -- C ABI of the MI355X reshard engine (libsuika_reshard.so).
+ *
+ * The engine executes the data movement of Suika's live state migration:
+ * every destination shard of every state field (param / master / exp_avg /
+ * exp_avg_sq) is assembled from 2-D regions of source shards.  The work is
+ * split in two stream-ordered phases so that an exchange (one message per
+ * peer) can sit between them:
+ *
+ *   pack   : source shards  -> one contiguous send buffer per peer
+ *   unpack : peer buffers   -> destination shards
+ *            (+ fused fp32 -> bf16 round-to-nearest-even recast,
+ *             + zero fill of padded vocabulary rows)
+ *
+ * Reference interfaces replaced (paths relative to the Suika repository):
+ *   - Suika/migration.py:290-312  TransferOp.get_send_tensor
+ *       chunk(n, dim)[k].contiguous() of a source shard          -> sr_pack
+ *   - Suika/migration.py:426-492  execute_param_transfer send/recv loop
+ *       one torch.distributed isend/irecv per tensor per field   -> per-peer
+ *       buffers sized by sr_plan_peer_bytes (one message per peer)
+ *   - Suika/migration.py:531-541  execute_param_transfer post-process
+ *       torch.cat(pieces, dim=slice_dim) / clone()               -> sr_unpack
+ *   - Suika/migration.py:322-381  schedule_param_transfer output (TransferOp
+ *       list) lowered by the Python host to sr_piece records     -> sr_plan_create
+ *
+ * Conventions
+ *   - Every tensor is a dense row-major 2-D view [rows, cols] of elements of
+ *     elem_bytes bytes (a 1-D tensor of n elements is [n, 1]).
+ *   - All device memory (sources, peer buffers, destinations) belongs to the
+ *     caller.  The library owns only the plan and its descriptor tables.
+ *   - Calls that take a hipStream_t are asynchronous and stream-ordered; the
+ *     caller synchronizes.  A plan may be used from one host thread at a time.
+ *   - Status codes: SR_OK (0) on success, a negative sr_status otherwise.
+ *     sr_last_error() returns a thread-local message for the last failure.
+ *     Invalid plans and pointers are rejected before any kernel launch.
+ */
+#ifndef SUIKA_RESHARD_H
+#define SUIKA_RESHARD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SR_ABI_VERSION 1
+
+typedef enum sr_status {
+  SR_OK = 0,
+  SR_EINVAL = -1,    /* malformed argument (null, bad enum, bad size) */
+  SR_EBOUNDS = -2,   /* region outside its tensor or buffer */
+  SR_EALIGN = -3,    /* pointer not aligned to its element size */
+  SR_EOVERLAP = -4,  /* destination regions overlap or leave holes */
+  SR_EHIP = -5,      /* HIP runtime error */
+  SR_ENOMEM = -6,    /* host or device allocation failed */
+  SR_EDTYPE = -7     /* dtype/element-size mismatch between src and dst */
+} sr_status;
+
+/* Element types.  Copies move bytes; only SR_PIECE_RECAST interprets them. */
+typedef enum sr_dtype {
+  SR_DT_U8 = 0,
+  SR_DT_BF16 = 1,
+  SR_DT_F16 = 2,
+  SR_DT_F32 = 3,
+  SR_DT_F64 = 4,
+  SR_DT_I32 = 5,
+  SR_DT_I64 = 6
+} sr_dtype;
+
+/* A tensor slot of the plan: dense row-major [rows, cols]. */
+typedef struct sr_tensor {
+  uint64_t rows;
+  uint64_t cols;
+  int32_t dtype;      /* sr_dtype */
+  int32_t reserved;   /* must be 0 */
+} sr_tensor;
+
+typedef enum sr_piece_kind {
+  SR_PIECE_COPY = 0,    /* src region -> buffer -> dst region (same dtype) */
+  SR_PIECE_RECAST = 1,  /* f32 src region -> buffer -> f32 dst region (if dst >= 0)
+                           and bf16 RNE(src) into dst2 region */
+  SR_PIECE_ZERO = 2     /* zero fill of a dst region (no source, no buffer bytes) */
+} sr_piece_kind;
+
+/* One region move.  Region origins/extents are in elements of the tensors. */
+typedef struct sr_piece {
+  int32_t kind;        /* sr_piece_kind */
+  int32_t peer;        /* buffer index in [0, n_peers); ignored for ZERO */
+  int32_t src;         /* source tensor slot; -1 for ZERO */
+  int32_t dst;         /* destination tensor slot; -1 allowed for RECAST (bf16 only) */
+  int32_t dst2;        /* RECAST: bf16 destination slot; otherwise -1 */
+  int32_t reserved;    /* must be 0 */
+  uint64_t rows;       /* region extent */
+  uint64_t cols;
+  uint64_t src_row;    /* region origin in src */
+  uint64_t src_col;
+  uint64_t dst_row;    /* region origin in dst (and in dst2 for RECAST) */
+  uint64_t dst_col;
+} sr_piece;
+
+/* Plan tuning; pass NULL to sr_plan_create for the defaults. */
+typedef struct sr_plan_options {
+  uint32_t tile_bytes;   /* bytes of source data per work tile; power of two in
+                            [4096, 16 MiB]; 0 = default (262144) */
+  uint32_t max_blocks;   /* cap on workgroups per launch (grid-stride beyond);
+                            0 = one workgroup per tile */
+  uint32_t flags;        /* SR_OPT_* bits */
+  uint32_t reserved;     /* must be 0 */
+} sr_plan_options;
+
+#define SR_OPT_NONTEMPORAL 0x1u   /* streaming (non-temporal) loads and stores */
+#define SR_OPT_SKIP_COVERAGE 0x2u /* skip the destination coverage check */
+
+typedef struct sr_plan sr_plan;
+
+typedef struct sr_plan_info {
+  int64_t n_pieces;
+  int64_t n_peers;
+  int64_t n_src;
+  int64_t n_dst;
+  int64_t pack_tiles;
+  int64_t unpack_tiles;
+  uint64_t pack_bytes_read;      /* algorithmic bytes of the pack phase */
+  uint64_t pack_bytes_written;
+  uint64_t unpack_bytes_read;    /* algorithmic bytes of the unpack phase */
+  uint64_t unpack_bytes_written;
+  uint64_t buffer_bytes;         /* sum over peers of sr_plan_peer_bytes */
+} sr_plan_info;
+
+/* ABI version of the loaded library (SR_ABI_VERSION). */
+int sr_abi_version(void);
+
+/* Thread-local message describing the last non-zero status. */
+const char* sr_last_error(void);
+
+/* Host-only arithmetic self test (division constants, tiling); SR_OK if good. */
+int sr_selftest(void);
+
+/*
+ * Validate the pieces against the tensor slots and build the plan: buffer
+ * offsets per peer (256-byte aligned, in piece order), work tiles of both
+ * phases.  Host only: no device memory is touched until the first
+ * sr_pack / sr_unpack.  Destinations must be covered exactly once by the
+ * pieces (copies, recasts and zero fills) unless SR_OPT_SKIP_COVERAGE.
+ * Replaces the plan construction of Suika/migration.py:322-381 + 426-492.
+ */
+int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src,
+                   const sr_tensor* dst_tensors, int32_t n_dst,
+                   int32_t n_peers,
+                   const sr_piece* pieces, int32_t n_pieces,
+                   const sr_plan_options* options,
+                   sr_plan** out_plan);
+
+/* Bytes the buffer of `peer` must hold. */
+int sr_plan_peer_bytes(const sr_plan* plan, int32_t peer, uint64_t* out_bytes);
+
+/* Byte offset of piece `piece` inside its peer buffer (UINT64_MAX for ZERO). */
+int sr_plan_piece_offset(const sr_plan* plan, int32_t piece, uint64_t* out_offset);
+
+int sr_plan_info_get(const sr_plan* plan, sr_plan_info* out_info);
+
+/*
+ * Pack: gather every non-ZERO piece's source region into its peer buffer.
+ * src_ptrs[n_src] are device addresses of the source slots, peer_bufs[n_peers]
+ * of the peer buffers (each >= sr_plan_peer_bytes).  Replaces
+ * TransferOp.get_send_tensor (Suika/migration.py:290-312) for every op.
+ */
+int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs,
+            hipStream_t stream);
+
+/*
+ * Unpack: scatter buffer contents into the destination slots, recast f32 ->
+ * bf16 (round-to-nearest-even, NaN -> 0x7FC0) for RECAST pieces, zero fill
+ * ZERO pieces.  Replaces the cat/clone post-process of
+ * Suika/migration.py:531-541.
+ */
+int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs,
+              hipStream_t stream);
+
+void sr_plan_destroy(sr_plan* plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUIKA_RESHARD_H */

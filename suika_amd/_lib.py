@@ -1,0 +1,182 @@
+"""ctypes binding of ``libsuika_reshard.so`` (C ABI in include/suika_reshard.h).
+
+The binding fails loudly: importing the package never falls back to a CPU or
+torch path.  If the library is missing, every entry point raises
+``RuntimeError`` telling the caller to run the build.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsuika_reshard.so"
+
+SR_OK = 0
+SR_EINVAL = -1
+SR_EBOUNDS = -2
+SR_EALIGN = -3
+SR_EOVERLAP = -4
+SR_EHIP = -5
+SR_ENOMEM = -6
+SR_EDTYPE = -7
+
+STATUS_NAMES = {
+    SR_OK: "SR_OK",
+    SR_EINVAL: "SR_EINVAL",
+    SR_EBOUNDS: "SR_EBOUNDS",
+    SR_EALIGN: "SR_EALIGN",
+    SR_EOVERLAP: "SR_EOVERLAP",
+    SR_EHIP: "SR_EHIP",
+    SR_ENOMEM: "SR_ENOMEM",
+    SR_EDTYPE: "SR_EDTYPE",
+}
+
+SR_DT_U8, SR_DT_BF16, SR_DT_F16, SR_DT_F32, SR_DT_F64, SR_DT_I32, SR_DT_I64 = range(7)
+
+SR_PIECE_COPY, SR_PIECE_RECAST, SR_PIECE_ZERO = 0, 1, 2
+
+SR_OPT_NONTEMPORAL = 0x1
+SR_OPT_SKIP_COVERAGE = 0x2
+
+# Every symbol the header declares; the CPU test-suite checks they resolve.
+EXPORTED_SYMBOLS = (
+    "sr_abi_version",
+    "sr_last_error",
+    "sr_selftest",
+    "sr_plan_create",
+    "sr_plan_peer_bytes",
+    "sr_plan_piece_offset",
+    "sr_plan_info_get",
+    "sr_pack",
+    "sr_unpack",
+    "sr_plan_destroy",
+)
+
+ABI_VERSION = 1
+
+
+class SrTensor(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_uint64),
+        ("cols", ctypes.c_uint64),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class SrPiece(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("peer", ctypes.c_int32),
+        ("src", ctypes.c_int32),
+        ("dst", ctypes.c_int32),
+        ("dst2", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("rows", ctypes.c_uint64),
+        ("cols", ctypes.c_uint64),
+        ("src_row", ctypes.c_uint64),
+        ("src_col", ctypes.c_uint64),
+        ("dst_row", ctypes.c_uint64),
+        ("dst_col", ctypes.c_uint64),
+    ]
+
+
+class SrPlanOptions(ctypes.Structure):
+    _fields_ = [
+        ("tile_bytes", ctypes.c_uint32),
+        ("max_blocks", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+class SrPlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("n_pieces", ctypes.c_int64),
+        ("n_peers", ctypes.c_int64),
+        ("n_src", ctypes.c_int64),
+        ("n_dst", ctypes.c_int64),
+        ("pack_tiles", ctypes.c_int64),
+        ("unpack_tiles", ctypes.c_int64),
+        ("pack_bytes_read", ctypes.c_uint64),
+        ("pack_bytes_written", ctypes.c_uint64),
+        ("unpack_bytes_read", ctypes.c_uint64),
+        ("unpack_bytes_written", ctypes.c_uint64),
+        ("buffer_bytes", ctypes.c_uint64),
+    ]
+
+
+class ReshardError(RuntimeError):
+    """HIP/runtime failure reported by the library (SR_EHIP, SR_ENOMEM)."""
+
+
+class PlanError(AssertionError):
+    """Invalid plan or argument; an AssertionError like the reference's
+    ``assert`` checks (Suika/migration.py:293-294, 311, 356, 436, 441)."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    vp = ctypes.c_void_p
+    lib.sr_abi_version.restype = ctypes.c_int
+    lib.sr_abi_version.argtypes = []
+    lib.sr_last_error.restype = ctypes.c_char_p
+    lib.sr_last_error.argtypes = []
+    lib.sr_selftest.restype = ctypes.c_int
+    lib.sr_selftest.argtypes = []
+    lib.sr_plan_create.restype = ctypes.c_int
+    lib.sr_plan_create.argtypes = [
+        ctypes.POINTER(SrTensor), ctypes.c_int32,
+        ctypes.POINTER(SrTensor), ctypes.c_int32,
+        ctypes.c_int32,
+        ctypes.POINTER(SrPiece), ctypes.c_int32,
+        ctypes.POINTER(SrPlanOptions),
+        ctypes.POINTER(vp),
+    ]
+    lib.sr_plan_peer_bytes.restype = ctypes.c_int
+    lib.sr_plan_peer_bytes.argtypes = [vp, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]
+    lib.sr_plan_piece_offset.restype = ctypes.c_int
+    lib.sr_plan_piece_offset.argtypes = [vp, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)]
+    lib.sr_plan_info_get.restype = ctypes.c_int
+    lib.sr_plan_info_get.argtypes = [vp, ctypes.POINTER(SrPlanInfo)]
+    lib.sr_pack.restype = ctypes.c_int
+    lib.sr_pack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_unpack.restype = ctypes.c_int
+    lib.sr_unpack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_plan_destroy.restype = None
+    lib.sr_plan_destroy.argtypes = [vp]
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is missing."""
+    global _lib
+    if _lib is None:
+        path = Path(os.environ.get("SUIKA_RESHARD_LIB", str(LIB_PATH)))
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python suika_amd/build.py`; there is no fallback path")
+        handle = ctypes.CDLL(str(path))
+        _declare(handle)
+        if handle.sr_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path}: ABI {handle.sr_abi_version()} != expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    return lib().sr_last_error().decode("utf-8", "replace")
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python exception matching a library status code."""
+    if rc == SR_OK:
+        return
+    msg = f"{what}: {STATUS_NAMES.get(rc, rc)}: {last_error()}"
+    if rc in (SR_EHIP, SR_ENOMEM):
+        raise ReshardError(msg)
+    raise PlanError(msg)

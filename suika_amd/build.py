@@ -1,0 +1,65 @@
+"""Build the in-tree HIP library ``suika_amd/lib/libsuika_reshard.so`` for gfx950.
+
+The library is compiled with ``hipcc`` directly (one translation unit, no
+torch extension machinery) so that it stays a plain C-ABI shared object that
+``ctypes`` -- or any other FFI -- can load.  hipcc cross-compiles for gfx950
+without a GPU present.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+SRC = PKG_DIR / "csrc" / "reshard.hip"
+INCLUDE = REPO_DIR / "include"
+LIB_DIR = PKG_DIR / "lib"
+LIB = LIB_DIR / "libsuika_reshard.so"
+
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # packed-FP32 instructions stay disabled for all device code
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (looked at $HIPCC, PATH, /opt/rocm/bin/hipcc)")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library (always recompiles) and return its path."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    noise = "packed-fp32-ops"
+    msgs = [l for l in (res.stdout + res.stderr).splitlines() if l.strip() and noise not in l]
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs), flush=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,974 @@
+// reshard.hip -- plan-driven pack / unpack engine for Suika state migration on
+// MI355X (gfx950).  One source file: the C ABI declared in
+// include/suika_reshard.h, the host-side plan builder, and the device kernels.
+//
+// Reference behaviour reproduced (paths relative to the Suika repository):
+//   Suika/migration.py:290-312  get_send_tensor: chunk(n, dim)[k].contiguous()
+//   Suika/migration.py:531-541  cat(pieces, dim=slice_dim) / clone()
+// Both are pure byte movement.  The Python host lowers every TransferOp x
+// sub-field into 2-D region moves (sr_piece); this file validates them, lays
+// out the per-peer buffers and executes the two phases as single launches.
+//
+// Device design
+//   * A phase (pack or unpack) is a list of items, one per piece.  An item is
+//     a 2-D byte region: `rows` rows of `row_bytes` bytes at a source and a
+//     destination stride.  Regions that are contiguous on both sides are
+//     collapsed to one long row.
+//   * Items are cut into tiles of `tile_bytes` source bytes.  One workgroup
+//     (256 lanes = 4 wave64) processes one tile; the grid is the tile count
+//     (or a grid-stride loop when capped).  Tiles are balanced regardless of
+//     the tensor sizes (3.5 KB norms to GB embeddings).
+//   * Lanes move 16-byte vectors (8/4/2/1 when a region is not 16-byte
+//     aligned), UNROLL independent loads in flight before the stores, so a
+//     wave keeps 4 KB of HBM reads outstanding.  Consecutive lanes touch
+//     consecutive 16-byte words of a row: every wave access is a fully
+//     coalesced 1 KB burst.
+//   * Strided regions (row-parallel dim -1 slices) map a tile-relative byte
+//     position to (row, col) with a multiply-high division by the row width
+//     (Granlund-Montgomery invariant-integer division), computed per item
+//     on the host.
+//   * The unpack RECAST item reads f32 once and writes the f32 copy and the
+//     bf16 round-to-nearest-even copy in the same pass.
+//   * No LDS: every region row is >= 768 bytes at the configured shapes, so a
+//     direct coalesced copy already issues full-width bursts; a transpose is
+//     never needed because no piece changes the element order within a row.
+//
+// Host design
+//   * sr_plan_create is host only (validation, buffer layout, tiling) so the
+//     CPU test-suite can exercise it without a GPU.
+//   * Static tile tables are uploaded on first use; item tables hold absolute
+//     addresses and are rebuilt only when the caller's pointers change.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "suika_reshard.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+constexpr uint32_t kDefaultTileBytes = 262144;
+constexpr uint64_t kBufAlign = 256;
+constexpr uint32_t kMaxGrid = (1u << 24) - 1;   // gridDim.x * 256 < 2^32
+
+// ---------------------------------------------------------------- errors
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define SR_HIP_TRY(expr)                                                      \
+  do {                                                                        \
+    hipError_t e_ = (expr);                                                   \
+    if (e_ != hipSuccess)                                                     \
+      return fail(SR_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));    \
+  } while (0)
+
+int dtype_size(int32_t dt) {
+  switch (dt) {
+    case SR_DT_U8: return 1;
+    case SR_DT_BF16: return 2;
+    case SR_DT_F16: return 2;
+    case SR_DT_F32: return 4;
+    case SR_DT_F64: return 8;
+    case SR_DT_I32: return 4;
+    case SR_DT_I64: return 8;
+    default: return 0;
+  }
+}
+
+// ------------------------------------------------ invariant integer division
+// Granlund & Montgomery, "Division by invariant integers using
+// multiplication" (PLDI 1994), Figure 4.1 with N = 32: for 1 <= d < 2^31 and
+// any 32-bit n, q = (t + ((n - t) >> s1)) >> s2 with t = mulhi(m, n).
+
+struct DivMagic {
+  uint32_t m;
+  uint32_t s1;
+  uint32_t s2;
+};
+
+DivMagic div_magic(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;               // l = ceil(log2 d)
+  const uint64_t num = (uint64_t(1) << 32) * ((uint64_t(1) << l) - d);
+  DivMagic r;
+  r.m = uint32_t(num / d + 1);
+  r.s1 = l < 1 ? l : 1;
+  r.s2 = l > 1 ? l - 1 : 0;
+  return r;
+}
+
+__host__ __device__ inline uint32_t div_apply(uint32_t n, uint32_t m, uint32_t s1,
+                                              uint32_t s2) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t t = __umulhi(m, n);
+#else
+  const uint32_t t = uint32_t((uint64_t(m) * n) >> 32);
+#endif
+  return (t + ((n - t) >> s1)) >> s2;
+}
+
+// ------------------------------------------------------- device structures
+
+enum : uint32_t {
+  kKindCopy = 0,
+  kKindRecast = 1,
+  kKindZero = 2,
+};
+
+// Item flags: bits 0-3 kind, 4-7 log2(vector bytes) (COPY/ZERO) or
+// log2(elements per lane vector) (RECAST), bit 8: RECAST also writes f32.
+struct alignas(16) DevItem {
+  uint64_t src;           // absolute address of the region origin
+  uint64_t dst;
+  uint64_t dst2;          // bf16 target of RECAST
+  uint64_t src_stride;    // bytes between rows
+  uint64_t dst_stride;
+  uint64_t dst2_stride;
+  uint32_t row_bytes;     // source bytes per row; 0 = contiguous (one row)
+  uint32_t magic;         // division by row_bytes
+  uint32_t shifts;        // s1 | s2 << 8
+  uint32_t flags;
+};
+static_assert(sizeof(DevItem) == 64, "DevItem layout");
+
+struct alignas(8) DevTile {
+  uint64_t start;    // contiguous: byte offset in the item; strided: first row
+  uint32_t item;
+  uint32_t nbytes;   // source bytes in this tile
+  uint32_t c_base;   // strided: byte column of the tile start in its first row
+  uint32_t pad;
+};
+static_assert(sizeof(DevTile) == 24, "DevTile layout");
+
+// -------------------------------------------------------------- device code
+
+template <int VB> struct VecOf;
+template <> struct VecOf<16> { typedef unsigned int type __attribute__((ext_vector_type(4))); };
+template <> struct VecOf<8> { typedef unsigned int type __attribute__((ext_vector_type(2))); };
+template <> struct VecOf<4> { typedef unsigned int type; };
+template <> struct VecOf<2> { typedef unsigned short type; };
+template <> struct VecOf<1> { typedef unsigned char type; };
+
+template <bool NT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+
+template <bool NT, typename T>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// Byte offsets (source side, destination side) of position i*VB of a tile.
+struct Pos {
+  uint64_t row;
+  uint32_t col;
+};
+
+__device__ __forceinline__ Pos tile_pos(const DevItem& it, const DevTile& t,
+                                        uint32_t byte_in_tile) {
+  Pos p;
+  if (it.row_bytes == 0) {
+    p.row = 0;
+    // contiguous: col carries nothing; caller uses start + byte_in_tile
+    p.col = 0;
+  } else {
+    const uint32_t x = t.c_base + byte_in_tile;
+    const uint32_t q = div_apply(x, it.magic, it.shifts & 0xffu, it.shifts >> 8);
+    p.row = t.start + q;
+    p.col = x - q * it.row_bytes;
+  }
+  return p;
+}
+
+template <int VB, bool NT>
+__device__ void copy_tile(const DevItem& it, const DevTile& t) {
+  typedef typename VecOf<VB>::type V;
+  const uint32_t nvec = t.nbytes / VB;
+  const bool contig = it.row_bytes == 0;
+  for (uint32_t base = 0; base < nvec; base += kBlock * kUnroll) {
+    V v[kUnroll];
+    uint64_t doff[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      if (i < nvec) {
+        uint64_t soff;
+        if (contig) {
+          soff = t.start + uint64_t(i) * VB;
+          doff[u] = soff;
+        } else {
+          const Pos p = tile_pos(it, t, i * VB);
+          soff = p.row * it.src_stride + p.col;
+          doff[u] = p.row * it.dst_stride + p.col;
+        }
+        v[u] = ld<NT>(reinterpret_cast<const V*>(it.src + soff));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      if (i < nvec) st<NT>(reinterpret_cast<V*>(it.dst + doff[u]), v[u]);
+    }
+  }
+}
+
+template <int VB, bool NT>
+__device__ void zero_tile(const DevItem& it, const DevTile& t) {
+  typedef typename VecOf<VB>::type V;
+  const uint32_t nvec = t.nbytes / VB;
+  const bool contig = it.row_bytes == 0;
+  const V z = V(0);
+  for (uint32_t i = threadIdx.x; i < nvec; i += kBlock) {
+    uint64_t doff;
+    if (contig) {
+      doff = t.start + uint64_t(i) * VB;
+    } else {
+      const Pos p = tile_pos(it, t, i * VB);
+      doff = p.row * it.dst_stride + p.col;
+    }
+    st<NT>(reinterpret_cast<V*>(it.dst + doff), z);
+  }
+}
+
+// float -> bfloat16, round to nearest, ties to even; NaN -> 0x7FC0.
+// This is the standard integer rounding of the upper half-word: add
+// 0x7FFF plus the lowest kept bit, then truncate.
+__device__ __forceinline__ uint32_t bf16_rne(uint32_t u) {
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <int NE, bool NT>
+__device__ void recast_tile(const DevItem& it, const DevTile& t) {
+  constexpr int SB = 4 * NE;   // source (f32) bytes per lane vector
+  typedef typename VecOf<SB>::type VS;   // NE f32
+  typedef typename VecOf<2 * NE>::type VH;  // NE bf16
+  const uint32_t nvec = t.nbytes / SB;
+  const bool contig = it.row_bytes == 0;
+  const bool has_dst = (it.flags >> 8) & 1u;
+  for (uint32_t base = 0; base < nvec; base += kBlock * kUnroll) {
+    VS v[kUnroll];
+    uint64_t doff[kUnroll], hoff[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      if (i < nvec) {
+        uint64_t soff;
+        if (contig) {
+          soff = t.start + uint64_t(i) * SB;
+          doff[u] = soff;
+          hoff[u] = soff >> 1;
+        } else {
+          const Pos p = tile_pos(it, t, i * SB);
+          soff = p.row * it.src_stride + p.col;
+          doff[u] = p.row * it.dst_stride + p.col;
+          hoff[u] = p.row * it.dst2_stride + (p.col >> 1);
+        }
+        v[u] = ld<NT>(reinterpret_cast<const VS*>(it.src + soff));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t i = base + u * kBlock + threadIdx.x;
+      if (i < nvec) {
+        if (has_dst) st<NT>(reinterpret_cast<VS*>(it.dst + doff[u]), v[u]);
+        VH h;
+        if constexpr (NE == 4) {
+          const uint32_t h0 = bf16_rne(v[u].x) | (bf16_rne(v[u].y) << 16);
+          const uint32_t h1 = bf16_rne(v[u].z) | (bf16_rne(v[u].w) << 16);
+          h.x = h0;
+          h.y = h1;
+        } else {
+          h = (unsigned short)bf16_rne(v[u]);
+        }
+        st<NT>(reinterpret_cast<VH*>(it.dst2 + hoff[u]), h);
+      }
+    }
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void exec_tiles(const DevItem* __restrict__ items,
+                                           const DevTile* __restrict__ tiles, uint32_t n_tiles) {
+  for (uint32_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x) {
+    const DevTile t = tiles[ti];
+    const DevItem it = items[t.item];
+    const uint32_t kind = it.flags & 0xfu;
+    const uint32_t lv = (it.flags >> 4) & 0xfu;
+    if (kind == kKindCopy) {
+      switch (lv) {
+        case 4: copy_tile<16, NT>(it, t); break;
+        case 3: copy_tile<8, NT>(it, t); break;
+        case 2: copy_tile<4, NT>(it, t); break;
+        case 1: copy_tile<2, NT>(it, t); break;
+        default: copy_tile<1, NT>(it, t); break;
+      }
+    } else if (kind == kKindRecast) {
+      if (lv == 2) recast_tile<4, NT>(it, t);
+      else recast_tile<1, NT>(it, t);
+    } else {
+      switch (lv) {
+        case 4: zero_tile<16, NT>(it, t); break;
+        case 3: zero_tile<8, NT>(it, t); break;
+        case 2: zero_tile<4, NT>(it, t); break;
+        case 1: zero_tile<2, NT>(it, t); break;
+        default: zero_tile<1, NT>(it, t); break;
+      }
+    }
+  }
+}
+
+// Two entry points with one body, so profiles tell the phases apart.
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void sr_pack_kernel(const DevItem* __restrict__ items,
+                                                         const DevTile* __restrict__ tiles,
+                                                         uint32_t n_tiles) {
+  exec_tiles<NT>(items, tiles, n_tiles);
+}
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void sr_unpack_kernel(const DevItem* __restrict__ items,
+                                                           const DevTile* __restrict__ tiles,
+                                                           uint32_t n_tiles) {
+  exec_tiles<NT>(items, tiles, n_tiles);
+}
+
+// ----------------------------------------------------------- host structures
+
+// Pointer-independent description of one item of a phase.
+struct HostItem {
+  uint32_t kind;
+  int32_t src_slot;       // pack: src tensor slot; unpack: peer index
+  int32_t dst_slot;       // pack: peer index; unpack: dst slot (-1: none)
+  int32_t dst2_slot;      // unpack RECAST: bf16 slot, else -1
+  uint64_t src_off;       // byte offset of region origin in the source object
+  uint64_t dst_off;
+  uint64_t dst2_off;
+  uint64_t src_stride;
+  uint64_t dst_stride;
+  uint64_t dst2_stride;
+  uint64_t rows;
+  uint64_t row_bytes;     // source bytes per row (dst bytes for ZERO)
+  bool contiguous;        // collapsed to one row of rows*row_bytes bytes
+  uint32_t esize;         // element bytes of the source (dst for ZERO)
+};
+
+struct Phase {
+  std::vector<HostItem> items;
+  std::vector<DevTile> tiles;           // static
+  std::vector<DevItem> bound;           // last uploaded item table
+  bool bound_valid = false;
+  DevItem* d_items = nullptr;
+  DevTile* d_tiles = nullptr;
+  DevItem* h_staging = nullptr;         // pinned
+  hipEvent_t ev_staging = nullptr;      // last copy out of h_staging
+  hipEvent_t ev_kernel = nullptr;       // last kernel reading d_items
+  bool tiles_uploaded = false;
+  uint64_t bytes_read = 0;
+  uint64_t bytes_written = 0;
+};
+
+}  // namespace
+
+struct sr_plan {
+  std::vector<sr_tensor> src;
+  std::vector<sr_tensor> dst;
+  std::vector<sr_piece> pieces;
+  std::vector<uint64_t> piece_offset;   // buffer offset, UINT64_MAX for ZERO
+  std::vector<uint64_t> peer_bytes;
+  int32_t n_peers = 0;
+  sr_plan_options opt{};
+  Phase pack;
+  Phase unpack;
+  int device = -1;
+};
+
+namespace {
+
+bool mul_overflows(uint64_t a, uint64_t b, uint64_t limit) {
+  return a != 0 && b > limit / a;
+}
+
+int check_tensor(const sr_tensor& t, const char* what, int32_t idx) {
+  if (t.reserved != 0) return fail(SR_EINVAL, "%s[%d]: reserved field must be 0", what, idx);
+  const int es = dtype_size(t.dtype);
+  if (es == 0) return fail(SR_EINVAL, "%s[%d]: unknown dtype %d", what, idx, t.dtype);
+  if (t.rows == 0 || t.cols == 0)
+    return fail(SR_EINVAL, "%s[%d]: empty tensor [%llu, %llu]", what, idx,
+                (unsigned long long)t.rows, (unsigned long long)t.cols);
+  const uint64_t lim = uint64_t(1) << 62;
+  if (mul_overflows(t.rows, t.cols, lim) || mul_overflows(t.rows * t.cols, es, lim))
+    return fail(SR_EINVAL, "%s[%d]: tensor too large", what, idx);
+  return SR_OK;
+}
+
+int check_region(const sr_tensor& t, uint64_t r0, uint64_t c0, uint64_t rows, uint64_t cols,
+                 const char* what, int32_t piece) {
+  if (r0 > t.rows || rows > t.rows - r0 || c0 > t.cols || cols > t.cols - c0)
+    return fail(SR_EBOUNDS,
+                "piece %d: %s region rows [%llu,+%llu) cols [%llu,+%llu) outside tensor [%llu, %llu]",
+                piece, what, (unsigned long long)r0, (unsigned long long)rows,
+                (unsigned long long)c0, (unsigned long long)cols, (unsigned long long)t.rows,
+                (unsigned long long)t.cols);
+  return SR_OK;
+}
+
+struct Box {
+  uint64_t r0, r1, c0, c1;
+  int32_t piece;
+};
+
+// Every destination slot must be written exactly once: boxes pairwise
+// disjoint and their areas summing to the slot's area.
+int check_coverage(const std::vector<std::vector<Box>>& boxes, const std::vector<sr_tensor>& dst) {
+  for (size_t s = 0; s < boxes.size(); ++s) {
+    std::vector<Box> b = boxes[s];
+    std::sort(b.begin(), b.end(), [](const Box& x, const Box& y) {
+      return x.r0 != y.r0 ? x.r0 < y.r0 : x.c0 < y.c0;
+    });
+    unsigned __int128 area = 0;
+    for (size_t i = 0; i < b.size(); ++i) {
+      area += (unsigned __int128)(b[i].r1 - b[i].r0) * (b[i].c1 - b[i].c0);
+      for (size_t j = i + 1; j < b.size() && b[j].r0 < b[i].r1; ++j) {
+        if (b[j].c0 < b[i].c1 && b[i].c0 < b[j].c1)
+          return fail(SR_EOVERLAP, "dst[%zu]: pieces %d and %d write overlapping regions", s,
+                      b[i].piece, b[j].piece);
+      }
+    }
+    const unsigned __int128 full = (unsigned __int128)dst[s].rows * dst[s].cols;
+    if (area != full)
+      return fail(SR_EOVERLAP, "dst[%zu]: pieces cover %llu of %llu elements", s,
+                  (unsigned long long)area, (unsigned long long)full);
+  }
+  return SR_OK;
+}
+
+void make_tiles(Phase& ph, uint32_t tile_bytes) {
+  ph.tiles.clear();
+  for (uint32_t k = 0; k < ph.items.size(); ++k) {
+    const HostItem& it = ph.items[k];
+    const uint64_t total = it.rows * it.row_bytes;
+    for (uint64_t start = 0; start < total; start += tile_bytes) {
+      DevTile t{};
+      t.item = k;
+      t.nbytes = uint32_t(std::min<uint64_t>(tile_bytes, total - start));
+      if (it.contiguous) {
+        t.start = start;
+        t.c_base = 0;
+      } else {
+        t.start = start / it.row_bytes;
+        t.c_base = uint32_t(start - t.start * it.row_bytes);
+      }
+      ph.tiles.push_back(t);
+    }
+  }
+}
+
+// Largest power-of-two vector width (<= 16, >= esize) dividing every value
+// OR-ed into `acc`.
+uint32_t pick_vb(uint64_t acc, uint32_t esize) {
+  uint32_t vb = 16;
+  while (vb > esize && (acc & (vb - 1))) vb >>= 1;
+  return vb;
+}
+
+uint32_t log2u(uint32_t v) {
+  uint32_t l = 0;
+  while ((1u << l) < v) ++l;
+  return l;
+}
+
+// Build the device item table of a phase from the caller's pointers.
+int bind_items(Phase& ph, const uint64_t* src_base, size_t n_src_base, const uint64_t* dst_base,
+               size_t n_dst_base, std::vector<DevItem>& out) {
+  out.resize(ph.items.size());
+  for (size_t k = 0; k < ph.items.size(); ++k) {
+    const HostItem& h = ph.items[k];
+    DevItem d{};
+    d.src = h.src_slot >= 0 && size_t(h.src_slot) < n_src_base ? src_base[h.src_slot] + h.src_off : 0;
+    d.dst = h.dst_slot >= 0 && size_t(h.dst_slot) < n_dst_base ? dst_base[h.dst_slot] + h.dst_off : 0;
+    d.dst2 = h.dst2_slot >= 0 && size_t(h.dst2_slot) < n_dst_base ? dst_base[h.dst2_slot] + h.dst2_off : 0;
+    d.src_stride = h.src_stride;
+    d.dst_stride = h.dst_stride;
+    d.dst2_stride = h.dst2_stride;
+    const uint64_t total = h.rows * h.row_bytes;
+    if (h.contiguous) {
+      d.row_bytes = 0;
+      d.magic = 0;
+      d.shifts = 0;
+    } else {
+      d.row_bytes = uint32_t(h.row_bytes);
+      const DivMagic m = div_magic(uint32_t(h.row_bytes));
+      d.magic = m.m;
+      d.shifts = m.s1 | (m.s2 << 8);
+    }
+    uint32_t lv = 0;
+    if (h.kind == kKindCopy) {
+      uint64_t acc = d.src | d.dst;
+      acc |= h.contiguous ? total : (h.row_bytes | h.src_stride | h.dst_stride);
+      lv = log2u(pick_vb(acc, h.esize));
+    } else if (h.kind == kKindZero) {
+      uint64_t acc = d.dst;
+      acc |= h.contiguous ? total : (h.row_bytes | h.dst_stride);
+      lv = log2u(pick_vb(acc, h.esize));
+    } else {
+      // RECAST: 4 f32 per lane when f32 sides are 16-byte and the bf16 side
+      // 8-byte aligned, otherwise one element per lane.
+      bool wide = ((d.src | (h.dst_slot >= 0 ? d.dst : 0)) & 15) == 0 && (d.dst2 & 7) == 0;
+      if (h.contiguous) {
+        wide = wide && (total & 15) == 0;
+      } else {
+        wide = wide && (h.row_bytes & 15) == 0 && (h.src_stride & 15) == 0 &&
+               (h.dst_slot < 0 || (h.dst_stride & 15) == 0) && (h.dst2_stride & 7) == 0;
+      }
+      lv = wide ? 2 : 0;
+    }
+    d.flags = h.kind | (lv << 4) | ((h.kind == kKindRecast && h.dst_slot >= 0) ? (1u << 8) : 0u);
+    out[k] = d;
+  }
+  return SR_OK;
+}
+
+int ensure_device(sr_plan* p) {
+  int dev = -1;
+  SR_HIP_TRY(hipGetDevice(&dev));
+  if (p->device < 0) {
+    p->device = dev;
+  } else if (p->device != dev) {
+    return fail(SR_EINVAL, "plan was first used on device %d, current device is %d", p->device, dev);
+  }
+  return SR_OK;
+}
+
+int upload_static(Phase& ph) {
+  if (ph.tiles_uploaded) return SR_OK;
+  if (!ph.tiles.empty()) {
+    SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_tiles), ph.tiles.size() * sizeof(DevTile)));
+    SR_HIP_TRY(hipMemcpy(ph.d_tiles, ph.tiles.data(), ph.tiles.size() * sizeof(DevTile),
+                         hipMemcpyHostToDevice));
+  }
+  if (!ph.items.empty()) {
+    SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_items), ph.items.size() * sizeof(DevItem)));
+    SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ph.h_staging), ph.items.size() * sizeof(DevItem),
+                             hipHostMallocDefault));
+  }
+  SR_HIP_TRY(hipEventCreateWithFlags(&ph.ev_staging, hipEventDisableTiming));
+  SR_HIP_TRY(hipEventCreateWithFlags(&ph.ev_kernel, hipEventDisableTiming));
+  ph.tiles_uploaded = true;
+  return SR_OK;
+}
+
+int run_phase(sr_plan* p, Phase& ph, bool is_pack, const uint64_t* src_base, size_t n_src_base,
+              const uint64_t* dst_base, size_t n_dst_base, hipStream_t stream) {
+  int rc = ensure_device(p);
+  if (rc != SR_OK) return rc;
+  rc = upload_static(ph);
+  if (rc != SR_OK) return rc;
+  if (ph.tiles.empty()) return SR_OK;
+
+  std::vector<DevItem> items;
+  rc = bind_items(ph, src_base, n_src_base, dst_base, n_dst_base, items);
+  if (rc != SR_OK) return rc;
+  const size_t nbytes = items.size() * sizeof(DevItem);
+  if (!ph.bound_valid || std::memcmp(items.data(), ph.bound.data(), nbytes) != 0) {
+    // The staging buffer may still feed the previous upload; the device
+    // table may still be read by the previous launch of this phase.
+    SR_HIP_TRY(hipEventSynchronize(ph.ev_staging));
+    std::memcpy(ph.h_staging, items.data(), nbytes);
+    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_kernel, 0));
+    SR_HIP_TRY(hipMemcpyAsync(ph.d_items, ph.h_staging, nbytes, hipMemcpyHostToDevice, stream));
+    SR_HIP_TRY(hipEventRecord(ph.ev_staging, stream));
+    ph.bound.swap(items);
+    ph.bound_valid = true;
+  }
+
+  const uint32_t n_tiles = uint32_t(ph.tiles.size());
+  uint32_t grid = n_tiles;
+  if (p->opt.max_blocks != 0) grid = std::min(grid, p->opt.max_blocks);
+  grid = std::min(grid, kMaxGrid);
+  const bool nt = (p->opt.flags & SR_OPT_NONTEMPORAL) != 0;
+  if (is_pack) {
+    if (nt)
+      hipLaunchKernelGGL(sr_pack_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
+                         ph.d_tiles, n_tiles);
+    else
+      hipLaunchKernelGGL(sr_pack_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
+                         ph.d_tiles, n_tiles);
+  } else {
+    if (nt)
+      hipLaunchKernelGGL(sr_unpack_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
+                         ph.d_tiles, n_tiles);
+    else
+      hipLaunchKernelGGL(sr_unpack_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
+                         ph.d_tiles, n_tiles);
+  }
+  SR_HIP_TRY(hipGetLastError());
+  SR_HIP_TRY(hipEventRecord(ph.ev_kernel, stream));
+  return SR_OK;
+}
+
+void free_phase(Phase& ph) {
+  if (ph.d_items) (void)hipFree(ph.d_items);
+  if (ph.d_tiles) (void)hipFree(ph.d_tiles);
+  if (ph.h_staging) (void)hipHostFree(ph.h_staging);
+  if (ph.ev_staging) (void)hipEventDestroy(ph.ev_staging);
+  if (ph.ev_kernel) (void)hipEventDestroy(ph.ev_kernel);
+  ph = Phase();
+}
+
+int check_ptrs(const void* const* ptrs, size_t n, const std::vector<uint32_t>& align,
+               const char* what) {
+  if (n > 0 && ptrs == nullptr) return fail(SR_EINVAL, "%s: pointer array is null", what);
+  for (size_t i = 0; i < n; ++i) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(ptrs[i]);
+    if (align[i] == 0) continue;   // slot unused by this phase
+    if (a == 0) return fail(SR_EINVAL, "%s[%zu] is null", what, i);
+    if (a % align[i] != 0)
+      return fail(SR_EALIGN, "%s[%zu] = %p is not %u-byte aligned", what, i, ptrs[i], align[i]);
+  }
+  return SR_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ C ABI
+
+extern "C" {
+
+int sr_abi_version(void) { return SR_ABI_VERSION; }
+
+const char* sr_last_error(void) { return g_last_error.c_str(); }
+
+int sr_selftest(void) {
+  // Division constants: exhaustive small divisors, then edge divisors, each
+  // against numerators at the edges of the range and a pseudo-random sweep.
+  uint64_t x = 0x9E3779B97F4A7C15ull;
+  auto rnd = [&x]() {
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    return uint32_t(x >> 16);
+  };
+  std::vector<uint32_t> divisors;
+  for (uint32_t d = 1; d <= 4096; ++d) divisors.push_back(d);
+  for (uint32_t s = 12; s < 31; ++s) {
+    divisors.push_back((1u << s) - 1);
+    divisors.push_back(1u << s);
+    divisors.push_back((1u << s) + 1);
+    divisors.push_back((1u << s) * 3 / 2);
+  }
+  divisors.push_back(0x7fffffffu);
+  for (uint32_t d : divisors) {
+    const DivMagic m = div_magic(d);
+    const uint32_t edge[] = {0u, 1u, d - 1, d, d + 1, 2 * d - 1, 0x7fffffffu, 0x80000000u,
+                             0xfffffffeu, 0xffffffffu};
+    for (uint32_t n : edge) {
+      if (div_apply(n, m.m, m.s1, m.s2) != n / d)
+        return fail(SR_EINVAL, "selftest: %u / %u gave %u", n, d, div_apply(n, m.m, m.s1, m.s2));
+    }
+    for (int k = 0; k < 64; ++k) {
+      const uint32_t n = rnd();
+      if (div_apply(n, m.m, m.s1, m.s2) != n / d)
+        return fail(SR_EINVAL, "selftest: %u / %u gave %u", n, d, div_apply(n, m.m, m.s1, m.s2));
+    }
+  }
+  return SR_OK;
+}
+
+int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor* dst_tensors,
+                   int32_t n_dst, int32_t n_peers, const sr_piece* pieces, int32_t n_pieces,
+                   const sr_plan_options* options, sr_plan** out_plan) {
+  if (out_plan == nullptr) return fail(SR_EINVAL, "out_plan is null");
+  *out_plan = nullptr;
+  if (n_src < 0 || n_dst < 0 || n_peers < 0 || n_pieces < 0)
+    return fail(SR_EINVAL, "negative count (n_src=%d n_dst=%d n_peers=%d n_pieces=%d)", n_src,
+                n_dst, n_peers, n_pieces);
+  if ((n_src > 0 && !src_tensors) || (n_dst > 0 && !dst_tensors) || (n_pieces > 0 && !pieces))
+    return fail(SR_EINVAL, "null array with non-zero count");
+
+  sr_plan_options opt{};
+  if (options) opt = *options;
+  if (opt.reserved != 0) return fail(SR_EINVAL, "options.reserved must be 0");
+  if (opt.flags & ~(SR_OPT_NONTEMPORAL | SR_OPT_SKIP_COVERAGE))
+    return fail(SR_EINVAL, "unknown option flags 0x%x", opt.flags);
+  if (opt.tile_bytes == 0) opt.tile_bytes = kDefaultTileBytes;
+  if (opt.tile_bytes < 4096 || opt.tile_bytes > (16u << 20) ||
+      (opt.tile_bytes & (opt.tile_bytes - 1)))
+    return fail(SR_EINVAL, "tile_bytes %u must be a power of two in [4096, 16 MiB]",
+                opt.tile_bytes);
+
+  int rc;
+  for (int32_t i = 0; i < n_src; ++i)
+    if ((rc = check_tensor(src_tensors[i], "src", i)) != SR_OK) return rc;
+  for (int32_t i = 0; i < n_dst; ++i)
+    if ((rc = check_tensor(dst_tensors[i], "dst", i)) != SR_OK) return rc;
+
+  sr_plan* p = new (std::nothrow) sr_plan();
+  if (!p) return fail(SR_ENOMEM, "out of host memory");
+  p->src.assign(src_tensors, src_tensors + n_src);
+  p->dst.assign(dst_tensors, dst_tensors + n_dst);
+  p->pieces.assign(pieces, pieces + n_pieces);
+  p->n_peers = n_peers;
+  p->opt = opt;
+  p->piece_offset.assign(n_pieces, UINT64_MAX);
+  p->peer_bytes.assign(n_peers, 0);
+
+  std::vector<std::vector<Box>> cover(n_dst);
+  const uint64_t max_row = (uint64_t(1) << 31) - opt.tile_bytes;
+
+  for (int32_t k = 0; k < n_pieces; ++k) {
+    const sr_piece& pc = pieces[k];
+    auto bad = [&](int code) {
+      delete p;
+      return code;
+    };
+    if (pc.reserved != 0) return bad(fail(SR_EINVAL, "piece %d: reserved field must be 0", k));
+    if (pc.rows == 0 || pc.cols == 0) return bad(fail(SR_EINVAL, "piece %d: empty region", k));
+    if (pc.kind != SR_PIECE_COPY && pc.kind != SR_PIECE_RECAST && pc.kind != SR_PIECE_ZERO)
+      return bad(fail(SR_EINVAL, "piece %d: unknown kind %d", k, pc.kind));
+
+    if (pc.kind == SR_PIECE_ZERO) {
+      if (pc.src != -1 || pc.dst2 != -1)
+        return bad(fail(SR_EINVAL, "piece %d: ZERO takes no src/dst2", k));
+      if (pc.dst < 0 || pc.dst >= n_dst) return bad(fail(SR_EINVAL, "piece %d: bad dst slot %d", k, pc.dst));
+      const sr_tensor& dt = p->dst[pc.dst];
+      if ((rc = check_region(dt, pc.dst_row, pc.dst_col, pc.rows, pc.cols, "dst", k)) != SR_OK) return bad(rc);
+      const uint32_t es = dtype_size(dt.dtype);
+      HostItem it{};
+      it.kind = kKindZero;
+      it.src_slot = -1;
+      it.dst_slot = pc.dst;
+      it.dst2_slot = -1;
+      it.dst_off = (pc.dst_row * dt.cols + pc.dst_col) * es;
+      it.dst_stride = dt.cols * es;
+      it.rows = pc.rows;
+      it.row_bytes = pc.cols * es;
+      it.esize = es;
+      it.contiguous = pc.rows == 1 || it.dst_stride == it.row_bytes;
+      if (it.contiguous) {
+        it.row_bytes *= it.rows;
+        it.rows = 1;
+      } else if (it.row_bytes > max_row) {
+        return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
+                        (unsigned long long)it.row_bytes));
+      }
+      p->unpack.items.push_back(it);
+      p->unpack.bytes_written += pc.rows * pc.cols * es;
+      cover[pc.dst].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+      continue;
+    }
+
+    if (pc.src < 0 || pc.src >= n_src) return bad(fail(SR_EINVAL, "piece %d: bad src slot %d", k, pc.src));
+    if (pc.peer < 0 || pc.peer >= n_peers) return bad(fail(SR_EINVAL, "piece %d: bad peer %d", k, pc.peer));
+    const sr_tensor& st = p->src[pc.src];
+    if ((rc = check_region(st, pc.src_row, pc.src_col, pc.rows, pc.cols, "src", k)) != SR_OK) return bad(rc);
+    const uint32_t es = dtype_size(st.dtype);
+
+    int32_t dst = pc.dst, dst2 = -1;
+    if (pc.kind == SR_PIECE_COPY) {
+      if (pc.dst2 != -1) return bad(fail(SR_EINVAL, "piece %d: COPY takes no dst2", k));
+      if (dst < 0 || dst >= n_dst) return bad(fail(SR_EINVAL, "piece %d: bad dst slot %d", k, dst));
+      if (p->dst[dst].dtype != st.dtype)
+        return bad(fail(SR_EDTYPE, "piece %d: src dtype %d != dst dtype %d", k, st.dtype, p->dst[dst].dtype));
+    } else {
+      dst2 = pc.dst2;
+      if (st.dtype != SR_DT_F32) return bad(fail(SR_EDTYPE, "piece %d: RECAST source must be f32", k));
+      if (dst2 < 0 || dst2 >= n_dst) return bad(fail(SR_EINVAL, "piece %d: bad dst2 slot %d", k, dst2));
+      if (p->dst[dst2].dtype != SR_DT_BF16)
+        return bad(fail(SR_EDTYPE, "piece %d: RECAST dst2 must be bf16", k));
+      if (dst < -1 || dst >= n_dst) return bad(fail(SR_EINVAL, "piece %d: bad dst slot %d", k, dst));
+      if (dst >= 0 && p->dst[dst].dtype != SR_DT_F32)
+        return bad(fail(SR_EDTYPE, "piece %d: RECAST dst must be f32", k));
+      if (dst == dst2) return bad(fail(SR_EINVAL, "piece %d: dst and dst2 are the same slot", k));
+      if ((rc = check_region(p->dst[dst2], pc.dst_row, pc.dst_col, pc.rows, pc.cols, "dst2", k)) != SR_OK)
+        return bad(rc);
+      cover[dst2].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+    }
+    if (dst >= 0) {
+      if ((rc = check_region(p->dst[dst], pc.dst_row, pc.dst_col, pc.rows, pc.cols, "dst", k)) != SR_OK)
+        return bad(rc);
+      cover[dst].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+    }
+
+    // Buffer placement: pieces of a peer in piece order, 256-byte aligned.
+    const uint64_t payload = pc.rows * pc.cols * es;
+    uint64_t& cur = p->peer_bytes[pc.peer];
+    const uint64_t off = (cur + kBufAlign - 1) / kBufAlign * kBufAlign;
+    p->piece_offset[k] = off;
+    cur = off + payload;
+
+    // Pack item: source region -> contiguous payload.
+    HostItem pk{};
+    pk.kind = kKindCopy;
+    pk.src_slot = pc.src;
+    pk.dst_slot = pc.peer;
+    pk.dst2_slot = -1;
+    pk.src_off = (pc.src_row * st.cols + pc.src_col) * es;
+    pk.src_stride = st.cols * es;
+    pk.dst_off = off;
+    pk.rows = pc.rows;
+    pk.row_bytes = pc.cols * es;
+    pk.dst_stride = pk.row_bytes;
+    pk.esize = es;
+    pk.contiguous = pc.rows == 1 || pk.src_stride == pk.row_bytes;
+    if (pk.contiguous) {
+      pk.row_bytes *= pk.rows;
+      pk.rows = 1;
+    } else if (pk.row_bytes > max_row) {
+      return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
+                      (unsigned long long)pk.row_bytes));
+    }
+    p->pack.items.push_back(pk);
+    p->pack.bytes_read += payload;
+    p->pack.bytes_written += payload;
+
+    // Unpack item: contiguous payload -> destination region(s).
+    HostItem up{};
+    up.kind = pc.kind == SR_PIECE_COPY ? kKindCopy : kKindRecast;
+    up.src_slot = pc.peer;
+    up.dst_slot = dst;
+    up.dst2_slot = dst2;
+    up.src_off = off;
+    up.rows = pc.rows;
+    up.row_bytes = pc.cols * es;
+    up.src_stride = up.row_bytes;
+    up.esize = es;
+    if (dst >= 0) {
+      up.dst_off = (pc.dst_row * p->dst[dst].cols + pc.dst_col) * es;
+      up.dst_stride = p->dst[dst].cols * es;
+    }
+    if (dst2 >= 0) {
+      up.dst2_off = (pc.dst_row * p->dst[dst2].cols + pc.dst_col) * 2;
+      up.dst2_stride = p->dst[dst2].cols * 2;
+    }
+    up.contiguous = pc.rows == 1 || ((dst < 0 || up.dst_stride == up.row_bytes) &&
+                                     (dst2 < 0 || up.dst2_stride * 2 == up.row_bytes));
+    if (up.contiguous) {
+      up.row_bytes *= up.rows;
+      up.rows = 1;
+    } else if (up.row_bytes > max_row) {
+      return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
+                      (unsigned long long)up.row_bytes));
+    }
+    p->unpack.items.push_back(up);
+    p->unpack.bytes_read += payload;
+    if (dst >= 0) p->unpack.bytes_written += payload;
+    if (dst2 >= 0) p->unpack.bytes_written += payload / 2;
+  }
+
+  if (!(opt.flags & SR_OPT_SKIP_COVERAGE)) {
+    if ((rc = check_coverage(cover, p->dst)) != SR_OK) {
+      delete p;
+      return rc;
+    }
+  }
+  make_tiles(p->pack, opt.tile_bytes);
+  make_tiles(p->unpack, opt.tile_bytes);
+  if (p->pack.tiles.size() > UINT32_MAX || p->unpack.tiles.size() > UINT32_MAX) {
+    delete p;
+    return fail(SR_EINVAL, "plan has too many tiles; raise tile_bytes");
+  }
+  *out_plan = p;
+  return SR_OK;
+}
+
+int sr_plan_peer_bytes(const sr_plan* plan, int32_t peer, uint64_t* out_bytes) {
+  if (!plan || !out_bytes) return fail(SR_EINVAL, "null argument");
+  if (peer < 0 || peer >= plan->n_peers) return fail(SR_EINVAL, "peer %d out of range", peer);
+  *out_bytes = plan->peer_bytes[peer];
+  return SR_OK;
+}
+
+int sr_plan_piece_offset(const sr_plan* plan, int32_t piece, uint64_t* out_offset) {
+  if (!plan || !out_offset) return fail(SR_EINVAL, "null argument");
+  if (piece < 0 || size_t(piece) >= plan->pieces.size())
+    return fail(SR_EINVAL, "piece %d out of range", piece);
+  *out_offset = plan->piece_offset[piece];
+  return SR_OK;
+}
+
+int sr_plan_info_get(const sr_plan* plan, sr_plan_info* out) {
+  if (!plan || !out) return fail(SR_EINVAL, "null argument");
+  out->n_pieces = int64_t(plan->pieces.size());
+  out->n_peers = plan->n_peers;
+  out->n_src = int64_t(plan->src.size());
+  out->n_dst = int64_t(plan->dst.size());
+  out->pack_tiles = int64_t(plan->pack.tiles.size());
+  out->unpack_tiles = int64_t(plan->unpack.tiles.size());
+  out->pack_bytes_read = plan->pack.bytes_read;
+  out->pack_bytes_written = plan->pack.bytes_written;
+  out->unpack_bytes_read = plan->unpack.bytes_read;
+  out->unpack_bytes_written = plan->unpack.bytes_written;
+  uint64_t b = 0;
+  for (uint64_t v : plan->peer_bytes) b += v;
+  out->buffer_bytes = b;
+  return SR_OK;
+}
+
+int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs, hipStream_t stream) {
+  if (!plan) return fail(SR_EINVAL, "plan is null");
+  // Alignment each pointer must satisfy: its element size; 0 = not read.
+  std::vector<uint32_t> sal(plan->src.size(), 0), bal(plan->n_peers, 0);
+  for (const sr_piece& pc : plan->pieces) {
+    if (pc.kind == SR_PIECE_ZERO) continue;
+    sal[pc.src] = dtype_size(plan->src[pc.src].dtype);
+    bal[pc.peer] = 16;
+  }
+  int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
+  if (rc != SR_OK) return rc;
+  rc = check_ptrs(reinterpret_cast<const void* const*>(peer_bufs), plan->n_peers, bal, "peer_bufs");
+  if (rc != SR_OK) return rc;
+  std::vector<uint64_t> sb(plan->src.size()), bb(plan->n_peers);
+  for (size_t i = 0; i < sb.size(); ++i) sb[i] = reinterpret_cast<uintptr_t>(src_ptrs ? src_ptrs[i] : nullptr);
+  for (size_t i = 0; i < bb.size(); ++i) bb[i] = reinterpret_cast<uintptr_t>(peer_bufs ? peer_bufs[i] : nullptr);
+  return run_phase(plan, plan->pack, true, sb.data(), sb.size(), bb.data(), bb.size(), stream);
+}
+
+int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs, hipStream_t stream) {
+  if (!plan) return fail(SR_EINVAL, "plan is null");
+  std::vector<uint32_t> bal(plan->n_peers, 0), dal(plan->dst.size(), 0);
+  for (const sr_piece& pc : plan->pieces) {
+    if (pc.kind != SR_PIECE_ZERO) bal[pc.peer] = 16;
+    if (pc.dst >= 0) dal[pc.dst] = dtype_size(plan->dst[pc.dst].dtype);
+    if (pc.dst2 >= 0) dal[pc.dst2] = dtype_size(plan->dst[pc.dst2].dtype);
+  }
+  int rc = check_ptrs(peer_bufs, plan->n_peers, bal, "peer_bufs");
+  if (rc != SR_OK) return rc;
+  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
+  if (rc != SR_OK) return rc;
+  std::vector<uint64_t> bb(plan->n_peers), db(plan->dst.size());
+  for (size_t i = 0; i < bb.size(); ++i) bb[i] = reinterpret_cast<uintptr_t>(peer_bufs ? peer_bufs[i] : nullptr);
+  for (size_t i = 0; i < db.size(); ++i) db[i] = reinterpret_cast<uintptr_t>(dst_ptrs ? dst_ptrs[i] : nullptr);
+  return run_phase(plan, plan->unpack, false, bb.data(), bb.size(), db.data(), db.size(), stream);
+}
+
+void sr_plan_destroy(sr_plan* plan) {
+  if (!plan) return;
+  free_phase(plan->pack);
+  free_phase(plan->unpack);
+  delete plan;
+}
+
+}  // extern "C"

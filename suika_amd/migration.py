@@ -1,0 +1,251 @@
+"""Drop-in state-migration operators running on the HIP reshard engine.
+
+Same names, arguments and error behaviour as the reference's operators:
+
+* ``execute_param_transfer``              -- Suika/migration.py:397-556
+* ``schedule_and_execute_param_transfer`` -- Suika/migration.py:558-598
+* ``merge_model_and_optimizer_state_dict`` / ``split_...``
+                                          -- Suika/migration.py:675-746
+
+``execute_param_transfer`` compiles the TransferOps that land on this rank
+into a ``ReshardPlan`` and runs pack -> peer buffers -> unpack on the GPU.
+Every source piece goes through its peer's buffer; on one GPU the buffers of
+all peers are resident in this GPU's HBM (``fake_source_state_dicts`` holds
+the peers' shards, as in the reference's checkpoint path,
+migration.py:1223-1244).  A cross-GPU exchange between pack and unpack is not
+part of this build: ops from a remote rank without a local copy of its shards
+raise ``NotImplementedError``.
+
+Deliberate difference: pieces are placed in ascending global order.  The
+reference appends pieces whose source is the executing rank after all others
+(migration.py:454-459, 492, 508-509), which concatenates a TP merge out of
+order when that rank owns a leading piece; this build implements the
+intended ``cat`` in ascending piece order.
+"""
+from __future__ import annotations
+
+from collections import OrderedDict
+from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
+
+import torch
+import torch.distributed as dist
+from torch import Tensor
+from torch.nn import Module
+from torch.optim import Optimizer
+
+from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
+                   schedule_param_transfer)
+from .plan import PlanOptions, ReshardPlan, SlotSpec
+
+StateDict = Dict[str, Dict[str, Tensor]]
+
+
+class _NoProf:
+    def start(self, *a, **k):
+        pass
+
+    def stop(self, *a, **k):
+        pass
+
+
+def _is_meta_field(field_type) -> bool:
+    return not (isinstance(field_type, str) and field_type == "normal")
+
+
+def forcefully_free_tensor(tensor: Tensor) -> None:
+    """Release a tensor's storage now (Suika/utils.py:255-260)."""
+    if isinstance(tensor, torch.Tensor):
+        if tensor.untyped_storage().resizable():
+            tensor.untyped_storage().resize_(0)
+        else:
+            tensor.data = torch.empty(0, device="meta")
+
+
+def _current_rank(world) -> int:
+    if dist.is_available() and dist.is_initialized():
+        return dist.get_rank(world)
+    return 0
+
+
+def execute_param_transfer(
+    transfer_ops: List[TransferOp],
+    source_state_dict: StateDict,
+    device: torch.device,
+    expected_sub_fields: List[Tuple[str, Union[str, TensorMeta]]],
+    world: Optional[dist.ProcessGroup] = None,
+    log_func: Optional[Callable] = None,
+    prof=None,
+    forcefully_free: bool = False,
+    fake_source_state_dicts: Optional[Dict[int, StateDict]] = None,
+    *,
+    rank: Optional[int] = None,
+    recast: Optional[Mapping[str, str]] = None,
+    plan_options: Optional[PlanOptions] = None,
+    stream: Optional[torch.cuda.Stream] = None,
+) -> StateDict:
+    """Execute a transfer schedule for this rank; returns its target state.
+
+    ``source_state_dict`` (this rank's own shards) is cleared in place, as in
+    the reference (migration.py:527).  Normal sub-fields move through the HIP
+    pack/unpack kernels; 1-element sub-fields (e.g. AdamW ``step``) are copied
+    whole (migration.py:443-446, 479-487).  Extensions: ``rank`` overrides
+    ``dist.get_rank(world)``; ``recast`` maps a bf16 target field to the f32
+    field it is rounded from; ``plan_options`` tunes the kernels.
+    """
+    if log_func is None:
+        log_func = lambda msg: None  # noqa: E731
+    if prof is None:
+        prof = _NoProf()
+    if not isinstance(device, torch.device):
+        device = torch.device(device)
+    assert device.type == "cuda", \
+        f"execute_param_transfer runs on the GPU reshard engine; got device {device}"
+    if rank is None:
+        rank = _current_rank(world)
+
+    ops = [op for op in transfer_ops if op.dst_rank == rank]
+    normal = [f for f, t in expected_sub_fields if not _is_meta_field(t)]
+    scalars = [f for f, t in expected_sub_fields if _is_meta_field(t)]
+    recast = dict(recast or {})
+
+    def source(r: int) -> StateDict:
+        if fake_source_state_dicts is not None and r in fake_source_state_dicts:
+            return fake_source_state_dicts[r]
+        if r == rank:
+            return source_state_dict
+        raise NotImplementedError(
+            f"[{rank}]: piece from rank {r} needs a cross-GPU exchange, which this one-GPU build "
+            "does not implement; pass the peer shards as fake_source_state_dicts")
+
+    src_specs: Dict[Tuple[int, str, str], SlotSpec] = {}
+    for op in ops:
+        sd = source(op.src_rank)
+        assert op.param_name in sd, f"[{rank}]: param missing in source {op.param_name}"
+        entry = sd[op.param_name]
+        for f in normal:
+            assert f in entry, f"expected_sub_fields mismatch: {op.param_name} has no {f}"
+            t = entry[f]
+            src_specs[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(t.shape), t.dtype)
+
+    prof.start("execute schedule lowering")
+    plan = ReshardPlan(ops, src_specs, normal, recast=recast, options=plan_options)
+    prof.stop("execute schedule lowering")
+    log_func(f"=== reshard plan: {plan.n_pieces} pieces, {len(plan.peers)} peers, "
+             f"{plan.info.buffer_bytes / 1e6:.1f} MB of buffers ===")
+
+    sources = {r: source(r) for r in plan.peers}
+    for r, sd in sources.items():
+        for name, entry in sd.items():
+            for f in normal:
+                t = entry.get(f)
+                if t is not None and t.device != device and (r, name, f) in src_specs:
+                    raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, "
+                                         f"not on {device}")
+
+    with torch.cuda.device(device):
+        buffers = plan.alloc_buffers(device)
+        target = plan.alloc_dst(device)
+        prof.start("execute pack")
+        plan.pack(sources, buffers, stream)
+        prof.stop("execute pack")
+        prof.start("execute unpack")
+        plan.unpack(buffers, target, stream)
+        prof.stop("execute unpack")
+
+    # 1-element sub-fields ride along whole; the first op's source wins,
+    # matching tensors[0].clone() of migration.py:538.
+    for f in scalars:
+        for op in ops:
+            entry = target.get(op.param_name)
+            if entry is None or f in entry:
+                continue
+            src_entry = source(op.src_rank)[op.param_name]
+            if f in src_entry:
+                entry[f] = src_entry[f].to(device).clone()
+
+    ordered: StateDict = {}
+    field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
+    for name, entry in target.items():
+        ordered[name] = {f: entry[f] for f in field_order if f in entry}
+
+    del buffers
+    if forcefully_free:
+        for sd in sources.values():
+            for entry in sd.values():
+                for f in normal:
+                    if f in entry:
+                        forcefully_free_tensor(entry[f])
+    source_state_dict.clear()
+    plan.close()
+    return ordered
+
+
+def schedule_and_execute_param_transfer(
+    source_param_layout: ParamLayout,
+    target_param_layout: ParamLayout,
+    source_state_dict: StateDict,
+    other_context_dict: Dict[str, Any],
+    device: torch.device,
+    world: Optional[dist.ProcessGroup],
+    prof,
+    forcefully_free: bool,
+    log_func=None,
+    **kwargs,
+) -> StateDict:
+    """Schedule + execute + synchronize (Suika/migration.py:558-598)."""
+    if not isinstance(device, torch.device):
+        device = torch.device(device)
+    if prof is None:
+        prof = _NoProf()
+    prof.start("schedule")
+    schedule = schedule_param_transfer(source_param_layout, target_param_layout)
+    prof.stop("schedule")
+    prof.start("execute")
+    target = execute_param_transfer(
+        transfer_ops=schedule, source_state_dict=source_state_dict, device=device,
+        expected_sub_fields=other_context_dict["expected_sub_fields"], world=world,
+        forcefully_free=forcefully_free, prof=prof, log_func=log_func, **kwargs)
+    if device.type == "cuda":
+        torch.cuda.synchronize(device=device)
+    prof.stop("execute")
+    return target
+
+
+def merge_model_and_optimizer_state_dict(model: Module, optimizer: Optional[Optimizer],
+                                         other_context: Optional[Any]) -> Tuple[Dict, Dict]:
+    """{name: {"param", **optimizer.state[idx]}} plus the sub-field list
+    (Suika/migration.py:675-711)."""
+    model_state_dict = model.state_dict()
+    if optimizer:
+        osd = optimizer.state_dict()
+        other_context_dict = {"other_context": other_context, "param_groups": osd["param_groups"]}
+        opt_state = osd["state"]
+    else:
+        opt_state = {}
+        other_context_dict = {"other_context": other_context}
+    merged: Dict[str, Dict[str, Tensor]] = {}
+    for idx, (name, _) in enumerate(get_named_parameters_and_persistent_buffers(model)):
+        entry = {"param": model_state_dict[name]}
+        entry.update(opt_state.get(idx, {}))
+        merged[name] = entry
+        if "expected_sub_fields" not in other_context_dict:
+            other_context_dict["expected_sub_fields"] = [
+                (f, TensorMeta(t) if t.numel() == 1 else "normal") for f, t in entry.items()]
+    return merged, other_context_dict
+
+
+def split_model_and_optimizer_state_dict(model: Module, merged_state_dict: Dict[str, Dict[str, Tensor]],
+                                         other_context_dict: Dict[str, Any]) -> Tuple[Dict, Dict, Any]:
+    """Inverse of the merge, re-indexed by the new model's order
+    (Suika/migration.py:722-746)."""
+    model_state_dict = {}
+    by_name = {}
+    for name, entry in merged_state_dict.items():
+        model_state_dict[name] = entry["param"]
+        del entry["param"]
+        by_name[name] = entry
+    by_index = {idx: by_name[name]
+                for idx, (name, _) in enumerate(get_named_parameters_and_persistent_buffers(model))}
+    optimizer_state_dict = {"state": by_index,
+                            "param_groups": other_context_dict.get("param_groups", None)}
+    return model_state_dict, optimizer_state_dict, other_context_dict["other_context"]

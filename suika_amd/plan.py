@@ -1,0 +1,318 @@
+"""Compile a destination rank's TransferOps into a library plan and run it.
+
+``ReshardPlan`` is the bridge between the reference-shaped host API
+(``TransferOp`` lists and ``{name: {field: Tensor}}`` state dicts, as used by
+Suika/migration.py:397-556) and the C ABI of ``libsuika_reshard.so``:
+
+* every (source rank, name, field) tensor becomes a source slot, every
+  (name, field) of the destination a destination slot;
+* every source rank becomes a peer with one contiguous buffer;
+* every TransferOp x region x normal field becomes one ``sr_piece`` (in
+  schedule order, fields in ``fields`` order), pad rows of vocab-parallel
+  shards become ZERO pieces, and a ``recast`` target field (bf16) is written by
+  the unpack of its f32 source field.
+
+The plan is built once from shapes and dtypes and can then be executed on any
+tensors of those shapes: ``pack`` and ``unpack`` are asynchronous on the
+current HIP stream.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, List, Mapping, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+from .geometry import infer_dst_shard, local_matrix, lower_op, pad_boxes, view_axis
+from .meta import TensorMeta, TransferOp
+
+SrcKey = Tuple[int, str, str]   # (source rank, name, field)
+DstKey = Tuple[str, str]        # (name, field)
+
+_DTYPES = {
+    torch.uint8: _lib.SR_DT_U8,
+    torch.int8: _lib.SR_DT_U8,
+    torch.bool: _lib.SR_DT_U8,
+    torch.bfloat16: _lib.SR_DT_BF16,
+    torch.float16: _lib.SR_DT_F16,
+    torch.float32: _lib.SR_DT_F32,
+    torch.float64: _lib.SR_DT_F64,
+    torch.int32: _lib.SR_DT_I32,
+    torch.int64: _lib.SR_DT_I64,
+}
+for _name in ("float8_e4m3fn", "float8_e5m2", "float8_e4m3fnuz", "float8_e5m2fnuz"):
+    if hasattr(torch, _name):
+        _DTYPES[getattr(torch, _name)] = _lib.SR_DT_U8
+
+
+def sr_dtype(dtype: torch.dtype) -> int:
+    assert dtype in _DTYPES, f"dtype {dtype} is not supported by the reshard engine"
+    return _DTYPES[dtype]
+
+
+@dataclass
+class PlanOptions:
+    tile_bytes: int = 0          # 0 = library default
+    max_blocks: int = 0          # 0 = one workgroup per tile
+    nontemporal: bool = False
+    skip_coverage: bool = False
+
+    def to_c(self) -> _lib.SrPlanOptions:
+        flags = (_lib.SR_OPT_NONTEMPORAL if self.nontemporal else 0) | \
+                (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0)
+        return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, flags, 0)
+
+
+@dataclass(frozen=True)
+class SlotSpec:
+    shape: Tuple[int, ...]
+    dtype: torch.dtype
+
+
+def _matrix_of(shape: Sequence[int], view: int) -> Tuple[int, int]:
+    shape = [int(s) for s in shape]
+    if not shape:
+        return 1, 1
+    if view == 1:
+        r = 1
+        for s in shape[:-1]:
+            r *= s
+        return r, shape[-1]
+    c = 1
+    for s in shape[1:]:
+        c *= s
+    return shape[0], c
+
+
+def _stream_handle(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    if isinstance(stream, torch.cuda.Stream):
+        return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(int(stream))
+
+
+class ReshardPlan:
+    """Pack/unpack plan of one destination rank's share of a reshard."""
+
+    def __init__(self, ops: Sequence[TransferOp],
+                 src_specs: Mapping[SrcKey, SlotSpec],
+                 fields: Sequence[str],
+                 recast: Optional[Mapping[str, str]] = None,
+                 options: Optional[PlanOptions] = None):
+        """``src_specs`` gives the shape/dtype of every source (rank, name,
+        field) the ops read; ``fields`` are the normal sub-fields moved;
+        ``recast`` maps a bf16 destination field to the f32 field it is
+        rounded from (e.g. ``{"param": "master"}``)."""
+        self._handle = ctypes.c_void_p()
+        recast = dict(recast or {})
+        for tgt, srcf in recast.items():
+            assert tgt not in fields or tgt == srcf, \
+                f"recast target {tgt!r} is also a copied field"
+            assert srcf in fields, f"recast source field {srcf!r} is not moved"
+        self.fields = list(fields)
+        self.recast = recast
+        self.options = options or PlanOptions()
+
+        by_name: Dict[str, List[TransferOp]] = {}
+        for op in ops:
+            by_name.setdefault(op.param_name, []).append(op)
+        dst_ranks = {op.dst_rank for op in ops}
+        assert len(dst_ranks) <= 1, f"ops target several ranks {sorted(dst_ranks)}"
+        self.dst_rank = dst_ranks.pop() if dst_ranks else None
+
+        self.peers: List[int] = sorted({op.src_rank for op in ops})
+        peer_index = {r: i for i, r in enumerate(self.peers)}
+
+        self.src_keys: List[SrcKey] = []
+        src_index: Dict[SrcKey, int] = {}
+        self.src_specs: Dict[SrcKey, SlotSpec] = {}
+        self.dst_keys: List[DstKey] = []
+        dst_index: Dict[DstKey, int] = {}
+        self.dst_specs: Dict[DstKey, SlotSpec] = {}
+        self.dst_metas: Dict[str, TensorMeta] = {}
+
+        c_src: List[_lib.SrTensor] = []
+        c_dst: List[_lib.SrTensor] = []
+        c_pieces: List[_lib.SrPiece] = []
+
+        def src_slot(key: SrcKey, view: int) -> int:
+            if key not in src_index:
+                assert key in src_specs, f"missing source tensor {key}"
+                spec = src_specs[key]
+                r, c = _matrix_of(spec.shape, view)
+                src_index[key] = len(self.src_keys)
+                self.src_keys.append(key)
+                self.src_specs[key] = spec
+                c_src.append(_lib.SrTensor(r, c, sr_dtype(spec.dtype), 0))
+            return src_index[key]
+
+        def dst_slot(key: DstKey, meta: TensorMeta, dtype: torch.dtype, view: int) -> int:
+            if key not in dst_index:
+                r, c = local_matrix(meta, view)
+                dst_index[key] = len(self.dst_keys)
+                self.dst_keys.append(key)
+                self.dst_specs[key] = SlotSpec(tuple(int(s) for s in meta.actual_shape()), dtype)
+                c_dst.append(_lib.SrTensor(r, c, sr_dtype(dtype), 0))
+            else:
+                assert self.dst_specs[key].dtype == dtype, \
+                    f"{key}: sources disagree on dtype ({self.dst_specs[key].dtype} vs {dtype})"
+            return dst_index[key]
+
+        self.piece_owner: List[Tuple[str, int]] = []   # (name, peer) per piece
+        for name, name_ops in by_name.items():
+            dst_shard = infer_dst_shard(name_ops)
+            self.dst_metas[name] = dst_shard
+            view = view_axis(dst_shard, *[op.src_meta for op in name_ops])
+            field_dtype: Dict[str, torch.dtype] = {}
+            for op in name_ops:
+                for f in self.fields:
+                    key = (op.src_rank, name, f)
+                    assert key in src_specs, f"[{op.src_rank}]: param missing in source {name}/{f}"
+                    op.check_send(src_specs[key].shape)
+                    field_dtype.setdefault(f, src_specs[key].dtype)
+                    assert field_dtype[f] == src_specs[key].dtype, \
+                        f"{name}/{f}: dtype differs between sources"
+            # destination slots of every field, then the pieces that fill them
+            dslot: Dict[str, int] = {}
+            for f in self.fields:
+                dslot[f] = dst_slot((name, f), dst_shard, field_dtype[f], view)
+                for tgt, sf in recast.items():
+                    if sf == f:
+                        assert field_dtype[f] == torch.float32, \
+                            f"{name}/{f}: recast source must be float32"
+                        dslot[tgt] = dst_slot((name, tgt), dst_shard, torch.bfloat16, view)
+            for op in name_ops:
+                peer = peer_index[op.src_rank]
+                for reg in lower_op(op, dst_shard):
+                    for f in self.fields:
+                        s = src_slot((op.src_rank, name, f), view)
+                        tgt = [t for t, sf in recast.items() if sf == f]
+                        if tgt:
+                            kind, d, d2 = _lib.SR_PIECE_RECAST, dslot[f], dslot[tgt[0]]
+                        else:
+                            kind, d, d2 = _lib.SR_PIECE_COPY, dslot[f], -1
+                        c_pieces.append(_lib.SrPiece(kind, peer, s, d, d2, 0, reg.rows, reg.cols,
+                                                     reg.src_row, reg.src_col,
+                                                     reg.dst_row, reg.dst_col))
+                        self.piece_owner.append((name, peer))
+            for box in pad_boxes(dst_shard, view):
+                for f, slot in dslot.items():
+                    c_pieces.append(_lib.SrPiece(_lib.SR_PIECE_ZERO, 0, -1, slot, -1, 0,
+                                                 box.rows, box.cols, 0, 0, box.row, box.col))
+                    self.piece_owner.append((name, -1))
+
+        self.n_pieces = len(c_pieces)
+        self.pieces = c_pieces
+        self.c_src = c_src
+        self.c_dst = c_dst
+        L = _lib.lib()
+        src_arr = (_lib.SrTensor * max(1, len(c_src)))(*c_src)
+        dst_arr = (_lib.SrTensor * max(1, len(c_dst)))(*c_dst)
+        pc_arr = (_lib.SrPiece * max(1, len(c_pieces)))(*c_pieces)
+        opt = self.options.to_c()
+        rc = L.sr_plan_create(src_arr, len(c_src), dst_arr, len(c_dst), len(self.peers),
+                              pc_arr, len(c_pieces), ctypes.byref(opt), ctypes.byref(self._handle))
+        _lib.check(rc, "sr_plan_create")
+        self.peer_bytes: List[int] = []
+        for i in range(len(self.peers)):
+            b = ctypes.c_uint64()
+            _lib.check(L.sr_plan_peer_bytes(self._handle, i, ctypes.byref(b)), "sr_plan_peer_bytes")
+            self.peer_bytes.append(int(b.value))
+        info = _lib.SrPlanInfo()
+        _lib.check(L.sr_plan_info_get(self._handle, ctypes.byref(info)), "sr_plan_info_get")
+        self.info = info
+
+    # -------------------------------------------------------------- sizes
+    @property
+    def pack_bytes(self) -> int:
+        return int(self.info.pack_bytes_read + self.info.pack_bytes_written)
+
+    @property
+    def unpack_bytes(self) -> int:
+        return int(self.info.unpack_bytes_read + self.info.unpack_bytes_written)
+
+    def piece_offset(self, k: int) -> int:
+        off = ctypes.c_uint64()
+        _lib.check(_lib.lib().sr_plan_piece_offset(self._handle, k, ctypes.byref(off)),
+                   "sr_plan_piece_offset")
+        return int(off.value)
+
+    # --------------------------------------------------------- allocation
+    def alloc_buffers(self, device) -> List[torch.Tensor]:
+        """One byte buffer per peer (torch's allocator aligns to 512 bytes)."""
+        return [torch.empty(max(1, n), dtype=torch.uint8, device=device) for n in self.peer_bytes]
+
+    def alloc_dst(self, device) -> Dict[str, Dict[str, torch.Tensor]]:
+        out: Dict[str, Dict[str, torch.Tensor]] = {}
+        for (name, field) in self.dst_keys:
+            spec = self.dst_specs[(name, field)]
+            out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
+        return out
+
+    # ---------------------------------------------------------- execution
+    @staticmethod
+    def _check_tensor(t: torch.Tensor, spec: SlotSpec, what) -> int:
+        assert isinstance(t, torch.Tensor), f"{what}: not a tensor"
+        assert t.is_cuda, f"{what}: tensor is on {t.device}, the reshard engine needs HBM"
+        assert t.is_contiguous(), f"{what}: tensor is not contiguous"
+        assert tuple(t.shape) == tuple(spec.shape), f"{what}: shape {tuple(t.shape)} != {spec.shape}"
+        assert t.dtype == spec.dtype, f"{what}: dtype {t.dtype} != {spec.dtype}"
+        return t.data_ptr()
+
+    def src_pointers(self, sources: Mapping[int, Mapping[str, Mapping[str, torch.Tensor]]]):
+        ptrs = []
+        for key in self.src_keys:
+            rank, name, field = key
+            t = sources[rank][name][field]
+            ptrs.append(self._check_tensor(t, self.src_specs[key], key))
+        return ptrs
+
+    def dst_pointers(self, dst: Mapping[str, Mapping[str, torch.Tensor]]):
+        return [self._check_tensor(dst[name][field], self.dst_specs[(name, field)], (name, field))
+                for (name, field) in self.dst_keys]
+
+    def buf_pointers(self, buffers: Sequence[torch.Tensor]):
+        assert len(buffers) == len(self.peers), f"{len(buffers)} buffers for {len(self.peers)} peers"
+        ptrs = []
+        for i, b in enumerate(buffers):
+            assert b.is_cuda and b.is_contiguous(), f"buffer {i} must be a contiguous HBM tensor"
+            assert b.numel() * b.element_size() >= self.peer_bytes[i], \
+                f"buffer {i} holds {b.numel() * b.element_size()} bytes, needs {self.peer_bytes[i]}"
+            ptrs.append(b.data_ptr())
+        return ptrs
+
+    @staticmethod
+    def _carray(ptrs: List[int]) -> ctypes.Array:
+        return (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
+
+    def pack_ptrs(self, src_ptrs: List[int], buf_ptrs: List[int], stream=None) -> None:
+        rc = _lib.lib().sr_pack(self._handle, self._carray(src_ptrs), self._carray(buf_ptrs),
+                                _stream_handle(stream))
+        _lib.check(rc, "sr_pack")
+
+    def unpack_ptrs(self, buf_ptrs: List[int], dst_ptrs: List[int], stream=None) -> None:
+        rc = _lib.lib().sr_unpack(self._handle, self._carray(buf_ptrs), self._carray(dst_ptrs),
+                                  _stream_handle(stream))
+        _lib.check(rc, "sr_unpack")
+
+    def pack(self, sources, buffers, stream=None) -> None:
+        """Source shards -> peer buffers (async on ``stream``)."""
+        self.pack_ptrs(self.src_pointers(sources), self.buf_pointers(buffers), stream)
+
+    def unpack(self, buffers, dst, stream=None) -> None:
+        """Peer buffers -> destination shards (async on ``stream``)."""
+        self.unpack_ptrs(self.buf_pointers(buffers), self.dst_pointers(dst), stream)
+
+    def close(self) -> None:
+        if getattr(self, "_handle", None) is not None and self._handle.value:
+            _lib.lib().sr_plan_destroy(self._handle)
+            self._handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,105 @@
+"""Small reshard cases shared by the CPU and GPU suites.
+
+* the reference's own test shapes -- GPT-TEST (gpt_model.py:152-158),
+  Llama-TEST (llama_model.py:169-176), Qwen2-TEST (qwen_model.py:178-189) --
+  under TP 1<->2<->4<->8 and PP 1<->2<->4 changes;
+* the five benchmark workloads at a small shape with the same plan change,
+  kinds and fields (vocab sizes chosen so padded rows appear);
+* Qwen2-TEST at TP2: ``down_proj [1024, 2028]`` split along the last dim gives
+  1014-element rows (4056 B f32 / 2028 B bf16) at an 8112 / 4056 B stride --
+  not multiples of 16 bytes -- so the kernels' narrow-vector paths run.
+"""
+from __future__ import annotations
+
+from dataclasses import replace
+from typing import Dict, List
+
+import torch
+
+from suika_amd.inventory import ModelSpec, Parallel
+from suika_amd.meta import vocab_padded
+from suika_amd.workloads import CONFIGS, Workload, scaled
+
+_F32_3 = (("param", torch.float32), ("exp_avg", torch.float32), ("exp_avg_sq", torch.float32))
+_BF16_4 = (("param", torch.bfloat16), ("master", torch.float32),
+           ("exp_avg", torch.float32), ("exp_avg_sq", torch.float32))
+
+GPT_TEST = ModelSpec("gpt", n_layer=4, hidden=16, n_head=4, ffn=64, vocab=128)
+LLAMA_TEST = ModelSpec("llama", n_layer=2, hidden=16, n_head=4, ffn=64, vocab=128)
+QWEN2_TEST = ModelSpec("qwen", n_layer=2, hidden=1024, n_head=4, n_kv_head=2, head_dim=256,
+                       ffn=2028, vocab=1024)
+
+
+def _w(key, model, src, dst, dst_pp, dst_tp, fields=_BF16_4, recast=(), seed=0,
+       param_dtype=torch.bfloat16) -> Workload:
+    src_fields = tuple(f for f, _ in fields if f not in dict(recast))
+    return Workload(key=key, model=model, src=src, dst=dst, dst_pp=dst_pp, dst_tp=dst_tp,
+                    src_fields=src_fields, field_dtypes=fields, recast=tuple(recast), seed=seed,
+                    param_dtype=param_dtype)
+
+
+def reference_test_cases() -> List[Workload]:
+    out = []
+    for (stp, spp), (dtp, dpp) in [((1, 1), (2, 1)), ((2, 1), (4, 1)), ((4, 1), (2, 1)),
+                                   ((4, 1), (1, 1)), ((2, 2), (4, 1)), ((1, 4), (2, 2)),
+                                   ((2, 1), (1, 2))]:
+        for dtp_i in sorted({0, dtp - 1}):
+            for dpp_i in sorted({0, dpp - 1}):
+                out.append(_w(f"gpt_test_tp{stp}pp{spp}_tp{dtp}pp{dpp}_d{dpp_i}.{dtp_i}",
+                              GPT_TEST, Parallel(stp, spp), Parallel(dtp, dpp), dpp_i, dtp_i,
+                              fields=_F32_3, param_dtype=torch.float32, seed=11))
+    for (stp, spp), (dtp, dpp) in [((4, 1), (2, 1)), ((2, 1), (4, 1)), ((1, 2), (4, 1)),
+                                   ((4, 2), (1, 1))]:
+        for dtp_i in sorted({0, dtp - 1}):
+            out.append(_w(f"llama_test_tp{stp}pp{spp}_tp{dtp}pp{dpp}_d0.{dtp_i}",
+                          LLAMA_TEST, Parallel(stp, spp), Parallel(dtp, dpp), 0, dtp_i, seed=12))
+    return out
+
+
+def alignment_cases() -> List[Workload]:
+    return [
+        _w("qwen2_test_tp2_tp1", QWEN2_TEST, Parallel(2), Parallel(1), 0, 0, seed=13),
+        _w("qwen2_test_tp1_tp2_d1", QWEN2_TEST, Parallel(1), Parallel(2), 0, 1, seed=14),
+        _w("qwen2_test_tp1_tp2_recast", QWEN2_TEST, Parallel(1), Parallel(2), 0, 0,
+           fields=(("master", torch.float32), ("exp_avg", torch.float32),
+                   ("exp_avg_sq", torch.float32), ("param", torch.bfloat16)),
+           recast=(("param", "master"),), seed=15),
+    ]
+
+
+def scaled_configs() -> Dict[str, Workload]:
+    """The five benchmark plan changes at a shape the oracle runs in seconds."""
+    c = CONFIGS
+    return {
+        "gpt125m_tp2_tp4": scaled(c["gpt125m_tp2_tp4"], n_layer=3, hidden=64, ffn=256, vocab=1000,
+                                  n_head=4),
+        "llama7b_tp4pp2_tp2pp2": scaled(c["llama7b_tp4pp2_tp2pp2"], n_layer=4, hidden=64, ffn=176,
+                                        vocab=1000, n_head=8),
+        "llama13b_tp8_tp4pp2": scaled(c["llama13b_tp8_tp4pp2"], n_layer=4, hidden=64, ffn=128,
+                                      vocab=1000, n_head=8),
+        "gpt6.7b_tp1pp4_tp8": scaled(c["gpt6.7b_tp1pp4_tp8"], n_layer=4, hidden=64, ffn=256,
+                                     vocab=1000, n_head=8, positions=32),
+        "qwen7b_tp2_tp4": scaled(c["qwen7b_tp2_tp4"], n_layer=2, hidden=64, ffn=96, vocab=1000,
+                                 n_head=8, n_kv_head=4, head_dim=8),
+    }
+
+
+def padded_vocab_cases() -> List[Workload]:
+    """Vocab-parallel tables whose padding shows up on both sides."""
+    m = ModelSpec("llama", n_layer=2, hidden=32, n_head=4, ffn=64, vocab=712, vocab_parallel=True,
+                  pad_multiple=64)
+    out = []
+    for stp, dtp in [(2, 4), (4, 2), (1, 8), (8, 1), (2, 8)]:
+        # last destination rank that still holds vocabulary rows (a shard of
+        # padding only is rejected by the schedule)
+        per = vocab_padded(m.vocab, dtp, m.pad_multiple) // dtp
+        last = (m.vocab - 1) // per
+        for d in sorted({0, last}):
+            out.append(_w(f"vocab_pad_tp{stp}_tp{dtp}_d{d}", m, Parallel(stp), Parallel(dtp), 0, d,
+                          seed=16))
+    return out
+
+
+def all_small_cases() -> List[Workload]:
+    return (reference_test_cases() + alignment_cases() + list(scaled_configs().values())
+            + padded_vocab_cases())

@@ -1,0 +1,155 @@
+"""The C ABI library: loads, exports what include/suika_reshard.h declares,
+and rejects invalid plans before anything reaches a GPU (host-only calls)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from suika_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "suika_reshard.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sr_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_loads_and_version():
+    L = _lib.lib()
+    assert L.sr_abi_version() == _lib.ABI_VERSION == 1
+
+
+def test_every_declared_symbol_is_exported():
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared:
+        assert hasattr(raw, name), f"{name} not exported"
+
+
+def test_selftest_division_constants():
+    assert _lib.lib().sr_selftest() == 0, _lib.last_error()
+
+
+def _plan(src, dst, n_peers, pieces, options=None):
+    L = _lib.lib()
+    s = (_lib.SrTensor * max(1, len(src)))(*[_lib.SrTensor(r, c, d, 0) for r, c, d in src])
+    d = (_lib.SrTensor * max(1, len(dst)))(*[_lib.SrTensor(r, c, t, 0) for r, c, t in dst])
+    p = (_lib.SrPiece * max(1, len(pieces)))(*pieces)
+    h = ctypes.c_void_p()
+    opt = ctypes.byref(options) if options is not None else None
+    rc = L.sr_plan_create(s, len(src), d, len(dst), n_peers, p, len(pieces), opt, ctypes.byref(h))
+    return rc, h
+
+
+def piece(kind=_lib.SR_PIECE_COPY, peer=0, src=0, dst=0, dst2=-1, rows=4, cols=8,
+          sr=0, sc=0, dr=0, dc=0):
+    return _lib.SrPiece(kind, peer, src, dst, dst2, 0, rows, cols, sr, sc, dr, dc)
+
+
+F32, BF16 = _lib.SR_DT_F32, _lib.SR_DT_BF16
+
+
+def test_valid_plan_and_buffer_layout():
+    # dst [4, 16] = two [4, 8] column halves from two sources (a row-parallel merge)
+    rc, h = _plan([(4, 8, F32), (4, 8, F32)], [(4, 16, F32)], 2,
+                  [piece(src=0, peer=0, dc=0), piece(src=1, peer=1, dc=8)])
+    assert rc == 0, _lib.last_error()
+    L = _lib.lib()
+    b = ctypes.c_uint64()
+    assert L.sr_plan_peer_bytes(h, 0, ctypes.byref(b)) == 0 and b.value == 4 * 8 * 4
+    info = _lib.SrPlanInfo()
+    assert L.sr_plan_info_get(h, ctypes.byref(info)) == 0
+    assert info.n_pieces == 2 and info.pack_bytes_read == 256 and info.unpack_bytes_written == 256
+    off = ctypes.c_uint64()
+    assert L.sr_plan_piece_offset(h, 1, ctypes.byref(off)) == 0 and off.value == 0
+    L.sr_plan_destroy(h)
+
+
+def test_buffer_offsets_are_256_aligned():
+    pcs = [piece(src=0, peer=0, rows=1, cols=3, sr=i, dr=i) for i in range(4)]
+    rc, h = _plan([(4, 3, F32)], [(4, 3, F32)], 1, pcs)
+    assert rc == 0, _lib.last_error()
+    L = _lib.lib()
+    offs = []
+    for k in range(4):
+        o = ctypes.c_uint64()
+        L.sr_plan_piece_offset(h, k, ctypes.byref(o))
+        offs.append(o.value)
+    assert offs == [0, 256, 512, 768]
+    b = ctypes.c_uint64()
+    L.sr_plan_peer_bytes(h, 0, ctypes.byref(b))
+    assert b.value == 768 + 12
+    L.sr_plan_destroy(h)
+
+
+@pytest.mark.parametrize("bad,code", [
+    (dict(sr=1), _lib.SR_EBOUNDS),                 # source rows past the end
+    (dict(dc=1), _lib.SR_EBOUNDS),                 # destination cols past the end
+    (dict(peer=3), _lib.SR_EINVAL),                # no such peer
+    (dict(src=5), _lib.SR_EINVAL),                 # no such source slot
+    (dict(rows=0), _lib.SR_EINVAL),                # empty region
+    (dict(kind=7), _lib.SR_EINVAL),                # unknown kind
+    (dict(dst2=0), _lib.SR_EINVAL),                # COPY with a second target
+])
+def test_invalid_pieces_rejected(bad, code):
+    kw = dict(src=0, peer=0)
+    kw.update(bad)
+    rc, h = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece(**kw)])
+    assert rc == code, (rc, _lib.last_error())
+    assert not h.value
+    assert _lib.last_error()
+
+
+def test_dtype_mismatch_rejected():
+    rc, _ = _plan([(4, 8, F32)], [(4, 8, BF16)], 1, [piece()])
+    assert rc == _lib.SR_EDTYPE
+
+
+def test_overlap_and_holes_rejected():
+    rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece(), piece(rows=1, cols=1, dr=2, dc=2)])
+    assert rc == _lib.SR_EOVERLAP and "overlapping" in _lib.last_error()
+    rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece(rows=3)])
+    assert rc == _lib.SR_EOVERLAP and "cover" in _lib.last_error()
+    opt = _lib.SrPlanOptions(0, 0, _lib.SR_OPT_SKIP_COVERAGE, 0)
+    rc, h = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece(rows=3)], options=opt)
+    assert rc == 0
+    _lib.lib().sr_plan_destroy(h)
+
+
+def test_recast_and_zero_rules():
+    # f32 source -> f32 dst 0 and bf16 dst 1; zero fill the remaining rows of both
+    pcs = [piece(kind=_lib.SR_PIECE_RECAST, dst=0, dst2=1, rows=3),
+           piece(kind=_lib.SR_PIECE_ZERO, src=-1, dst=0, rows=1, dr=3),
+           piece(kind=_lib.SR_PIECE_ZERO, src=-1, dst=1, rows=1, dr=3)]
+    rc, h = _plan([(4, 8, F32)], [(4, 8, F32), (4, 8, BF16)], 1, pcs)
+    assert rc == 0, _lib.last_error()
+    info = _lib.SrPlanInfo()
+    _lib.lib().sr_plan_info_get(h, ctypes.byref(info))
+    assert info.unpack_bytes_written == 3 * 8 * 4 + 3 * 8 * 2 + 8 * 4 + 8 * 2
+    _lib.lib().sr_plan_destroy(h)
+    # bf16 source cannot be recast
+    rc, _ = _plan([(4, 8, BF16)], [(4, 8, F32), (4, 8, BF16)], 1,
+                  [piece(kind=_lib.SR_PIECE_RECAST, dst=0, dst2=1)])
+    assert rc == _lib.SR_EDTYPE
+    # ZERO takes no source
+    rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece(kind=_lib.SR_PIECE_ZERO, src=0)])
+    assert rc == _lib.SR_EINVAL
+
+
+def test_options_validation():
+    for opt in (_lib.SrPlanOptions(3000, 0, 0, 0), _lib.SrPlanOptions(0, 0, 0x80, 0),
+                _lib.SrPlanOptions(0, 0, 0, 1)):
+        rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece()], options=opt)
+        assert rc == _lib.SR_EINVAL
+
+
+def test_python_errors_are_assertion_errors():
+    with pytest.raises(AssertionError):
+        _lib.check(_lib.SR_EBOUNDS, "x")
+    with pytest.raises(_lib.ReshardError):
+        _lib.check(_lib.SR_EHIP, "x")

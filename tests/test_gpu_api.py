@@ -1,0 +1,101 @@
+"""Reference-shaped API semantics of the GPU path (Suika/migration.py:397-556)
+and the boundary's error handling, which rejects bad input before any launch."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from suika_amd import PlanError, TensorMeta, TransferOp, execute_param_transfer
+from suika_amd.plan import ReshardPlan, SlotSpec
+from tests import cases
+from tests.harness import global_state, oracle_dest, source_shards, t2np, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def _names(w):
+    spl, _ = w.layouts()
+    return {n for metas in spl.layout.values() for n in metas}
+
+
+def test_execute_semantics_step_and_clear():
+    w = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
+    print(f"[gpu api] {w.key}", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    dev = torch.device("cuda")
+    fake = to_device(srcs, w, dev)
+    step_meta = TensorMeta(torch.tensor(7.0))
+    for r, sd in fake.items():
+        for name, e in sd.items():
+            e["step"] = torch.tensor(float(r + 10))   # CPU scalar, as AdamW keeps it
+    own = fake[w.dst_rank] if w.dst_rank in fake else {}
+    own_copy = dict(own)
+    fields = [("param", "normal"), ("step", step_meta), ("master", "normal"),
+              ("exp_avg", "normal"), ("exp_avg_sq", "normal")]
+    out = execute_param_transfer(w.ops(), own_copy, dev, fields, rank=w.dst_rank,
+                                 fake_source_state_dicts=fake)
+    torch.cuda.synchronize()
+    assert own_copy == {}, "source_state_dict is cleared in place"
+    for name, e in want.items():
+        assert list(out[name]) == ["param", "step", "master", "exp_avg", "exp_avg_sq"]
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+        assert out[name]["step"].device.type == "cuda" and out[name]["step"].numel() == 1
+
+
+def test_execute_rejects_remote_without_exchange():
+    w = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
+    ops = w.ops()
+    with pytest.raises(NotImplementedError, match="cross-GPU exchange"):
+        execute_param_transfer(ops, {}, torch.device("cuda"), [("param", "normal")], rank=w.dst_rank)
+
+
+def test_execute_rejects_cpu_and_bad_shapes():
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    cpu = to_device(srcs, w, "cpu")
+    fields = [(f, "normal") for f in w.src_fields]
+    with pytest.raises(AssertionError):
+        execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                               fake_source_state_dicts=cpu)
+    gpu = to_device(srcs, w, "cuda")
+    r = next(iter(gpu))
+    name = next(iter(gpu[r]))
+    gpu[r][name]["param"] = gpu[r][name]["param"].reshape(-1)[:-1].clone()
+    with pytest.raises(AssertionError, match="shape"):
+        execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                               fake_source_state_dicts=gpu)
+
+
+def test_boundary_rejects_misaligned_and_null_pointers():
+    src = TensorMeta(name="a", dtype=torch.float32, shape=(64, 32), tp_meta=(0, 0, 2))
+    dst = TensorMeta(name="a", dtype=torch.float32, shape=(64, 32), tp_meta=(0, 0, 1))
+    ops = [TransferOp("a", 0, 0, src, TensorMeta(name="a", dtype=torch.float32, shape=(64, 32),
+                                                 tp_meta=(0, 0, 2)), dst),
+           TransferOp("a", 1, 0, TensorMeta(name="a", dtype=torch.float32, shape=(64, 32),
+                                            tp_meta=(0, 1, 2)),
+                      TensorMeta(name="a", dtype=torch.float32, shape=(64, 32), tp_meta=(0, 1, 2)), dst)]
+    specs = {(0, "a", "param"): SlotSpec((32, 32), torch.float32),
+             (1, "a", "param"): SlotSpec((32, 32), torch.float32)}
+    plan = ReshardPlan(ops, specs, ["param"])
+    s0 = torch.randn(32, 32, device="cuda")
+    s1 = torch.randn(32, 32, device="cuda")
+    bufs = plan.alloc_buffers("cuda")
+    bp = plan.buf_pointers(bufs)
+    with pytest.raises(PlanError, match="aligned"):
+        plan.pack_ptrs([s0.data_ptr() + 2, s1.data_ptr()], bp)
+    with pytest.raises(PlanError, match="aligned"):
+        plan.pack_ptrs([s0.data_ptr(), s1.data_ptr()], [bp[0] + 8, bp[1]])
+    with pytest.raises(PlanError, match="null"):
+        plan.pack_ptrs([0, s1.data_ptr()], bp)
+    # the valid call still works after the rejected ones
+    dst_t = plan.alloc_dst("cuda")
+    plan.pack({0: {"a": {"param": s0}}, 1: {"a": {"param": s1}}}, bufs)
+    plan.unpack(bufs, dst_t)
+    torch.cuda.synchronize()
+    assert torch.equal(dst_t["a"]["param"], torch.cat([s0, s1], 0))
+    plan.close()

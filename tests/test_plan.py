@@ -1,0 +1,145 @@
+"""Host side of the product path, checked on the CPU:
+
+* ``schedule_param_transfer`` (suika_amd.meta) chooses the same source and
+  piece for every op as the oracle's restatement of the reference schedule;
+* executing a ``ReshardPlan``'s pieces with numpy (pack into the library's
+  buffer layout, then unpack) reproduces the oracle bit for bit -- this pins
+  the lowering (geometry), the buffer offsets and the coverage check;
+* the benchmark plans have the documented sizes (P, D, pieces).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import reshard_oracle as O
+from suika_amd import ParamLayout, TensorMeta, schedule_param_transfer
+from suika_amd.geometry import lower_op
+from suika_amd.plan import ReshardPlan, SlotSpec
+from suika_amd.workloads import CONFIG_ORDER, CONFIGS, fields_of
+from tests import cases
+from tests.harness import (expected_dest, global_state, index_state, oracle_dest, simulate_plan,
+                           source_shards, to_olayout)
+
+SMALL = cases.all_small_cases()
+
+
+def _names(w):
+    spl, _ = w.layouts()
+    out = set()
+    for metas in spl.layout.values():
+        out |= set(metas)
+    return out
+
+
+def _sig(m):
+    return (tuple(m.tp) if m.tp else None, m.rows)
+
+
+@pytest.mark.parametrize("w", SMALL + [CONFIGS[k] for k in CONFIG_ORDER],
+                         ids=[w.key for w in SMALL] + CONFIG_ORDER)
+@pytest.mark.parametrize("min_peers", [1, 2])
+def test_schedule_matches_oracle(w, min_peers):
+    spl, tpl = w.layouts()
+    ours = schedule_param_transfer(spl, tpl, minimum_est_peers=min_peers)
+    ref = O.schedule(to_olayout(spl), to_olayout(tpl), minimum_est_peers=min_peers)
+    assert len(ours) == len(ref)
+    for a, b in zip(ours, ref):
+        assert (a.param_name, a.src_rank, a.dst_rank) == (b.name, b.src, b.dst)
+        assert (tuple(a.dst_meta.tp_meta) if a.dst_meta.tp_meta else None, a.dst_meta.rows) == _sig(b.dst_meta)
+
+
+def test_schedule_respects_nccl_ib_disable(monkeypatch):
+    w = cases.scaled_configs()["gpt6.7b_tp1pp4_tp8"]
+    spl, tpl = w.layouts()
+    monkeypatch.setenv("NCCL_IB_DISABLE", "1")
+    a = schedule_param_transfer(spl, tpl)
+    b = schedule_param_transfer(spl, tpl, minimum_est_peers=2)
+    assert [(o.param_name, o.src_rank) for o in a] == [(o.param_name, o.src_rank) for o in b]
+
+
+def test_schedule_rejects_missing_source():
+    spl = ParamLayout.from_metas({0: {"a": TensorMeta(name="a", dtype=torch.float32, shape=(4, 4),
+                                                      tp_meta=(0, 0, 2))}})
+    tpl = ParamLayout.from_metas({0: {"a": TensorMeta(name="a", dtype=torch.float32, shape=(4, 4),
+                                                      tp_meta=(0, 0, 1))}})
+    with pytest.raises(AssertionError, match="not present in any source"):
+        schedule_param_transfer(spl, tpl)
+
+
+def _plan_for(w, srcs_np=None):
+    ops = w.ops()
+    dt = w.dtypes
+    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
+             for op in ops for f in w.src_fields}
+    return ReshardPlan(ops, specs, fields_of(w), recast=w.recast_map)
+
+
+def _esize(dt_code):
+    from suika_amd import _lib
+    return {_lib.SR_DT_U8: 1, _lib.SR_DT_BF16: 2, _lib.SR_DT_F16: 2, _lib.SR_DT_F32: 4,
+            _lib.SR_DT_F64: 8, _lib.SR_DT_I32: 4, _lib.SR_DT_I64: 8}[dt_code]
+
+
+@pytest.mark.parametrize("w", SMALL, ids=[w.key for w in SMALL])
+@pytest.mark.parametrize("payload", ["seeded", "index"])
+def test_plan_simulation_matches_oracle(w, payload):
+    glob = (global_state if payload == "seeded" else index_state)(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    plan = _plan_for(w)
+    got = simulate_plan(plan, srcs, _esize)
+    want = oracle_dest(w, srcs)
+    closed = expected_dest(w, glob)
+    assert {k[0] for k in got} == set(want)
+    for (name, f), arr in got.items():
+        np.testing.assert_array_equal(arr, want[name][f], err_msg=f"{name}/{f}")
+        np.testing.assert_array_equal(arr, closed[name][f], err_msg=f"{name}/{f}")
+    plan.close()
+
+
+# P (bytes read by pack), D (bytes written by unpack), pieces per field.
+DOCUMENTED = {
+    "gpt125m_tp2_tp4": (0.835e9, 0.835e9, 147),
+    "llama7b_tp4pp2_tp2pp2": (23.585e9, 23.585e9, 258),
+    "llama13b_tp8_tp4pp2": (22.780e9, 22.780e9, 323),
+    "gpt6.7b_tp1pp4_tp8": (12.132e9, 12.132e9, 388),
+    "qwen7b_tp2_tp4": (22.849e9, 26.657e9, 339),
+}
+
+
+@pytest.mark.parametrize("key", CONFIG_ORDER)
+def test_benchmark_plan_sizes(key):
+    w = CONFIGS[key]
+    plan = _plan_for(w)
+    info = plan.info
+    P, D, pieces = DOCUMENTED[key]
+    assert abs(info.pack_bytes_read - P) < 0.0005e9
+    assert info.pack_bytes_written == info.pack_bytes_read == info.unpack_bytes_read
+    assert abs(info.unpack_bytes_written - D) < 0.0005e9
+    copies = [p for p in plan.pieces if p.kind != 2]
+    assert len(copies) == pieces * len(w.src_fields)
+    # every buffer offset is 256-byte aligned
+    for k in range(0, plan.n_pieces, 37):
+        off = plan.piece_offset(k)
+        assert off == np.iinfo(np.uint64).max or off % 256 == 0
+    plan.close()
+
+
+def test_benchmark_shortest_row_runs():
+    """Strided (last-dim) destination rows are >= 1 KB and 16-B multiples at
+    the benchmark shapes, so the 16-byte vector path covers all of them."""
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        plan = _plan_for(w)
+        for p in plan.pieces:
+            es = _esize(plan.c_dst[p.dst].dtype) if p.dst >= 0 else 2
+            if p.rows > 1 and p.cols != plan.c_dst[p.dst].cols:
+                assert (p.cols * es) % 16 == 0 and p.cols * es >= 512, (key, p.rows, p.cols)
+        plan.close()
+
+
+def test_lower_op_rejects_uncovered_piece():
+    from suika_amd import TransferOp
+    src = TensorMeta(name="a", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 1, 2))
+    dst = TensorMeta(name="a", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    with pytest.raises(AssertionError, match="holds 0 of"):
+        lower_op(TransferOp("a", 1, 0, src, dst), dst)
