@@ -39,7 +39,8 @@ def parse_args(argv=None):
     ap.add_argument("--config", default=None, help="workload key (default: the Llama2-7B share)")
     ap.add_argument("--tile-bytes", type=int, default=0)
     ap.add_argument("--max-blocks", type=int, default=0)
-    ap.add_argument("--nontemporal", action="store_true")
+    ap.add_argument("--temporal", action="store_true",
+                    help="ordinary cached loads/stores instead of streaming ones")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=8,
                     help="decoder layers on the destination stage in the CPU sample")
@@ -136,7 +137,7 @@ def main(argv=None) -> int:
     specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
              for op in ops for f in w.src_fields}
     opts = PlanOptions(tile_bytes=args.tile_bytes, max_blocks=args.max_blocks,
-                       nontemporal=args.nontemporal)
+                       nontemporal=not args.temporal)
     plan = ReshardPlan(ops, specs, list(w.src_fields), recast=w.recast_map, options=opts)
     info = plan.info
     P = int(info.pack_bytes_read)
@@ -197,7 +198,7 @@ def main(argv=None) -> int:
             tdata = json.loads(tf.read_text())
             ent = tdata.get(key, {}).get(dom)
             if ent is not None and ent.get("tile_bytes", 0) == args.tile_bytes \
-                    and bool(ent.get("nontemporal", False)) == args.nontemporal:
+                    and bool(ent.get("nontemporal", True)) == (not args.temporal):
                 traffic = ent["bytes_per_launch"]
         except Exception as e:  # a malformed file must not hide the measurement
             print(f"[bench] ignoring {tf}: {e}", file=sys.stderr)
@@ -225,7 +226,8 @@ def main(argv=None) -> int:
             "B_alg_bytes": b_alg,
             "B_min_bytes": b_min,
             "tile_bytes": args.tile_bytes or 262144,
-            "nontemporal": args.nontemporal,
+            "max_blocks": args.max_blocks,
+            "nontemporal": not args.temporal,
         },
         "reshard_ms": round(total_ms, 4),
         "pack_ms": round(pack_ms, 4),

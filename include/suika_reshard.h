@@ -30,6 +30,8 @@
  *     caller.  The library owns only the plan and its descriptor tables.
  *   - Calls that take a hipStream_t are asynchronous and stream-ordered; the
  *     caller synchronizes.  A plan may be used from one host thread at a time.
+ *   - Device pointers must be aligned to their element size; peer buffers
+ *     to 16 bytes (torch allocations are 512-byte aligned).
  *   - Status codes: SR_OK (0) on success, a negative sr_status otherwise.
  *     sr_last_error() returns a thread-local message for the last failure.
  *     Invalid plans and pointers are rejected before any kernel launch.
@@ -109,7 +111,8 @@ typedef struct sr_plan_options {
   uint32_t reserved;     /* must be 0 */
 } sr_plan_options;
 
-#define SR_OPT_NONTEMPORAL 0x1u   /* streaming (non-temporal) loads and stores */
+#define SR_OPT_TEMPORAL 0x1u      /* ordinary cached loads/stores instead of the
+                                     default streaming (non-temporal) ones */
 #define SR_OPT_SKIP_COVERAGE 0x2u /* skip the destination coverage check */
 
 typedef struct sr_plan sr_plan;

@@ -37,7 +37,7 @@ SR_DT_U8, SR_DT_BF16, SR_DT_F16, SR_DT_F32, SR_DT_F64, SR_DT_I32, SR_DT_I64 = ra
 
 SR_PIECE_COPY, SR_PIECE_RECAST, SR_PIECE_ZERO = 0, 1, 2
 
-SR_OPT_NONTEMPORAL = 0x1
+SR_OPT_TEMPORAL = 0x1
 SR_OPT_SKIP_COVERAGE = 0x2
 
 # Every symbol the header declares; the CPU test-suite checks they resolve.
@@ -168,15 +168,15 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
-def last_error() -> str:
-    return lib().sr_last_error().decode("utf-8", "replace")
+def last_error(handle: Optional[ctypes.CDLL] = None) -> str:
+    return (handle or lib()).sr_last_error().decode("utf-8", "replace")
 
 
-def check(rc: int, what: str) -> None:
+def check(rc: int, what: str, handle: Optional[ctypes.CDLL] = None) -> None:
     """Raise the Python exception matching a library status code."""
     if rc == SR_OK:
         return
-    msg = f"{what}: {STATUS_NAMES.get(rc, rc)}: {last_error()}"
+    msg = f"{what}: {STATUS_NAMES.get(rc, rc)}: {last_error(handle)}"
     if rc in (SR_EHIP, SR_ENOMEM):
         raise ReshardError(msg)
     raise PlanError(msg)

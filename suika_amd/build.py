@@ -42,11 +42,16 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, PATH, /opt/rocm/bin/hipcc)")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library (always recompiles) and return its path."""
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE}", str(SRC), "-o", str(tmp)]
+def build(verbose: bool = False, out: Path = LIB, defines=()) -> Path:
+    """Compile the library (always recompiles) and return its path.
+
+    ``defines`` are extra ``NAME=VALUE`` macros (kernel tuning knobs such as
+    SR_UNROLL / SR_BLOCK) for building variants elsewhere than ``out``."""
+    out = Path(out)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc_path(), *HIPCC_FLAGS, *[f"-D{d}" for d in defines], f"-I{INCLUDE}", str(SRC),
+           "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,8 +62,8 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
     if verbose and msgs:
         print("\n".join(msgs), flush=True)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

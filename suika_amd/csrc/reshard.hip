@@ -15,14 +15,15 @@
 //     destination stride.  Regions that are contiguous on both sides are
 //     collapsed to one long row.
 //   * Items are cut into tiles of `tile_bytes` source bytes.  One workgroup
-//     (256 lanes = 4 wave64) processes one tile; the grid is the tile count
+//     (1024 lanes = 16 wave64) processes one tile; the grid is the tile count
 //     (or a grid-stride loop when capped).  Tiles are balanced regardless of
 //     the tensor sizes (3.5 KB norms to GB embeddings).
 //   * Lanes move 16-byte vectors (8/4/2/1 when a region is not 16-byte
 //     aligned), UNROLL independent loads in flight before the stores, so a
-//     wave keeps 4 KB of HBM reads outstanding.  Consecutive lanes touch
+//     wave keeps 2 KB of HBM reads outstanding.  Consecutive lanes touch
 //     consecutive 16-byte words of a row: every wave access is a fully
-//     coalesced 1 KB burst.
+//     coalesced 1 KB burst.  Loads and stores are non-temporal by default:
+//     every byte is touched once, so nothing is worth keeping in L2/MALL.
 //   * Strided regions (row-parallel dim -1 slices) map a tile-relative byte
 //     position to (row, col) with a multiply-high division by the row width
 //     (Granlund-Montgomery invariant-integer division), computed per item
@@ -54,11 +55,17 @@
 
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+#ifndef SR_BLOCK
+#define SR_BLOCK 1024
+#endif
+#ifndef SR_UNROLL
+#define SR_UNROLL 2
+#endif
+constexpr int kBlock = SR_BLOCK;
+constexpr int kUnroll = SR_UNROLL;
 constexpr uint32_t kDefaultTileBytes = 262144;
 constexpr uint64_t kBufAlign = 256;
-constexpr uint32_t kMaxGrid = (1u << 24) - 1;   // gridDim.x * 256 < 2^32
+constexpr uint32_t kMaxGrid = (1u << 24) - 1;   // gridDim.x * kBlock < 2^32
 
 // ---------------------------------------------------------------- errors
 
@@ -608,7 +615,7 @@ int run_phase(sr_plan* p, Phase& ph, bool is_pack, const uint64_t* src_base, siz
   uint32_t grid = n_tiles;
   if (p->opt.max_blocks != 0) grid = std::min(grid, p->opt.max_blocks);
   grid = std::min(grid, kMaxGrid);
-  const bool nt = (p->opt.flags & SR_OPT_NONTEMPORAL) != 0;
+  const bool nt = (p->opt.flags & SR_OPT_TEMPORAL) == 0;
   if (is_pack) {
     if (nt)
       hipLaunchKernelGGL(sr_pack_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
@@ -711,7 +718,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
   sr_plan_options opt{};
   if (options) opt = *options;
   if (opt.reserved != 0) return fail(SR_EINVAL, "options.reserved must be 0");
-  if (opt.flags & ~(SR_OPT_NONTEMPORAL | SR_OPT_SKIP_COVERAGE))
+  if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE))
     return fail(SR_EINVAL, "unknown option flags 0x%x", opt.flags);
   if (opt.tile_bytes == 0) opt.tile_bytes = kDefaultTileBytes;
   if (opt.tile_bytes < 4096 || opt.tile_bytes > (16u << 20) ||

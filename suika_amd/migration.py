@@ -100,6 +100,8 @@ def execute_param_transfer(
         device = torch.device(device)
     assert device.type == "cuda", \
         f"execute_param_transfer runs on the GPU reshard engine; got device {device}"
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
     if rank is None:
         rank = _current_rank(world)
 

@@ -56,11 +56,11 @@ def sr_dtype(dtype: torch.dtype) -> int:
 class PlanOptions:
     tile_bytes: int = 0          # 0 = library default
     max_blocks: int = 0          # 0 = one workgroup per tile
-    nontemporal: bool = False
+    nontemporal: bool = True     # streaming loads/stores (library default)
     skip_coverage: bool = False
 
     def to_c(self) -> _lib.SrPlanOptions:
-        flags = (_lib.SR_OPT_NONTEMPORAL if self.nontemporal else 0) | \
+        flags = (0 if self.nontemporal else _lib.SR_OPT_TEMPORAL) | \
                 (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0)
         return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, flags, 0)
 
@@ -208,21 +208,21 @@ class ReshardPlan:
         self.pieces = c_pieces
         self.c_src = c_src
         self.c_dst = c_dst
-        L = _lib.lib()
+        L = self._L = _lib.lib()
         src_arr = (_lib.SrTensor * max(1, len(c_src)))(*c_src)
         dst_arr = (_lib.SrTensor * max(1, len(c_dst)))(*c_dst)
         pc_arr = (_lib.SrPiece * max(1, len(c_pieces)))(*c_pieces)
         opt = self.options.to_c()
         rc = L.sr_plan_create(src_arr, len(c_src), dst_arr, len(c_dst), len(self.peers),
                               pc_arr, len(c_pieces), ctypes.byref(opt), ctypes.byref(self._handle))
-        _lib.check(rc, "sr_plan_create")
+        _lib.check(rc, "sr_plan_create", L)
         self.peer_bytes: List[int] = []
         for i in range(len(self.peers)):
             b = ctypes.c_uint64()
-            _lib.check(L.sr_plan_peer_bytes(self._handle, i, ctypes.byref(b)), "sr_plan_peer_bytes")
+            _lib.check(L.sr_plan_peer_bytes(self._handle, i, ctypes.byref(b)), "sr_plan_peer_bytes", L)
             self.peer_bytes.append(int(b.value))
         info = _lib.SrPlanInfo()
-        _lib.check(L.sr_plan_info_get(self._handle, ctypes.byref(info)), "sr_plan_info_get")
+        _lib.check(L.sr_plan_info_get(self._handle, ctypes.byref(info)), "sr_plan_info_get", L)
         self.info = info
 
     # -------------------------------------------------------------- sizes
@@ -236,8 +236,8 @@ class ReshardPlan:
 
     def piece_offset(self, k: int) -> int:
         off = ctypes.c_uint64()
-        _lib.check(_lib.lib().sr_plan_piece_offset(self._handle, k, ctypes.byref(off)),
-                   "sr_plan_piece_offset")
+        _lib.check(self._L.sr_plan_piece_offset(self._handle, k, ctypes.byref(off)),
+                   "sr_plan_piece_offset", self._L)
         return int(off.value)
 
     # --------------------------------------------------------- allocation
@@ -289,14 +289,14 @@ class ReshardPlan:
         return (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
 
     def pack_ptrs(self, src_ptrs: List[int], buf_ptrs: List[int], stream=None) -> None:
-        rc = _lib.lib().sr_pack(self._handle, self._carray(src_ptrs), self._carray(buf_ptrs),
+        rc = self._L.sr_pack(self._handle, self._carray(src_ptrs), self._carray(buf_ptrs),
                                 _stream_handle(stream))
-        _lib.check(rc, "sr_pack")
+        _lib.check(rc, "sr_pack", self._L)
 
     def unpack_ptrs(self, buf_ptrs: List[int], dst_ptrs: List[int], stream=None) -> None:
-        rc = _lib.lib().sr_unpack(self._handle, self._carray(buf_ptrs), self._carray(dst_ptrs),
+        rc = self._L.sr_unpack(self._handle, self._carray(buf_ptrs), self._carray(dst_ptrs),
                                   _stream_handle(stream))
-        _lib.check(rc, "sr_unpack")
+        _lib.check(rc, "sr_unpack", self._L)
 
     def pack(self, sources, buffers, stream=None) -> None:
         """Source shards -> peer buffers (async on ``stream``)."""
@@ -308,7 +308,7 @@ class ReshardPlan:
 
     def close(self) -> None:
         if getattr(self, "_handle", None) is not None and self._handle.value:
-            _lib.lib().sr_plan_destroy(self._handle)
+            self._L.sr_plan_destroy(self._handle)
             self._handle = ctypes.c_void_p()
 
     def __del__(self):

@@ -49,7 +49,15 @@ def test_execute_semantics_step_and_clear():
 def test_execute_rejects_remote_without_exchange():
     w = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     ops = w.ops()
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    own = to_device({w.dst_rank: srcs[w.dst_rank]}, w, "cuda")[w.dst_rank]
+    assert any(op.src_rank != w.dst_rank for op in ops)
     with pytest.raises(NotImplementedError, match="cross-GPU exchange"):
+        execute_param_transfer(ops, own, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                               rank=w.dst_rank)
+    # a missing own shard is the reference's assertion (migration.py:436)
+    with pytest.raises(AssertionError, match="param missing in source"):
         execute_param_transfer(ops, {}, torch.device("cuda"), [("param", "normal")], rank=w.dst_rank)
 
 

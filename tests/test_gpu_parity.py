@@ -52,9 +52,9 @@ SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
 @pytest.mark.parametrize("opt", [
     PlanOptions(tile_bytes=4096),
     PlanOptions(tile_bytes=8192, max_blocks=7),
-    PlanOptions(nontemporal=True),
-    PlanOptions(tile_bytes=1 << 20, nontemporal=True, max_blocks=300),
-], ids=["tile4k", "tile8k_grid7", "nt", "tile1m_nt_grid300"])
+    PlanOptions(nontemporal=False),
+    PlanOptions(tile_bytes=1 << 20, nontemporal=False, max_blocks=300),
+], ids=["tile4k", "tile8k_grid7", "temporal", "tile1m_temporal_grid300"])
 def test_gpu_tunings_match_oracle(w, opt):
     _check(w, "index", opt)
 
