@@ -42,8 +42,12 @@ def parse_args(argv=None):
     ap.add_argument("--temporal", action="store_true",
                     help="ordinary cached loads/stores instead of streaming ones")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=8,
-                    help="decoder layers on the destination stage in the CPU sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum timed CPU work per thread count")
+    ap.add_argument("--cpu-layers", type=int, default=0,
+                    help="time a sample with this many destination-stage layers (0: the full share)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run a flat copy of BYTES through the library (counter calibration)")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -57,17 +61,21 @@ def to_ometa(m):
                    kind_args=tuple(m.kind_args), rows=m.rows)
 
 
-def cpu_baseline(w, layers: int, threads: int):
-    """Time the torch-CPU restatement of the reference's CPU reshard on a
-    sample of ``w`` whose destination stage holds ``layers`` decoder layers."""
+def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0):
+    """Time the torch-CPU restatement of the reference's CPU reshard on the
+    destination share of ``w`` (or, with ``layers`` > 0, on a sample whose
+    destination stage holds that many decoder layers): one untimed run, then
+    timed runs until ``min_seconds`` have passed.  Returns (seconds per run,
+    algorithmic bytes of the share, runs, decoder layers of the share)."""
     import torch
     from oracle import reshard_oracle as O
     from oracle.torch_ref import execute_torch_cpu
+    from suika_amd.inventory import layer_partition
 
-    pp = w.dst.pp if w.dst.pp > 1 else 1
-    # sample: same plan change, fewer layers (destination stage = ``layers``)
-    n_layer = max(w.src.pp, pp) * layers
-    ws = replace(w, model=replace(w.model, n_layer=n_layer))
+    ws = w
+    if layers:
+        n_layer = max(w.src.pp, w.dst.pp) * layers
+        ws = replace(w, model=replace(w.model, n_layer=n_layer))
     spl, tpl = ws.layouts()
     osrc = {r: {n: to_ometa(m) for n, m in metas.items()} for r, metas in spl.layout.items()}
     odst = {r: {n: to_ometa(m) for n, m in metas.items()} for r, metas in tpl.layout.items()}
@@ -77,23 +85,26 @@ def cpu_baseline(w, layers: int, threads: int):
     torch.set_num_threads(threads)
     try:
         srcs = {}
-        P = 0
         for op in ops:
             for f in ws.src_fields:
-                key = (op.src, op.name, f)
                 ent = srcs.setdefault(op.src, {}).setdefault(op.name, {})
                 if f not in ent:
                     t = torch.empty(O.actual_shape(op.src_meta), dtype=dt[f])
                     t.fill_(0.5)
                     ent[f] = t
-        out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)  # warm
-        del out
-        t0 = time.perf_counter()
         out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)
-        dt_s = time.perf_counter() - t0
+        del out
+        runs, total = 0, 0.0
+        while total < min_seconds or runs == 0:
+            t0 = time.perf_counter()
+            out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)
+            total += time.perf_counter() - t0
+            del out
+            runs += 1
+        del srcs
     finally:
         torch.set_num_threads(prev)
-    # algorithmic bytes of the sample, same definition as the GPU figure
+    # algorithmic bytes of the share, same definition as the GPU figure
     from suika_amd.plan import ReshardPlan, SlotSpec
     ops_p = ws.ops()
     specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
@@ -101,7 +112,40 @@ def cpu_baseline(w, layers: int, threads: int):
     plan = ReshardPlan(ops_p, specs, list(ws.src_fields), recast=ws.recast_map)
     b_alg = plan.pack_bytes + plan.unpack_bytes
     plan.close()
-    return dt_s, b_alg, n_layer
+    dst_pp = ws.dst.coord(ws.dst_rank)[0]
+    n_dst_layers = layer_partition(ws.model.n_layer, ws.dst.pp)[dst_pp]
+    return total / runs, b_alg, runs, n_dst_layers
+
+
+def calibrate_copy(nbytes: int, steps: int) -> dict:
+    """A flat device copy of ``nbytes`` through the library (one piece): the
+    known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    from suika_amd.plan import PlanOptions, ReshardPlan, SlotSpec
+    from suika_amd.meta import TensorMeta, TransferOp
+    cols = 4096
+    rows = nbytes // 4 // cols
+    m = TensorMeta(name="copy", dtype=torch.float32, shape=(rows, cols))
+    op = TransferOp("copy", 0, 0, m, m, m)
+    plan = ReshardPlan([op], {(0, "copy", "param"): SlotSpec((rows, cols), torch.float32)}, ["param"])
+    dev = torch.device("cuda", 0)
+    a = torch.empty((rows, cols), dtype=torch.float32, device=dev).fill_(1.0)
+    bufs = plan.alloc_buffers(dev)
+    sp, bp = plan.src_pointers({0: {"copy": {"param": a}}}), plan.buf_pointers(bufs)
+    s = torch.cuda.current_stream()
+    plan.pack_ptrs(sp, bp, s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        plan.pack_ptrs(sp, bp, s)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    plan.close()
+    return {"calibration": "flat copy through sr_pack_kernel", "bytes_read": rows * cols * 4,
+            "bytes_written": rows * cols * 4, "ms": round(ms, 4),
+            "GBps": round(2 * rows * cols * 4 / ms / 1e6, 1)}
 
 
 def cpu_model() -> str:
@@ -126,6 +170,11 @@ def main(argv=None) -> int:
     import torch
     from suika_amd.plan import PlanOptions, ReshardPlan, SlotSpec
     from suika_amd.workloads import BENCH_CONFIG, CONFIGS, make_source_state
+
+    if args.calibrate_copy:
+        torch.cuda.set_device(0)
+        print(json.dumps(calibrate_copy(args.calibrate_copy, args.steps)), flush=True)
+        return 0
 
     key = args.config or BENCH_CONFIG
     w = CONFIGS[key]
@@ -253,23 +302,26 @@ def main(argv=None) -> int:
 
     if not args.no_cpu_baseline:
         threads = len(os.sched_getaffinity(0))
-        print(f"[bench] CPU baseline: torch-CPU reshard sample, {threads} threads", file=sys.stderr,
+        print(f"[bench] CPU baseline: torch-CPU reshard, {threads} threads", file=sys.stderr,
               flush=True)
-        t_n, b_n, nl = cpu_baseline(w, args.cpu_layers, threads)
-        t_1, b_1, nl1 = cpu_baseline(w, max(1, args.cpu_layers // 4), 1)
+        t_n, b_n, runs_n, nl = cpu_baseline(w, threads, args.cpu_seconds, args.cpu_layers)
+        t_1, b_1, runs_1, nl1 = cpu_baseline(w, 1, args.cpu_seconds, args.cpu_layers)
         rate_n = b_n / t_n / 1e9
         rate_1 = b_1 / t_1 / 1e9
         full_ms = b_alg / (rate_n * 1e9) * 1e3
+        what = "the full destination share" if not args.cpu_layers else \
+            f"a sample with {nl} destination-stage layers"
         result["cpu_baseline"] = {
             "value": round(rate_n, 2),
             "unit": "GB/s",
             "cores": threads,
             "kind": "port",
-            "sample": (f"torch-CPU chunk/contiguous/cat reshard of the same plan change with "
-                       f"{nl} layers ({b_n / 1e9:.2f} GB algorithmic), {t_n:.2f} s"),
-            "full_share_ms_estimate": round(full_ms, 1),
+            "sample": (f"torch-CPU chunk/contiguous/cat reshard (oracle/torch_ref.py) of {what}, "
+                       f"{b_n / 1e9:.2f} GB algorithmic, {runs_n} timed runs of {t_n:.3f} s"),
+            "ms": round(full_ms, 1),
             "one_thread_GBps": round(rate_1, 2),
-            "one_thread_sample": f"{nl1} layers, {b_1 / 1e9:.2f} GB, {t_1:.2f} s",
+            "one_thread_ms": round(b_alg / (rate_1 * 1e9) * 1e3, 1),
+            "one_thread_sample": f"{runs_1} timed runs of {t_1:.3f} s",
             "cpu_model": cpu_model(),
             "speedup_gpu_vs_cpu": round(full_ms / total_ms, 1),
         }

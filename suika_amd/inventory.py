@@ -182,10 +182,27 @@ def rank_params(m: ModelSpec, par: Parallel, rank: int) -> List[ParamSpec]:
     return stage_params(m, sum(part[:pp_i]), part[pp_i])
 
 
+def check_divisible(spec: ParamSpec, tp: int) -> None:
+    """A TP split must be exact, as ColumnParallelLinear / RowParallelLinear
+    allocate ``features // tp`` rows or columns (tensor_parallel.py:189-204,
+    368-381)."""
+    if spec.kind == COL:
+        assert spec.shape[0] % tp == 0, f"{spec.name}: {spec.shape[0]} rows not divisible by tp {tp}"
+    elif spec.kind == ROW:
+        assert spec.shape[-1] % tp == 0, f"{spec.name}: {spec.shape[-1]} cols not divisible by tp {tp}"
+    elif spec.kind == QKV:
+        n_q, n_kv, _ = spec.kind_args
+        assert n_q % tp == 0 and n_kv % tp == 0, \
+            f"{spec.name}: {n_q} q / {n_kv} kv heads not divisible by tp {tp}"
+
+
 def build_layout(m: ModelSpec, par: Parallel, dtype: torch.dtype) -> ParamLayout:
     """ParamLayout of every rank of a plan (what ParamLayout.gather collects)."""
     metas: Dict[int, Dict[str, TensorMeta]] = {}
     for rank in range(par.world):
         _, _, tp_i = par.coord(rank)
-        metas[rank] = {s.name: param_meta(s, par.tp, tp_i, dtype) for s in rank_params(m, par, rank)}
+        specs = rank_params(m, par, rank)
+        for s in specs:
+            check_divisible(s, par.tp)
+        metas[rank] = {s.name: param_meta(s, par.tp, tp_i, dtype) for s in specs}
     return ParamLayout.from_metas(metas)

@@ -103,3 +103,36 @@ def padded_vocab_cases() -> List[Workload]:
 def all_small_cases() -> List[Workload]:
     return (reference_test_cases() + alignment_cases() + list(scaled_configs().values())
             + padded_vocab_cases())
+
+
+def golden_cases() -> Dict[str, Workload]:
+    """Tiny cases whose inputs and expected outputs are committed under
+    tests/golden/ (a few KB): every kind, a TP merge and split, a PP move, an
+    all-padding vocabulary shard, the bf16 recast and rows that are not a
+    multiple of 16 bytes."""
+    gpt = ModelSpec("gpt", n_layer=2, hidden=8, n_head=2, ffn=16, vocab=24)
+    llama_v = ModelSpec("llama", n_layer=2, hidden=8, n_head=2, ffn=12, vocab=20,
+                        vocab_parallel=True, pad_multiple=4)
+    qkv = ModelSpec("llama", n_layer=1, hidden=8, n_head=4, n_kv_head=2, head_dim=2, ffn=8,
+                    vocab=16, fused_qkv=True)
+    vocab = ModelSpec("llama", n_layer=1, hidden=4, n_head=2, ffn=8, vocab=12,
+                      vocab_parallel=True, pad_multiple=5)
+    qwen = ModelSpec("qwen", n_layer=1, hidden=8, n_head=2, n_kv_head=2, ffn=8, vocab=12)
+    odd = ModelSpec("llama", n_layer=1, hidden=6, n_head=2, ffn=10, vocab=14)
+    recast = (("master", torch.float32), ("exp_avg", torch.float32),
+              ("exp_avg_sq", torch.float32), ("param", torch.bfloat16))
+    return {
+        "gpt_tp1_tp2_d1": _w("gpt_tp1_tp2_d1", gpt, Parallel(1), Parallel(2), 0, 1, fields=_F32_3,
+                             param_dtype=torch.float32, seed=21),
+        "llama_tp2pp1_tp1pp2_d1": _w("llama_tp2pp1_tp1pp2_d1", llama_v, Parallel(2), Parallel(1, 2),
+                                     1, 0, seed=22),
+        "llama_tp1pp2_tp2pp1_d0": _w("llama_tp1pp2_tp2pp1_d0", llama_v, Parallel(1, 2), Parallel(2),
+                                     0, 0, seed=23),
+        "qkv_tp1_tp2_d1": _w("qkv_tp1_tp2_d1", qkv, Parallel(1), Parallel(2), 0, 1, seed=24),
+        "qkv_tp2_tp1": _w("qkv_tp2_tp1", qkv, Parallel(2), Parallel(1), 0, 0, seed=25),
+        "vocab_tp2_tp4_d2": _w("vocab_tp2_tp4_d2", vocab, Parallel(2), Parallel(4), 0, 2, seed=26),
+        "vocab_tp2_tp4_d3": _w("vocab_tp2_tp4_d3", vocab, Parallel(2), Parallel(4), 0, 3, seed=27),
+        "qwen_recast_tp2_tp1": _w("qwen_recast_tp2_tp1", qwen, Parallel(2), Parallel(1), 0, 0,
+                                  fields=recast, recast=(("param", "master"),), seed=28),
+        "odd_rows_tp2_tp1": _w("odd_rows_tp2_tp1", odd, Parallel(2), Parallel(1), 0, 0, seed=29),
+    }

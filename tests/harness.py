@@ -225,3 +225,36 @@ def simulate_plan(plan, srcs_np, esize_of) -> Dict[Tuple[str, str], np.ndarray]:
         spec = plan.dst_specs[key]
         out[key] = raw.view(BITS[spec.dtype]).reshape(spec.shape)
     return out
+
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def load_reshard_vectors():
+    """{payload: {case: (sources, expected destination)}} from the fixture."""
+    import json as _json
+    z = np.load(GOLDEN / "reshard_vectors.npz")
+    blob = z["blob"]
+    manifest = _json.loads(bytes(z["manifest"]).decode())
+    out: Dict[str, Dict[str, tuple]] = {}
+    for key, (off, dtstr, shape) in manifest.items():
+        dt = np.dtype(dtstr)
+        n = int(np.prod(shape)) if shape else 1
+        a = blob[off:off + n * dt.itemsize].view(dt).reshape(shape)
+        parts = key.split("|")
+        payload, case, side = parts[0], parts[1], parts[2]
+        srcs, dst = out.setdefault(payload, {}).setdefault(case, ({}, {}))
+        if side == "src":
+            r, name, f = int(parts[3]), parts[4], parts[5]
+            srcs.setdefault(r, {}).setdefault(name, {})[f] = a
+        else:
+            name, f = parts[3], parts[4]
+            dst.setdefault(name, {})[f] = a
+    return out
+
+
+def load_schedule_vectors():
+    import gzip
+    import json as _json
+    with gzip.open(GOLDEN / "schedule_vectors.json.gz", "rt") as fh:
+        return _json.load(fh)

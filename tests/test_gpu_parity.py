@@ -93,3 +93,18 @@ def test_gpu_repeat_and_streams():
                 np.testing.assert_array_equal(t2np(dst[name][f]), want[name][f],
                                               err_msg=f"iter {it}: {name}/{f}")
     plan.close()
+
+
+@pytest.mark.parametrize("payload", ["seeded", "index"])
+@pytest.mark.parametrize("case", sorted(cases.golden_cases()))
+def test_gpu_reproduces_golden_vectors(payload, case):
+    """The committed fixtures through the HIP path, bit for bit."""
+    from tests.harness import load_reshard_vectors
+    w = cases.golden_cases()[case]
+    print(f"[gpu golden] {case} {payload}", flush=True)
+    srcs, want = load_reshard_vectors()[payload][case]
+    got = gpu_execute(w, srcs)
+    assert set(got) == set(want)
+    for name, ent in want.items():
+        for f, a in ent.items():
+            np.testing.assert_array_equal(got[name][f], a, err_msg=f"{case}: {name}/{f}")
