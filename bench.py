@@ -28,6 +28,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+DEFAULT_TILE = 16384   # the library's default tile size (sr_plan_options.tile_bytes = 0)
 METRIC = "reshard ms and achieved HBM GB/s (% of peak) per GPU share; speedup vs CPU ref"
 
 
@@ -246,7 +247,8 @@ def main(argv=None) -> int:
         try:
             tdata = json.loads(tf.read_text())
             ent = tdata.get(key, {}).get(dom)
-            if ent is not None and ent.get("tile_bytes", 0) == args.tile_bytes \
+            if ent is not None and ent.get("tile_bytes") == (args.tile_bytes or DEFAULT_TILE) \
+                    and ent.get("max_blocks", 0) == args.max_blocks \
                     and bool(ent.get("nontemporal", True)) == (not args.temporal):
                 traffic = ent["bytes_per_launch"]
         except Exception as e:  # a malformed file must not hide the measurement
@@ -274,7 +276,7 @@ def main(argv=None) -> int:
             "D_bytes": D,
             "B_alg_bytes": b_alg,
             "B_min_bytes": b_min,
-            "tile_bytes": args.tile_bytes or 262144,
+            "tile_bytes": args.tile_bytes or DEFAULT_TILE,
             "max_blocks": args.max_blocks,
             "nontemporal": not args.temporal,
         },

@@ -104,7 +104,7 @@ typedef struct sr_piece {
 /* Plan tuning; pass NULL to sr_plan_create for the defaults. */
 typedef struct sr_plan_options {
   uint32_t tile_bytes;   /* bytes of source data per work tile; power of two in
-                            [4096, 16 MiB]; 0 = default (262144) */
+                            [4096, 16 MiB]; 0 = default (16384) */
   uint32_t max_blocks;   /* cap on workgroups per launch (grid-stride beyond);
                             0 = one workgroup per tile */
   uint32_t flags;        /* SR_OPT_* bits */
@@ -114,6 +114,11 @@ typedef struct sr_plan_options {
 #define SR_OPT_TEMPORAL 0x1u      /* ordinary cached loads/stores instead of the
                                      default streaming (non-temporal) ones */
 #define SR_OPT_SKIP_COVERAGE 0x2u /* skip the destination coverage check */
+#define SR_OPT_PIECE_ORDER 0x4u   /* run pieces in plan order instead of ordered by
+                                     the tensor address they start at */
+#define SR_OPT_NO_XCD_INTERLEAVE 0x8u /* keep the tile list linear instead of
+                                     interleaving it 8 ways (by default each XCD, fed
+                                     round-robin, walks one contiguous eighth) */
 
 typedef struct sr_plan sr_plan;
 

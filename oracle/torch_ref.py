@@ -1,4 +1,4 @@
-"""Torch-CPU restatement of the reference's CPU reshard -- TEST/BASELINE ONLY.
+"""Torch-CPU restatement of the reference's CPU reshard -- test and CPU-baseline use only.
 
 The reference reshards on the CPU in ``checkpoint_load`` by running
 ``execute_param_transfer`` in fake-source mode on CPU tensors

@@ -14,16 +14,22 @@
 //     a 2-D byte region: `rows` rows of `row_bytes` bytes at a source and a
 //     destination stride.  Regions that are contiguous on both sides are
 //     collapsed to one long row.
-//   * Items are cut into tiles of `tile_bytes` source bytes.  One workgroup
-//     (1024 lanes = 16 wave64) processes one tile; the grid is the tile count
-//     (or a grid-stride loop when capped).  Tiles are balanced regardless of
-//     the tensor sizes (3.5 KB norms to GB embeddings).
+//   * Items are cut into tiles of `tile_bytes` (16 KiB) source bytes; one
+//     workgroup (512 lanes = 8 wave64) processes one tile in a single pass,
+//     and the grid is the tile count (or a grid-stride loop when capped).
+//     Tiles balance the work whatever the tensor sizes (8 KB norms to GB
+//     embeddings).
+//   * The tile list follows the tensor address each item starts at and is
+//     interleaved 8 ways: workgroups go to the 8 XCDs round-robin, so each XCD
+//     walks one contiguous eighth of the work and the tiles in flight come
+//     from 8 distant regions.  On the Llama2-7B share this takes the unpack
+//     from 8.5 to 7.4 ms; a single window of consecutive tiles keeps the read
+//     and write streams at a fixed distance and leaves HBM bandwidth idle.
 //   * Lanes move 16-byte vectors (8/4/2/1 when a region is not 16-byte
-//     aligned), UNROLL independent loads in flight before the stores, so a
-//     wave keeps 2 KB of HBM reads outstanding.  Consecutive lanes touch
-//     consecutive 16-byte words of a row: every wave access is a fully
-//     coalesced 1 KB burst.  Loads and stores are non-temporal by default:
-//     every byte is touched once, so nothing is worth keeping in L2/MALL.
+//     aligned), two independent loads in flight before the stores.
+//     Consecutive lanes touch consecutive 16-byte words of a row, so every
+//     wave access is a coalesced 1 KB burst.  Loads and stores are
+//     non-temporal by default: every byte is touched once.
 //   * Strided regions (row-parallel dim -1 slices) map a tile-relative byte
 //     position to (row, col) with a multiply-high division by the row width
 //     (Granlund-Montgomery invariant-integer division), computed per item
@@ -56,15 +62,23 @@
 namespace {
 
 #ifndef SR_BLOCK
-#define SR_BLOCK 1024
+#define SR_BLOCK 512
 #endif
 #ifndef SR_UNROLL
 #define SR_UNROLL 2
 #endif
 constexpr int kBlock = SR_BLOCK;
 constexpr int kUnroll = SR_UNROLL;
-constexpr uint32_t kDefaultTileBytes = 262144;
+// Strided and recast paths carry two or three 64-bit offsets per vector;
+// a smaller unroll keeps the kernel's register count (and so its occupancy)
+// set by the contiguous copy path.
+#ifndef SR_UNROLL_STRIDED
+#define SR_UNROLL_STRIDED (SR_UNROLL < 4 ? SR_UNROLL : 4)
+#endif
+constexpr int kUnrollStrided = SR_UNROLL_STRIDED;
+constexpr uint32_t kDefaultTileBytes = 16384;   // one 512-lane x 2 x 16 B pass
 constexpr uint64_t kBufAlign = 256;
+constexpr uint32_t kXcds = 8;                    // accelerator complex dies per MI355X
 constexpr uint32_t kMaxGrid = (1u << 24) - 1;   // gridDim.x * kBlock < 2^32
 
 // ---------------------------------------------------------------- errors
@@ -175,87 +189,112 @@ template <> struct VecOf<4> { typedef unsigned int type; };
 template <> struct VecOf<2> { typedef unsigned short type; };
 template <> struct VecOf<1> { typedef unsigned char type; };
 
-template <bool NT, typename T>
-__device__ __forceinline__ T ld(const T* p) {
+// Global-memory accessors.  Descriptor tables carry addresses as integers,
+// so the global address space is stated here: the compiler then emits
+// global_load/global_store (VMEM only) instead of flat instructions, which
+// would also wait on the LDS counter.
+#define SR_GLOBAL __attribute__((address_space(1)))
+
+template <typename T, bool NT>
+__device__ __forceinline__ T ld(uint64_t addr) {
+  const SR_GLOBAL T* p = (const SR_GLOBAL T*)addr;
   if constexpr (NT) return __builtin_nontemporal_load(p);
   else return *p;
 }
 
-template <bool NT, typename T>
-__device__ __forceinline__ void st(T* p, T v) {
+template <typename T, bool NT>
+__device__ __forceinline__ void st(uint64_t addr, T v) {
+  SR_GLOBAL T* p = (SR_GLOBAL T*)addr;
   if constexpr (NT) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
 
-// Byte offsets (source side, destination side) of position i*VB of a tile.
-struct Pos {
-  uint64_t row;
-  uint32_t col;
+// Byte offsets, relative to the item's origins, of the source byte `b`
+// (counted from the start of the tile): source side, destination side and
+// bf16 side (half the destination column).  Contiguous items are one long
+// row; strided items divide by the row width.
+template <bool CONTIG>
+struct TileMap {
+  uint64_t start;
+  uint32_t c_base, width, magic, s1, s2;
+  uint64_t src_stride, dst_stride, dst2_stride;
+
+  __device__ __forceinline__ TileMap(const DevItem& it, const DevTile& t)
+      : start(t.start), c_base(t.c_base), width(it.row_bytes), magic(it.magic),
+        s1(it.shifts & 0xffu), s2(it.shifts >> 8), src_stride(it.src_stride),
+        dst_stride(it.dst_stride), dst2_stride(it.dst2_stride) {}
+
+  __device__ __forceinline__ void at(uint32_t b, uint64_t& so, uint64_t& dof) const {
+    if constexpr (CONTIG) {
+      so = start + b;
+      dof = so;
+    } else {
+      const uint32_t x = c_base + b;
+      const uint32_t q = div_apply(x, magic, s1, s2);
+      const uint64_t row = start + q;
+      const uint32_t col = x - q * width;
+      so = row * src_stride + col;
+      dof = row * dst_stride + col;
+    }
+  }
+
+  __device__ __forceinline__ void at(uint32_t b, uint64_t& so, uint64_t& dof, uint64_t& ho) const {
+    if constexpr (CONTIG) {
+      so = start + b;
+      dof = so;
+      ho = so >> 1;
+    } else {
+      const uint32_t x = c_base + b;
+      const uint32_t q = div_apply(x, magic, s1, s2);
+      const uint64_t row = start + q;
+      const uint32_t col = x - q * width;
+      so = row * src_stride + col;
+      dof = row * dst_stride + col;
+      ho = row * dst2_stride + (col >> 1);
+    }
+  }
 };
 
-__device__ __forceinline__ Pos tile_pos(const DevItem& it, const DevTile& t,
-                                        uint32_t byte_in_tile) {
-  Pos p;
-  if (it.row_bytes == 0) {
-    p.row = 0;
-    // contiguous: col carries nothing; caller uses start + byte_in_tile
-    p.col = 0;
-  } else {
-    const uint32_t x = t.c_base + byte_in_tile;
-    const uint32_t q = div_apply(x, it.magic, it.shifts & 0xffu, it.shifts >> 8);
-    p.row = t.start + q;
-    p.col = x - q * it.row_bytes;
-  }
-  return p;
-}
-
-template <int VB, bool NT>
+// Copy one tile.  The main loop covers whole groups of kBlock * kUnroll
+// vectors with no bounds test, so each lane issues its kUnroll loads back to
+// back before the stores; the tail takes the remaining vectors one by one.
+template <int VB, bool NT, bool CONTIG>
 __device__ void copy_tile(const DevItem& it, const DevTile& t) {
   typedef typename VecOf<VB>::type V;
+  constexpr int U = CONTIG ? kUnroll : kUnrollStrided;
+  const TileMap<CONTIG> map(it, t);
   const uint32_t nvec = t.nbytes / VB;
-  const bool contig = it.row_bytes == 0;
-  for (uint32_t base = 0; base < nvec; base += kBlock * kUnroll) {
-    V v[kUnroll];
-    uint64_t doff[kUnroll];
+  constexpr uint32_t kStep = kBlock * U;
+  const uint32_t nfull = nvec / kStep * kStep;
+  for (uint32_t base = 0; base < nfull; base += kStep) {
+    V v[U];
+    uint64_t doff[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = base + u * kBlock + threadIdx.x;
-      if (i < nvec) {
-        uint64_t soff;
-        if (contig) {
-          soff = t.start + uint64_t(i) * VB;
-          doff[u] = soff;
-        } else {
-          const Pos p = tile_pos(it, t, i * VB);
-          soff = p.row * it.src_stride + p.col;
-          doff[u] = p.row * it.dst_stride + p.col;
-        }
-        v[u] = ld<NT>(reinterpret_cast<const V*>(it.src + soff));
-      }
+    for (int u = 0; u < U; ++u) {
+      uint64_t soff;
+      map.at((base + u * kBlock + threadIdx.x) * VB, soff, doff[u]);
+      v[u] = ld<V, NT>(it.src + soff);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = base + u * kBlock + threadIdx.x;
-      if (i < nvec) st<NT>(reinterpret_cast<V*>(it.dst + doff[u]), v[u]);
-    }
+    for (int u = 0; u < U; ++u) st<V, NT>(it.dst + doff[u], v[u]);
+  }
+  for (uint32_t i = nfull + threadIdx.x; i < nvec; i += kBlock) {
+    uint64_t soff, doff;
+    map.at(i * VB, soff, doff);
+    st<V, NT>(it.dst + doff, ld<V, NT>(it.src + soff));
   }
 }
 
-template <int VB, bool NT>
+template <int VB, bool NT, bool CONTIG>
 __device__ void zero_tile(const DevItem& it, const DevTile& t) {
   typedef typename VecOf<VB>::type V;
+  const TileMap<CONTIG> map(it, t);
   const uint32_t nvec = t.nbytes / VB;
-  const bool contig = it.row_bytes == 0;
   const V z = V(0);
   for (uint32_t i = threadIdx.x; i < nvec; i += kBlock) {
-    uint64_t doff;
-    if (contig) {
-      doff = t.start + uint64_t(i) * VB;
-    } else {
-      const Pos p = tile_pos(it, t, i * VB);
-      doff = p.row * it.dst_stride + p.col;
-    }
-    st<NT>(reinterpret_cast<V*>(it.dst + doff), z);
+    uint64_t soff, doff;
+    map.at(i * VB, soff, doff);
+    st<V, NT>(it.dst + doff, z);
   }
 }
 
@@ -267,51 +306,76 @@ __device__ __forceinline__ uint32_t bf16_rne(uint32_t u) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-template <int NE, bool NT>
+template <int NE>
+__device__ __forceinline__ typename VecOf<2 * NE>::type to_bf16(typename VecOf<4 * NE>::type v) {
+  typename VecOf<2 * NE>::type h;
+  if constexpr (NE == 4) {
+    h.x = bf16_rne(v.x) | (bf16_rne(v.y) << 16);
+    h.y = bf16_rne(v.z) | (bf16_rne(v.w) << 16);
+  } else {
+    h = (unsigned short)bf16_rne(v);
+  }
+  return h;
+}
+
+// f32 region -> f32 copy (when the item has one) + bf16 RNE copy.
+template <int NE, bool NT, bool CONTIG>
 __device__ void recast_tile(const DevItem& it, const DevTile& t) {
-  constexpr int SB = 4 * NE;   // source (f32) bytes per lane vector
-  typedef typename VecOf<SB>::type VS;   // NE f32
-  typedef typename VecOf<2 * NE>::type VH;  // NE bf16
+  constexpr int SB = 4 * NE;                 // source (f32) bytes per lane vector
+  typedef typename VecOf<SB>::type VS;       // NE f32
+  typedef typename VecOf<2 * NE>::type VH;   // NE bf16
+  const TileMap<CONTIG> map(it, t);
   const uint32_t nvec = t.nbytes / SB;
-  const bool contig = it.row_bytes == 0;
   const bool has_dst = (it.flags >> 8) & 1u;
-  for (uint32_t base = 0; base < nvec; base += kBlock * kUnroll) {
-    VS v[kUnroll];
-    uint64_t doff[kUnroll], hoff[kUnroll];
+  constexpr int U = kUnrollStrided;
+  constexpr uint32_t kStep = kBlock * U;
+  const uint32_t nfull = nvec / kStep * kStep;
+  for (uint32_t base = 0; base < nfull; base += kStep) {
+    VS v[U];
+    uint64_t doff[U], hoff[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = base + u * kBlock + threadIdx.x;
-      if (i < nvec) {
-        uint64_t soff;
-        if (contig) {
-          soff = t.start + uint64_t(i) * SB;
-          doff[u] = soff;
-          hoff[u] = soff >> 1;
-        } else {
-          const Pos p = tile_pos(it, t, i * SB);
-          soff = p.row * it.src_stride + p.col;
-          doff[u] = p.row * it.dst_stride + p.col;
-          hoff[u] = p.row * it.dst2_stride + (p.col >> 1);
-        }
-        v[u] = ld<NT>(reinterpret_cast<const VS*>(it.src + soff));
-      }
+    for (int u = 0; u < U; ++u) {
+      uint64_t soff;
+      map.at((base + u * kBlock + threadIdx.x) * SB, soff, doff[u], hoff[u]);
+      v[u] = ld<VS, NT>(it.src + soff);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t i = base + u * kBlock + threadIdx.x;
-      if (i < nvec) {
-        if (has_dst) st<NT>(reinterpret_cast<VS*>(it.dst + doff[u]), v[u]);
-        VH h;
-        if constexpr (NE == 4) {
-          const uint32_t h0 = bf16_rne(v[u].x) | (bf16_rne(v[u].y) << 16);
-          const uint32_t h1 = bf16_rne(v[u].z) | (bf16_rne(v[u].w) << 16);
-          h.x = h0;
-          h.y = h1;
-        } else {
-          h = (unsigned short)bf16_rne(v[u]);
-        }
-        st<NT>(reinterpret_cast<VH*>(it.dst2 + hoff[u]), h);
-      }
+    for (int u = 0; u < U; ++u) {
+      if (has_dst) st<VS, NT>(it.dst + doff[u], v[u]);
+      st<VH, NT>(it.dst2 + hoff[u], to_bf16<NE>(v[u]));
+    }
+  }
+  for (uint32_t i = nfull + threadIdx.x; i < nvec; i += kBlock) {
+    uint64_t soff, doff, hoff;
+    map.at(i * SB, soff, doff, hoff);
+    const VS v = ld<VS, NT>(it.src + soff);
+    if (has_dst) st<VS, NT>(it.dst + doff, v);
+    st<VH, NT>(it.dst2 + hoff, to_bf16<NE>(v));
+  }
+}
+
+template <bool NT, bool CONTIG>
+__device__ __forceinline__ void exec_tile(const DevItem& it, const DevTile& t) {
+  const uint32_t kind = it.flags & 0xfu;
+  const uint32_t lv = (it.flags >> 4) & 0xfu;
+  if (kind == kKindCopy) {
+    switch (lv) {
+      case 4: copy_tile<16, NT, CONTIG>(it, t); break;
+      case 3: copy_tile<8, NT, CONTIG>(it, t); break;
+      case 2: copy_tile<4, NT, CONTIG>(it, t); break;
+      case 1: copy_tile<2, NT, CONTIG>(it, t); break;
+      default: copy_tile<1, NT, CONTIG>(it, t); break;
+    }
+  } else if (kind == kKindRecast) {
+    if (lv == 2) recast_tile<4, NT, CONTIG>(it, t);
+    else recast_tile<1, NT, CONTIG>(it, t);
+  } else {
+    switch (lv) {
+      case 4: zero_tile<16, NT, CONTIG>(it, t); break;
+      case 3: zero_tile<8, NT, CONTIG>(it, t); break;
+      case 2: zero_tile<4, NT, CONTIG>(it, t); break;
+      case 1: zero_tile<2, NT, CONTIG>(it, t); break;
+      default: zero_tile<1, NT, CONTIG>(it, t); break;
     }
   }
 }
@@ -322,28 +386,8 @@ __device__ __forceinline__ void exec_tiles(const DevItem* __restrict__ items,
   for (uint32_t ti = blockIdx.x; ti < n_tiles; ti += gridDim.x) {
     const DevTile t = tiles[ti];
     const DevItem it = items[t.item];
-    const uint32_t kind = it.flags & 0xfu;
-    const uint32_t lv = (it.flags >> 4) & 0xfu;
-    if (kind == kKindCopy) {
-      switch (lv) {
-        case 4: copy_tile<16, NT>(it, t); break;
-        case 3: copy_tile<8, NT>(it, t); break;
-        case 2: copy_tile<4, NT>(it, t); break;
-        case 1: copy_tile<2, NT>(it, t); break;
-        default: copy_tile<1, NT>(it, t); break;
-      }
-    } else if (kind == kKindRecast) {
-      if (lv == 2) recast_tile<4, NT>(it, t);
-      else recast_tile<1, NT>(it, t);
-    } else {
-      switch (lv) {
-        case 4: zero_tile<16, NT>(it, t); break;
-        case 3: zero_tile<8, NT>(it, t); break;
-        case 2: zero_tile<4, NT>(it, t); break;
-        case 1: zero_tile<2, NT>(it, t); break;
-        default: zero_tile<1, NT>(it, t); break;
-      }
-    }
+    if (it.row_bytes == 0) exec_tile<NT, true>(it, t);
+    else exec_tile<NT, false>(it, t);
   }
 }
 
@@ -472,9 +516,12 @@ int check_coverage(const std::vector<std::vector<Box>>& boxes, const std::vector
   return SR_OK;
 }
 
-void make_tiles(Phase& ph, uint32_t tile_bytes) {
+void make_tiles(Phase& ph, uint32_t tile_bytes, const std::vector<uint32_t>& order) {
   ph.tiles.clear();
-  for (uint32_t k = 0; k < ph.items.size(); ++k) {
+  uint64_t n = 0;
+  for (const HostItem& it : ph.items) n += (it.rows * it.row_bytes + tile_bytes - 1) / tile_bytes;
+  ph.tiles.reserve(n);
+  for (uint32_t k : order) {
     const HostItem& it = ph.items[k];
     const uint64_t total = it.rows * it.row_bytes;
     for (uint64_t start = 0; start < total; start += tile_bytes) {
@@ -491,6 +538,49 @@ void make_tiles(Phase& ph, uint32_t tile_bytes) {
       ph.tiles.push_back(t);
     }
   }
+}
+
+// Order a phase's items by the tensor address they start at: the source
+// side for pack, the destination side for unpack.  Pieces of one tensor then
+// run next to each other (tiles are generated in this order).
+std::vector<uint32_t> item_order(const Phase& ph, bool by_src) {
+  struct Key {
+    int64_t slot;
+    uint64_t off;
+    uint32_t idx;
+  };
+  std::vector<Key> keys(ph.items.size());
+  for (uint32_t i = 0; i < ph.items.size(); ++i) {
+    const HostItem& it = ph.items[i];
+    if (by_src) keys[i] = {it.src_slot, it.src_off, i};
+    else if (it.dst_slot >= 0) keys[i] = {it.dst_slot, it.dst_off, i};
+    else keys[i] = {it.dst2_slot, it.dst2_off * 2, i};
+  }
+  std::stable_sort(keys.begin(), keys.end(), [](const Key& x, const Key& y) {
+    return x.slot != y.slot ? x.slot < y.slot : x.off < y.off;
+  });
+  std::vector<uint32_t> order(keys.size());
+  for (size_t i = 0; i < keys.size(); ++i) order[i] = keys[i].idx;
+  return order;
+}
+
+// Interleave the (ordered) tile list `ways` ways: the list is cut into `ways`
+// contiguous segments and tile j of segment s goes to position j * ways + s.
+// Workgroups are dispatched to the 8 XCDs round-robin, so with ways = 8 each
+// XCD walks one contiguous eighth of the work, and the tiles in flight at any
+// time come from 8 distant regions instead of one window.
+void interleave_tiles(Phase& ph, uint32_t ways) {
+  const size_t n = ph.tiles.size();
+  if (ways < 2 || n < 2 * size_t(ways)) return;
+  const size_t seg = (n + ways - 1) / ways;
+  std::vector<DevTile> out;
+  out.reserve(n);
+  for (size_t j = 0; j < seg; ++j)
+    for (size_t s = 0; s < ways; ++s) {
+      const size_t i = s * seg + j;
+      if (i < n) out.push_back(ph.tiles[i]);
+    }
+  ph.tiles.swap(out);
 }
 
 // Largest power-of-two vector width (<= 16, >= esize) dividing every value
@@ -718,7 +808,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
   sr_plan_options opt{};
   if (options) opt = *options;
   if (opt.reserved != 0) return fail(SR_EINVAL, "options.reserved must be 0");
-  if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE))
+  if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE | SR_OPT_PIECE_ORDER | SR_OPT_NO_XCD_INTERLEAVE))
     return fail(SR_EINVAL, "unknown option flags 0x%x", opt.flags);
   if (opt.tile_bytes == 0) opt.tile_bytes = kDefaultTileBytes;
   if (opt.tile_bytes < 4096 || opt.tile_bytes > (16u << 20) ||
@@ -891,8 +981,21 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       return rc;
     }
   }
-  make_tiles(p->pack, opt.tile_bytes);
-  make_tiles(p->unpack, opt.tile_bytes);
+  {
+    std::vector<uint32_t> po(p->pack.items.size()), uo(p->unpack.items.size());
+    for (uint32_t i = 0; i < po.size(); ++i) po[i] = i;
+    for (uint32_t i = 0; i < uo.size(); ++i) uo[i] = i;
+    if (!(opt.flags & SR_OPT_PIECE_ORDER)) {
+      po = item_order(p->pack, true);
+      uo = item_order(p->unpack, false);
+    }
+    make_tiles(p->pack, opt.tile_bytes, po);
+    make_tiles(p->unpack, opt.tile_bytes, uo);
+  }
+  if (!(opt.flags & SR_OPT_NO_XCD_INTERLEAVE)) {
+    interleave_tiles(p->pack, kXcds);
+    interleave_tiles(p->unpack, kXcds);
+  }
   if (p->pack.tiles.size() > UINT32_MAX || p->unpack.tiles.size() > UINT32_MAX) {
     delete p;
     return fail(SR_EINVAL, "plan has too many tiles; raise tile_bytes");

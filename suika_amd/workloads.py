@@ -109,7 +109,7 @@ CONFIGS: Dict[str, Workload] = {
         description="Qwen2-7B GQA f32 master/m/v + bf16 recast, TP2->TP4, dest tp3"),
 }
 
-# Order of BASELINE.json "configs".
+# Order of the benchmark configurations (GPT-125M, Llama2-7B, Llama2-13B, GPT-6.7B, Qwen2-7B).
 CONFIG_ORDER = ["gpt125m_tp2_tp4", "llama7b_tp4pp2_tp2pp2", "llama13b_tp8_tp4pp2",
                 "gpt6.7b_tp1pp4_tp8", "qwen7b_tp2_tp4"]
 BENCH_CONFIG = "llama7b_tp4pp2_tp2pp2"

@@ -54,7 +54,10 @@ SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
     PlanOptions(tile_bytes=8192, max_blocks=7),
     PlanOptions(nontemporal=False),
     PlanOptions(tile_bytes=1 << 20, nontemporal=False, max_blocks=300),
-], ids=["tile4k", "tile8k_grid7", "temporal", "tile1m_temporal_grid300"])
+    PlanOptions(tile_bytes=4096, address_order=False),
+    PlanOptions(tile_bytes=4096, xcd_order=False, max_blocks=33),
+], ids=["tile4k", "tile8k_grid7", "temporal", "tile1m_temporal_grid300", "tile4k_piece_order",
+        "tile4k_linear_grid33"])
 def test_gpu_tunings_match_oracle(w, opt):
     _check(w, "index", opt)
 
