@@ -13,6 +13,8 @@ and writes D); ``roofline`` is for the slower of the two kernels, timed with
 HIP events on the stream the kernels run on; ``cpu_baseline`` times the
 reference-style torch-CPU reshard (chunk/contiguous/cat) on a bounded sample
 of the same workload on this host's cores, scaled to the same unit.
+``direct_gather`` reports the buffer-free route (one launch, P + D bytes) that
+applies when every source shard is resident on this GPU.
 """
 from __future__ import annotations
 
@@ -233,6 +235,20 @@ def main(argv=None) -> int:
     print(f"[bench] pack {pack_ms:.3f} ms  unpack {unpack_ms:.3f} ms  step {total_ms:.3f} ms  "
           f"wall {wall_s * 1e3 / K:.3f} ms/step", file=sys.stderr, flush=True)
 
+    # The direct route (sources resident on this GPU, no buffers): one gather
+    # launch per reshard, P read + D written.  Reported beside the main line.
+    for _ in range(2):
+        plan.gather_ptrs(sp, dp, stream)
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    g0.record(stream)
+    for _ in range(K):
+        plan.gather_ptrs(sp, dp, stream)
+    g1.record(stream)
+    torch.cuda.synchronize()
+    gather_ms = g0.elapsed_time(g1) / K
+    b_gather = plan.gather_bytes
+
     value = b_alg / (total_ms * 1e-3) / 1e9
     pack_gbps = b_pack / (pack_ms * 1e-3) / 1e9
     unpack_gbps = b_unpack / (unpack_ms * 1e-3) / 1e9
@@ -287,6 +303,9 @@ def main(argv=None) -> int:
         "B_min_GBps": round(b_min / (total_ms * 1e-3) / 1e9, 1),
         "pack_GBps": round(pack_gbps, 1),
         "unpack_GBps": round(unpack_gbps, 1),
+        "direct_gather": {"ms": round(gather_ms, 4), "bytes": b_gather,
+                          "GBps": round(b_gather / (gather_ms * 1e-3) / 1e9, 1),
+                          "pct_of_peak": round(100 * b_gather / (gather_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)},
         "roofline": {
             "bound": "hbm",
             "kernel": dom,

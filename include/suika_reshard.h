@@ -12,6 +12,10 @@
  *            (+ fused fp32 -> bf16 round-to-nearest-even recast,
  *             + zero fill of padded vocabulary rows)
  *
+ * When every source shard is resident on this GPU (a checkpoint reshard, or
+ * the pieces a rank keeps for itself), sr_gather moves the same pieces from
+ * source to destination in one pass, without buffers.
+ *
  * Reference interfaces replaced (paths relative to the Suika repository):
  *   - Suika/migration.py:290-312  TransferOp.get_send_tensor
  *       chunk(n, dim)[k].contiguous() of a source shard          -> sr_pack
@@ -46,7 +50,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 1
+#define SR_ABI_VERSION 2
 
 typedef enum sr_status {
   SR_OK = 0,
@@ -134,6 +138,9 @@ typedef struct sr_plan_info {
   uint64_t unpack_bytes_read;    /* algorithmic bytes of the unpack phase */
   uint64_t unpack_bytes_written;
   uint64_t buffer_bytes;         /* sum over peers of sr_plan_peer_bytes */
+  int64_t gather_tiles;
+  uint64_t gather_bytes_read;    /* algorithmic bytes of sr_gather */
+  uint64_t gather_bytes_written;
 } sr_plan_info;
 
 /* ABI version of the loaded library (SR_ABI_VERSION). */
@@ -184,6 +191,17 @@ int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs,
  * Suika/migration.py:531-541.
  */
 int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs,
+              hipStream_t stream);
+
+/*
+ * Gather: every piece straight from its source region to its destination
+ * region(s), with the unpack's recast and zero fill, in one launch; reads P
+ * and writes D bytes instead of the 3P + D of pack + unpack.  For sources
+ * resident on this GPU: the fake-source (checkpoint) mode of
+ * execute_param_transfer (Suika/migration.py:477-482) and its self transfers
+ * (migration.py:448-459).
+ */
+int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
               hipStream_t stream);
 
 void sr_plan_destroy(sr_plan* plan);

@@ -53,10 +53,11 @@ EXPORTED_SYMBOLS = (
     "sr_plan_info_get",
     "sr_pack",
     "sr_unpack",
+    "sr_gather",
     "sr_plan_destroy",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class SrTensor(ctypes.Structure):
@@ -107,6 +108,9 @@ class SrPlanInfo(ctypes.Structure):
         ("unpack_bytes_read", ctypes.c_uint64),
         ("unpack_bytes_written", ctypes.c_uint64),
         ("buffer_bytes", ctypes.c_uint64),
+        ("gather_tiles", ctypes.c_int64),
+        ("gather_bytes_read", ctypes.c_uint64),
+        ("gather_bytes_written", ctypes.c_uint64),
     ]
 
 
@@ -149,6 +153,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_pack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.sr_unpack.restype = ctypes.c_int
     lib.sr_unpack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_gather.restype = ctypes.c_int
+    lib.sr_gather.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
 

@@ -406,6 +406,13 @@ __global__ __launch_bounds__(kBlock) void sr_unpack_kernel(const DevItem* __rest
   exec_tiles<NT>(items, tiles, n_tiles);
 }
 
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void sr_gather_kernel(const DevItem* __restrict__ items,
+                                                           const DevTile* __restrict__ tiles,
+                                                           uint32_t n_tiles) {
+  exec_tiles<NT>(items, tiles, n_tiles);
+}
+
 // ----------------------------------------------------------- host structures
 
 // Pointer-independent description of one item of a phase.
@@ -453,6 +460,7 @@ struct sr_plan {
   sr_plan_options opt{};
   Phase pack;
   Phase unpack;
+  Phase gather;   // direct source -> destination, no buffers
   int device = -1;
 };
 
@@ -677,7 +685,9 @@ int upload_static(Phase& ph) {
   return SR_OK;
 }
 
-int run_phase(sr_plan* p, Phase& ph, bool is_pack, const uint64_t* src_base, size_t n_src_base,
+enum PhaseKind { kPack, kUnpack, kGather };
+
+int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const uint64_t* src_base, size_t n_src_base,
               const uint64_t* dst_base, size_t n_dst_base, hipStream_t stream) {
   int rc = ensure_device(p);
   if (rc != SR_OK) return rc;
@@ -706,21 +716,14 @@ int run_phase(sr_plan* p, Phase& ph, bool is_pack, const uint64_t* src_base, siz
   if (p->opt.max_blocks != 0) grid = std::min(grid, p->opt.max_blocks);
   grid = std::min(grid, kMaxGrid);
   const bool nt = (p->opt.flags & SR_OPT_TEMPORAL) == 0;
-  if (is_pack) {
-    if (nt)
-      hipLaunchKernelGGL(sr_pack_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
-                         ph.d_tiles, n_tiles);
-    else
-      hipLaunchKernelGGL(sr_pack_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
-                         ph.d_tiles, n_tiles);
-  } else {
-    if (nt)
-      hipLaunchKernelGGL(sr_unpack_kernel<true>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
-                         ph.d_tiles, n_tiles);
-    else
-      hipLaunchKernelGGL(sr_unpack_kernel<false>, dim3(grid), dim3(kBlock), 0, stream, ph.d_items,
-                         ph.d_tiles, n_tiles);
+  typedef void (*KernelFn)(const DevItem*, const DevTile*, uint32_t);
+  KernelFn fn;
+  switch (kind) {
+    case kPack: fn = nt ? sr_pack_kernel<true> : sr_pack_kernel<false>; break;
+    case kUnpack: fn = nt ? sr_unpack_kernel<true> : sr_unpack_kernel<false>; break;
+    default: fn = nt ? sr_gather_kernel<true> : sr_gather_kernel<false>; break;
   }
+  hipLaunchKernelGGL(fn, dim3(grid), dim3(kBlock), 0, stream, ph.d_items, ph.d_tiles, n_tiles);
   SR_HIP_TRY(hipGetLastError());
   SR_HIP_TRY(hipEventRecord(ph.ev_kernel, stream));
   return SR_OK;
@@ -873,6 +876,8 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       }
       p->unpack.items.push_back(it);
       p->unpack.bytes_written += pc.rows * pc.cols * es;
+      p->gather.items.push_back(it);
+      p->gather.bytes_written += pc.rows * pc.cols * es;
       cover[pc.dst].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
       continue;
     }
@@ -973,6 +978,28 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
     p->unpack.bytes_read += payload;
     if (dst >= 0) p->unpack.bytes_written += payload;
     if (dst2 >= 0) p->unpack.bytes_written += payload / 2;
+
+    // Gather item: source region -> destination region(s), no buffer.
+    HostItem ga = up;
+    ga.src_slot = pc.src;
+    ga.src_off = pk.src_off;
+    ga.src_stride = st.cols * es;
+    ga.rows = pc.rows;
+    ga.row_bytes = pc.cols * es;
+    ga.contiguous = pc.rows == 1 ||
+                    (ga.src_stride == ga.row_bytes && (dst < 0 || ga.dst_stride == ga.row_bytes) &&
+                     (dst2 < 0 || ga.dst2_stride * 2 == ga.row_bytes));
+    if (ga.contiguous) {
+      ga.row_bytes *= ga.rows;
+      ga.rows = 1;
+    } else if (ga.row_bytes > max_row) {
+      return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
+                      (unsigned long long)ga.row_bytes));
+    }
+    p->gather.items.push_back(ga);
+    p->gather.bytes_read += payload;
+    if (dst >= 0) p->gather.bytes_written += payload;
+    if (dst2 >= 0) p->gather.bytes_written += payload / 2;
   }
 
   if (!(opt.flags & SR_OPT_SKIP_COVERAGE)) {
@@ -991,12 +1018,18 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
     }
     make_tiles(p->pack, opt.tile_bytes, po);
     make_tiles(p->unpack, opt.tile_bytes, uo);
+    std::vector<uint32_t> go(p->gather.items.size());
+    for (uint32_t i = 0; i < go.size(); ++i) go[i] = i;
+    if (!(opt.flags & SR_OPT_PIECE_ORDER)) go = item_order(p->gather, false);
+    make_tiles(p->gather, opt.tile_bytes, go);
   }
   if (!(opt.flags & SR_OPT_NO_XCD_INTERLEAVE)) {
     interleave_tiles(p->pack, kXcds);
     interleave_tiles(p->unpack, kXcds);
+    interleave_tiles(p->gather, kXcds);
   }
-  if (p->pack.tiles.size() > UINT32_MAX || p->unpack.tiles.size() > UINT32_MAX) {
+  if (p->pack.tiles.size() > UINT32_MAX || p->unpack.tiles.size() > UINT32_MAX ||
+      p->gather.tiles.size() > UINT32_MAX) {
     delete p;
     return fail(SR_EINVAL, "plan has too many tiles; raise tile_bytes");
   }
@@ -1031,6 +1064,9 @@ int sr_plan_info_get(const sr_plan* plan, sr_plan_info* out) {
   out->pack_bytes_written = plan->pack.bytes_written;
   out->unpack_bytes_read = plan->unpack.bytes_read;
   out->unpack_bytes_written = plan->unpack.bytes_written;
+  out->gather_tiles = int64_t(plan->gather.tiles.size());
+  out->gather_bytes_read = plan->gather.bytes_read;
+  out->gather_bytes_written = plan->gather.bytes_written;
   uint64_t b = 0;
   for (uint64_t v : plan->peer_bytes) b += v;
   out->buffer_bytes = b;
@@ -1053,7 +1089,7 @@ int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs, 
   std::vector<uint64_t> sb(plan->src.size()), bb(plan->n_peers);
   for (size_t i = 0; i < sb.size(); ++i) sb[i] = reinterpret_cast<uintptr_t>(src_ptrs ? src_ptrs[i] : nullptr);
   for (size_t i = 0; i < bb.size(); ++i) bb[i] = reinterpret_cast<uintptr_t>(peer_bufs ? peer_bufs[i] : nullptr);
-  return run_phase(plan, plan->pack, true, sb.data(), sb.size(), bb.data(), bb.size(), stream);
+  return run_phase(plan, plan->pack, kPack, sb.data(), sb.size(), bb.data(), bb.size(), stream);
 }
 
 int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs, hipStream_t stream) {
@@ -1071,13 +1107,32 @@ int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs
   std::vector<uint64_t> bb(plan->n_peers), db(plan->dst.size());
   for (size_t i = 0; i < bb.size(); ++i) bb[i] = reinterpret_cast<uintptr_t>(peer_bufs ? peer_bufs[i] : nullptr);
   for (size_t i = 0; i < db.size(); ++i) db[i] = reinterpret_cast<uintptr_t>(dst_ptrs ? dst_ptrs[i] : nullptr);
-  return run_phase(plan, plan->unpack, false, bb.data(), bb.size(), db.data(), db.size(), stream);
+  return run_phase(plan, plan->unpack, kUnpack, bb.data(), bb.size(), db.data(), db.size(), stream);
+}
+
+int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs, hipStream_t stream) {
+  if (!plan) return fail(SR_EINVAL, "plan is null");
+  std::vector<uint32_t> sal(plan->src.size(), 0), dal(plan->dst.size(), 0);
+  for (const sr_piece& pc : plan->pieces) {
+    if (pc.src >= 0) sal[pc.src] = dtype_size(plan->src[pc.src].dtype);
+    if (pc.dst >= 0) dal[pc.dst] = dtype_size(plan->dst[pc.dst].dtype);
+    if (pc.dst2 >= 0) dal[pc.dst2] = dtype_size(plan->dst[pc.dst2].dtype);
+  }
+  int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
+  if (rc != SR_OK) return rc;
+  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
+  if (rc != SR_OK) return rc;
+  std::vector<uint64_t> sb(plan->src.size()), db(plan->dst.size());
+  for (size_t i = 0; i < sb.size(); ++i) sb[i] = reinterpret_cast<uintptr_t>(src_ptrs ? src_ptrs[i] : nullptr);
+  for (size_t i = 0; i < db.size(); ++i) db[i] = reinterpret_cast<uintptr_t>(dst_ptrs ? dst_ptrs[i] : nullptr);
+  return run_phase(plan, plan->gather, kGather, sb.data(), sb.size(), db.data(), db.size(), stream);
 }
 
 void sr_plan_destroy(sr_plan* plan) {
   if (!plan) return;
   free_phase(plan->pack);
   free_phase(plan->unpack);
+  free_phase(plan->gather);
   delete plan;
 }
 

@@ -8,11 +8,11 @@ Same names, arguments and error behaviour as the reference's operators:
                                           -- Suika/migration.py:675-746
 
 ``execute_param_transfer`` compiles the TransferOps that land on this rank
-into a ``ReshardPlan`` and runs pack -> peer buffers -> unpack on the GPU.
-Every source piece goes through its peer's buffer; on one GPU the buffers of
-all peers are resident in this GPU's HBM (``fake_source_state_dicts`` holds
-the peers' shards, as in the reference's checkpoint path,
-migration.py:1223-1244).  A cross-GPU exchange between pack and unpack is not
+into a ``ReshardPlan`` and runs it on the GPU, either as one gather pass
+(sources -> destination) or as pack -> per-peer buffers -> unpack.  On one
+GPU all peers' shards are resident in this GPU's HBM
+(``fake_source_state_dicts`` holds them, as in the reference's checkpoint
+path, migration.py:1223-1244).  A cross-GPU exchange between pack and unpack is not
 part of this build: ops from a remote rank without a local copy of its shards
 raise ``NotImplementedError``.
 
@@ -82,16 +82,21 @@ def execute_param_transfer(
     recast: Optional[Mapping[str, str]] = None,
     plan_options: Optional[PlanOptions] = None,
     stream: Optional[torch.cuda.Stream] = None,
+    route: str = "direct",
 ) -> StateDict:
     """Execute a transfer schedule for this rank; returns its target state.
 
     ``source_state_dict`` (this rank's own shards) is cleared in place, as in
     the reference (migration.py:527).  Normal sub-fields move through the HIP
-    pack/unpack kernels; 1-element sub-fields (e.g. AdamW ``step``) are copied
-    whole (migration.py:443-446, 479-487).  Extensions: ``rank`` overrides
+    kernels; 1-element sub-fields (e.g. AdamW ``step``) are copied whole
+    (migration.py:443-446, 479-487).  Extensions: ``rank`` overrides
     ``dist.get_rank(world)``; ``recast`` maps a bf16 target field to the f32
-    field it is rounded from; ``plan_options`` tunes the kernels.
+    field it is rounded from; ``plan_options`` tunes the kernels; ``route``
+    is ``"direct"`` (one gather pass from the resident sources, the default
+    since every source is on this GPU) or ``"buffers"`` (pack into per-peer
+    buffers, then unpack: the path an exchange between GPUs goes through).
     """
+    assert route in ("direct", "buffers"), f"unknown route {route!r}"
     if log_func is None:
         log_func = lambda msg: None  # noqa: E731
     if prof is None:
@@ -145,14 +150,20 @@ def execute_param_transfer(
                                          f"not on {device}")
 
     with torch.cuda.device(device):
-        buffers = plan.alloc_buffers(device)
         target = plan.alloc_dst(device)
-        prof.start("execute pack")
-        plan.pack(sources, buffers, stream)
-        prof.stop("execute pack")
-        prof.start("execute unpack")
-        plan.unpack(buffers, target, stream)
-        prof.stop("execute unpack")
+        buffers = []
+        if route == "direct":
+            prof.start("execute gather")
+            plan.gather(sources, target, stream)
+            prof.stop("execute gather")
+        else:
+            buffers = plan.alloc_buffers(device)
+            prof.start("execute pack")
+            plan.pack(sources, buffers, stream)
+            prof.stop("execute pack")
+            prof.start("execute unpack")
+            plan.unpack(buffers, target, stream)
+            prof.stop("execute unpack")
 
     # 1-element sub-fields ride along whole; the first op's source wins,
     # matching tensors[0].clone() of migration.py:538.

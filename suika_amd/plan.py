@@ -302,6 +302,19 @@ class ReshardPlan:
                                   _stream_handle(stream))
         _lib.check(rc, "sr_unpack", self._L)
 
+    def gather_ptrs(self, src_ptrs: List[int], dst_ptrs: List[int], stream=None) -> None:
+        rc = self._L.sr_gather(self._handle, self._carray(src_ptrs), self._carray(dst_ptrs),
+                               _stream_handle(stream))
+        _lib.check(rc, "sr_gather", self._L)
+
+    def gather(self, sources, dst, stream=None) -> None:
+        """Source shards -> destination shards directly (async on ``stream``)."""
+        self.gather_ptrs(self.src_pointers(sources), self.dst_pointers(dst), stream)
+
+    @property
+    def gather_bytes(self) -> int:
+        return int(self.info.gather_bytes_read + self.info.gather_bytes_written)
+
     def pack(self, sources, buffers, stream=None) -> None:
         """Source shards -> peer buffers (async on ``stream``)."""
         self.pack_ptrs(self.src_pointers(sources), self.buf_pointers(buffers), stream)

@@ -160,7 +160,7 @@ def to_device(srcs, w: Workload, device) -> Dict[int, Dict[str, Dict[str, torch.
             for r, sd in srcs.items()}
 
 
-def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None):
+def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers"):
     """Product path: execute_param_transfer on the GPU with peer shards resident."""
     from suika_amd import execute_param_transfer
     ops = w.ops()
@@ -168,7 +168,7 @@ def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None):
     expected_sub_fields = [(f, "normal") for f in w.src_fields]
     out = execute_param_transfer(ops, {}, torch.device(device), expected_sub_fields,
                                  rank=w.dst_rank, fake_source_state_dicts=fake,
-                                 recast=w.recast_map, plan_options=plan_options)
+                                 recast=w.recast_map, plan_options=plan_options, route=route)
     torch.cuda.synchronize()
     return {n: {f: t2np(t) for f, t in e.items()} for n, e in out.items()}
 

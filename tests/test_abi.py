@@ -19,7 +19,7 @@ def header_functions():
 
 def test_library_loads_and_version():
     L = _lib.lib()
-    assert L.sr_abi_version() == _lib.ABI_VERSION == 1
+    assert L.sr_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_every_declared_symbol_is_exported():
@@ -65,6 +65,7 @@ def test_valid_plan_and_buffer_layout():
     info = _lib.SrPlanInfo()
     assert L.sr_plan_info_get(h, ctypes.byref(info)) == 0
     assert info.n_pieces == 2 and info.pack_bytes_read == 256 and info.unpack_bytes_written == 256
+    assert info.gather_bytes_read == 256 and info.gather_bytes_written == 256
     off = ctypes.c_uint64()
     assert L.sr_plan_piece_offset(h, 1, ctypes.byref(off)) == 0 and off.value == 0
     L.sr_plan_destroy(h)
@@ -131,6 +132,8 @@ def test_recast_and_zero_rules():
     info = _lib.SrPlanInfo()
     _lib.lib().sr_plan_info_get(h, ctypes.byref(info))
     assert info.unpack_bytes_written == 3 * 8 * 4 + 3 * 8 * 2 + 8 * 4 + 8 * 2
+    assert info.gather_bytes_written == info.unpack_bytes_written
+    assert info.gather_bytes_read == 3 * 8 * 4
     _lib.lib().sr_plan_destroy(h)
     # bf16 source cannot be recast
     rc, _ = _plan([(4, 8, BF16)], [(4, 8, F32), (4, 8, BF16)], 1,

@@ -96,7 +96,7 @@ def test_fuzz_gpu(seed):
     glob = index_state(w, _names(w))
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     want = oracle_dest(w, srcs)
-    got = gpu_execute(w, srcs)
+    got = gpu_execute(w, srcs, route="direct" if seed % 2 else "buffers")
     assert set(got) == set(want)
     for name, ent in want.items():
         for f, a in ent.items():

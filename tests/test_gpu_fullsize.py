@@ -66,10 +66,22 @@ def test_fullsize_index_coded(key):
     plan.pack(sources, bufs)
     plan.unpack(bufs, dst)
     torch.cuda.synchronize()
-    del sources, bufs
+    del bufs
+    # the direct route into a second destination set must agree bit for bit
+    dst2 = plan.alloc_dst(dev)
+    for e in dst2.values():
+        for t in e.values():
+            t.view(torch.uint8).fill_(0x5A)
+    plan.gather(sources, dst2)
+    torch.cuda.synchronize()
+    del sources
 
     recast = w.recast_map
     bad = []
+    for (name, f) in plan.dst_keys:
+        if not torch.equal(dst[name][f].view(torch.uint8), dst2[name][f].view(torch.uint8)):
+            bad.append((name, f, "gather"))
+    del dst2
     for (name, f) in plan.dst_keys:
         gidx = O.shard_index(odst[w.dst_rank][name], xp=torch, device=dev)
         if f in recast:

@@ -27,12 +27,12 @@ def _names(w):
     return out
 
 
-def _check(w, payload="seeded", options=None):
-    print(f"[gpu parity] {w.key} payload={payload} options={options}", flush=True)
+def _check(w, payload="seeded", options=None, route="buffers"):
+    print(f"[gpu parity] {w.key} payload={payload} options={options} route={route}", flush=True)
     glob = (global_state if payload == "seeded" else index_state)(w, _names(w))
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     want = oracle_dest(w, srcs)
-    got = gpu_execute(w, srcs, plan_options=options)
+    got = gpu_execute(w, srcs, plan_options=options, route=route)
     assert set(got) == set(want)
     for name in want:
         assert set(got[name]) == set(want[name]), name
@@ -40,9 +40,10 @@ def _check(w, payload="seeded", options=None):
             np.testing.assert_array_equal(got[name][f], want[name][f], err_msg=f"{w.key}: {name}/{f}")
 
 
+@pytest.mark.parametrize("route", ["buffers", "direct"])
 @pytest.mark.parametrize("w", SMALL, ids=[w.key for w in SMALL])
-def test_gpu_matches_oracle(w):
-    _check(w)
+def test_gpu_matches_oracle(w, route):
+    _check(w, route=route)
 
 
 SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
@@ -60,6 +61,7 @@ SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
         "tile4k_linear_grid33"])
 def test_gpu_tunings_match_oracle(w, opt):
     _check(w, "index", opt)
+    _check(w, "index", opt, route="direct")
 
 
 def test_gpu_repeat_and_streams():
@@ -106,7 +108,7 @@ def test_gpu_reproduces_golden_vectors(payload, case):
     w = cases.golden_cases()[case]
     print(f"[gpu golden] {case} {payload}", flush=True)
     srcs, want = load_reshard_vectors()[payload][case]
-    got = gpu_execute(w, srcs)
+    got = gpu_execute(w, srcs, route="direct" if payload == "index" else "buffers")
     assert set(got) == set(want)
     for name, ent in want.items():
         for f, a in ent.items():
