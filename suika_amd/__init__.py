@@ -3,7 +3,8 @@
 Public API mirrors the reference's migration module (Suika/migration.py):
 ``TensorMeta``, ``ParamLayout``, ``TransferOp``, ``schedule_param_transfer``,
 ``execute_param_transfer``, ``schedule_and_execute_param_transfer``,
-``merge_model_and_optimizer_state_dict``, ``split_model_and_optimizer_state_dict``.
+``merge_model_and_optimizer_state_dict``, ``split_model_and_optimizer_state_dict``,
+``checkpoint_save``, ``checkpoint_load``, ``migration_save``, ``migration_load``.
 The data movement runs in HIP kernels behind the C ABI of
 ``lib/libsuika_reshard.so`` (include/suika_reshard.h).
 """
@@ -14,6 +15,7 @@ from .migration import (execute_param_transfer, merge_model_and_optimizer_state_
                         schedule_and_execute_param_transfer, split_model_and_optimizer_state_dict)
 from .plan import PlanOptions, ReshardPlan, SlotSpec
 from ._lib import PlanError, ReshardError
+from .checkpoint import checkpoint_load, checkpoint_save, migration_load, migration_save
 
 __all__ = [
     "CHUNK", "QKV_HEADS", "VOCAB_PAD", "ParamLayout", "TensorMeta", "TransferOp",
@@ -21,5 +23,6 @@ __all__ = [
     "schedule_param_transfer", "vocab_padded", "execute_param_transfer",
     "merge_model_and_optimizer_state_dict", "schedule_and_execute_param_transfer",
     "split_model_and_optimizer_state_dict", "PlanOptions", "ReshardPlan", "SlotSpec",
-    "PlanError", "ReshardError",
+    "PlanError", "ReshardError", "checkpoint_save", "checkpoint_load", "migration_save",
+    "migration_load",
 ]

@@ -1,0 +1,230 @@
+"""Checkpoint-resume resharding on the GPU engine.
+
+Same names, arguments, files and control flow as the reference's
+``checkpoint_save`` / ``checkpoint_load`` (Suika/migration.py:1156-1305):
+
+* save: every rank writes ``state_dict_{rank}.pt`` (its merged model +
+  optimizer state); rank 0 writes ``param_layout.pt`` and
+  ``other_context.pt``;
+* load: the target layout is gathered from the new model, the transfer is
+  scheduled against the saved layout, the shards this rank needs are loaded
+  from disk, resharded, split back into model and optimizer state and loaded.
+
+The reference reshards on the CPU (``execute_param_transfer`` with
+``device="cpu"``, migration.py:1235-1244); here the needed shards are loaded
+straight into HBM and resharded by the HIP engine (``route="direct"``: one
+gather launch).  Files hold only tensors, numbers, strings and plain
+containers -- layouts are stored as dicts -- so they load with
+``torch.load(weights_only=True)``.
+"""
+from __future__ import annotations
+
+import os
+from collections import OrderedDict
+from typing import Any, Callable, Dict, Optional, Union
+
+import torch
+import torch.distributed as dist
+from torch.nn import Module
+from torch.optim import Optimizer
+
+from .meta import ParamLayout, TensorMeta, schedule_param_transfer
+from .migration import (execute_param_transfer, merge_model_and_optimizer_state_dict,
+                        split_model_and_optimizer_state_dict)
+
+LAYOUT_FILE = "param_layout.pt"
+CONTEXT_FILE = "other_context.pt"
+
+
+def _dtype_name(dt: torch.dtype) -> str:
+    return str(dt).replace("torch.", "")
+
+
+def meta_to_plain(m: TensorMeta) -> Dict[str, Any]:
+    return {"name": m.name, "dtype": _dtype_name(m.dtype), "shape": [int(s) for s in m.shape],
+            "tp_meta": None if m.tp_meta is None else [int(v) for v in m.tp_meta],
+            "kind": m.kind, "kind_args": [int(v) for v in m.kind_args]}
+
+
+def meta_from_plain(d: Dict[str, Any]) -> TensorMeta:
+    return TensorMeta(name=d["name"], dtype=getattr(torch, d["dtype"]), shape=tuple(d["shape"]),
+                      tp_meta=None if d["tp_meta"] is None else tuple(d["tp_meta"]),
+                      kind=d["kind"], kind_args=tuple(d["kind_args"]))
+
+
+def layout_to_plain(pl: ParamLayout) -> Dict[int, Dict[str, Dict[str, Any]]]:
+    return {int(r): {n: meta_to_plain(m) for n, m in metas.items()} for r, metas in pl.layout.items()}
+
+
+def layout_from_plain(d: Dict[int, Dict[str, Dict[str, Any]]]) -> ParamLayout:
+    return ParamLayout.from_metas({int(r): {n: meta_from_plain(m) for n, m in metas.items()}
+                                   for r, metas in d.items()})
+
+
+def _context_to_plain(ctx: Dict[str, Any]) -> Dict[str, Any]:
+    out = dict(ctx)
+    out["expected_sub_fields"] = [[f, t if isinstance(t, str) else meta_to_plain(t)]
+                                  for f, t in ctx["expected_sub_fields"]]
+    return out
+
+
+def _context_from_plain(ctx: Dict[str, Any]) -> Dict[str, Any]:
+    out = dict(ctx)
+    out["expected_sub_fields"] = [(f, t if isinstance(t, str) else meta_from_plain(t))
+                                  for f, t in ctx["expected_sub_fields"]]
+    return out
+
+
+def _rank_and_world(world) -> tuple:
+    if dist.is_available() and dist.is_initialized():
+        return dist.get_rank(world), dist.get_world_size(world)
+    return 0, 1
+
+
+def _gather_layout(model: Module, world) -> ParamLayout:
+    layout = ParamLayout()
+    if dist.is_available() and dist.is_initialized():
+        layout.gather(model, world)
+    else:
+        from .meta import get_param_tensor_meta
+        layout.layout[0] = get_param_tensor_meta(model)
+    return layout
+
+
+def _barrier(world) -> None:
+    if dist.is_available() and dist.is_initialized():
+        dist.barrier(world)
+
+
+def checkpoint_save(model: Module, optimizer: Optional[Optimizer], other_context: Any,
+                    checkpoint_dir: str, world: Optional[dist.ProcessGroup] = None,
+                    log_func: Optional[Callable] = None) -> None:
+    """Write this rank's shard and (rank 0) the layout (migration.py:1156-1184)."""
+    if log_func is None:
+        log_func = lambda msg: None  # noqa: E731
+    log_func("checkpoint_save: begin")
+    os.makedirs(checkpoint_dir, exist_ok=True)
+    layout = _gather_layout(model, world)
+    state_dict, other_context_dict = merge_model_and_optimizer_state_dict(model, optimizer, other_context)
+    rank, _ = _rank_and_world(world)
+    if rank == 0:
+        torch.save(layout_to_plain(layout), os.path.join(checkpoint_dir, LAYOUT_FILE))
+        torch.save(_context_to_plain(other_context_dict), os.path.join(checkpoint_dir, CONTEXT_FILE))
+    torch.save(state_dict, os.path.join(checkpoint_dir, f"state_dict_{rank}.pt"))
+    log_func("checkpoint_save: end")
+
+
+def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Optimizer, None],
+                    checkpoint_dir: str, world: Optional[dist.ProcessGroup] = None,
+                    log_func: Optional[Callable] = None, *, device: Optional[torch.device] = None,
+                    route: str = "direct", remove_files: bool = True):
+    """Reshard a checkpoint written under another layout into ``model`` (and
+    the optimizer) on the GPU (migration.py:1186-1305).
+
+    Returns ``other_context``, or ``(optimizer, other_context)`` when
+    ``optimizer`` is a provider callable; a missing checkpoint returns
+    ``None`` / ``(optimizer_provider(), None)`` as the reference does.
+    Extensions: ``device`` (default: the current CUDA device), ``route``
+    (``"direct"`` or ``"buffers"``), ``remove_files`` (rank 0 deletes the
+    checkpoint after loading, as the reference always does).
+    """
+    if log_func is None:
+        log_func = lambda msg: None  # noqa: E731
+    log_func("checkpoint_load: begin")
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    elif not isinstance(device, torch.device):
+        device = torch.device(device)
+    if callable(optimizer) and not isinstance(optimizer, Optimizer):
+        optimizer_provider, optimizer = optimizer, None
+    elif isinstance(optimizer, Optimizer) or optimizer is None:
+        optimizer_provider = None
+    else:
+        raise TypeError(f"optimizer should be Optimizer or Callable, but got {type(optimizer)}")
+    rank, _ = _rank_and_world(world)
+
+    try:
+        source_layout = layout_from_plain(
+            torch.load(os.path.join(checkpoint_dir, LAYOUT_FILE), weights_only=True, map_location="cpu"))
+        other_context_dict = _context_from_plain(
+            torch.load(os.path.join(checkpoint_dir, CONTEXT_FILE), weights_only=True, map_location="cpu"))
+    except FileNotFoundError as e:
+        log_func(f"checkpoint_load: [warning] checkpoint file not found, skip loading\n{e}")
+        return (optimizer_provider(), None) if optimizer_provider else None
+
+    target_layout = _gather_layout(model, world)
+    ops = schedule_param_transfer(source_layout, target_layout)
+    srcs = {op.src_rank for op in ops if op.dst_rank == rank}
+    if rank in source_layout.layout:
+        srcs.add(rank)
+    _barrier(world)
+    fake = {src: torch.load(os.path.join(checkpoint_dir, f"state_dict_{src}.pt"), weights_only=True,
+                            map_location=device)
+            for src in sorted(srcs)}
+    self_source = fake.get(rank, {})
+    target = execute_param_transfer(
+        transfer_ops=ops, source_state_dict=dict(self_source), device=device,
+        expected_sub_fields=other_context_dict["expected_sub_fields"], world=world,
+        fake_source_state_dicts=fake, log_func=log_func, rank=rank, route=route)
+    torch.cuda.synchronize(device)
+    del fake
+
+    model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
+        model, merged_state_dict=target, other_context_dict=other_context_dict)
+    model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
+    on_meta = any(p.is_meta for p in model.parameters())
+    model.load_state_dict(model_state_dict, assign=on_meta)
+    if optimizer_provider:
+        optimizer = optimizer_provider()
+    if optimizer is not None and optimizer_state_dict["param_groups"] is not None:
+        # one param group, as the reference (migration.py:1267)
+        optimizer_state_dict["param_groups"][0]["params"] = \
+            optimizer.state_dict()["param_groups"][0]["params"]
+        optimizer.load_state_dict(optimizer_state_dict)
+
+    _barrier(world)
+    if remove_files and rank == 0:
+        os.remove(os.path.join(checkpoint_dir, LAYOUT_FILE))
+        os.remove(os.path.join(checkpoint_dir, CONTEXT_FILE))
+        r = 0
+        while True:
+            try:
+                os.remove(os.path.join(checkpoint_dir, f"state_dict_{r}.pt"))
+            except FileNotFoundError:
+                break
+            r += 1
+    log_func("checkpoint_load: end")
+    return (optimizer, other_context) if optimizer_provider else other_context
+
+
+def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = None,
+                   other_context: Any = None, device: Optional[torch.device] = None,
+                   world: Optional[dist.ProcessGroup] = None, log_func: Optional[Callable] = None,
+                   checkpoint_resume: Optional[str] = None):
+    """Suika's save-side migration API (Suika/migration.py:1357-1486).
+
+    With ``checkpoint_resume`` it writes the checkpoint (as the reference
+    does at :1382-1392).  The live hand-off to a new process -- CUDA IPC of
+    every tensor plus a cross-GPU exchange -- is not part of this one-GPU
+    build and raises ``NotImplementedError``."""
+    if checkpoint_resume is not None:
+        return checkpoint_save(model=model, optimizer=optimizer, other_context=other_context,
+                               checkpoint_dir=checkpoint_resume, world=world, log_func=log_func)
+    raise NotImplementedError("live migration between processes (IPC hand-off and cross-GPU "
+                              "exchange) is not part of this build; use checkpoint_resume or "
+                              "execute_param_transfer with the shards resident on this GPU")
+
+
+def migration_load(IPC_queues, model: Module,
+                   optimizer: Union[Optimizer, Callable[[], Optimizer], None] = None,
+                   device: Optional[torch.device] = None, world: Optional[dist.ProcessGroup] = None,
+                   log_func: Optional[Callable] = None, checkpoint_resume: Optional[str] = None):
+    """Suika's load-side migration API (Suika/migration.py:1546-1727); see
+    ``migration_save``.  With ``checkpoint_resume`` the checkpoint is
+    resharded into ``model`` on the GPU (:1566-1575)."""
+    if checkpoint_resume is not None:
+        return checkpoint_load(model=model, optimizer=optimizer, checkpoint_dir=checkpoint_resume,
+                               world=world, log_func=log_func, device=device)
+    raise NotImplementedError("live migration between processes (IPC hand-off and cross-GPU "
+                              "exchange) is not part of this build; use checkpoint_resume or "
+                              "execute_param_transfer with the shards resident on this GPU")

@@ -79,7 +79,7 @@ constexpr int kUnrollStrided = SR_UNROLL_STRIDED;
 constexpr uint32_t kDefaultTileBytes = 16384;   // one 512-lane x 2 x 16 B pass
 constexpr uint64_t kBufAlign = 256;
 constexpr uint32_t kXcds = 8;                    // accelerator complex dies per MI355X
-constexpr uint32_t kMaxGrid = (1u << 24) - 1;   // gridDim.x * kBlock < 2^32
+constexpr uint32_t kMaxGrid = 0xffffffffu / kBlock;    // grid work-items stay below 2^32
 
 // ---------------------------------------------------------------- errors
 

@@ -206,3 +206,48 @@ def build_layout(m: ModelSpec, par: Parallel, dtype: torch.dtype) -> ParamLayout
             check_divisible(s, par.tp)
         metas[rank] = {s.name: param_meta(s, par.tp, tp_i, dtype) for s in specs}
     return ParamLayout.from_metas(metas)
+
+
+def set_tp_attrs(param: torch.Tensor, spec: ParamSpec, tp: int, tp_i: int) -> None:
+    """The attributes TensorMeta(tensor) reads: the reference's slice_dim /
+    tp_index / tp_deg (tensor_parallel.py:255-261, 435-441) and, for the
+    build's extra kinds, shard_kind with its arguments."""
+    if spec.kind == REPL:
+        return
+    param.slice_dim = -1 if spec.kind == ROW else 0
+    param.tp_index = tp_i
+    param.tp_deg = tp
+    if spec.kind == VOCAB:
+        param.shard_kind = VOCAB_PAD
+        param.vocab_size = spec.shape[0]
+        param.pad_multiple = spec.kind_args[0]
+    elif spec.kind == QKV:
+        param.shard_kind = QKV_HEADS
+        param.qkv_heads = tuple(spec.kind_args)
+
+
+def build_module(m: ModelSpec, par: Parallel, rank: int, dtype: torch.dtype = torch.float32,
+                 device="cpu") -> "torch.nn.Module":
+    """An nn.Module holding one rank's shard of every parameter, with the
+    reference's names, registration order and TP attributes -- the state a
+    Suika stage model exposes to the migration API (``named_parameters`` /
+    ``state_dict``).  Values are uninitialised."""
+    import torch.nn as nn
+
+    _, _, tp_i = par.coord(rank)
+    root = nn.Module()
+    for spec in rank_params(m, par, rank):
+        check_divisible(spec, par.tp)
+        meta = param_meta(spec, par.tp, tp_i, dtype)
+        *path, leaf = spec.name.split(".")
+        mod = root
+        for part in path:
+            child = mod._modules.get(part)
+            if child is None:
+                child = nn.Module()
+                mod.add_module(part, child)
+            mod = child
+        p = nn.Parameter(torch.empty(tuple(meta.actual_shape()), dtype=dtype, device=device))
+        set_tp_attrs(p, spec, par.tp, tp_i)
+        mod.register_parameter(leaf, p)
+    return root

@@ -1,0 +1,175 @@
+"""checkpoint_save / checkpoint_load (and migration_* with checkpoint_resume),
+end to end through the reference-shaped API.
+
+A checkpoint is written by a gloo world of CPU processes, each holding its
+rank's module shard (names, TP attributes and AdamW state as a Suika stage
+exposes them); it is then loaded under another TP/PP layout and resharded on
+the GPU.  Expected values are the oracle's closed-form shards of the seeded
+global tensors.
+"""
+import os
+import socket
+
+import numpy as np
+import pytest
+import torch
+import torch.distributed as dist
+import torch.multiprocessing as mp
+
+from oracle import reshard_oracle as O
+from suika_amd import checkpoint_load, checkpoint_save, migration_load, migration_save, schedule_param_transfer
+from suika_amd.checkpoint import layout_from_plain, layout_to_plain
+from suika_amd.inventory import ModelSpec, Parallel, build_layout, build_module
+from tests.harness import t2np, to_ometa
+
+MODEL = ModelSpec("llama", n_layer=4, hidden=32, n_head=4, ffn=64, vocab=100, vocab_parallel=True,
+                  pad_multiple=4)
+SAVE_PAR = (2, 2)     # tp, pp of the writing world
+SEED = 31
+
+
+def global_tensors(seed=SEED):
+    metas = {}
+    for ms in build_layout(MODEL, Parallel(1), torch.float32).layout.values():
+        metas.update(ms)
+    gen = torch.Generator("cpu").manual_seed(seed)
+    out = {}
+    for name in sorted(metas):
+        shape = tuple(int(s) for s in metas[name].shape)
+        out[name] = {"param": (torch.randn(shape, generator=gen) * 0.02).numpy(),
+                     "exp_avg": (torch.randn(shape, generator=gen) * 1e-3).numpy(),
+                     "exp_avg_sq": (torch.randn(shape, generator=gen) * 1e-6).abs().numpy()}
+    return out
+
+
+def rank_state(par: Parallel, rank: int, glob, device="cpu"):
+    mod = build_module(MODEL, par, rank, torch.float32, device)
+    metas = build_layout(MODEL, par, torch.float32).layout[rank]
+    opt = torch.optim.AdamW(mod.parameters(), lr=1e-3)
+    for name, p in mod.named_parameters():
+        om = to_ometa(metas[name])
+        p.data.copy_(torch.from_numpy(np.ascontiguousarray(O.shard_of(glob[name]["param"], om))))
+        opt.state[p] = {
+            "step": torch.tensor(float(rank + 3)),
+            "exp_avg": torch.from_numpy(np.ascontiguousarray(O.shard_of(glob[name]["exp_avg"], om))),
+            "exp_avg_sq": torch.from_numpy(np.ascontiguousarray(O.shard_of(glob[name]["exp_avg_sq"], om))),
+        }
+    return mod, opt
+
+
+def _save_worker(rank, world, port, ckpt):
+    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank, world_size=world)
+    try:
+        mod, opt = rank_state(Parallel(*SAVE_PAR), rank, global_tensors())
+        checkpoint_save(mod, opt, {"iteration": 7, "tag": "ckpt"}, ckpt)
+        dist.barrier()
+    finally:
+        dist.destroy_process_group()
+
+
+def _free_port():
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        return s.getsockname()[1]
+
+
+def write_checkpoint(ckpt):
+    par = Parallel(*SAVE_PAR)
+    mp.spawn(_save_worker, args=(par.world, _free_port(), str(ckpt)), nprocs=par.world, join=True)
+
+
+def test_layout_plain_roundtrip():
+    pl = build_layout(MODEL, Parallel(2, 2), torch.bfloat16)
+    back = layout_from_plain(layout_to_plain(pl))
+    assert list(back.layout) == list(pl.layout)
+    for r in pl.layout:
+        assert list(back.layout[r]) == list(pl.layout[r])
+        for n, m in pl.layout[r].items():
+            b = back.layout[r][n]
+            assert b == m and b.tp_meta == m.tp_meta and tuple(b.actual_shape()) == tuple(m.actual_shape())
+
+
+def test_checkpoint_save_files(tmp_path):
+    """A gloo world of 4 CPU ranks writes the reference's files; every shard
+    holds the closed-form slice of the global state."""
+    write_checkpoint(tmp_path)
+    par = Parallel(*SAVE_PAR)
+    layout = torch.load(tmp_path / "param_layout.pt", weights_only=True)
+    assert layout == layout_to_plain(build_layout(MODEL, par, torch.float32))
+    ctx = torch.load(tmp_path / "other_context.pt", weights_only=True)
+    assert ctx["other_context"] == {"iteration": 7, "tag": "ckpt"}
+    assert [f for f, _ in ctx["expected_sub_fields"]] == ["param", "step", "exp_avg", "exp_avg_sq"]
+    glob = global_tensors()
+    metas = build_layout(MODEL, par, torch.float32).layout
+    for r in range(par.world):
+        sd = torch.load(tmp_path / f"state_dict_{r}.pt", weights_only=True)
+        assert list(sd) == list(metas[r])
+        for name, ent in sd.items():
+            om = to_ometa(metas[r][name])
+            for f in ("param", "exp_avg", "exp_avg_sq"):
+                np.testing.assert_array_equal(ent[f].numpy(), O.shard_of(glob[name][f], om))
+            assert float(ent["step"]) == r + 3
+
+
+def test_migration_without_checkpoint_is_not_in_this_build():
+    mod = build_module(MODEL, Parallel(1), 0)
+    with pytest.raises(NotImplementedError):
+        migration_save(None, mod)
+    with pytest.raises(NotImplementedError):
+        migration_load(None, mod)
+
+
+def _check_loaded(model, opt, par, rank, glob):
+    metas = build_layout(MODEL, par, torch.float32).layout[rank]
+    src_layout = build_layout(MODEL, Parallel(*SAVE_PAR), torch.float32)
+    ops = [op for op in schedule_param_transfer(src_layout, build_layout(MODEL, par, torch.float32))
+           if op.dst_rank == rank]
+    first_src = {}
+    for op in ops:
+        first_src.setdefault(op.param_name, op.src_rank)
+    state = opt.state_dict()["state"]
+    for idx, (name, p) in enumerate(model.named_parameters()):
+        om = to_ometa(metas[name])
+        np.testing.assert_array_equal(t2np(p.data), O.shard_of(glob[name]["param"], om).view(np.uint32),
+                                      err_msg=name)
+        for f in ("exp_avg", "exp_avg_sq"):
+            np.testing.assert_array_equal(t2np(state[idx][f]),
+                                          O.shard_of(glob[name][f], om).view(np.uint32), err_msg=f"{name}/{f}")
+        assert float(state[idx]["step"]) == first_src[name] + 3
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ["direct", "buffers"])
+def test_checkpoint_reshard_to_tp1(tmp_path, route):
+    """TP2xPP2 checkpoint -> one rank holding everything (stages merged,
+    TP shards concatenated, padded vocabulary rows dropped)."""
+    print(f"[gpu checkpoint] tp1 route={route}", flush=True)
+    write_checkpoint(tmp_path)
+    par = Parallel(1)
+    model = build_module(MODEL, par, 0, torch.float32, "cuda")
+    opt, ctx = checkpoint_load(model, lambda: torch.optim.AdamW(model.parameters(), lr=1e-3),
+                               str(tmp_path), route=route)
+    assert ctx == {"iteration": 7, "tag": "ckpt"}
+    _check_loaded(model, opt, par, 0, global_tensors())
+    assert not (tmp_path / "param_layout.pt").exists(), "rank 0 removes the checkpoint"
+
+
+@pytest.mark.gpu
+def test_migration_load_checkpoint_resume_tp4_stage(tmp_path):
+    """migration_load(checkpoint_resume=...) into rank 0 of a TP4 layout,
+    with an Optimizer instance (not a provider)."""
+    print("[gpu checkpoint] migration_load tp4", flush=True)
+    write_checkpoint(tmp_path)
+    par = Parallel(4)
+    model = build_module(MODEL, par, 0, torch.float32, "cuda")
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    ctx = migration_load(None, model, opt, checkpoint_resume=str(tmp_path))
+    assert ctx == {"iteration": 7, "tag": "ckpt"}
+    _check_loaded(model, opt, par, 0, global_tensors())
+
+
+@pytest.mark.gpu
+def test_checkpoint_missing_returns_fresh_optimizer(tmp_path):
+    model = build_module(MODEL, Parallel(1), 0, torch.float32, "cuda")
+    opt, ctx = checkpoint_load(model, lambda: torch.optim.AdamW(model.parameters()), str(tmp_path / "none"))
+    assert ctx is None and isinstance(opt, torch.optim.AdamW)
