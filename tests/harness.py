@@ -5,6 +5,7 @@ The oracle (oracle/reshard_oracle.py) is the checker; the product path is
 """
 from __future__ import annotations
 
+import contextlib
 from typing import Dict, Iterable, List, Mapping, Optional, Sequence, Tuple
 
 import numpy as np
@@ -160,15 +161,48 @@ def to_device(srcs, w: Workload, device) -> Dict[int, Dict[str, Dict[str, torch.
             for r, sd in srcs.items()}
 
 
+POISON = 0xA5
+
+
+@contextlib.contextmanager
+def poisoned_allocations():
+    """Fill every destination tensor and peer buffer the plan allocates with
+    POISON bytes, so a byte the kernels never write cannot pass as correct
+    by holding a previous run's value."""
+    from suika_amd.plan import ReshardPlan
+    alloc_dst, alloc_buffers = ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers
+
+    def dst(self, device):
+        out = alloc_dst(self, device)
+        for ent in out.values():
+            for t in ent.values():
+                t.view(torch.uint8).fill_(POISON)
+        return out
+
+    def buffers(self, device):
+        out = alloc_buffers(self, device)
+        for b in out:
+            b.fill_(POISON)
+        return out
+
+    ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers = dst, buffers
+    try:
+        yield
+    finally:
+        ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers = alloc_dst, alloc_buffers
+
+
 def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers"):
-    """Product path: execute_param_transfer on the GPU with peer shards resident."""
+    """Product path: execute_param_transfer on the GPU with peer shards
+    resident; destinations and buffers start as POISON bytes."""
     from suika_amd import execute_param_transfer
     ops = w.ops()
     fake = to_device(srcs_np, w, device)
     expected_sub_fields = [(f, "normal") for f in w.src_fields]
-    out = execute_param_transfer(ops, {}, torch.device(device), expected_sub_fields,
-                                 rank=w.dst_rank, fake_source_state_dicts=fake,
-                                 recast=w.recast_map, plan_options=plan_options, route=route)
+    with poisoned_allocations():
+        out = execute_param_transfer(ops, {}, torch.device(device), expected_sub_fields,
+                                     rank=w.dst_rank, fake_source_state_dicts=fake,
+                                     recast=w.recast_map, plan_options=plan_options, route=route)
     torch.cuda.synchronize()
     return {n: {f: t2np(t) for f, t in e.items()} for n, e in out.items()}
 
