@@ -123,6 +123,9 @@ typedef struct sr_plan_options {
 #define SR_OPT_NO_XCD_INTERLEAVE 0x8u /* keep the tile list linear instead of
                                      interleaving it 8 ways (by default each XCD, fed
                                      round-robin, walks one contiguous eighth) */
+#define SR_OPT_NO_ROW_GROUPS 0x10u /* keep each strided piece's tiles together instead
+                                     of dealing out the tiles of side-by-side pieces
+                                     (a dim -1 concatenation) row block by row block */
 
 typedef struct sr_plan sr_plan;
 

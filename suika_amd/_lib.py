@@ -41,6 +41,7 @@ SR_OPT_TEMPORAL = 0x1
 SR_OPT_SKIP_COVERAGE = 0x2
 SR_OPT_PIECE_ORDER = 0x4
 SR_OPT_NO_XCD_INTERLEAVE = 0x8
+SR_OPT_NO_ROW_GROUPS = 0x10
 
 # Every symbol the header declares; the CPU test-suite checks they resolve.
 EXPORTED_SYMBOLS = (

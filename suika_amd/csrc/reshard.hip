@@ -455,8 +455,10 @@ struct alignas(8) DevRel {
   int32_t dst_slot;
   int32_t dst2_slot;
   int32_t piece;           // piece whose buffer offset the buffer side uses
+  uint32_t group_size;     // items whose tiles are dealt out row block by row block
+  uint32_t group_index;    // this item's place in its group
 };
-static_assert(sizeof(DevRel) == 88, "DevRel layout");
+static_assert(sizeof(DevRel) == 96, "DevRel layout");
 
 // Exclusive prefix sum across a workgroup of NT lanes: an inclusive scan
 // inside each wave64 by shuffles, then the wave totals through LDS.  Every
@@ -551,8 +553,13 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
   for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
     const uint64_t total = rel[k].total;
     const uint32_t width = rel[k].row_bytes;
-    const uint64_t b = tile_base[k];
-    const uint64_t cnt = tile_base[k + 1] - b;
+    const uint64_t cnt = tile_base[k + 1] - tile_base[k];
+    // Items of a group have equal tile counts; tile j of member m goes to
+    // group_start + j*M + m, so the members' tiles over the same rows are
+    // adjacent in the list.
+    const uint64_t gm = rel[k].group_index;
+    const uint64_t gsize = rel[k].group_size;
+    const uint64_t b = tile_base[k] - gm * cnt + gm;
     for (uint64_t j = threadIdx.x; j < cnt; j += kSetupBlock) {
       const uint64_t start = j << tile_shift;
       const uint64_t left = total - start;
@@ -568,7 +575,7 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
         t.start = row;
         t.c_base = uint32_t(start - row * width);
       }
-      const uint64_t i = b + j;
+      const uint64_t i = b + j * gsize;
       tiles[ways > 1 ? xcd_position(i, seg, q, r) : i] = t;
     }
   }
@@ -772,8 +779,16 @@ int check_coverage(const std::vector<std::vector<Box>>& boxes, const std::vector
 // first, then destinations (offset by n_src_base).  `buf_src` / `buf_dst`
 // mark the side that is a peer buffer (its address is the buffer base plus
 // the piece's offset, computed on the device).
+//
+// With `row_groups`, runs of consecutive strided items that sit side by side
+// on the ordering side (the source for pack, the destination otherwise:
+// same tensor, rows, row width and stride, each starting where the previous
+// one's rows end) form a group whose tiles are dealt out row block by row
+// block.  A destination row assembled from several pieces (a dim -1 `cat`)
+// is then written by adjacent tiles instead of once per piece, far apart in
+// time, so each DRAM page is opened once rather than once per piece.
 void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_bytes, bool buf_src,
-               bool buf_dst) {
+               bool buf_dst, bool group_by_src, bool row_groups) {
   ph.rel.clear();
   ph.rel.reserve(order.size());
   ph.n_tiles = 0;
@@ -802,8 +817,40 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     r.dst_slot = h.dst_slot >= 0 ? int32_t(ph.n_src_base) + h.dst_slot : -1;
     r.dst2_slot = h.dst2_slot >= 0 ? int32_t(ph.n_src_base) + h.dst2_slot : -1;
     r.piece = h.piece;
+    r.group_size = 1;
+    r.group_index = 0;
     ph.rel.push_back(r);
     ph.n_tiles += (r.total + tile_bytes - 1) / tile_bytes;
+  }
+  if (!row_groups) return;
+  struct Side {
+    int64_t slot;
+    uint64_t off, stride, width;
+  };
+  auto side = [&](const HostItem& h) -> Side {
+    if (group_by_src) return {h.src_slot, h.src_off, h.src_stride, h.row_bytes};
+    if (h.dst_slot >= 0) return {h.dst_slot, h.dst_off, h.dst_stride, h.row_bytes};
+    return {h.dst2_slot, h.dst2_off, h.dst2_stride, h.row_bytes / 2};
+  };
+  size_t first = 0;
+  for (size_t i = 1; i <= order.size(); ++i) {
+    bool chain = false;
+    if (i < order.size()) {
+      const HostItem& a = ph.items[order[i - 1]];
+      const HostItem& b = ph.items[order[i]];
+      const Side sa = side(a), sb = side(b);
+      chain = !a.contiguous && !b.contiguous && a.kind == b.kind && a.rows == b.rows &&
+              a.row_bytes == b.row_bytes && sa.slot >= 0 && sa.slot == sb.slot &&
+              sa.stride == sb.stride && sb.off == sa.off + sa.width;
+    }
+    if (!chain) {
+      const uint32_t m = uint32_t(i - first);
+      for (size_t g = first; g < i; ++g) {
+        ph.rel[g].group_size = m;
+        ph.rel[g].group_index = uint32_t(g - first);
+      }
+      first = i;
+    }
   }
 }
 
@@ -1056,7 +1103,8 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
   sr_plan_options opt{};
   if (options) opt = *options;
   if (opt.reserved != 0) return fail(SR_EINVAL, "options.reserved must be 0");
-  if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE | SR_OPT_PIECE_ORDER | SR_OPT_NO_XCD_INTERLEAVE))
+  if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE | SR_OPT_PIECE_ORDER | SR_OPT_NO_XCD_INTERLEAVE |
+                    SR_OPT_NO_ROW_GROUPS))
     return fail(SR_EINVAL, "unknown option flags 0x%x", opt.flags);
   if (opt.tile_bytes == 0) opt.tile_bytes = kDefaultTileBytes;
   if (opt.tile_bytes < 4096 || opt.tile_bytes > (16u << 20) ||
@@ -1269,12 +1317,13 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
     p->unpack.n_dst_base = uint32_t(n_dst);
     p->gather.n_src_base = uint32_t(n_src);
     p->gather.n_dst_base = uint32_t(n_dst);
+    const bool groups = !(opt.flags & SR_OPT_NO_ROW_GROUPS);
     build_rel(p->pack, by_piece ? identity(p->pack.items.size()) : item_order(p->pack, true),
-              opt.tile_bytes, false, true);
+              opt.tile_bytes, false, true, true, groups);
     build_rel(p->unpack, by_piece ? identity(p->unpack.items.size()) : item_order(p->unpack, false),
-              opt.tile_bytes, true, false);
+              opt.tile_bytes, true, false, false, groups);
     build_rel(p->gather, by_piece ? identity(p->gather.items.size()) : item_order(p->gather, false),
-              opt.tile_bytes, false, false);
+              opt.tile_bytes, false, false, false, groups);
   }
   for (Phase* ph : {&p->pack, &p->unpack, &p->gather}) {
     if (ph->n_tiles > UINT32_MAX) {

@@ -60,12 +60,14 @@ class PlanOptions:
     skip_coverage: bool = False
     address_order: bool = True   # tiles ordered by tensor address (library default)
     xcd_order: bool = True       # tiles interleaved 8 ways, one eighth per XCD (default)
+    row_groups: bool = True      # side-by-side strided pieces dealt out by row block (default)
 
     def to_c(self) -> _lib.SrPlanOptions:
         flags = (0 if self.nontemporal else _lib.SR_OPT_TEMPORAL) | \
                 (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0) | \
                 (0 if self.address_order else _lib.SR_OPT_PIECE_ORDER) | \
-                (0 if self.xcd_order else _lib.SR_OPT_NO_XCD_INTERLEAVE)
+                (0 if self.xcd_order else _lib.SR_OPT_NO_XCD_INTERLEAVE) | \
+                (0 if self.row_groups else _lib.SR_OPT_NO_ROW_GROUPS)
         return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, flags, 0)
 
 

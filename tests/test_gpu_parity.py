@@ -57,8 +57,9 @@ SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
     PlanOptions(tile_bytes=1 << 20, nontemporal=False, max_blocks=300),
     PlanOptions(tile_bytes=4096, address_order=False),
     PlanOptions(tile_bytes=4096, xcd_order=False, max_blocks=33),
+    PlanOptions(tile_bytes=4096, row_groups=False),
 ], ids=["tile4k", "tile8k_grid7", "temporal", "tile1m_temporal_grid300", "tile4k_piece_order",
-        "tile4k_linear_grid33"])
+        "tile4k_linear_grid33", "tile4k_no_row_groups"])
 def test_gpu_tunings_match_oracle(w, opt):
     _check(w, "index", opt)
     _check(w, "index", opt, route="direct")
