@@ -173,3 +173,30 @@ def test_checkpoint_missing_returns_fresh_optimizer(tmp_path):
     model = build_module(MODEL, Parallel(1), 0, torch.float32, "cuda")
     opt, ctx = checkpoint_load(model, lambda: torch.optim.AdamW(model.parameters()), str(tmp_path / "none"))
     assert ctx is None and isinstance(opt, torch.optim.AdamW)
+
+
+def _load_worker(rank, world, port, ckpt, tp, pp):
+    # a failure propagates to mp.spawn in the parent with this rank's traceback
+    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank, world_size=world)
+    try:
+        torch.cuda.set_device(0)
+        par = Parallel(tp, pp)
+        model = build_module(MODEL, par, rank, torch.float32, "cuda")
+        opt, ctx = checkpoint_load(model, lambda: torch.optim.AdamW(model.parameters(), lr=1e-3), ckpt,
+                                   world=dist.group.WORLD)
+        assert ctx == {"iteration": 7, "tag": "ckpt"}
+        _check_loaded(model, opt, par, rank, global_tensors())
+    finally:
+        dist.destroy_process_group()
+
+
+@pytest.mark.gpu
+def test_checkpoint_load_two_ranks_share_the_gpu(tmp_path):
+    """TP2xPP2 checkpoint -> TP1xPP2, loaded by a gloo world of two ranks that
+    share the one GPU: rank 1 (the second stage) resolves its own pieces, the
+    layout is all-gathered over gloo, and rank 0 removes the files only after
+    both have loaded."""
+    print("[gpu checkpoint] two ranks tp1 pp2", flush=True)
+    write_checkpoint(tmp_path)
+    mp.spawn(_load_worker, args=(2, _free_port(), str(tmp_path), 1, 2), nprocs=2, join=True)
+    assert not (tmp_path / "param_layout.pt").exists()
