@@ -86,7 +86,12 @@ constexpr int kUnroll = SR_UNROLL;
 constexpr int kUnrollStrided = SR_UNROLL_STRIDED;
 constexpr uint32_t kDefaultTileBytes = 16384;   // one 512-lane x 2 x 16 B pass
 constexpr uint64_t kBufAlign = 256;
-constexpr uint32_t kXcds = 8;                    // accelerator complex dies per MI355X
+// Tile-list interleave width: the accelerator complex dies (XCDs) of an
+// MI355X, which take workgroups round-robin.
+#ifndef SR_INTERLEAVE_WAYS
+#define SR_INTERLEAVE_WAYS 8
+#endif
+constexpr uint32_t kXcds = SR_INTERLEAVE_WAYS;
 constexpr uint32_t kMaxGrid = 0xffffffffu / kBlock;    // grid work-items stay below 2^32
 
 // ---------------------------------------------------------------- errors

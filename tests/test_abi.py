@@ -146,9 +146,37 @@ def test_recast_and_zero_rules():
 
 def test_options_validation():
     for opt in (_lib.SrPlanOptions(3000, 0, 0, 0), _lib.SrPlanOptions(0, 0, 0x80, 0),
-                _lib.SrPlanOptions(0, 0, 0, 1)):
+                _lib.SrPlanOptions(0, 0, 0x20, 0), _lib.SrPlanOptions(0, 0, 0, 1)):
         rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece()], options=opt)
         assert rc == _lib.SR_EINVAL
+    every = (_lib.SR_OPT_TEMPORAL | _lib.SR_OPT_SKIP_COVERAGE | _lib.SR_OPT_PIECE_ORDER |
+             _lib.SR_OPT_NO_XCD_INTERLEAVE | _lib.SR_OPT_NO_ROW_GROUPS)
+    rc, h = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece()], options=_lib.SrPlanOptions(0, 0, every, 0))
+    assert rc == _lib.SR_OK, _lib.last_error()
+    _lib.lib().sr_plan_destroy(h)
+
+
+def test_tile_counts():
+    """Tiles per phase = sum over items of ceil(item bytes / tile_bytes); a
+    strided item counts its source bytes, a ZERO item its destination bytes."""
+    # dst [64, 3000] f32: column bands of 1000 and 1500 from two peers
+    # (strided on the destination) and a band of 500 zero-filled columns.
+    src = [(64, 1000, F32), (64, 2000, F32)]
+    pcs = [piece(src=0, peer=0, rows=64, cols=1000, dc=0),
+           piece(src=1, peer=1, rows=64, cols=1500, dc=1000),
+           piece(kind=_lib.SR_PIECE_ZERO, peer=0, src=-1, rows=64, cols=500, dc=2500)]
+    tile = 4096
+    rc, h = _plan(src, [(64, 3000, F32)], 2, pcs, options=_lib.SrPlanOptions(tile, 0, 0, 0))
+    assert rc == _lib.SR_OK, _lib.last_error()
+    info = _lib.SrPlanInfo()
+    assert _lib.lib().sr_plan_info_get(h, ctypes.byref(info)) == 0
+    ceil = lambda n: -(-n // tile)  # noqa: E731
+    copies = ceil(64 * 1000 * 4) + ceil(64 * 1500 * 4)
+    zero = ceil(64 * 500 * 4)
+    assert info.pack_tiles == copies
+    assert info.unpack_tiles == copies + zero
+    assert info.gather_tiles == copies + zero
+    _lib.lib().sr_plan_destroy(h)
 
 
 def test_python_errors_are_assertion_errors():
