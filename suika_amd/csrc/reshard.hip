@@ -902,21 +902,19 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
   if (!p->ev_offsets) SR_HIP_TRY(hipEventCreateWithFlags(&p->ev_offsets, hipEventDisableTiming));
   if (p->n_peers > 0 && !p->peer_list.empty()) {
     const size_t np = p->pieces.size();
+    // Allocations survive a failed attempt (and are reused by the retry);
+    // the uploads are always redone.
     if (!p->d_offset) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_offset), np * sizeof(uint64_t)));
-    if (!p->d_payload) {
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_payload), np * sizeof(uint64_t)));
-      SR_HIP_TRY(hipMemcpy(p->d_payload, p->payload.data(), np * sizeof(uint64_t), hipMemcpyHostToDevice));
-    }
-    if (!p->d_peer_begin) {
+    if (!p->d_payload) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_payload), np * sizeof(uint64_t)));
+    if (!p->d_peer_begin)
       SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_peer_begin), p->peer_begin.size() * sizeof(uint32_t)));
-      SR_HIP_TRY(hipMemcpy(p->d_peer_begin, p->peer_begin.data(), p->peer_begin.size() * sizeof(uint32_t),
-                           hipMemcpyHostToDevice));
-    }
-    if (!p->d_peer_list) {
+    if (!p->d_peer_list)
       SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_peer_list), p->peer_list.size() * sizeof(uint32_t)));
-      SR_HIP_TRY(hipMemcpy(p->d_peer_list, p->peer_list.data(), p->peer_list.size() * sizeof(uint32_t),
-                           hipMemcpyHostToDevice));
-    }
+    SR_HIP_TRY(hipMemcpy(p->d_payload, p->payload.data(), np * sizeof(uint64_t), hipMemcpyHostToDevice));
+    SR_HIP_TRY(hipMemcpy(p->d_peer_begin, p->peer_begin.data(), p->peer_begin.size() * sizeof(uint32_t),
+                         hipMemcpyHostToDevice));
+    SR_HIP_TRY(hipMemcpy(p->d_peer_list, p->peer_list.data(), p->peer_list.size() * sizeof(uint32_t),
+                         hipMemcpyHostToDevice));
     hipLaunchKernelGGL(sr_offsets_kernel, dim3(uint32_t(p->n_peers)), dim3(kSetupBlock), 0, stream,
                        p->d_peer_begin, p->d_peer_list, p->d_payload, p->d_offset);
     SR_HIP_TRY(hipGetLastError());
@@ -936,10 +934,7 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
-    if (!ph.d_rel) {
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_rel), n * sizeof(DevRel)));
-      SR_HIP_TRY(hipMemcpy(ph.d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice));
-    }
+    if (!ph.d_rel) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_rel), n * sizeof(DevRel)));
     if (!ph.d_items) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_items), n * sizeof(DevItem)));
     if (!ph.d_tile_base)
       SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_tile_base), (size_t(n) + 1) * sizeof(uint64_t)));
@@ -949,6 +944,7 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
     if (!ph.h_staging)
       SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ph.h_staging), nptr * sizeof(uint64_t),
                                hipHostMallocDefault));
+    SR_HIP_TRY(hipMemcpy(ph.d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice));
     if (needs_offsets) {
       int rc = setup_offsets(p, stream);
       if (rc != SR_OK) return rc;
