@@ -184,3 +184,24 @@ def test_python_errors_are_assertion_errors():
         _lib.check(_lib.SR_EBOUNDS, "x")
     with pytest.raises(_lib.ReshardError):
         _lib.check(_lib.SR_EHIP, "x")
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    """Without the built library every entry point raises: there is no CPU
+    or torch fallback.  Run in a child interpreter so this process keeps its
+    loaded library."""
+    import os
+    import subprocess
+    import sys
+    code = ("import torch\n"
+            "from suika_amd import execute_param_transfer\n"
+            "try:\n"
+            "    execute_param_transfer([], {}, torch.device('cuda', 0), [('param', 'normal')], rank=0)\n"
+            "except RuntimeError as e:\n"
+            "    assert 'missing' in str(e) and 'no fallback' in str(e), e\n"
+            "    print('raised')\n")
+    env = dict(os.environ, SUIKA_RESHARD_LIB=str(tmp_path / "absent.so"))
+    root = Path(__file__).resolve().parents[1]
+    out = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0 and "raised" in out.stdout, out.stderr[-2000:]
