@@ -17,7 +17,7 @@ from suika_amd.workloads import FIELD_STD, Workload
 
 BITS = {torch.bfloat16: np.uint16, torch.float16: np.uint16, torch.float32: np.uint32,
         torch.float64: np.uint64, torch.int32: np.uint32, torch.int64: np.uint64,
-        torch.uint8: np.uint8}
+        torch.uint8: np.uint8, torch.int8: np.uint8, torch.bool: np.uint8}
 TORCH_BITS = {torch.bfloat16: torch.int16, torch.float16: torch.int16, torch.float32: torch.int32,
               torch.float64: torch.int64, torch.int32: torch.int32, torch.int64: torch.int64,
               torch.uint8: torch.uint8}
