@@ -7,10 +7,12 @@
 //   Suika/migration.py:531-541  cat(pieces, dim=slice_dim) / clone()
 // Both are pure byte movement.  The Python host lowers every TransferOp x
 // sub-field into 2-D region moves (sr_piece); this file validates them, lays
-// out the per-peer buffers and executes the two phases as single launches.
+// out the per-peer buffers and executes each phase -- pack (sources -> peer
+// buffers), unpack (peer buffers -> destinations) or gather (sources ->
+// destinations directly) -- as a single launch.
 //
 // Device design
-//   * A phase (pack or unpack) is a list of items, one per piece.  An item is
+//   * A phase is a list of items, one per piece.  An item is
 //     a 2-D byte region: `rows` rows of `row_bytes` bytes at a source and a
 //     destination stride.  Regions that are contiguous on both sides are
 //     collapsed to one long row.
@@ -25,6 +27,9 @@
 //     from 8 distant regions.  On the Llama2-7B share this takes the unpack
 //     from 8.5 to 7.4 ms; a single window of consecutive tiles keeps the read
 //     and write streams at a fixed distance and leaves HBM bandwidth idle.
+//     Side-by-side strided items (the column bands of one dim -1 `cat`) deal
+//     out their tiles row block by row block, so each destination row is
+//     written by adjacent tiles.
 //   * Lanes move 16-byte vectors (8/4/2/1 when a region is not 16-byte
 //     aligned), two independent loads in flight before the stores.
 //     Consecutive lanes touch consecutive 16-byte words of a row, so every
@@ -36,9 +41,10 @@
 //     on the host.
 //   * The unpack RECAST item reads f32 once and writes the f32 copy and the
 //     bf16 round-to-nearest-even copy in the same pass.
-//   * No LDS: every region row is >= 768 bytes at the configured shapes, so a
-//     direct coalesced copy already issues full-width bursts; a transpose is
-//     never needed because no piece changes the element order within a row.
+//   * The copy kernels use no LDS: every region row is >= 768 bytes at the
+//     configured shapes, so a direct coalesced copy already issues full-width
+//     bursts; a transpose is never needed because no piece changes the
+//     element order within a row.
 //
 // Host design
 //   * sr_plan_create is host only and O(pieces): validation, coverage, the
