@@ -205,3 +205,32 @@ def test_missing_library_fails_loudly(tmp_path):
     out = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True,
                          text=True, timeout=300)
     assert out.returncode == 0 and "raised" in out.stdout, out.stderr[-2000:]
+
+
+def test_c_caller(tmp_path):
+    """The header and library serve a plain C11 program (the FFI view a
+    cgo / JNI / N-API binding has), not only ctypes."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler on this host")
+    root = Path(__file__).resolve().parents[1]
+    exe = tmp_path / "abi_host_calls"
+    cmd = [gcc, "-std=c11", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+           f"-I{root / 'include'}", "-I/opt/rocm/include", str(root / "tests" / "c" / "abi_host_calls.c"),
+           f"-L{_lib.LIB_PATH.parent}", "-lsuika_reshard", f"-Wl,-rpath,{_lib.LIB_PATH.parent}",
+           "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-3000:]
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stdout + out.stderr
+    lines = out.stdout.splitlines()
+    assert lines == [
+        f"abi {_lib.ABI_VERSION}",
+        "peer_bytes 128 128",          # 4 x 8 f32 per peer
+        "piece1_offset 0",             # first (only) piece of peer 1
+        "pieces 2 peers 2 pack_bytes_read 256",
+        f"hole {_lib.SR_EOVERLAP} null",
+        "message mentions coverage",
+    ], out.stdout
