@@ -125,16 +125,25 @@ def test_benchmark_plan_sizes(key):
 
 
 def test_benchmark_shortest_row_runs():
-    """Strided (last-dim) destination rows are >= 1 KB and 16-B multiples at
-    the benchmark shapes, so the 16-byte vector path covers all of them."""
+    """Every strided run (a region narrower than its tensor, on the source,
+    destination or bf16 side) is a 16-B multiple of at least 768 bytes at the
+    benchmark shapes (GPT-125M attn c_proj: 192 f32 columns), so the 16-byte
+    vector path covers all of them and no LDS staging is needed."""
+    shortest = {}
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         plan = _plan_for(w)
         for p in plan.pieces:
-            es = _esize(plan.c_dst[p.dst].dtype) if p.dst >= 0 else 2
-            if p.rows > 1 and p.cols != plan.c_dst[p.dst].cols:
-                assert (p.cols * es) % 16 == 0 and p.cols * es >= 512, (key, p.rows, p.cols)
+            sides = [(plan.c_dst[d], _esize(plan.c_dst[d].dtype)) for d in (p.dst, p.dst2) if d >= 0]
+            if p.src >= 0:
+                sides.append((plan.c_src[p.src], _esize(plan.c_src[p.src].dtype)))
+            for t, es in sides:
+                if p.rows > 1 and p.cols != t.cols:
+                    run = p.cols * es
+                    assert run % 16 == 0, (key, p.rows, p.cols)
+                    shortest[key] = min(shortest.get(key, run), run)
         plan.close()
+    assert min(shortest.values()) == 768 and shortest["gpt125m_tp2_tp4"] == 768, shortest
 
 
 def test_lower_op_rejects_uncovered_piece():
