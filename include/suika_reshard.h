@@ -207,6 +207,11 @@ int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs
 int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
               hipStream_t stream);
 
+/*
+ * Release a plan and its device tables.  Waits for the plan's own launches
+ * still in flight (it may follow an asynchronous call directly); does not
+ * synchronize anything else.  NULL is ignored.
+ */
 void sr_plan_destroy(sr_plan* plan);
 
 #ifdef __cplusplus

@@ -1016,7 +1016,13 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   return SR_OK;
 }
 
+// Frees a phase's device tables.  Waits first for the last launches that
+// read them (bind, copy kernel, setup), so a plan can be destroyed right
+// after an asynchronous call.
 void free_phase(Phase& ph) {
+  if (ph.ev_kernel) (void)hipEventSynchronize(ph.ev_kernel);
+  if (ph.ev_staging) (void)hipEventSynchronize(ph.ev_staging);
+  if (ph.ev_setup) (void)hipEventSynchronize(ph.ev_setup);
   if (ph.d_rel) (void)hipFree(ph.d_rel);
   if (ph.d_items) (void)hipFree(ph.d_items);
   if (ph.d_tiles) (void)hipFree(ph.d_tiles);
@@ -1453,6 +1459,7 @@ void sr_plan_destroy(sr_plan* plan) {
   free_phase(plan->pack);
   free_phase(plan->unpack);
   free_phase(plan->gather);
+  if (plan->ev_offsets) (void)hipEventSynchronize(plan->ev_offsets);
   if (plan->d_offset) (void)hipFree(plan->d_offset);
   if (plan->d_payload) (void)hipFree(plan->d_payload);
   if (plan->d_peer_begin) (void)hipFree(plan->d_peer_begin);

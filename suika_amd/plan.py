@@ -260,31 +260,38 @@ class ReshardPlan:
 
     # ---------------------------------------------------------- execution
     @staticmethod
-    def _check_tensor(t: torch.Tensor, spec: SlotSpec, what) -> int:
+    def _check_tensor(t: torch.Tensor, spec: SlotSpec, what, device: int) -> int:
         assert isinstance(t, torch.Tensor), f"{what}: not a tensor"
         assert t.is_cuda, f"{what}: tensor is on {t.device}, the reshard engine needs HBM"
+        assert t.get_device() == device, \
+            f"{what}: tensor is on cuda:{t.get_device()}, the kernels run on the current device cuda:{device}"
         assert t.is_contiguous(), f"{what}: tensor is not contiguous"
         assert tuple(t.shape) == tuple(spec.shape), f"{what}: shape {tuple(t.shape)} != {spec.shape}"
         assert t.dtype == spec.dtype, f"{what}: dtype {t.dtype} != {spec.dtype}"
         return t.data_ptr()
 
     def src_pointers(self, sources: Mapping[int, Mapping[str, Mapping[str, torch.Tensor]]]):
+        dev = torch.cuda.current_device()
         ptrs = []
         for key in self.src_keys:
             rank, name, field = key
             t = sources[rank][name][field]
-            ptrs.append(self._check_tensor(t, self.src_specs[key], key))
+            ptrs.append(self._check_tensor(t, self.src_specs[key], key, dev))
         return ptrs
 
     def dst_pointers(self, dst: Mapping[str, Mapping[str, torch.Tensor]]):
-        return [self._check_tensor(dst[name][field], self.dst_specs[(name, field)], (name, field))
+        dev = torch.cuda.current_device()
+        return [self._check_tensor(dst[name][field], self.dst_specs[(name, field)], (name, field), dev)
                 for (name, field) in self.dst_keys]
 
     def buf_pointers(self, buffers: Sequence[torch.Tensor]):
         assert len(buffers) == len(self.peers), f"{len(buffers)} buffers for {len(self.peers)} peers"
+        dev = torch.cuda.current_device()
         ptrs = []
         for i, b in enumerate(buffers):
             assert b.is_cuda and b.is_contiguous(), f"buffer {i} must be a contiguous HBM tensor"
+            assert b.get_device() == dev, \
+                f"buffer {i} is on cuda:{b.get_device()}, the kernels run on the current device cuda:{dev}"
             assert b.numel() * b.element_size() >= self.peer_bytes[i], \
                 f"buffer {i} holds {b.numel() * b.element_size()} bytes, needs {self.peer_bytes[i]}"
             ptrs.append(b.data_ptr())
