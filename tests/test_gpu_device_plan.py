@@ -131,3 +131,38 @@ def test_rebind_on_new_pointers_and_stream():
             assert torch.equal(dst.cpu(), src_h), i
     finally:
         L.sr_plan_destroy(h)
+
+
+@pytest.mark.gpu
+def test_destroy_right_after_async_launch():
+    """sr_plan_destroy directly after sr_gather / sr_pack + sr_unpack, with
+    no synchronisation in between: the destroy waits for the plan's own
+    launches, so the results are complete and exact."""
+    print("[gpu device-plan] destroy after async launch", flush=True)
+    L = _lib.lib()
+    pcs = _pieces(seed=13)
+    t = (_lib.SrTensor * 1)(_lib.SrTensor(ROWS, COLS, _lib.SR_DT_U8, 0))
+    arr = (_lib.SrPiece * len(pcs))(*pcs)
+    gen = torch.Generator("cpu").manual_seed(21)
+    src_h = torch.randint(0, 256, (ROWS, COLS), dtype=torch.uint8, generator=gen)
+    src = src_h.cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    for route in ("gather", "buffers"):
+        h = ctypes.c_void_p()
+        _lib.check(L.sr_plan_create(t, 1, t, 1, N_PEERS, arr, len(pcs), None, ctypes.byref(h)), "create")
+        dst = torch.full((ROWS, COLS), POISON, dtype=torch.uint8, device="cuda")
+        if route == "gather":
+            _lib.check(L.sr_gather(h, _vp([src.data_ptr()]), _vp([dst.data_ptr()]), stream), "gather")
+        else:
+            sizes = []
+            for q in range(N_PEERS):
+                b = ctypes.c_uint64()
+                _lib.check(L.sr_plan_peer_bytes(h, q, ctypes.byref(b)), "peer_bytes")
+                sizes.append(b.value)
+            bufs = [torch.empty(max(1, n), dtype=torch.uint8, device="cuda") for n in sizes]
+            bp = _vp([b.data_ptr() for b in bufs])
+            _lib.check(L.sr_pack(h, _vp([src.data_ptr()]), bp, stream), "pack")
+            _lib.check(L.sr_unpack(h, bp, _vp([dst.data_ptr()]), stream), "unpack")
+        L.sr_plan_destroy(h)
+        torch.cuda.synchronize()
+        assert torch.equal(dst.cpu(), src_h), route
