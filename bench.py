@@ -164,25 +164,28 @@ def api_latency(w, sources, dev, repeats: int = 3) -> dict:
 
     spl, tpl = w.layouts()
     fields = [(f, "normal") for f in w.src_fields]
-    sched_ms, exec_ms = [], []
-    for i in range(repeats + 1):
-        t0 = time.perf_counter()
-        ops = schedule_param_transfer(spl, tpl)
-        t1 = time.perf_counter()
-        fake = {r: {n: dict(e) for n, e in sd.items()} for r, sd in sources.items()}
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        out = execute_param_transfer(ops, {}, dev, fields, rank=w.dst_rank,
-                                     fake_source_state_dicts=fake, recast=w.recast_map)
-        torch.cuda.synchronize()
-        t3 = time.perf_counter()
-        del out, fake
-        if i:
-            sched_ms.append((t1 - t0) * 1e3)
-            exec_ms.append((t3 - t2) * 1e3)
+    sched_ms, exec_ms = [], {False: [], True: []}
+    for arena in (False, True):
+        for i in range(repeats + 1):
+            t0 = time.perf_counter()
+            ops = schedule_param_transfer(spl, tpl)
+            t1 = time.perf_counter()
+            fake = {r: {n: dict(e) for n, e in sd.items()} for r, sd in sources.items()}
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            out = execute_param_transfer(ops, {}, dev, fields, rank=w.dst_rank,
+                                         fake_source_state_dicts=fake, recast=w.recast_map,
+                                         arena=arena)
+            torch.cuda.synchronize()
+            t3 = time.perf_counter()
+            del out, fake
+            if i:
+                sched_ms.append((t1 - t0) * 1e3)
+                exec_ms[arena].append((t3 - t2) * 1e3)
     return {"route": "direct",
             "schedule_param_transfer_ms": round(statistics.median(sched_ms), 2),
-            "execute_param_transfer_ms": round(statistics.median(exec_ms), 2),
+            "execute_param_transfer_ms": round(statistics.median(exec_ms[False]), 2),
+            "execute_param_transfer_arena_ms": round(statistics.median(exec_ms[True]), 2),
             "runs": repeats,
             "includes": "region lowering, sr_plan_create, destination allocation (warm caching "
                         "allocator), device-side tile/offset/item tables, gather launch, synchronize"}

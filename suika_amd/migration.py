@@ -83,6 +83,7 @@ def execute_param_transfer(
     plan_options: Optional[PlanOptions] = None,
     stream: Optional[torch.cuda.Stream] = None,
     route: str = "direct",
+    arena: bool = False,
 ) -> StateDict:
     """Execute a transfer schedule for this rank; returns its target state.
 
@@ -94,7 +95,10 @@ def execute_param_transfer(
     field it is rounded from; ``plan_options`` tunes the kernels; ``route``
     is ``"direct"`` (one gather pass from the resident sources, the default
     since every source is on this GPU) or ``"buffers"`` (pack into per-peer
-    buffers, then unpack: the path an exchange between GPUs goes through).
+    buffers, then unpack: the path an exchange between GPUs goes through);
+    ``arena`` places every destination tensor in one allocation
+    (``ReshardPlan.arena_layout``: field by field, 256-byte aligned), for a
+    model that adopts them with ``load_state_dict(assign=True)``.
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     if log_func is None:
@@ -150,7 +154,7 @@ def execute_param_transfer(
                                          f"not on {device}")
 
     with torch.cuda.device(device):
-        target = plan.alloc_dst(device)
+        target = plan.alloc_dst(device, arena=arena)
         buffers = []
         if route == "direct":
             prof.start("execute gather")

@@ -77,6 +77,13 @@ class SlotSpec:
     dtype: torch.dtype
 
 
+def _numel(shape: Sequence[int]) -> int:
+    n = 1
+    for s in shape:
+        n *= int(s)
+    return n
+
+
 def _matrix_of(shape: Sequence[int], view: int) -> Tuple[int, int]:
     shape = [int(s) for s in shape]
     if not shape:
@@ -251,11 +258,49 @@ class ReshardPlan:
         """One byte buffer per peer (torch's allocator aligns to 512 bytes)."""
         return [torch.empty(max(1, n), dtype=torch.uint8, device=device) for n in self.peer_bytes]
 
-    def alloc_dst(self, device) -> Dict[str, Dict[str, torch.Tensor]]:
+    ARENA_ALIGN = 256
+
+    def arena_layout(self) -> Tuple[int, Dict[DstKey, int]]:
+        """Byte size of a destination arena and the offset of every
+        destination tensor in it: field by field (all ``param`` tensors, then
+        ``master``, ...), tensors in plan order within a field, each at a
+        256-byte aligned offset.  A field's tensors are thus one contiguous
+        span, e.g. a flat parameter buffer."""
+        fields: List[str] = []
+        for _, f in self.dst_keys:
+            if f not in fields:
+                fields.append(f)
+        offsets: Dict[DstKey, int] = {}
+        end = 0
+        a = self.ARENA_ALIGN
+        for f in fields:
+            for key in self.dst_keys:
+                if key[1] != f:
+                    continue
+                spec = self.dst_specs[key]
+                end = (end + a - 1) // a * a
+                offsets[key] = end
+                end += _numel(spec.shape) * spec.dtype.itemsize
+        return end, offsets
+
+    def alloc_dst(self, device, arena: bool = False) -> Dict[str, Dict[str, torch.Tensor]]:
+        """Fresh destination tensors, one per (name, field).  With ``arena``
+        they are views of one allocation laid out by ``arena_layout`` (one
+        allocator call instead of one per tensor; a model adopting them with
+        ``load_state_dict(assign=True)`` keeps them in place)."""
         out: Dict[str, Dict[str, torch.Tensor]] = {}
+        if not arena:
+            for (name, field) in self.dst_keys:
+                spec = self.dst_specs[(name, field)]
+                out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
+            return out
+        total, offsets = self.arena_layout()
+        buf = torch.empty(max(1, total), dtype=torch.uint8, device=device)
         for (name, field) in self.dst_keys:
             spec = self.dst_specs[(name, field)]
-            out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
+            off = offsets[(name, field)]
+            n = _numel(spec.shape) * spec.dtype.itemsize
+            out.setdefault(name, {})[field] = buf[off:off + n].view(spec.dtype).view(spec.shape)
         return out
 
     # ---------------------------------------------------------- execution

@@ -107,3 +107,34 @@ def test_boundary_rejects_misaligned_and_null_pointers():
     torch.cuda.synchronize()
     assert torch.equal(dst_t["a"]["param"], torch.cat([s0, s1], 0))
     plan.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ["direct", "buffers"])
+def test_arena_destinations_and_adoption(route):
+    """execute_param_transfer(arena=True): bit-identical to the oracle, every
+    destination a view of one allocation, and a stage module adopting the
+    params with load_state_dict(assign=True) keeps them in place (no copy)."""
+    from suika_amd.inventory import build_module
+    from tests.cases import scaled_configs
+    from tests.harness import index_state, oracle_dest, source_shards, t2np, to_device
+
+    w = scaled_configs()["llama7b_tp4pp2_tp2pp2"]
+    print(f"[gpu api] arena {w.key} {route}", flush=True)
+    names = {n for metas in w.layouts()[0].layout.values() for n in metas}
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), index_state(w, names))
+    want = oracle_dest(w, srcs)
+    out = execute_param_transfer(w.ops(), {}, torch.device("cuda", 0),
+                                 [(f, "normal") for f in w.src_fields], rank=w.dst_rank,
+                                 fake_source_state_dicts=to_device(srcs, w, "cuda"),
+                                 recast=w.recast_map, route=route, arena=True)
+    torch.cuda.synchronize()
+    storages = {t.untyped_storage().data_ptr() for e in out.values() for t in e.values()}
+    assert len(storages) == 1
+    for name, ent in want.items():
+        for f, a in ent.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+    module = build_module(w.model, w.dst, w.dst_rank, w.dtypes["param"], "cuda")
+    module.load_state_dict({n: e["param"] for n, e in out.items()}, assign=True)
+    for n, p in module.named_parameters():
+        assert p.data_ptr() == out[n]["param"].data_ptr(), n

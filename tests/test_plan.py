@@ -152,3 +152,39 @@ def test_lower_op_rejects_uncovered_piece():
     dst = TensorMeta(name="a", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
     with pytest.raises(AssertionError, match="holds 0 of"):
         lower_op(TransferOp("a", 1, 0, src, dst), dst)
+
+
+def test_arena_layout_and_views():
+    """Destination arena: field by field, plan order within a field, every
+    tensor 256-byte aligned and disjoint; alloc_dst(arena=True) returns views
+    of one storage with the planned shapes and dtypes."""
+    w = CONFIGS["llama7b_tp4pp2_tp2pp2"]
+    plan = _plan_for(w)
+    total, offs = plan.arena_layout()
+    spans = []
+    for key in plan.dst_keys:
+        spec = plan.dst_specs[key]
+        n = int(np.prod(spec.shape)) * spec.dtype.itemsize
+        assert offs[key] % 256 == 0
+        spans.append((offs[key], offs[key] + n, key))
+    spans.sort()
+    for (a0, a1, ka), (b0, b1, kb) in zip(spans, spans[1:]):
+        assert a1 <= b0, (ka, kb)
+    assert spans[-1][1] == total
+    fields = [k[1] for _, _, k in spans]
+    assert fields == sorted(fields, key=list(dict.fromkeys(k[1] for k in plan.dst_keys)).index)
+    plan.close()
+
+    small = cases.scaled_configs()["qwen7b_tp2_tp4"]          # includes a recast bf16 field
+    plan = _plan_for(small)
+    dst = plan.alloc_dst("cpu", arena=True)
+    base = None
+    total, offs = plan.arena_layout()
+    for (name, f), spec in plan.dst_specs.items():
+        t = dst[name][f]
+        assert tuple(t.shape) == tuple(spec.shape) and t.dtype == spec.dtype and t.is_contiguous()
+        ptr = t.untyped_storage().data_ptr()
+        base = ptr if base is None else base
+        assert ptr == base, "all destinations share one storage"
+        assert t.data_ptr() - base == offs[(name, f)]
+    plan.close()
