@@ -174,6 +174,7 @@ class ReshardPlan:
                     f"{key}: sources disagree on dtype ({self.dst_specs[key].dtype} vs {dtype})"
             return dst_index[key]
 
+        self.empty_dst: Dict[DstKey, SlotSpec] = {}   # zero-element destinations (no pieces)
         self.piece_owner: List[Tuple[str, int]] = []   # (name, peer) per piece
         for name, name_ops in by_name.items():
             dst_shard = infer_dst_shard(name_ops)
@@ -188,6 +189,16 @@ class ReshardPlan:
                     field_dtype.setdefault(f, src_specs[key].dtype)
                     assert field_dtype[f] == src_specs[key].dtype, \
                         f"{name}/{f}: dtype differs between sources"
+            shape = tuple(int(d) for d in dst_shard.actual_shape())
+            if _numel(shape) == 0:
+                # nothing to move: an empty tensor per field, as clone() of an
+                # empty piece gives in the reference (migration.py:538)
+                for f in self.fields:
+                    self.empty_dst[(name, f)] = SlotSpec(shape, field_dtype[f])
+                    for tgt, sf in recast.items():
+                        if sf == f:
+                            self.empty_dst[(name, tgt)] = SlotSpec(shape, torch.bfloat16)
+                continue
             # destination slots of every field, then the pieces that fill them
             dslot: Dict[str, int] = {}
             for f in self.fields:
@@ -289,6 +300,8 @@ class ReshardPlan:
         allocator call instead of one per tensor; a model adopting them with
         ``load_state_dict(assign=True)`` keeps them in place)."""
         out: Dict[str, Dict[str, torch.Tensor]] = {}
+        for (name, field), spec in self.empty_dst.items():
+            out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
         if not arena:
             for (name, field) in self.dst_keys:
                 spec = self.dst_specs[(name, field)]

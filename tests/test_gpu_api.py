@@ -138,3 +138,22 @@ def test_arena_destinations_and_adoption(route):
     module.load_state_dict({n: e["param"] for n, e in out.items()}, assign=True)
     for n, p in module.named_parameters():
         assert p.data_ptr() == out[n]["param"].data_ptr(), n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("route", ["direct", "buffers"])
+def test_zero_element_tensors(route):
+    from tests.test_plan import _empty_case
+    print(f"[gpu api] zero-element tensors {route}", flush=True)
+    ops = _empty_case(2, 1)
+    gen = torch.Generator("cpu").manual_seed(3)
+    w = torch.randn((8, 4), generator=gen)
+    fake = {r: {"w": {"param": w.chunk(2, 0)[r].contiguous().cuda()},
+                "none": {"param": torch.empty(0, device="cuda")},
+                "none2d": {"param": torch.empty((0, 2), device="cuda")}} for r in range(2)}
+    for arena in (False, True):
+        out = execute_param_transfer(ops, {}, torch.device("cuda", 0), [("param", "normal")], rank=0,
+                                     fake_source_state_dicts=fake, route=route, arena=arena)
+        torch.cuda.synchronize()
+        assert torch.equal(out["w"]["param"].cpu(), w)
+        assert tuple(out["none"]["param"].shape) == (0,) and tuple(out["none2d"]["param"].shape) == (0, 4)

@@ -188,3 +188,30 @@ def test_arena_layout_and_views():
         assert ptr == base, "all destinations share one storage"
         assert t.data_ptr() - base == offs[(name, f)]
     plan.close()
+
+
+def _empty_case(tp_src, tp_dst):
+    def metas(tp):
+        return ParamLayout.from_metas({r: {
+            "w": TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, r, tp)),
+            "none": TensorMeta(name="none", dtype=torch.float32, shape=(0,)),
+            "none2d": TensorMeta(name="none2d", dtype=torch.float32, shape=(0, 4), tp_meta=(-1, r, tp)),
+        } for r in range(tp)})
+    return schedule_param_transfer(metas(tp_src), metas(tp_dst))
+
+
+def test_zero_element_tensors_are_planned_as_empty():
+    """A parameter with no elements moves nothing; its destination is an
+    empty tensor of the right shape and dtype per field (the reference's
+    clone() of an empty piece), on both allocation paths."""
+    ops = [o for o in _empty_case(2, 1) if o.dst_rank == 0]
+    specs = {(o.src_rank, o.param_name, f): SlotSpec(tuple(o.src_meta.actual_shape()), torch.float32)
+             for o in ops for f in ("master", "exp_avg")}
+    plan = ReshardPlan(ops, specs, ["master", "exp_avg"], recast={"param": "master"})
+    assert {k[0] for k in plan.dst_keys} == {"w"}
+    for arena in (False, True):
+        dst = plan.alloc_dst("cpu", arena=arena)
+        assert tuple(dst["none"]["master"].shape) == (0,) and dst["none"]["param"].dtype == torch.bfloat16
+        assert tuple(dst["none2d"]["exp_avg"].shape) == (0, 4)
+        assert tuple(dst["w"]["master"].shape) == (8, 4)
+    plan.close()
