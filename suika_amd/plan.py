@@ -77,6 +77,13 @@ class SlotSpec:
     dtype: torch.dtype
 
 
+def _geometry_key(m: TensorMeta) -> tuple:
+    """What region lowering depends on: global shape, shard and kind (not
+    the name or dtype; TensorMeta's own equality ignores the shard index)."""
+    return (tuple(int(d) for d in m.shape), None if m.tp_meta is None else tuple(m.tp_meta),
+            m.kind, tuple(m.kind_args), m.rows)
+
+
 def _numel(shape: Sequence[int]) -> int:
     n = 1
     for s in shape:
@@ -175,6 +182,7 @@ class ReshardPlan:
             return dst_index[key]
 
         self.empty_dst: Dict[DstKey, SlotSpec] = {}   # zero-element destinations (no pieces)
+        lowered: Dict[tuple, list] = {}
         self.piece_owner: List[Tuple[str, int]] = []   # (name, peer) per piece
         for name, name_ops in by_name.items():
             dst_shard = infer_dst_shard(name_ops)
@@ -182,10 +190,14 @@ class ReshardPlan:
             view = view_axis(dst_shard, *[op.src_meta for op in name_ops])
             field_dtype: Dict[str, torch.dtype] = {}
             for op in name_ops:
+                checked = set()
                 for f in self.fields:
                     key = (op.src_rank, name, f)
                     assert key in src_specs, f"[{op.src_rank}]: param missing in source {name}/{f}"
-                    op.check_send(src_specs[key].shape)
+                    shape = tuple(src_specs[key].shape)
+                    if shape not in checked:
+                        op.check_send(shape)
+                        checked.add(shape)
                     field_dtype.setdefault(f, src_specs[key].dtype)
                     assert field_dtype[f] == src_specs[key].dtype, \
                         f"{name}/{f}: dtype differs between sources"
@@ -210,7 +222,13 @@ class ReshardPlan:
                         dslot[tgt] = dst_slot((name, tgt), dst_shard, torch.bfloat16, view)
             for op in name_ops:
                 peer = peer_index[op.src_rank]
-                for reg in lower_op(op, dst_shard):
+                # regions depend only on the shard geometry, which repeats
+                # from layer to layer: lower each distinct geometry once
+                gkey = (_geometry_key(op.src_meta), _geometry_key(op.dst_meta), _geometry_key(dst_shard))
+                regions = lowered.get(gkey)
+                if regions is None:
+                    regions = lowered[gkey] = lower_op(op, dst_shard)
+                for reg in regions:
                     for f in self.fields:
                         s = src_slot((op.src_rank, name, f), view)
                         tgt = [t for t, sf in recast.items() if sf == f]
