@@ -109,8 +109,9 @@ typedef struct sr_piece {
 typedef struct sr_plan_options {
   uint32_t tile_bytes;   /* bytes of source data per work tile; power of two in
                             [4096, 16 MiB]; 0 = default (16384) */
-  uint32_t max_blocks;   /* cap on workgroups per launch (grid-stride beyond);
-                            0 = one workgroup per tile */
+  uint32_t max_blocks;   /* cap on workgroups per launch (grid-stride beyond;
+                            rounded down to a multiple of 8 when the tile list
+                            is XCD-interleaved); 0 = one workgroup per tile */
   uint32_t flags;        /* SR_OPT_* bits */
   uint32_t reserved;     /* must be 0 */
 } sr_plan_options;

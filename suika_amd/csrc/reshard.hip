@@ -1002,6 +1002,9 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   uint32_t grid = n_tiles;
   if (p->opt.max_blocks != 0) grid = std::min(grid, p->opt.max_blocks);
   grid = std::min(grid, kMaxGrid);
+  // A capped grid strides over the tile list; a multiple of the interleave
+  // width keeps every position on the XCD the interleave placed it for.
+  if (ph.interleave && grid < n_tiles && grid >= kXcds) grid -= grid % kXcds;
   const bool nt = (p->opt.flags & SR_OPT_TEMPORAL) == 0;
   typedef void (*KernelFn)(const DevItem*, const DevTile*, uint32_t);
   KernelFn fn;

@@ -172,8 +172,8 @@ def poisoned_allocations():
     from suika_amd.plan import ReshardPlan
     alloc_dst, alloc_buffers = ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers
 
-    def dst(self, device):
-        out = alloc_dst(self, device)
+    def dst(self, device, **kw):
+        out = alloc_dst(self, device, **kw)
         for ent in out.values():
             for t in ent.values():
                 t.view(torch.uint8).fill_(POISON)
