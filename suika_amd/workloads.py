@@ -39,10 +39,11 @@ class Workload:
     seed: int = 0
     param_dtype: torch.dtype = torch.bfloat16  # TensorMeta dtype (schedule volumes)
     description: str = ""
+    dst_dp: int = 0                           # data-parallel replica of the destination
 
     @property
     def dst_rank(self) -> int:
-        return self.dst.rank(self.dst_pp, self.dst_tp)
+        return self.dst.rank(self.dst_pp, self.dst_tp, self.dst_dp)
 
     @property
     def dtypes(self) -> Dict[str, torch.dtype]:

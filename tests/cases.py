@@ -56,6 +56,26 @@ def reference_test_cases() -> List[Workload]:
     return out
 
 
+def dp_cases() -> List[Workload]:
+    """Data-parallel replicas on either side: every piece has several owners
+    holding identical bytes, so the schedule's greedy choice among them (self
+    first, least accumulated volume, reuse of connected peers:
+    Suika/migration.py:355-379) decides which peer sends it."""
+    out = []
+    for model, (src, dst, dpp_i, ddp_i, dtp_i), fields, seed in [
+            (GPT_TEST, ((2, 1, 2), (1, 2, 2), 1, 1, 0), _F32_3, 41),
+            (GPT_TEST, ((4, 1, 2), (2, 2, 1), 0, 0, 1), _F32_3, 42),
+            (LLAMA_TEST, ((2, 2, 2), (4, 1, 2), 0, 1, 3), _BF16_4, 43),
+            (LLAMA_TEST, ((1, 1, 4), (2, 1, 2), 0, 1, 1), _BF16_4, 44)]:
+        s, d = Parallel(*src), Parallel(*dst)
+        key = (f"{model.family}_test_tp{s.tp}pp{s.pp}dp{s.dp}_tp{d.tp}pp{d.pp}dp{d.dp}"
+               f"_d{dpp_i}.{ddp_i}.{dtp_i}")
+        w = _w(key, model, s, d, dpp_i, dtp_i, fields=fields, seed=seed,
+               param_dtype=torch.float32 if fields is _F32_3 else torch.bfloat16)
+        out.append(replace(w, dst_dp=ddp_i))
+    return out
+
+
 def alignment_cases() -> List[Workload]:
     return [
         _w("qwen2_test_tp2_tp1", QWEN2_TEST, Parallel(2), Parallel(1), 0, 0, seed=13),
@@ -101,8 +121,8 @@ def padded_vocab_cases() -> List[Workload]:
 
 
 def all_small_cases() -> List[Workload]:
-    return (reference_test_cases() + alignment_cases() + list(scaled_configs().values())
-            + padded_vocab_cases())
+    return (reference_test_cases() + dp_cases() + alignment_cases()
+            + list(scaled_configs().values()) + padded_vocab_cases())
 
 
 def golden_cases() -> Dict[str, Workload]:
