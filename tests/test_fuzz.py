@@ -1,5 +1,6 @@
 """Randomised reshard cases: families, shapes, uneven stage partitions, TP
-degrees 1/2/4/8 on both sides, every shard kind, random destination rank.
+degrees 1/2/4/8 and DP replicas on both sides, every shard kind, random
+destination rank.
 
 CPU: the numpy execution of the product plan equals the oracle and the
 closed form on index-coded state.  GPU: the HIP path equals the oracle.
@@ -53,11 +54,14 @@ def random_case(seed: int) -> Workload:
     fields = {"bf16": _BF16_4, "f32": _F32_3, "recast": _RECAST}[kind]
     recast = (("param", "master"),) if kind == "recast" else ()
     src_fields = tuple(f for f, _ in fields if f not in dict(recast))
-    dst = Parallel(dtp, dpp)
-    return Workload(key=f"fuzz{seed}", model=model, src=Parallel(stp, spp), dst=dst,
+    # data-parallel replicas on either side (one case in three)
+    sdp, ddp = (rng.choice([1, 2]), rng.choice([1, 2])) if rng.random() < 0.34 else (1, 1)
+    dst = Parallel(dtp, dpp, ddp)
+    return Workload(key=f"fuzz{seed}", model=model, src=Parallel(stp, spp, sdp), dst=dst,
                     dst_pp=rng.randrange(dpp), dst_tp=rng.randrange(dtp), src_fields=src_fields,
                     field_dtypes=fields, recast=recast, seed=seed,
-                    param_dtype=torch.float32 if kind == "f32" else torch.bfloat16)
+                    param_dtype=torch.float32 if kind == "f32" else torch.bfloat16,
+                    dst_dp=rng.randrange(ddp))
 
 
 SEEDS = list(range(60))
