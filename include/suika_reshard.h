@@ -57,7 +57,9 @@ typedef enum sr_status {
   SR_EINVAL = -1,    /* malformed argument (null, bad enum, bad size) */
   SR_EBOUNDS = -2,   /* region outside its tensor or buffer */
   SR_EALIGN = -3,    /* pointer not aligned to its element size */
-  SR_EOVERLAP = -4,  /* destination regions overlap or leave holes */
+  SR_EOVERLAP = -4,  /* destination regions overlap or leave holes; or, at a
+                        call, objects one launch writes overlap each other or
+                        an object it reads */
   SR_EHIP = -5,      /* HIP runtime error */
   SR_ENOMEM = -6,    /* host or device allocation failed */
   SR_EDTYPE = -7     /* dtype/element-size mismatch between src and dst */

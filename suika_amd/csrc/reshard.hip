@@ -682,6 +682,10 @@ struct Phase {
   uint64_t n_tiles = 0;
   uint32_t n_src_base = 0;              // pointer table: sources, then destinations
   uint32_t n_dst_base = 0;
+  std::vector<uint64_t> obj_bytes;      // per pointer-table slot: object size
+  std::vector<uint8_t> obj_use;         // per slot: 1 read, 2 written (0: unused)
+  const char* src_name = "src_ptrs";    // caller-side names of the two tables
+  const char* dst_name = "dst_ptrs";
   bool interleave = false;
   uint64_t bytes_read = 0;
   uint64_t bytes_written = 0;
@@ -827,6 +831,10 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     r.src_slot = h.src_slot;
     r.dst_slot = h.dst_slot >= 0 ? int32_t(ph.n_src_base) + h.dst_slot : -1;
     r.dst2_slot = h.dst2_slot >= 0 ? int32_t(ph.n_src_base) + h.dst2_slot : -1;
+    ph.obj_use.resize(size_t(ph.n_src_base) + ph.n_dst_base, 0);
+    if (r.src_slot >= 0) ph.obj_use[r.src_slot] |= 1;
+    if (r.dst_slot >= 0) ph.obj_use[r.dst_slot] |= 2;
+    if (r.dst2_slot >= 0) ph.obj_use[r.dst2_slot] |= 2;
     r.piece = h.piece;
     r.group_size = 1;
     r.group_index = 0;
@@ -970,17 +978,56 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
   return SR_OK;
 }
 
+// One launch reads and writes the caller's objects concurrently: objects it
+// writes must be pairwise disjoint and must not overlap any object it reads.
+int check_disjoint(const Phase& ph, const std::vector<uint64_t>& ptrs) {
+  struct Span {
+    uint64_t lo, hi;
+    size_t slot;
+  };
+  std::vector<Span> w, r;
+  for (size_t i = 0; i < ph.obj_use.size(); ++i) {
+    if (!ph.obj_use[i]) continue;
+    const Span sp{ptrs[i], ptrs[i] + ph.obj_bytes[i], i};
+    if (ph.obj_use[i] & 2) w.push_back(sp);
+    if (ph.obj_use[i] & 1) r.push_back(sp);
+  }
+  auto name = [&](size_t slot, char* buf, size_t n) {
+    if (slot < ph.n_src_base) snprintf(buf, n, "%s[%zu]", ph.src_name, slot);
+    else snprintf(buf, n, "%s[%zu]", ph.dst_name, slot - ph.n_src_base);
+    return buf;
+  };
+  char a[64], b[64];
+  std::sort(w.begin(), w.end(), [](const Span& x, const Span& y) { return x.lo < y.lo; });
+  for (size_t k = 1; k < w.size(); ++k)
+    if (w[k].lo < w[k - 1].hi)
+      return fail(SR_EOVERLAP, "%s and %s are written by one launch and overlap",
+                  name(w[k - 1].slot, a, sizeof a), name(w[k].slot, b, sizeof b));
+  for (const Span& x : r) {
+    // the written span starting last below x.hi is the only candidate
+    auto it = std::lower_bound(w.begin(), w.end(), x.hi,
+                               [](const Span& s, uint64_t v) { return s.lo < v; });
+    if (it != w.begin() && std::prev(it)->hi > x.lo)
+      return fail(SR_EOVERLAP, "%s is read while %s, which overlaps it, is written",
+                  name(x.slot, a, sizeof a), name(std::prev(it)->slot, b, sizeof b));
+  }
+  return SR_OK;
+}
+
 int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>& ptrs,
               hipStream_t stream) {
-  int rc = ensure_device(p);
-  if (rc != SR_OK) return rc;
   if (ph.rel.empty()) return SR_OK;
+  const bool rebind = !ph.bound_valid || ptrs != ph.bound;
+  int rc;
+  if (rebind && (rc = check_disjoint(ph, ptrs)) != SR_OK) return rc;
+  rc = ensure_device(p);
+  if (rc != SR_OK) return rc;
   rc = setup_phase(p, ph, kind != kGather, stream);
   if (rc != SR_OK) return rc;
   SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
 
   const uint32_t n = uint32_t(ph.rel.size());
-  if (!ph.bound_valid || ptrs != ph.bound) {
+  if (rebind) {
     // The staging buffer may still feed the previous bind; the item table
     // may still be read by the previous launch of this phase.
     SR_HIP_TRY(hipEventSynchronize(ph.ev_staging));
@@ -1340,6 +1387,25 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
               opt.tile_bytes, true, false, false, groups);
     build_rel(p->gather, by_piece ? identity(p->gather.items.size()) : item_order(p->gather, false),
               opt.tile_bytes, false, false, false, groups);
+  }
+  {
+    // object sizes of each phase's pointer table, and the caller's names
+    std::vector<uint64_t> sb(n_src), db(n_dst);
+    for (int32_t i = 0; i < n_src; ++i)
+      sb[i] = p->src[i].rows * p->src[i].cols * uint64_t(dtype_size(p->src[i].dtype));
+    for (int32_t i = 0; i < n_dst; ++i)
+      db[i] = p->dst[i].rows * p->dst[i].cols * uint64_t(dtype_size(p->dst[i].dtype));
+    auto fill = [](Phase& ph, const std::vector<uint64_t>& a, const std::vector<uint64_t>& b,
+                   const char* an, const char* bn) {
+      ph.obj_bytes = a;
+      ph.obj_bytes.insert(ph.obj_bytes.end(), b.begin(), b.end());
+      ph.obj_use.resize(ph.obj_bytes.size(), 0);
+      ph.src_name = an;
+      ph.dst_name = bn;
+    };
+    fill(p->pack, sb, p->peer_bytes, "src_ptrs", "peer_bufs");
+    fill(p->unpack, p->peer_bytes, db, "peer_bufs", "dst_ptrs");
+    fill(p->gather, sb, db, "src_ptrs", "dst_ptrs");
   }
   for (Phase* ph : {&p->pack, &p->unpack, &p->gather}) {
     if (ph->n_tiles > UINT32_MAX) {

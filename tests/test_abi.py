@@ -234,3 +234,30 @@ def test_c_caller(tmp_path):
         f"hole {_lib.SR_EOVERLAP} null",
         "message mentions coverage",
     ], out.stdout
+
+
+def test_overlapping_objects_rejected_before_launch():
+    """Objects one launch writes must be disjoint from each other and from
+    what it reads.  The check runs on the host before any HIP call, so fake
+    addresses suffice here."""
+    L = _lib.lib()
+    vp = ctypes.c_void_p
+    # two [4, 8] f32 destinations, each filled from its own source
+    rc, h = _plan([(4, 8, F32), (4, 8, F32)], [(4, 8, F32), (4, 8, F32)], 2,
+                  [piece(src=0, peer=0, dst=0), piece(src=1, peer=1, dst=1)])
+    assert rc == _lib.SR_OK, _lib.last_error()
+    base = 1 << 40
+    src = (vp * 2)(base, base + 4096)
+    # destinations overlap each other (128-byte objects 64 bytes apart)
+    dst = (vp * 2)(base + 8192, base + 8192 + 64)
+    assert L.sr_gather(h, src, dst, None) == _lib.SR_EOVERLAP
+    assert "dst_ptrs[0] and dst_ptrs[1]" in _lib.last_error()
+    # a destination overlaps a source (in place)
+    dst = (vp * 2)(base + 64, base + 8192)
+    assert L.sr_gather(h, src, dst, None) == _lib.SR_EOVERLAP
+    assert "src_ptrs[0] is read" in _lib.last_error()
+    # pack: two peer buffers overlapping
+    bufs = (vp * 2)(base + 8192, base + 8192 + 32)
+    assert L.sr_pack(h, src, bufs, None) == _lib.SR_EOVERLAP
+    assert "peer_bufs[0] and peer_bufs[1]" in _lib.last_error()
+    L.sr_plan_destroy(h)
