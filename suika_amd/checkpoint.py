@@ -11,11 +11,11 @@ Same names, arguments, files and control flow as the reference's
   from disk, resharded, split back into model and optimizer state and loaded.
 
 The reference reshards on the CPU (``execute_param_transfer`` with
-``device="cpu"``, migration.py:1235-1244); here the needed shards are loaded
-straight into HBM and resharded by the HIP engine (``route="direct"``: one
-gather launch).  Files hold only tensors, numbers, strings and plain
-containers -- layouts are stored as dicts -- so they load with
-``torch.load(weights_only=True)``.
+``device="cpu"``, migration.py:1235-1244); here the source files are
+memory-mapped, only the tensors this rank's pieces read are copied to HBM,
+and the HIP engine reshards them (``route="direct"``: one gather launch).
+Files hold only tensors, numbers, strings and plain containers -- layouts
+are stored as dicts -- so they load with ``torch.load(weights_only=True)``.
 """
 from __future__ import annotations
 
@@ -154,13 +154,21 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
 
     target_layout = _gather_layout(model, world)
     ops = schedule_param_transfer(source_layout, target_layout)
-    srcs = {op.src_rank for op in ops if op.dst_rank == rank}
-    if rank in source_layout.layout:
-        srcs.add(rank)
+    # (source rank -> names) this rank's pieces read; only those tensors go to HBM
+    needed: Dict[int, set] = {}
+    for op in ops:
+        if op.dst_rank == rank:
+            needed.setdefault(op.src_rank, set()).add(op.param_name)
     _barrier(world)
-    fake = {src: torch.load(os.path.join(checkpoint_dir, f"state_dict_{src}.pt"), weights_only=True,
-                            map_location=device)
-            for src in sorted(srcs)}
+    fake = {}
+    for src in sorted(needed):
+        # memory-mapped, so the shards this rank does not read are never
+        # paged in; the reference loads whole files to the CPU (migration.py:1223-1233)
+        sd = torch.load(os.path.join(checkpoint_dir, f"state_dict_{src}.pt"), weights_only=True,
+                        map_location="cpu", mmap=True)
+        fake[src] = {name: {f: t.to(device) for f, t in sd[name].items()}
+                     for name in needed[src] if name in sd}
+        del sd
     self_source = fake.get(rank, {})
     target = execute_param_transfer(
         transfer_ops=ops, source_state_dict=dict(self_source), device=device,
