@@ -166,3 +166,44 @@ def test_destroy_right_after_async_launch():
         L.sr_plan_destroy(h)
         torch.cuda.synchronize()
         assert torch.equal(dst.cpu(), src_h), route
+
+
+@pytest.mark.gpu
+def test_two_plans_concurrently_on_two_streams():
+    """Independent plans own their tables, staging and events: a gather of
+    one plan and a pack + unpack of another, issued on two streams without
+    synchronisation in between, both come out exact."""
+    print("[gpu device-plan] two plans, two streams", flush=True)
+    L = _lib.lib()
+    t = (_lib.SrTensor * 1)(_lib.SrTensor(ROWS, COLS, _lib.SR_DT_U8, 0))
+    plans = []
+    for seed in (31, 32):
+        pcs = _pieces(seed=seed)
+        arr = (_lib.SrPiece * len(pcs))(*pcs)
+        h = ctypes.c_void_p()
+        _lib.check(L.sr_plan_create(t, 1, t, 1, N_PEERS, arr, len(pcs), None, ctypes.byref(h)), "create")
+        plans.append(h)
+    try:
+        gen = torch.Generator("cpu").manual_seed(41)
+        srcs_h = [torch.randint(0, 256, (ROWS, COLS), dtype=torch.uint8, generator=gen) for _ in range(2)]
+        srcs = [s.cuda() for s in srcs_h]
+        dsts = [torch.full((ROWS, COLS), POISON, dtype=torch.uint8, device="cuda") for _ in range(2)]
+        sizes = []
+        for q in range(N_PEERS):
+            b = ctypes.c_uint64()
+            _lib.check(L.sr_plan_peer_bytes(plans[1], q, ctypes.byref(b)), "peer_bytes")
+            sizes.append(b.value)
+        bufs = [torch.empty(max(1, n), dtype=torch.uint8, device="cuda") for n in sizes]
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Stream(), torch.cuda.Stream()
+        _lib.check(L.sr_gather(plans[0], _vp([srcs[0].data_ptr()]), _vp([dsts[0].data_ptr()]),
+                               s0.cuda_stream), "gather")
+        bp = _vp([b.data_ptr() for b in bufs])
+        _lib.check(L.sr_pack(plans[1], _vp([srcs[1].data_ptr()]), bp, s1.cuda_stream), "pack")
+        _lib.check(L.sr_unpack(plans[1], bp, _vp([dsts[1].data_ptr()]), s1.cuda_stream), "unpack")
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(dsts[i].cpu(), srcs_h[i]), i
+    finally:
+        for h in plans:
+            L.sr_plan_destroy(h)
