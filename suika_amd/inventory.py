@@ -28,7 +28,7 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from .meta import CHUNK, QKV_HEADS, VOCAB_PAD, ParamLayout, TensorMeta
+from .meta import QKV_HEADS, VOCAB_PAD, ParamLayout, TensorMeta
 
 COL, ROW, REPL, VOCAB, QKV = "col", "row", "repl", "vocab", "qkv"
 

@@ -24,7 +24,6 @@ intended ``cat`` in ascending piece order.
 """
 from __future__ import annotations
 
-from collections import OrderedDict
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
 import torch

@@ -13,8 +13,8 @@ exp_avg ~ N(0, 1e-3), exp_avg_sq = |N(0, 1e-6)|, param = bf16(master)
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field, replace
-from typing import Dict, Iterable, List, Mapping, Optional, Sequence, Tuple
+from dataclasses import dataclass, replace
+from typing import Dict, Iterable, List, Optional, Tuple
 
 import torch
 

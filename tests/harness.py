@@ -6,7 +6,7 @@ The oracle (oracle/reshard_oracle.py) is the checker; the product path is
 from __future__ import annotations
 
 import contextlib
-from typing import Dict, Iterable, List, Mapping, Optional, Sequence, Tuple
+from typing import Dict, Iterable, List, Mapping, Optional, Tuple
 
 import numpy as np
 import torch

@@ -7,7 +7,6 @@ exposes them); it is then loaded under another TP/PP layout and resharded on
 the GPU.  Expected values are the oracle's closed-form shards of the seeded
 global tensors.
 """
-import os
 import socket
 
 import numpy as np

@@ -1,7 +1,5 @@
 """Reference-shaped API semantics of the GPU path (Suika/migration.py:397-556)
 and the boundary's error handling, which rejects bad input before any launch."""
-import ctypes
-
 import numpy as np
 import pytest
 import torch

@@ -68,7 +68,7 @@ def test_gpu_tunings_match_oracle(w, opt):
 def test_gpu_repeat_and_streams():
     """A plan reused across calls, streams and rebound pointers stays exact."""
     from suika_amd.plan import ReshardPlan, SlotSpec
-    from tests.harness import np2t, t2np, to_device
+    from tests.harness import t2np, to_device
     w = cases.scaled_configs()["qwen7b_tp2_tp4"]
     print(f"[gpu repeat] {w.key}", flush=True)
     glob = global_state(w, _names(w))

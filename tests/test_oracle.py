@@ -16,8 +16,8 @@ import torch
 
 from oracle import reshard_oracle as O
 from tests import cases
-from tests.harness import (expected_dest, global_state, index_state, needed_names, oracle_dest,
-                           source_shards, t2np, to_olayout)
+from tests.harness import (expected_dest, global_state, index_state, oracle_dest, source_shards,
+                           t2np)
 
 SMALL = cases.all_small_cases()
 

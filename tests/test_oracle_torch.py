@@ -2,7 +2,6 @@
 equals the numpy oracle on every small case."""
 import numpy as np
 import pytest
-import torch
 
 from oracle import reshard_oracle as O
 from oracle.torch_ref import execute_torch_cpu
