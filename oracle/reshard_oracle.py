@@ -12,18 +12,21 @@ its own schedule, ``torch.chunk`` / ``torch.cat`` semantics restated on numpy
 arrays.  Tensors are raw bit patterns (bf16 -> uint16, f32 -> uint32 or
 float32), so every comparison is bit-exact.
 
-Pins (tests/test_oracle_*.py):
+Pins (tests/test_oracle*.py, tests/test_golden.py):
   * ``chunk``/``cat``             vs torch.chunk / torch.cat (the library the
                                   reference calls), incl. uneven splits
   * ``execute_fake_source``       vs ``shard_of(G, dest)`` closed forms on
                                   seeded and index-coded global tensors, for
-                                  every kind and TP/PP change in the suite
-  * ``schedule``                  vs brute-force ownership, coverage and
-                                  load invariants; greedy choices are
-                                  "parity unpinned" (no reference vectors)
+                                  every kind and TP/PP/DP change in the suite
+  * ``schedule``                  vs the reference's own
+                                  ``schedule_param_transfer`` output on 96
+                                  recorded cases (greedy source choices
+                                  included, data-parallel replicas too), and
+                                  brute-force ownership / coverage invariants
   * ``rne_bf16``                  vs torch.Tensor.to(torch.bfloat16) on CPU,
                                   incl. ties, subnormals, inf and NaN
   * index maps                    vs brute force on tiny shapes
+No function here is left unpinned.
 Extensions the reference lacks (vocab padding, head-granular fused QKV, bf16
 recast, fp32 master, wpe) are defined by the closed forms in ``shard_of``.
 """
