@@ -1,10 +1,12 @@
 """GPU parity: the HIP pack/unpack path against the CPU oracle, bit-exact.
 
-Every small case (reference TEST shapes, scaled benchmark plans, padded vocab,
-non-16-byte rows) runs through ``execute_param_transfer`` on the GPU and must
-equal the oracle's reshard of the same seeded source shards.  Kernel tunings
-that change the tiling (tile size, grid cap, non-temporal access) are swept on
-a subset, so tiles that start mid-row and grid-stride loops are covered.
+Every small case (reference TEST shapes under TP/PP/DP changes, scaled
+benchmark plans, padded vocab, non-16-byte rows) runs through
+``execute_param_transfer`` on the GPU and must equal the oracle's reshard of
+the same seeded source shards.  Kernel tunings that change the tiling or its
+order (tile size, grid cap, cached access, plan order, linear order, row
+groups off) are swept on a subset, so tiles that start mid-row and
+grid-stride loops are covered.
 """
 import numpy as np
 import pytest
