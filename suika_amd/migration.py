@@ -34,6 +34,7 @@ from torch.optim import Optimizer
 
 from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
                    schedule_param_transfer)
+from . import _lib
 from .plan import PlanOptions, ReshardPlan, SlotSpec
 
 StateDict = Dict[str, Dict[str, Tensor]]
@@ -83,6 +84,7 @@ def execute_param_transfer(
     stream: Optional[torch.cuda.Stream] = None,
     route: str = "direct",
     arena: bool = False,
+    pipeline: int = 4,
 ) -> StateDict:
     """Execute a transfer schedule for this rank; returns its target state.
 
@@ -97,9 +99,13 @@ def execute_param_transfer(
     buffers, then unpack: the path an exchange between GPUs goes through);
     ``arena`` places every destination tensor in one allocation
     (``ReshardPlan.arena_layout``: field by field, 256-byte aligned), for a
-    model that adopts them with ``load_state_dict(assign=True)``.
+    model that adopts them with ``load_state_dict(assign=True)``;
+    ``pipeline`` cuts the transfer into up to that many launch groups of
+    whole tensors, each planned on the host while the GPU runs the previous
+    one (one group for an arena; groups of at least 2 GB of pieces).
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
+    _lib.lib()   # raises when the HIP library is missing: there is no other path
     if log_func is None:
         log_func = lambda msg: None  # noqa: E731
     if prof is None:
@@ -137,36 +143,51 @@ def execute_param_transfer(
             t = entry[f]
             src_specs[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(t.shape), t.dtype)
 
-    prof.start("execute schedule lowering")
-    plan = ReshardPlan(ops, src_specs, normal, recast=recast, options=plan_options)
-    prof.stop("execute schedule lowering")
-    log_func(f"=== reshard plan: {plan.n_pieces} pieces, {len(plan.peers)} peers, "
-             f"{plan.info.buffer_bytes / 1e6:.1f} MB of buffers ===")
-
-    sources = {r: source(r) for r in plan.peers}
-    for r, sd in sources.items():
-        for name, entry in sd.items():
-            for f in normal:
-                t = entry.get(f)
-                if t is not None and t.device != device and (r, name, f) in src_specs:
-                    raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, "
-                                         f"not on {device}")
-
-    with torch.cuda.device(device):
-        target = plan.alloc_dst(device, arena=arena)
-        buffers = []
-        if route == "direct":
-            prof.start("execute gather")
-            plan.gather(sources, target, stream)
-            prof.stop("execute gather")
-        else:
-            buffers = plan.alloc_buffers(device)
-            prof.start("execute pack")
-            plan.pack(sources, buffers, stream)
-            prof.stop("execute pack")
-            prof.start("execute unpack")
-            plan.unpack(buffers, target, stream)
-            prof.stop("execute unpack")
+    groups = _pipeline_groups(ops, src_specs, normal, 1 if arena else pipeline)
+    target: StateDict = {}
+    plans: List[ReshardPlan] = []
+    buffers: List[List[Tensor]] = []
+    used_sources: Dict[int, StateDict] = {}
+    try:
+        with torch.cuda.device(device):
+            # Each group is planned on the host while the GPU runs the
+            # previous group's launch.
+            for group in groups:
+                prof.start("execute schedule lowering")
+                plan = ReshardPlan(group, src_specs, normal, recast=recast, options=plan_options)
+                prof.stop("execute schedule lowering")
+                plans.append(plan)
+                sources = {r: source(r) for r in plan.peers}
+                for r, sd in sources.items():
+                    for (sr, name, f) in plan.src_keys:
+                        t = sd[name][f] if sr == r else None
+                        if t is not None and t.device != device:
+                            raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, "
+                                                 f"not on {device}")
+                used_sources.update(sources)
+                part = plan.alloc_dst(device, arena=arena)
+                if route == "direct":
+                    prof.start("execute gather")
+                    plan.gather(sources, part, stream)
+                    prof.stop("execute gather")
+                else:
+                    bufs = plan.alloc_buffers(device)
+                    buffers.append(bufs)
+                    prof.start("execute pack")
+                    plan.pack(sources, bufs, stream)
+                    prof.stop("execute pack")
+                    prof.start("execute unpack")
+                    plan.unpack(bufs, part, stream)
+                    prof.stop("execute unpack")
+                target.update(part)
+        log_func(f"=== reshard plan: {sum(p.n_pieces for p in plans)} pieces in {len(plans)} "
+                 f"launch group(s), {sum(p.info.buffer_bytes for p in plans) / 1e6:.1f} MB of buffers ===")
+    finally:
+        # destroying a plan waits for its launches: buffers and sources may
+        # be released afterwards whatever stream the kernels ran on
+        for plan in plans:
+            plan.close()
+    del buffers
 
     # 1-element sub-fields ride along whole; the first op's source wins,
     # matching tensors[0].clone() of migration.py:538.
@@ -181,19 +202,53 @@ def execute_param_transfer(
 
     ordered: StateDict = {}
     field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
-    for name, entry in target.items():
+    for name in dict.fromkeys(op.param_name for op in ops):
+        entry = target[name]
         ordered[name] = {f: entry[f] for f in field_order if f in entry}
 
-    del buffers
     if forcefully_free:
-        for sd in sources.values():
+        for sd in used_sources.values():
             for entry in sd.values():
                 for f in normal:
                     if f in entry:
                         forcefully_free_tensor(entry[f])
     source_state_dict.clear()
-    plan.close()
     return ordered
+
+
+# Bytes of piece data per launch group at least: a group's GPU time (about
+# 0.3 ms per GB at the measured rate) must cover the next group's host
+# planning for the overlap to pay; below 2 GB a single launch is faster.
+PIPELINE_GROUP_BYTES = 2 << 30
+
+
+def _pipeline_groups(ops: List[TransferOp], src_specs: Mapping[Tuple[int, str, str], SlotSpec],
+                     fields: List[str], pipeline: int) -> List[List[TransferOp]]:
+    """Cut the ops into at most ``pipeline`` groups of whole tensors (all ops
+    of a name stay together, so each group's plan covers its destinations
+    completely), contiguous in schedule order and of about equal bytes."""
+    by_name: Dict[str, List[TransferOp]] = {}
+    for op in ops:
+        by_name.setdefault(op.param_name, []).append(op)
+    sizes = []
+    for name, name_ops in by_name.items():
+        n = 0
+        for op in name_ops:
+            numel = 1
+            for d in op.dst_meta.actual_shape():
+                numel *= int(d)
+            n += numel * sum(src_specs[(op.src_rank, name, f)].dtype.itemsize for f in fields)
+        sizes.append(n)
+    total = sum(sizes)
+    k = max(1, min(int(pipeline), len(sizes), total // PIPELINE_GROUP_BYTES))
+    groups: List[List[TransferOp]] = [[]]
+    acc = 0
+    for (name, name_ops), n in zip(by_name.items(), sizes):
+        if groups[-1] and acc >= total * len(groups) / k and len(groups) < k:
+            groups.append([])
+        groups[-1].extend(name_ops)
+        acc += n
+    return groups
 
 
 def schedule_and_execute_param_transfer(

@@ -48,6 +48,19 @@ def test_gpu_matches_oracle(w, route):
     _check(w, route=route)
 
 
+PIPELINED = list(cases.scaled_configs().values()) + cases.dp_cases()[:2]
+
+
+@pytest.mark.parametrize("route", ["buffers", "direct"])
+@pytest.mark.parametrize("w", PIPELINED, ids=[w.key for w in PIPELINED])
+def test_gpu_pipelined_launch_groups_match_oracle(w, route, monkeypatch):
+    """execute_param_transfer in several launch groups (each planned while
+    the previous one runs), forced on small cases by a tiny group size."""
+    from suika_amd import migration
+    monkeypatch.setattr(migration, "PIPELINE_GROUP_BYTES", 1 << 10)
+    _check(w, payload="index", route=route)
+
+
 SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
 
 

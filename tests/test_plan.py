@@ -215,3 +215,29 @@ def test_zero_element_tensors_are_planned_as_empty():
         assert tuple(dst["none2d"]["exp_avg"].shape) == (0, 4)
         assert tuple(dst["w"]["master"].shape) == (8, 4)
     plan.close()
+
+
+def test_pipeline_groups_keep_tensors_whole():
+    """Launch groups of execute_param_transfer: contiguous in schedule order,
+    every op of a tensor in one group, at most ``pipeline`` groups, each
+    carrying at least PIPELINE_GROUP_BYTES unless it is the only one."""
+    from suika_amd import migration
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        ops = w.ops()
+        specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), w.dtypes[f])
+                 for op in ops for f in w.src_fields}
+        for pipeline in (1, 3, 4, 100):
+            groups = migration._pipeline_groups(ops, specs, list(w.src_fields), pipeline)
+            assert [op for g in groups for op in g] == ops
+            assert 1 <= len(groups) <= pipeline
+            seen = set()
+            for g in groups:
+                names = {op.param_name for op in g}
+                assert not names & seen, "a tensor split across groups"
+                seen |= names
+    small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
+    ops = small.ops()
+    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), small.dtypes[f])
+             for op in ops for f in small.src_fields}
+    assert len(migration._pipeline_groups(ops, specs, list(small.src_fields), 4)) == 1
