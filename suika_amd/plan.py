@@ -158,28 +158,29 @@ class ReshardPlan:
         c_dst: List[_lib.SrTensor] = []
         c_pieces: List[_lib.SrPiece] = []
 
-        def src_slot(key: SrcKey, view: int) -> int:
+        # Slots are made once per (tensor, field); the 2-D view ``rc`` is the
+        # same for every field of a tensor and is computed by the caller.
+        def src_slot(key: SrcKey, rc: Tuple[int, int]) -> int:
             if key not in src_index:
-                assert key in src_specs, f"missing source tensor {key}"
                 spec = src_specs[key]
-                r, c = _matrix_of(spec.shape, view)
                 src_index[key] = len(self.src_keys)
                 self.src_keys.append(key)
                 self.src_specs[key] = spec
-                c_src.append(_lib.SrTensor(r, c, sr_dtype(spec.dtype), 0))
+                c_src.append(_lib.SrTensor(rc[0], rc[1], sr_dtype(spec.dtype), 0))
             return src_index[key]
 
-        def dst_slot(key: DstKey, meta: TensorMeta, dtype: torch.dtype, view: int) -> int:
+        def dst_slot(key: DstKey, shape: Tuple[int, ...], rc: Tuple[int, int], dtype: torch.dtype) -> int:
             if key not in dst_index:
-                r, c = local_matrix(meta, view)
                 dst_index[key] = len(self.dst_keys)
                 self.dst_keys.append(key)
-                self.dst_specs[key] = SlotSpec(tuple(int(s) for s in meta.actual_shape()), dtype)
-                c_dst.append(_lib.SrTensor(r, c, sr_dtype(dtype), 0))
+                self.dst_specs[key] = SlotSpec(shape, dtype)
+                c_dst.append(_lib.SrTensor(rc[0], rc[1], sr_dtype(dtype), 0))
             else:
                 assert self.dst_specs[key].dtype == dtype, \
                     f"{key}: sources disagree on dtype ({self.dst_specs[key].dtype} vs {dtype})"
             return dst_index[key]
+
+        recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
 
         self.empty_dst: Dict[DstKey, SlotSpec] = {}   # zero-element destinations (no pieces)
         lowered: Dict[tuple, list] = {}
@@ -212,16 +213,20 @@ class ReshardPlan:
                             self.empty_dst[(name, tgt)] = SlotSpec(shape, torch.bfloat16)
                 continue
             # destination slots of every field, then the pieces that fill them
+            drc = local_matrix(dst_shard, view)
             dslot: Dict[str, int] = {}
             for f in self.fields:
-                dslot[f] = dst_slot((name, f), dst_shard, field_dtype[f], view)
-                for tgt, sf in recast.items():
-                    if sf == f:
-                        assert field_dtype[f] == torch.float32, \
-                            f"{name}/{f}: recast source must be float32"
-                        dslot[tgt] = dst_slot((name, tgt), dst_shard, torch.bfloat16, view)
+                dslot[f] = dst_slot((name, f), shape, drc, field_dtype[f])
+                tgt = recast_of.get(f)
+                if tgt is not None:
+                    assert field_dtype[f] == torch.float32, f"{name}/{f}: recast source must be float32"
+                    dslot[tgt] = dst_slot((name, tgt), shape, drc, torch.bfloat16)
             for op in name_ops:
                 peer = peer_index[op.src_rank]
+                if not self.fields:
+                    continue
+                src_rc = _matrix_of(src_specs[(op.src_rank, name, self.fields[0])].shape, view)
+                sslot = {f: src_slot((op.src_rank, name, f), src_rc) for f in self.fields}
                 # regions depend only on the shard geometry, which repeats
                 # from layer to layer: lower each distinct geometry once
                 gkey = (_geometry_key(op.src_meta), _geometry_key(op.dst_meta), _geometry_key(dst_shard))
@@ -230,10 +235,10 @@ class ReshardPlan:
                     regions = lowered[gkey] = lower_op(op, dst_shard)
                 for reg in regions:
                     for f in self.fields:
-                        s = src_slot((op.src_rank, name, f), view)
-                        tgt = [t for t, sf in recast.items() if sf == f]
-                        if tgt:
-                            kind, d, d2 = _lib.SR_PIECE_RECAST, dslot[f], dslot[tgt[0]]
+                        s = sslot[f]
+                        tgt = recast_of.get(f)
+                        if tgt is not None:
+                            kind, d, d2 = _lib.SR_PIECE_RECAST, dslot[f], dslot[tgt]
                         else:
                             kind, d, d2 = _lib.SR_PIECE_COPY, dslot[f], -1
                         c_pieces.append(_lib.SrPiece(kind, peer, s, d, d2, 0, reg.rows, reg.cols,
