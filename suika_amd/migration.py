@@ -133,17 +133,25 @@ def execute_param_transfer(
             f"[{rank}]: piece from rank {r} needs a cross-GPU exchange, which this one-GPU build "
             "does not implement; pass the peer shards as fake_source_state_dicts")
 
-    src_specs: Dict[Tuple[int, str, str], SlotSpec] = {}
-    for op in ops:
-        sd = source(op.src_rank)
-        assert op.param_name in sd, f"[{rank}]: param missing in source {op.param_name}"
-        entry = sd[op.param_name]
-        for f in normal:
-            assert f in entry, f"expected_sub_fields mismatch: {op.param_name} has no {f}"
-            t = entry[f]
-            src_specs[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(t.shape), t.dtype)
+    def source_specs(group: List[TransferOp]) -> Dict[Tuple[int, str, str], SlotSpec]:
+        specs: Dict[Tuple[int, str, str], SlotSpec] = {}
+        for op in group:
+            sd = source(op.src_rank)
+            assert op.param_name in sd, f"[{rank}]: param missing in source {op.param_name}"
+            entry = sd[op.param_name]
+            for f in normal:
+                assert f in entry, f"expected_sub_fields mismatch: {op.param_name} has no {f}"
+                t = entry[f]
+                specs[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(t.shape), t.dtype)
+        return specs
 
-    groups = _pipeline_groups(ops, src_specs, normal, 1 if arena else pipeline)
+    # bytes per element over the moved fields, from the first op's sources
+    # (only used to balance the launch groups)
+    elem_bytes = 0
+    if ops and normal:
+        first = source(ops[0].src_rank).get(ops[0].param_name, {})
+        elem_bytes = sum(first[f].element_size() for f in normal if f in first)
+    groups = _pipeline_groups(ops, elem_bytes, 1 if arena else pipeline)
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
@@ -154,7 +162,8 @@ def execute_param_transfer(
             # previous group's launch.
             for group in groups:
                 prof.start("execute schedule lowering")
-                plan = ReshardPlan(group, src_specs, normal, recast=recast, options=plan_options)
+                plan = ReshardPlan(group, source_specs(group), normal, recast=recast,
+                                   options=plan_options)
                 prof.stop("execute schedule lowering")
                 plans.append(plan)
                 sources = {r: source(r) for r in plan.peers}
@@ -222,29 +231,35 @@ def execute_param_transfer(
 PIPELINE_GROUP_BYTES = 2 << 30
 
 
-def _pipeline_groups(ops: List[TransferOp], src_specs: Mapping[Tuple[int, str, str], SlotSpec],
-                     fields: List[str], pipeline: int) -> List[List[TransferOp]]:
+def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:
     """Cut the ops into at most ``pipeline`` groups of whole tensors (all ops
     of a name stay together, so each group's plan covers its destinations
-    completely), contiguous in schedule order and of about equal bytes."""
+    completely), contiguous in schedule order.  The first group carries half
+    a share of the bytes, so the GPU starts early; the others share the rest
+    about equally.  ``elem_bytes`` (bytes per element over all moved fields)
+    only scales the estimate."""
     by_name: Dict[str, List[TransferOp]] = {}
     for op in ops:
         by_name.setdefault(op.param_name, []).append(op)
     sizes = []
-    for name, name_ops in by_name.items():
+    for name_ops in by_name.values():
         n = 0
         for op in name_ops:
             numel = 1
             for d in op.dst_meta.actual_shape():
                 numel *= int(d)
-            n += numel * sum(src_specs[(op.src_rank, name, f)].dtype.itemsize for f in fields)
-        sizes.append(n)
+            n += numel
+        sizes.append(n * elem_bytes)
     total = sum(sizes)
     k = max(1, min(int(pipeline), len(sizes), total // PIPELINE_GROUP_BYTES))
+    if k == 1:
+        return [list(ops)]
+    first = total / (2 * k)
+    bounds = [first + j * (total - first) / (k - 1) for j in range(k - 1)]
     groups: List[List[TransferOp]] = [[]]
     acc = 0
-    for (name, name_ops), n in zip(by_name.items(), sizes):
-        if groups[-1] and acc >= total * len(groups) / k and len(groups) < k:
+    for name_ops, n in zip(by_name.values(), sizes):
+        if groups[-1] and len(groups) < k and acc >= bounds[len(groups) - 1]:
             groups.append([])
         groups[-1].extend(name_ops)
         acc += n

@@ -225,10 +225,9 @@ def test_pipeline_groups_keep_tensors_whole():
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         ops = w.ops()
-        specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), w.dtypes[f])
-                 for op in ops for f in w.src_fields}
+        elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
         for pipeline in (1, 3, 4, 100):
-            groups = migration._pipeline_groups(ops, specs, list(w.src_fields), pipeline)
+            groups = migration._pipeline_groups(ops, elem, pipeline)
             assert [op for g in groups for op in g] == ops
             assert 1 <= len(groups) <= pipeline
             seen = set()
@@ -237,7 +236,5 @@ def test_pipeline_groups_keep_tensors_whole():
                 assert not names & seen, "a tensor split across groups"
                 seen |= names
     small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
-    ops = small.ops()
-    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), small.dtypes[f])
-             for op in ops for f in small.src_fields}
-    assert len(migration._pipeline_groups(ops, specs, list(small.src_fields), 4)) == 1
+    elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
+    assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1
