@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+from collections import namedtuple
 from pathlib import Path
 from typing import Optional
 
@@ -85,6 +86,36 @@ class SrPiece(ctypes.Structure):
         ("dst_row", ctypes.c_uint64),
         ("dst_col", ctypes.c_uint64),
     ]
+
+
+def _struct_dtype(struct) -> "np.dtype":
+    """numpy dtype with the field names, types and offsets of a ctypes struct."""
+    import numpy as np
+    kinds = {ctypes.c_int32: np.int32, ctypes.c_uint32: np.uint32, ctypes.c_int64: np.int64,
+             ctypes.c_uint64: np.uint64}
+    names = [n for n, _ in struct._fields_]
+    dt = np.dtype({"names": names, "formats": [kinds[t] for _, t in struct._fields_],
+                   "offsets": [getattr(struct, n).offset for n in names],
+                   "itemsize": ctypes.sizeof(struct)})
+    return dt
+
+
+SR_TENSOR_DTYPE = _struct_dtype(SrTensor)
+SR_PIECE_DTYPE = _struct_dtype(SrPiece)
+TensorRecord = namedtuple("TensorRecord", [n for n, _ in SrTensor._fields_])
+PieceRecord = namedtuple("PieceRecord", [n for n, _ in SrPiece._fields_])
+
+
+def as_tensors(arr) -> "ctypes.POINTER(SrTensor)":
+    """Pointer to a contiguous SR_TENSOR_DTYPE array (kept alive by the caller)."""
+    assert arr.dtype == SR_TENSOR_DTYPE and arr.flags["C_CONTIGUOUS"]
+    return arr.ctypes.data_as(ctypes.POINTER(SrTensor))
+
+
+def as_pieces(arr) -> "ctypes.POINTER(SrPiece)":
+    """Pointer to a contiguous SR_PIECE_DTYPE array (kept alive by the caller)."""
+    assert arr.dtype == SR_PIECE_DTYPE and arr.flags["C_CONTIGUOUS"]
+    return arr.ctypes.data_as(ctypes.POINTER(SrPiece))
 
 
 class SrPlanOptions(ctypes.Structure):

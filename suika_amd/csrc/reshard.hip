@@ -689,14 +689,17 @@ struct Phase {
   bool interleave = false;
   uint64_t bytes_read = 0;
   uint64_t bytes_written = 0;
-  // device state, created on first use
+  // device state, created on first use: one device allocation carved into
+  // the tables, one pinned host buffer for their uploads
   bool ready = false;
+  void* d_mem = nullptr;
   DevRel* d_rel = nullptr;
   DevItem* d_items = nullptr;
   DevTile* d_tiles = nullptr;
   uint64_t* d_tile_base = nullptr;
   uint64_t* d_ptrs = nullptr;
-  uint64_t* h_staging = nullptr;        // pinned copy of the pointer table
+  unsigned char* h_staging = nullptr;   // pinned: descriptors, then the pointer table
+  uint64_t* h_ptrs = nullptr;           // the pointer-table part of h_staging
   std::vector<uint64_t> bound;          // pointer table of the last bind
   bool bound_valid = false;
   hipEvent_t ev_setup = nullptr;        // tile table and offsets written
@@ -723,6 +726,8 @@ struct sr_plan {
   std::vector<uint32_t> peer_list;
   std::vector<uint64_t> payload;        // per piece, 0 for ZERO
   bool offsets_ready = false;
+  void* d_offmem = nullptr;             // carved: offsets, payloads, peer lists
+  unsigned char* h_offmem = nullptr;    // pinned upload of payloads and peer lists
   uint64_t* d_offset = nullptr;
   uint32_t* d_peer_begin = nullptr;
   uint32_t* d_peer_list = nullptr;
@@ -910,25 +915,40 @@ int ensure_device(sr_plan* p) {
 
 enum PhaseKind { kPack, kUnpack, kGather };
 
-// Per-peer buffer offsets on the device (shared by pack and unpack).
+// Next 256-byte aligned offset for a carved sub-buffer of `bytes`.
+size_t carve(size_t& end, size_t bytes) {
+  const size_t at = (end + 255) & ~size_t(255);
+  end = at + bytes;
+  return at;
+}
+
+// Per-peer buffer offsets on the device (shared by pack and unpack).  The
+// inputs go up asynchronously on `stream` from pinned memory, so the call
+// never waits for earlier work on the stream.
 int setup_offsets(sr_plan* p, hipStream_t stream) {
   if (p->offsets_ready) return SR_OK;
   if (!p->ev_offsets) SR_HIP_TRY(hipEventCreateWithFlags(&p->ev_offsets, hipEventDisableTiming));
   if (p->n_peers > 0 && !p->peer_list.empty()) {
     const size_t np = p->pieces.size();
-    // Allocations survive a failed attempt (and are reused by the retry);
-    // the uploads are always redone.
-    if (!p->d_offset) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_offset), np * sizeof(uint64_t)));
-    if (!p->d_payload) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_payload), np * sizeof(uint64_t)));
-    if (!p->d_peer_begin)
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_peer_begin), p->peer_begin.size() * sizeof(uint32_t)));
-    if (!p->d_peer_list)
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->d_peer_list), p->peer_list.size() * sizeof(uint32_t)));
-    SR_HIP_TRY(hipMemcpy(p->d_payload, p->payload.data(), np * sizeof(uint64_t), hipMemcpyHostToDevice));
-    SR_HIP_TRY(hipMemcpy(p->d_peer_begin, p->peer_begin.data(), p->peer_begin.size() * sizeof(uint32_t),
-                         hipMemcpyHostToDevice));
-    SR_HIP_TRY(hipMemcpy(p->d_peer_list, p->peer_list.data(), p->peer_list.size() * sizeof(uint32_t),
-                         hipMemcpyHostToDevice));
+    size_t in_end = 0;   // layout of the uploaded part: payloads, peer_begin, peer_list
+    const size_t o_pay = carve(in_end, np * sizeof(uint64_t));
+    const size_t o_beg = carve(in_end, p->peer_begin.size() * sizeof(uint32_t));
+    const size_t o_lst = carve(in_end, p->peer_list.size() * sizeof(uint32_t));
+    size_t dev_end = in_end;
+    const size_t o_off = carve(dev_end, np * sizeof(uint64_t));
+    // allocations survive a failed attempt and are reused by the retry
+    if (!p->d_offmem) SR_HIP_TRY(hipMalloc(&p->d_offmem, dev_end));
+    if (!p->h_offmem)
+      SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&p->h_offmem), in_end, hipHostMallocDefault));
+    unsigned char* d = static_cast<unsigned char*>(p->d_offmem);
+    p->d_payload = reinterpret_cast<uint64_t*>(d + o_pay);
+    p->d_peer_begin = reinterpret_cast<uint32_t*>(d + o_beg);
+    p->d_peer_list = reinterpret_cast<uint32_t*>(d + o_lst);
+    p->d_offset = reinterpret_cast<uint64_t*>(d + o_off);
+    std::memcpy(p->h_offmem + o_pay, p->payload.data(), np * sizeof(uint64_t));
+    std::memcpy(p->h_offmem + o_beg, p->peer_begin.data(), p->peer_begin.size() * sizeof(uint32_t));
+    std::memcpy(p->h_offmem + o_lst, p->peer_list.data(), p->peer_list.size() * sizeof(uint32_t));
+    SR_HIP_TRY(hipMemcpyAsync(p->d_offmem, p->h_offmem, in_end, hipMemcpyHostToDevice, stream));
     hipLaunchKernelGGL(sr_offsets_kernel, dim3(uint32_t(p->n_peers)), dim3(kSetupBlock), 0, stream,
                        p->d_peer_begin, p->d_peer_list, p->d_payload, p->d_offset);
     SR_HIP_TRY(hipGetLastError());
@@ -948,17 +968,28 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
-    if (!ph.d_rel) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_rel), n * sizeof(DevRel)));
-    if (!ph.d_items) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_items), n * sizeof(DevItem)));
-    if (!ph.d_tile_base)
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_tile_base), (size_t(n) + 1) * sizeof(uint64_t)));
-    if (!ph.d_tiles)
-      SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_tiles), ph.n_tiles * sizeof(DevTile)));
-    if (!ph.d_ptrs) SR_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&ph.d_ptrs), nptr * sizeof(uint64_t)));
-    if (!ph.h_staging)
-      SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ph.h_staging), nptr * sizeof(uint64_t),
+    size_t end = 0;
+    const size_t o_rel = carve(end, n * sizeof(DevRel));
+    const size_t o_ptr = carve(end, nptr * sizeof(uint64_t));
+    const size_t o_items = carve(end, n * sizeof(DevItem));
+    const size_t o_base = carve(end, (size_t(n) + 1) * sizeof(uint64_t));
+    const size_t o_tiles = carve(end, ph.n_tiles * sizeof(DevTile));
+    // allocations survive a failed attempt and are reused by the retry
+    if (!ph.d_mem) SR_HIP_TRY(hipMalloc(&ph.d_mem, end));
+    if (!ph.h_staging)   // descriptors + pointer table, the same layout as the device start
+      SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ph.h_staging), o_ptr + nptr * sizeof(uint64_t),
                                hipHostMallocDefault));
-    SR_HIP_TRY(hipMemcpy(ph.d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice));
+    unsigned char* d = static_cast<unsigned char*>(ph.d_mem);
+    ph.d_rel = reinterpret_cast<DevRel*>(d + o_rel);
+    ph.d_ptrs = reinterpret_cast<uint64_t*>(d + o_ptr);
+    ph.d_items = reinterpret_cast<DevItem*>(d + o_items);
+    ph.d_tile_base = reinterpret_cast<uint64_t*>(d + o_base);
+    ph.d_tiles = reinterpret_cast<DevTile*>(d + o_tiles);
+    ph.h_ptrs = reinterpret_cast<uint64_t*>(ph.h_staging + o_ptr);
+    // the descriptors go up once, asynchronously on the caller's stream
+    std::memcpy(ph.h_staging + o_rel, ph.rel.data(), n * sizeof(DevRel));
+    SR_HIP_TRY(hipMemcpyAsync(ph.d_rel, ph.h_staging + o_rel, n * sizeof(DevRel), hipMemcpyHostToDevice,
+                              stream));
     if (needs_offsets) {
       int rc = setup_offsets(p, stream);
       if (rc != SR_OK) return rc;
@@ -1031,9 +1062,9 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
     // The staging buffer may still feed the previous bind; the item table
     // may still be read by the previous launch of this phase.
     SR_HIP_TRY(hipEventSynchronize(ph.ev_staging));
-    std::memcpy(ph.h_staging, ptrs.data(), ptrs.size() * sizeof(uint64_t));
+    std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
     SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_kernel, 0));
-    SR_HIP_TRY(hipMemcpyAsync(ph.d_ptrs, ph.h_staging, ptrs.size() * sizeof(uint64_t),
+    SR_HIP_TRY(hipMemcpyAsync(ph.d_ptrs, ph.h_ptrs, ptrs.size() * sizeof(uint64_t),
                               hipMemcpyHostToDevice, stream));
     hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0,
                        stream, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
@@ -1073,11 +1104,7 @@ void free_phase(Phase& ph) {
   if (ph.ev_kernel) (void)hipEventSynchronize(ph.ev_kernel);
   if (ph.ev_staging) (void)hipEventSynchronize(ph.ev_staging);
   if (ph.ev_setup) (void)hipEventSynchronize(ph.ev_setup);
-  if (ph.d_rel) (void)hipFree(ph.d_rel);
-  if (ph.d_items) (void)hipFree(ph.d_items);
-  if (ph.d_tiles) (void)hipFree(ph.d_tiles);
-  if (ph.d_tile_base) (void)hipFree(ph.d_tile_base);
-  if (ph.d_ptrs) (void)hipFree(ph.d_ptrs);
+  if (ph.d_mem) (void)hipFree(ph.d_mem);
   if (ph.h_staging) (void)hipHostFree(ph.h_staging);
   if (ph.ev_setup) (void)hipEventDestroy(ph.ev_setup);
   if (ph.ev_staging) (void)hipEventDestroy(ph.ev_staging);
@@ -1529,10 +1556,8 @@ void sr_plan_destroy(sr_plan* plan) {
   free_phase(plan->unpack);
   free_phase(plan->gather);
   if (plan->ev_offsets) (void)hipEventSynchronize(plan->ev_offsets);
-  if (plan->d_offset) (void)hipFree(plan->d_offset);
-  if (plan->d_payload) (void)hipFree(plan->d_payload);
-  if (plan->d_peer_begin) (void)hipFree(plan->d_peer_begin);
-  if (plan->d_peer_list) (void)hipFree(plan->d_peer_list);
+  if (plan->d_offmem) (void)hipFree(plan->d_offmem);
+  if (plan->h_offmem) (void)hipHostFree(plan->h_offmem);
   if (plan->ev_offsets) (void)hipEventDestroy(plan->ev_offsets);
   delete plan;
 }

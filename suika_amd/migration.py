@@ -24,6 +24,7 @@ intended ``cat`` in ascending piece order.
 """
 from __future__ import annotations
 
+import gc
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
 import torch
@@ -84,7 +85,7 @@ def execute_param_transfer(
     stream: Optional[torch.cuda.Stream] = None,
     route: str = "direct",
     arena: bool = False,
-    pipeline: int = 4,
+    pipeline: int = 6,
 ) -> StateDict:
     """Execute a transfer schedule for this rank; returns its target state.
 
@@ -156,6 +157,11 @@ def execute_param_transfer(
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
     used_sources: Dict[int, StateDict] = {}
+    # A full pass of Python's cyclic collector over a large heap (tens of ms)
+    # would stall the host between launch groups and idle the GPU; it is
+    # paused for the call (reference counting still frees memory).
+    gc_was_enabled = gc.isenabled()
+    gc.disable()
     try:
         with torch.cuda.device(device):
             # Each group is planned on the host while the GPU runs the
@@ -196,6 +202,8 @@ def execute_param_transfer(
         # be released afterwards whatever stream the kernels ran on
         for plan in plans:
             plan.close()
+        if gc_was_enabled:
+            gc.enable()
     del buffers
 
     # 1-element sub-fields ride along whole; the first op's source wins,
@@ -234,10 +242,9 @@ PIPELINE_GROUP_BYTES = 2 << 30
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:
     """Cut the ops into at most ``pipeline`` groups of whole tensors (all ops
     of a name stay together, so each group's plan covers its destinations
-    completely), contiguous in schedule order.  The first group carries half
-    a share of the bytes, so the GPU starts early; the others share the rest
-    about equally.  ``elem_bytes`` (bytes per element over all moved fields)
-    only scales the estimate."""
+    completely), contiguous in schedule order and of about equal bytes
+    (``elem_bytes``, bytes per element over all moved fields, only scales
+    the estimate)."""
     by_name: Dict[str, List[TransferOp]] = {}
     for op in ops:
         by_name.setdefault(op.param_name, []).append(op)
@@ -254,8 +261,7 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
     k = max(1, min(int(pipeline), len(sizes), total // PIPELINE_GROUP_BYTES))
     if k == 1:
         return [list(ops)]
-    first = total / (2 * k)
-    bounds = [first + j * (total - first) / (k - 1) for j in range(k - 1)]
+    bounds = [total * (j + 1) / k for j in range(k - 1)]
     groups: List[List[TransferOp]] = [[]]
     acc = 0
     for name_ops, n in zip(by_name.values(), sizes):

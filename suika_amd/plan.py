@@ -22,6 +22,7 @@ import ctypes
 from dataclasses import dataclass
 from typing import Dict, List, Mapping, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -154,9 +155,11 @@ class ReshardPlan:
         self.dst_specs: Dict[DstKey, SlotSpec] = {}
         self.dst_metas: Dict[str, TensorMeta] = {}
 
-        c_src: List[_lib.SrTensor] = []
-        c_dst: List[_lib.SrTensor] = []
-        c_pieces: List[_lib.SrPiece] = []
+        # rows of the C tables (sr_tensor / sr_piece field order), converted
+        # to arrays in one step: thousands of ctypes records cost milliseconds
+        c_src: List[tuple] = []
+        c_dst: List[tuple] = []
+        c_pieces: List[tuple] = []
 
         # Slots are made once per (tensor, field); the 2-D view ``rc`` is the
         # same for every field of a tensor and is computed by the caller.
@@ -166,7 +169,7 @@ class ReshardPlan:
                 src_index[key] = len(self.src_keys)
                 self.src_keys.append(key)
                 self.src_specs[key] = spec
-                c_src.append(_lib.SrTensor(rc[0], rc[1], sr_dtype(spec.dtype), 0))
+                c_src.append((rc[0], rc[1], sr_dtype(spec.dtype), 0))
             return src_index[key]
 
         def dst_slot(key: DstKey, shape: Tuple[int, ...], rc: Tuple[int, int], dtype: torch.dtype) -> int:
@@ -174,7 +177,7 @@ class ReshardPlan:
                 dst_index[key] = len(self.dst_keys)
                 self.dst_keys.append(key)
                 self.dst_specs[key] = SlotSpec(shape, dtype)
-                c_dst.append(_lib.SrTensor(rc[0], rc[1], sr_dtype(dtype), 0))
+                c_dst.append((rc[0], rc[1], sr_dtype(dtype), 0))
             else:
                 assert self.dst_specs[key].dtype == dtype, \
                     f"{key}: sources disagree on dtype ({self.dst_specs[key].dtype} vs {dtype})"
@@ -241,27 +244,26 @@ class ReshardPlan:
                             kind, d, d2 = _lib.SR_PIECE_RECAST, dslot[f], dslot[tgt]
                         else:
                             kind, d, d2 = _lib.SR_PIECE_COPY, dslot[f], -1
-                        c_pieces.append(_lib.SrPiece(kind, peer, s, d, d2, 0, reg.rows, reg.cols,
-                                                     reg.src_row, reg.src_col,
-                                                     reg.dst_row, reg.dst_col))
+                        c_pieces.append((kind, peer, s, d, d2, 0, reg.rows, reg.cols,
+                                         reg.src_row, reg.src_col, reg.dst_row, reg.dst_col))
                         self.piece_owner.append((name, peer))
             for box in pad_boxes(dst_shard, view):
                 for f, slot in dslot.items():
-                    c_pieces.append(_lib.SrPiece(_lib.SR_PIECE_ZERO, 0, -1, slot, -1, 0,
-                                                 box.rows, box.cols, 0, 0, box.row, box.col))
+                    c_pieces.append((_lib.SR_PIECE_ZERO, 0, -1, slot, -1, 0,
+                                     box.rows, box.cols, 0, 0, box.row, box.col))
                     self.piece_owner.append((name, -1))
 
         self.n_pieces = len(c_pieces)
-        self.pieces = c_pieces
-        self.c_src = c_src
-        self.c_dst = c_dst
+        self._src_arr = np.array(c_src, dtype=_lib.SR_TENSOR_DTYPE).reshape(-1)
+        self._dst_arr = np.array(c_dst, dtype=_lib.SR_TENSOR_DTYPE).reshape(-1)
+        self._piece_arr = np.array(c_pieces, dtype=_lib.SR_PIECE_DTYPE).reshape(-1)
+        self._pieces_view = self._c_src_view = self._c_dst_view = None
         L = self._L = _lib.lib()
-        src_arr = (_lib.SrTensor * max(1, len(c_src)))(*c_src)
-        dst_arr = (_lib.SrTensor * max(1, len(c_dst)))(*c_dst)
-        pc_arr = (_lib.SrPiece * max(1, len(c_pieces)))(*c_pieces)
         opt = self.options.to_c()
-        rc = L.sr_plan_create(src_arr, len(c_src), dst_arr, len(c_dst), len(self.peers),
-                              pc_arr, len(c_pieces), ctypes.byref(opt), ctypes.byref(self._handle))
+        rc = L.sr_plan_create(_lib.as_tensors(self._src_arr), len(c_src),
+                              _lib.as_tensors(self._dst_arr), len(c_dst), len(self.peers),
+                              _lib.as_pieces(self._piece_arr), len(c_pieces), ctypes.byref(opt),
+                              ctypes.byref(self._handle))
         _lib.check(rc, "sr_plan_create", L)
         self.peer_bytes: List[int] = []
         for i in range(len(self.peers)):
@@ -286,6 +288,28 @@ class ReshardPlan:
         _lib.check(self._L.sr_plan_piece_offset(self._handle, k, ctypes.byref(off)),
                    "sr_plan_piece_offset", self._L)
         return int(off.value)
+
+    # ------------------------------------------------- the C tables, read back
+    @property
+    def pieces(self) -> list:
+        """The sr_piece records, as named tuples (built on first use)."""
+        if self._pieces_view is None:
+            self._pieces_view = [_lib.PieceRecord(*r) for r in self._piece_arr.tolist()]
+        return self._pieces_view
+
+    @property
+    def c_src(self) -> list:
+        """The source sr_tensor records, as named tuples."""
+        if self._c_src_view is None:
+            self._c_src_view = [_lib.TensorRecord(*r) for r in self._src_arr.tolist()]
+        return self._c_src_view
+
+    @property
+    def c_dst(self) -> list:
+        """The destination sr_tensor records, as named tuples."""
+        if self._c_dst_view is None:
+            self._c_dst_view = [_lib.TensorRecord(*r) for r in self._dst_arr.tolist()]
+        return self._c_dst_view
 
     # --------------------------------------------------------- allocation
     def alloc_buffers(self, device) -> List[torch.Tensor]:
