@@ -14,7 +14,9 @@ HIP events on the stream the kernels run on; ``cpu_baseline`` times the
 reference-style torch-CPU reshard (chunk/contiguous/cat) on a bounded sample
 of the same workload on this host's cores, scaled to the same unit.
 ``direct_gather`` reports the buffer-free route (one launch, P + D bytes) that
-applies when every source shard is resident on this GPU.
+applies when every source shard is resident on this GPU; ``api`` times the
+drop-in operator end to end (``schedule_param_transfer`` for every rank, then
+``execute_param_transfer`` with the sources resident).
 """
 from __future__ import annotations
 
