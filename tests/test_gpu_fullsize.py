@@ -6,15 +6,18 @@ Sources are index-coded on the GPU from the oracle's closed-form shard maps
 within a tensor.  After pack + unpack, each destination tensor must equal the
 codes of its own closed-form index map, pad rows must be zero, and a recast
 ``param`` must be the bf16 rounding of the destination ``master``.  Any
-misrouted, dropped or duplicated element changes a code.
+misrouted, dropped or duplicated element changes a code.  The direct gather
+and the drop-in ``execute_param_transfer`` (in launch groups) must then
+reproduce the same bytes.
 """
 import pytest
 import torch
 
 from oracle import reshard_oracle as O
+from suika_amd import execute_param_transfer
 from suika_amd.plan import ReshardPlan, SlotSpec
 from suika_amd.workloads import CONFIG_ORDER, CONFIGS
-from tests.harness import to_olayout
+from tests.harness import poisoned_allocations, to_olayout
 
 pytestmark = pytest.mark.gpu
 
@@ -74,7 +77,6 @@ def test_fullsize_index_coded(key):
             t.view(torch.uint8).fill_(0x5A)
     plan.gather(sources, dst2)
     torch.cuda.synchronize()
-    del sources
 
     recast = w.recast_map
     bad = []
@@ -82,6 +84,17 @@ def test_fullsize_index_coded(key):
         if not torch.equal(dst[name][f].view(torch.uint8), dst2[name][f].view(torch.uint8)):
             bad.append((name, f, "gather"))
     del dst2
+    # the drop-in operator (launch groups planned while the GPU runs, poisoned
+    # destinations) must agree bit for bit as well
+    print(f"[gpu fullsize] {key}: execute_param_transfer", flush=True)
+    with poisoned_allocations():
+        out = execute_param_transfer(ops, {}, dev, [(f, "normal") for f in w.src_fields],
+                                     rank=w.dst_rank, fake_source_state_dicts=sources, recast=recast)
+    torch.cuda.synchronize()
+    for (name, f) in plan.dst_keys:
+        if not torch.equal(dst[name][f].view(torch.uint8), out[name][f].view(torch.uint8)):
+            bad.append((name, f, "execute_param_transfer"))
+    del out, sources
     for (name, f) in plan.dst_keys:
         gidx = O.shard_index(odst[w.dst_rank][name], xp=torch, device=dev)
         if f in recast:
