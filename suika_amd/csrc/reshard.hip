@@ -214,17 +214,26 @@ template <> struct VecOf<1> { typedef unsigned char type; };
 // would also wait on the LDS counter.
 #define SR_GLOBAL __attribute__((address_space(1)))
 
+// Streaming (non-temporal) access applies to loads and stores separately
+// (compile-time knobs, both on by default).
+#ifndef SR_NT_LOADS
+#define SR_NT_LOADS 1
+#endif
+#ifndef SR_NT_STORES
+#define SR_NT_STORES 1
+#endif
+
 template <typename T, bool NT>
 __device__ __forceinline__ T ld(uint64_t addr) {
   const SR_GLOBAL T* p = (const SR_GLOBAL T*)addr;
-  if constexpr (NT) return __builtin_nontemporal_load(p);
+  if constexpr (NT && SR_NT_LOADS) return __builtin_nontemporal_load(p);
   else return *p;
 }
 
 template <typename T, bool NT>
 __device__ __forceinline__ void st(uint64_t addr, T v) {
   SR_GLOBAL T* p = (SR_GLOBAL T*)addr;
-  if constexpr (NT) __builtin_nontemporal_store(v, p);
+  if constexpr (NT && SR_NT_STORES) __builtin_nontemporal_store(v, p);
   else *p = v;
 }
 
