@@ -33,6 +33,7 @@ from torch import Tensor
 from torch.nn import Module
 from torch.optim import Optimizer
 
+from .geometry import infer_dst_shard
 from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
                    schedule_param_transfer)
 from . import _lib
@@ -98,12 +99,13 @@ def execute_param_transfer(
     is ``"direct"`` (one gather pass from the resident sources, the default
     since every source is on this GPU) or ``"buffers"`` (pack into per-peer
     buffers, then unpack: the path an exchange between GPUs goes through);
-    ``arena`` places every destination tensor in one allocation
-    (``ReshardPlan.arena_layout``: field by field, 256-byte aligned), for a
+    ``arena`` places every destination tensor in one allocation (field by
+    field over all tensors, schedule order within a field, 256-byte
+    aligned), for a
     model that adopts them with ``load_state_dict(assign=True)``;
     ``pipeline`` cuts the transfer into up to that many launch groups of
     whole tensors, each planned on the host while the GPU runs the previous
-    one (one group for an arena; groups of at least 2 GB of pieces).
+    one (groups of at least 2 GB of pieces).
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     _lib.lib()   # raises when the HIP library is missing: there is no other path
@@ -152,7 +154,8 @@ def execute_param_transfer(
     if ops and normal:
         first = source(ops[0].src_rank).get(ops[0].param_name, {})
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
-    groups = _pipeline_groups(ops, elem_bytes, 1 if arena else pipeline)
+    groups = _pipeline_groups(ops, elem_bytes, pipeline)
+    arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
@@ -180,7 +183,10 @@ def execute_param_transfer(
                             raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, "
                                                  f"not on {device}")
                 used_sources.update(sources)
-                part = plan.alloc_dst(device, arena=arena)
+                if arena_views is None:
+                    part = plan.alloc_dst(device)
+                else:
+                    part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
                 if route == "direct":
                     prof.start("execute gather")
                     plan.gather(sources, part, stream)
@@ -237,6 +243,50 @@ def execute_param_transfer(
 # 0.3 ms per GB at the measured rate) must cover the next group's host
 # planning for the overlap to pay; below 2 GB a single launch is faster.
 PIPELINE_GROUP_BYTES = 2 << 30
+ARENA_ALIGN = 256
+
+
+def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fields: List[str],
+                 recast: Mapping[str, str], device: torch.device) -> StateDict:
+    """Every destination tensor of the transfer as a view of one allocation,
+    laid out before any plan is built: field by field (bf16 recast targets
+    first, then the moved fields), tensors in schedule order within a field,
+    each at a 256-byte aligned offset.  Launch groups then write into it."""
+    by_name: Dict[str, List[TransferOp]] = {}
+    for op in ops:
+        by_name.setdefault(op.param_name, []).append(op)
+    shapes: Dict[str, Tuple[int, ...]] = {}
+    dtypes: Dict[Tuple[str, str], torch.dtype] = {}
+    for name, name_ops in by_name.items():
+        shapes[name] = tuple(int(d) for d in infer_dst_shard(name_ops).actual_shape())
+        entry = source(name_ops[0].src_rank)[name]
+        for f in fields:
+            dtypes[(name, f)] = entry[f].dtype
+        for tgt, sf in recast.items():
+            if sf in fields:
+                dtypes[(name, tgt)] = torch.bfloat16
+    order = list(recast) + [f for f in fields if f not in recast]
+    offsets: Dict[Tuple[str, str], int] = {}
+    end = 0
+    for f in order:
+        for name in by_name:
+            if (name, f) not in dtypes:
+                continue
+            end = (end + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
+            offsets[(name, f)] = end
+            n = 1
+            for d in shapes[name]:
+                n *= d
+            end += n * dtypes[(name, f)].itemsize
+    buf = torch.empty(max(1, end), dtype=torch.uint8, device=device)
+    out: StateDict = {}
+    for (name, f), off in offsets.items():
+        dt = dtypes[(name, f)]
+        n = 1
+        for d in shapes[name]:
+            n *= d
+        out.setdefault(name, {})[f] = buf[off:off + n * dt.itemsize].view(dt).view(shapes[name])
+    return out
 
 
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:

@@ -108,11 +108,16 @@ def test_boundary_rejects_misaligned_and_null_pointers():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("groups", ["one", "many"])
 @pytest.mark.parametrize("route", ["direct", "buffers"])
-def test_arena_destinations_and_adoption(route):
+def test_arena_destinations_and_adoption(route, groups, monkeypatch):
     """execute_param_transfer(arena=True): bit-identical to the oracle, every
-    destination a view of one allocation, and a stage module adopting the
-    params with load_state_dict(assign=True) keeps them in place (no copy)."""
+    destination a view of one allocation -- also when the transfer runs as
+    several launch groups -- and a stage module adopting the params with
+    load_state_dict(assign=True) keeps them in place (no copy)."""
+    if groups == "many":
+        from suika_amd import migration
+        monkeypatch.setattr(migration, "PIPELINE_GROUP_BYTES", 1 << 10)
     from suika_amd.inventory import build_module
     from tests.cases import scaled_configs
     from tests.harness import index_state, oracle_dest, source_shards, t2np, to_device
