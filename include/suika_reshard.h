@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 2
+#define SR_ABI_VERSION 3
 
 typedef enum sr_status {
   SR_OK = 0,

@@ -1,4 +1,5 @@
-"""ctypes binding of ``libsuika_reshard.so`` (C ABI in include/suika_reshard.h).
+"""ctypes binding of ``libsuika_reshard.so`` (C ABI in include/suika_reshard.h
+and include/suika_schedule.h).
 
 The binding fails loudly: importing the package never falls back to a CPU or
 torch path.  If the library is missing, every entry point raises
@@ -44,6 +45,9 @@ SR_OPT_PIECE_ORDER = 0x4
 SR_OPT_NO_XCD_INTERLEAVE = 0x8
 SR_OPT_NO_ROW_GROUPS = 0x10
 
+SR_MAX_DIMS = 8
+SR_KIND_CHUNK, SR_KIND_VOCAB_PAD, SR_KIND_QKV_HEADS = 0, 1, 2
+
 # Every symbol the header declares; the CPU test-suite checks they resolve.
 EXPORTED_SYMBOLS = (
     "sr_abi_version",
@@ -57,9 +61,10 @@ EXPORTED_SYMBOLS = (
     "sr_unpack",
     "sr_gather",
     "sr_plan_destroy",
+    "sr_schedule",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class SrTensor(ctypes.Structure):
@@ -116,6 +121,51 @@ def as_pieces(arr) -> "ctypes.POINTER(SrPiece)":
     """Pointer to a contiguous SR_PIECE_DTYPE array (kept alive by the caller)."""
     assert arr.dtype == SR_PIECE_DTYPE and arr.flags["C_CONTIGUOUS"]
     return arr.ctypes.data_as(ctypes.POINTER(SrPiece))
+
+
+class SrMeta(ctypes.Structure):
+    """One TensorMeta of a layout (sr_meta)."""
+    _fields_ = [
+        ("rank", ctypes.c_int64),
+        ("name", ctypes.c_int64),
+        ("itemsize", ctypes.c_int64),
+        ("ndim", ctypes.c_int64),
+        ("shape", ctypes.c_int64 * SR_MAX_DIMS),
+        ("slice_dim", ctypes.c_int64),
+        ("tp_index", ctypes.c_int64),
+        ("tp_deg", ctypes.c_int64),
+        ("kind", ctypes.c_int64),
+        ("kind_args", ctypes.c_int64 * 3),
+        ("row0", ctypes.c_int64),
+        ("row1", ctypes.c_int64),
+    ]
+
+
+class SrOp(ctypes.Structure):
+    """One scheduled piece (sr_op)."""
+    _fields_ = [
+        ("name", ctypes.c_int64),
+        ("src_rank", ctypes.c_int64),
+        ("dst_rank", ctypes.c_int64),
+        ("src_meta", ctypes.c_int64),
+        ("dst_shard", ctypes.c_int64),
+        ("piece_tp_index", ctypes.c_int64),
+        ("piece_tp_deg", ctypes.c_int64),
+        ("row0", ctypes.c_int64),
+        ("row1", ctypes.c_int64),
+    ]
+
+
+# Both records are all-int64, so tables are plain [n, k] int64 matrices.
+SR_META_WORDS = ctypes.sizeof(SrMeta) // 8
+SR_OP_WORDS = ctypes.sizeof(SrOp) // 8
+
+
+def as_int64_ptr(arr) -> "ctypes.c_void_p":
+    """Address of a C-contiguous int64 matrix (kept alive by the caller)."""
+    import numpy as np
+    assert arr.dtype == np.int64 and arr.flags["C_CONTIGUOUS"]
+    return ctypes.c_void_p(arr.ctypes.data)
 
 
 class SrPlanOptions(ctypes.Structure):
@@ -189,6 +239,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_gather.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
+    i64 = ctypes.c_int64
+    lib.sr_schedule.restype = ctypes.c_int
+    lib.sr_schedule.argtypes = [vp, i64, i64, vp, i64, i64, i64, vp, i64, ctypes.POINTER(i64)]
 
 
 def lib() -> ctypes.CDLL:

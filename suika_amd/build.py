@@ -1,9 +1,10 @@
 """Build the in-tree HIP library ``suika_amd/lib/libsuika_reshard.so`` for gfx950.
 
-The library is compiled with ``hipcc`` directly (one translation unit, no
-torch extension machinery) so that it stays a plain C-ABI shared object that
-``ctypes`` -- or any other FFI -- can load.  hipcc cross-compiles for gfx950
-without a GPU present.
+The library is compiled with ``hipcc`` directly (no torch extension
+machinery) so that it stays a plain C-ABI shared object that ``ctypes`` -- or
+any other FFI -- can load.  hipcc cross-compiles for gfx950 without a GPU
+present.  Sources: ``reshard.hip`` (plan builder and kernels) and
+``schedule.cpp`` (the host-only transfer scheduler).
 """
 from __future__ import annotations
 
@@ -15,7 +16,7 @@ from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
-SRC = PKG_DIR / "csrc" / "reshard.hip"
+SOURCES = [PKG_DIR / "csrc" / "reshard.hip", PKG_DIR / "csrc" / "schedule.cpp"]
 INCLUDE = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "lib"
 LIB = LIB_DIR / "libsuika_reshard.so"
@@ -50,7 +51,7 @@ def build(verbose: bool = False, out: Path = LIB, defines=()) -> Path:
     out = Path(out)
     out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, *[f"-D{d}" for d in defines], f"-I{INCLUDE}", str(SRC),
+    cmd = [hipcc_path(), *HIPCC_FLAGS, *[f"-D{d}" for d in defines], f"-I{INCLUDE}", *map(str, SOURCES),
            "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -72,6 +72,25 @@
 #include <vector>
 
 #include "suika_reshard.h"
+#include "sr_internal.h"
+
+namespace sr_internal {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+const char* last_error() { return g_last_error.c_str(); }
+
+}  // namespace sr_internal
 
 namespace {
 
@@ -102,17 +121,7 @@ constexpr uint32_t kMaxGrid = 0xffffffffu / kBlock;    // grid work-items stay b
 
 // ---------------------------------------------------------------- errors
 
-thread_local std::string g_last_error;
-
-int fail(int code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return code;
-}
+using sr_internal::fail;
 
 #define SR_HIP_TRY(expr)                                                      \
   do {                                                                        \
@@ -1150,7 +1159,7 @@ extern "C" {
 
 int sr_abi_version(void) { return SR_ABI_VERSION; }
 
-const char* sr_last_error(void) { return g_last_error.c_str(); }
+const char* sr_last_error(void) { return sr_internal::last_error(); }
 
 int sr_selftest(void) {
   // Division constants: exhaustive small divisors, then edge divisors, each

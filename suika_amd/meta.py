@@ -8,7 +8,8 @@ Host-side mirror of the reference's plan types, same names and semantics:
 * ``ParamLayout``           -- Suika/migration.py:161-254
 * ``TransferOp``            -- Suika/migration.py:257-312 (geometry only: the
                                bytes are moved by the HIP pack/unpack kernels)
-* ``schedule_param_transfer`` -- Suika/migration.py:322-381 (same greedy)
+* ``schedule_param_transfer`` -- Suika/migration.py:322-381 (same greedy,
+                               run by the library's ``sr_schedule``)
 
 Two shard kinds extend the reference's ``torch.chunk`` layout; both are
 declared on a tensor through extra attributes next to the reference's
@@ -25,7 +26,9 @@ declared on a tensor through extra attributes next to the reference's
 """
 from __future__ import annotations
 
+import ctypes
 import os
+import re
 from itertools import chain
 from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
@@ -344,25 +347,42 @@ class TransferOp:
              f"{self.src_meta.slice_dim()} and dst {self.dst_meta.slice_dim()}")
 
 
-def _vocab_pieces(dst_meta: TensorMeta, spl: ParamLayout) -> List[TensorMeta]:
-    """Split a vocab_pad destination shard at every source shard boundary."""
-    lo, hi = dst_meta.valid_rows()
-    if lo == hi:
-        # a shard of padding only: one empty piece, zero filled on unpack
-        return [dst_meta.with_rows(lo, lo)]
-    cuts = {lo, hi}
-    for metas in spl.layout.values():
-        src = metas.get(dst_meta.name)
-        if src is None:
-            continue
-        assert src.kind == VOCAB_PAD, f"shard kind mismatch for {dst_meta.name}"
-        assert int(src.shape[0]) == int(dst_meta.shape[0]), \
-            f"vocab size mismatch for {dst_meta.name}: {src.shape[0]} vs {dst_meta.shape[0]}"
-        for b in src.valid_rows():
-            if lo < b < hi:
-                cuts.add(b)
-    edges = sorted(cuts)
-    return [dst_meta.with_rows(a, b) for a, b in zip(edges[:-1], edges[1:]) if b > a]
+_KIND_CODE = {CHUNK: 0, VOCAB_PAD: 1, QKV_HEADS: 2}
+_SHAPE_PAD = [(0,) * (8 - n) for n in range(9)]
+_ARGS_PAD = [(0,) * (3 - n) for n in range(4)]
+_NO_TP = (0, 0, 0)
+_NO_ROWS = (-1, -1)
+
+
+def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta]):
+    """A layout as an [n, 21] int64 sr_meta table, rank by rank in the
+    layout's order; ``objs`` receives the TensorMeta of every row."""
+    import numpy as np
+    out: List[int] = []
+    ext = out.extend
+    keep = objs.append
+    for rank, metas in pl.layout.items():
+        for name, m in metas.items():
+            nid = names.get(name)
+            if nid is None:
+                nid = names[name] = len(names)
+            shape, args = m.shape, m.kind_args
+            nd = len(shape)
+            assert nd <= 8 and len(args) <= 3, f"{name}: {nd}-D shape / {len(args)} kind args"
+            ext((rank, nid, m.dtype.itemsize, nd, *shape, *_SHAPE_PAD[nd], *(m.tp_meta or _NO_TP),
+                 _KIND_CODE[m.kind], *args, *_ARGS_PAD[len(args)], *(m.rows or _NO_ROWS)))
+            keep(m)
+    return np.array(out, dtype=np.int64).reshape(-1, 21)
+
+
+def _derived(shard: TensorMeta, tp_meta: Optional[TPMeta], rows: Optional[Tuple[int, int]]) -> TensorMeta:
+    """A piece of ``shard``: the same tensor with another tp meta or a row
+    interval (what scale_to_tp / with_rows build), without re-validating."""
+    m = TensorMeta.__new__(TensorMeta)
+    m.__dict__.update(shard.__dict__)
+    m.tp_meta = tp_meta
+    m.rows = rows
+    return m
 
 
 def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layout: ParamLayout,
@@ -370,48 +390,62 @@ def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layou
                             minimum_est_peers: Optional[int] = None) -> List[TransferOp]:
     """Greedy piece -> source assignment of Suika/migration.py:322-381.
 
-    Every target tensor is cut into pieces at the largest source TP degree;
-    each piece goes to its own rank when owned there, otherwise to the owner
-    with the smallest accumulated volume, preferring already-connected peers
-    once ``minimum_est_peers`` are connected (1 with InfiniBand, else 2).
+    Every target tensor is cut into pieces at the largest source TP degree
+    (``vocab_pad`` tensors: at the source shard boundaries); each piece goes
+    to its own rank when owned there, otherwise to the owner with the
+    smallest accumulated volume, preferring already-connected peers once
+    ``minimum_est_peers`` are connected (1 with InfiniBand, else 2).  The
+    greedy runs in the library (``sr_schedule``) on the layouts encoded as
+    tables; the TransferOps reference the layouts' own TensorMeta objects.
     """
-    if log_func is None:
-        log_func = lambda msg: None  # noqa: E731
+    import numpy as np
+    from . import _lib
     spl, tpl = source_param_layout, target_param_layout
-    max_tp_degree = max([p.tp_deg() for params in spl.layout.values() for p in params.values()])
-    schedule: List[TransferOp] = []
-    latency_vec = [0.0 for _ in spl.layout.keys()]
     if minimum_est_peers is None:
         minimum_est_peers = 1 if is_ib_enabled() else 2
+    names: Dict[str, int] = {}
+    src_objs: List[TensorMeta] = []
+    dst_objs: List[TensorMeta] = []
+    src = _encode_layout(spl, names, src_objs)
+    dst = _encode_layout(tpl, names, dst_objs)
+    if not src_objs:
+        max([])   # the reference's max_tp_degree over an empty layout: ValueError
+    n_ranks = len(spl.layout)
+    max_tp = max(1, int(src[:, 14].max()))     # column 14: tp_deg
+    cap = len(dst_objs) * max(max_tp, 2 * n_ranks + 1)
+    ops = np.empty((max(cap, 1), _lib.SR_OP_WORDS), dtype=np.int64)
+    n_ops = ctypes.c_int64()
+    L = _lib.lib()
+    rc = L.sr_schedule(_lib.as_int64_ptr(src), len(src_objs), n_ranks, _lib.as_int64_ptr(dst),
+                       len(dst_objs), len(names), int(minimum_est_peers), _lib.as_int64_ptr(ops),
+                       cap, ctypes.byref(n_ops))
+    if rc != _lib.SR_OK:
+        by_id = list(names)
+        msg = re.sub(r"#(\d+)", lambda g: by_id[int(g.group(1))], _lib.last_error(L))
+        raise _lib.PlanError(f"schedule_param_transfer: {msg}")
 
-    def latency(param: TensorMeta) -> float:
-        return param.volumn()
-
-    for dst, dist_params in tpl.layout.items():
-        est_peers = set()
-        for name, orig_dst_param in dist_params.items():
-            if orig_dst_param.kind == VOCAB_PAD and orig_dst_param.is_tp():
-                tp_scaled_params = _vocab_pieces(orig_dst_param, spl)
-            else:
-                tp_scaled_params = orig_dst_param.scale_to_tp(max_tp_degree)
-            for dst_param in tp_scaled_params:
-                srcs = spl.owners(dst_param)
-                assert len(srcs) > 0, \
-                    f"illegal transfer, target param {dst_param} is not present in any source"
-                if dst in srcs:
-                    best_src = dst
-                else:
-                    est_srcs = [s for s in srcs if s in est_peers]
-                    if len(est_srcs) > 0 and len(est_peers) >= minimum_est_peers:
-                        best_src = min(est_srcs, key=lambda s: latency_vec[s] + latency(dst_param))
-                    else:
-                        best_src = min(srcs, key=lambda s: latency_vec[s] + latency(dst_param))
-                if best_src != dst:
-                    log_func(f"schedule_param_transfer: {best_src} > {dst} transfer {name}")
-                src_param = spl.layout[best_src][name]
-                est_peers.add(best_src)
-                schedule.append(TransferOp(param_name=name, src_rank=best_src, dst_rank=dst,
-                                           src_meta=src_param, dst_meta=dst_param,
-                                           dst_shard_meta=orig_dst_param))
-                latency_vec[best_src] += latency(dst_param)
+    schedule: List[TransferOp] = []
+    append = schedule.append
+    by_id = list(names)
+    new_op = TransferOp.__new__
+    for nid, s_rank, d_rank, s_row, d_row, p_idx, p_deg, r0, r1 in ops[:n_ops.value].tolist():
+        shard = dst_objs[d_row]
+        if r0 >= 0:
+            piece = _derived(shard, shard.tp_meta, (r0, r1))
+        elif p_deg:
+            piece = _derived(shard, (shard.tp_meta[0], p_idx, p_deg), None)
+        else:
+            piece = shard
+        op = new_op(TransferOp)
+        op.param_name = by_id[nid]
+        op.src_rank = s_rank
+        op.dst_rank = d_rank
+        op.src_meta = src_objs[s_row]
+        op.dst_meta = piece
+        op.dst_shard_meta = shard
+        append(op)
+    if log_func is not None:
+        for op in schedule:
+            if op.src_rank != op.dst_rank:
+                log_func(f"schedule_param_transfer: {op.src_rank} > {op.dst_rank} transfer {op.param_name}")
     return schedule

@@ -1,10 +1,29 @@
-/* A C11 caller of include/suika_reshard.h: plan creation, buffer layout and
- * error reporting (host-only calls, no GPU needed).  Prints one line per
- * check; the test compares them. */
+/* A C11 caller of include/suika_reshard.h and include/suika_schedule.h:
+ * scheduling, plan creation, buffer layout and error reporting (host-only
+ * calls, no GPU needed).  Prints one line per check; the test compares them. */
 #include <stdio.h>
 #include <string.h>
 
 #include "suika_reshard.h"
+#include "suika_schedule.h"
+
+/* one [4, 16] f32 row-parallel weight: rank `rank` holds column shard idx/deg */
+static sr_meta weight(int64_t rank, int64_t idx, int64_t deg) {
+  sr_meta m;
+  memset(&m, 0, sizeof(m));
+  m.rank = rank;
+  m.name = 0;
+  m.itemsize = 4;
+  m.ndim = 2;
+  m.shape[0] = 4;
+  m.shape[1] = 16;
+  m.slice_dim = -1;
+  m.tp_index = idx;
+  m.tp_deg = deg;
+  m.kind = SR_KIND_CHUNK;
+  m.row0 = m.row1 = -1;
+  return m;
+}
 
 int main(void) {
   /* row-parallel merge: dst [4, 16] f32 = two [4, 8] column halves, two peers */
@@ -37,5 +56,16 @@ int main(void) {
   rc = sr_plan_create(src, 2, dst, 1, 2, pcs, 1, NULL, &bad);
   printf("hole %d %s\n", rc, bad == NULL ? "null" : "set");
   printf("message %s\n", strstr(sr_last_error(), "cover") ? "mentions coverage" : sr_last_error());
+
+  /* the schedule of the same merge: TP2 -> TP1 on rank 0, one piece per source */
+  sr_meta from[2] = {weight(0, 0, 2), weight(1, 1, 2)};
+  sr_meta to[1] = {weight(0, 0, 1)};
+  sr_op ops[4];
+  int64_t n_ops = 0;
+  rc = sr_schedule(from, 2, 2, to, 1, 1, 1, ops, 4, &n_ops);
+  printf("schedule %d ops %lld\n", rc, (long long)n_ops);
+  for (int64_t k = 0; k < n_ops; ++k)
+    printf("op %lld -> %lld piece %lld/%lld\n", (long long)ops[k].src_rank, (long long)ops[k].dst_rank,
+           (long long)ops[k].piece_tp_index, (long long)ops[k].piece_tp_deg);
   return 0;
 }

@@ -1,5 +1,5 @@
-"""The C ABI library: loads, exports what include/suika_reshard.h declares,
-and rejects invalid plans before anything reaches a GPU (host-only calls)."""
+"""The C ABI library: loads, exports what include/*.h declares, and rejects
+invalid plans before anything reaches a GPU (host-only calls)."""
 import ctypes
 import re
 from pathlib import Path
@@ -8,18 +8,20 @@ import pytest
 
 from suika_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "suika_reshard.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def header_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(sr_[a-z_0-9]+)\s*\(", text)))
+    found = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        found |= set(re.findall(r"\b(sr_[a-z_0-9]+)\s*\(", text))
+    return sorted(found)
 
 
 def test_library_loads_and_version():
     L = _lib.lib()
-    assert L.sr_abi_version() == _lib.ABI_VERSION == 2
+    assert L.sr_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_every_declared_symbol_is_exported():
@@ -208,8 +210,8 @@ def test_missing_library_fails_loudly(tmp_path):
 
 
 def test_c_caller(tmp_path):
-    """The header and library serve a plain C11 program (the FFI view a
-    cgo / JNI / N-API binding has), not only ctypes."""
+    """The headers and library serve a plain C11 program (the FFI view a
+    cgo / JNI / N-API binding has), not only ctypes: schedule, plan, layout."""
     import shutil
     import subprocess
     gcc = shutil.which("gcc")
@@ -233,6 +235,9 @@ def test_c_caller(tmp_path):
         "pieces 2 peers 2 pack_bytes_read 256",
         f"hole {_lib.SR_EOVERLAP} null",
         "message mentions coverage",
+        "schedule 0 ops 2",
+        "op 0 -> 0 piece 0/2",
+        "op 1 -> 0 piece 1/2",
     ], out.stdout
 
 
