@@ -1,12 +1,14 @@
 /*
- * suika_schedule.h -- native transfer scheduler of libsuika_reshard.so.
+ * suika_planner.h -- native planner of libsuika_reshard.so: the transfer
+ * schedule and its lowering to the engine's region moves.
  *
  * Host-only C ABI: no device memory, no HIP calls; usable without a GPU.
  * A C caller goes from two parameter layouts to the library's plan without
  * Python objects:
  *
  *   layouts (sr_meta tables) --sr_schedule--> transfer ops (sr_op table)
- *   ops --(lowering to sr_piece)--> sr_plan_create --> sr_gather / sr_pack ...
+ *   one rank's ops --sr_lower--> slots + sr_piece table --sr_plan_create-->
+ *   sr_gather / sr_pack + sr_unpack (include/suika_reshard.h)
  *
  * Reference interfaces replaced (paths relative to the Suika repository):
  *   - Suika/migration.py:29-131   TensorMeta          -> sr_meta (one row)
@@ -15,13 +17,18 @@
  *       is_tensor_tp_overlap are evaluated inside sr_schedule
  *   - Suika/migration.py:257-312  TransferOp          -> sr_op (one row)
  *   - Suika/migration.py:322-381  schedule_param_transfer -> sr_schedule
+ *   - Suika/migration.py:290-312, 531-541  TransferOp.get_send_tensor's
+ *       chunk(n, dim)[k] and execute_param_transfer's cat(pieces, dim) per
+ *       tensor and sub-field, as region moves                  -> sr_lower
  *
  * Status codes and sr_last_error() are those of suika_reshard.h.
  */
-#ifndef SUIKA_SCHEDULE_H
-#define SUIKA_SCHEDULE_H
+#ifndef SUIKA_PLANNER_H
+#define SUIKA_PLANNER_H
 
 #include <stdint.h>
+
+#include "suika_reshard.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -100,8 +107,62 @@ int sr_schedule(const sr_meta* src, int64_t n_src, int64_t n_src_ranks,
                 int64_t n_names, int64_t minimum_est_peers,
                 sr_op* ops, int64_t cap, int64_t* n_ops);
 
+/* The tensor a source slot binds to: the caller's shard of one sub-field. */
+typedef struct sr_src_spec {
+  int64_t dtype;                 /* sr_dtype */
+  int64_t ndim;
+  int64_t shape[SR_MAX_DIMS];
+} sr_src_spec;
+
+/* What a tensor slot of a lowering holds. */
+typedef struct sr_slot_key {
+  int64_t op;                    /* an op of the tensor (the first one that uses it) */
+  int64_t field;                 /* sub-field index in [0, n_fields) */
+  int64_t recast;                /* 1: the bf16 copy rounded from `field` */
+  int64_t dtype;                 /* sr_dtype */
+  int64_t ndim;
+  int64_t shape[SR_MAX_DIMS];    /* source: as given; destination: actual_shape of the shard */
+} sr_slot_key;
+
+/* Tables of one lowering, owned by the library until sr_lowering_destroy. */
+typedef struct sr_lowering {
+  int64_t n_src, n_dst, n_pieces, n_peers, n_empty;
+  const sr_tensor* src;          /* [n_src] source slots, for sr_plan_create */
+  const sr_slot_key* src_key;    /* [n_src] */
+  const sr_tensor* dst;          /* [n_dst] destination slots */
+  const sr_slot_key* dst_key;    /* [n_dst] */
+  const sr_piece* pieces;        /* [n_pieces] */
+  const int64_t* peer_rank;      /* [n_peers] source rank of each peer index, ascending */
+  const sr_slot_key* empty;      /* [n_empty] zero-element destinations: no slot, no piece */
+} sr_lowering;
+
+/*
+ * Lower one destination rank's ops to the engine's tables: for every tensor
+ * (in order of first appearance) and sub-field, a destination slot of the
+ * shard's 2-D view; for every op, source slots and one sr_piece per region x
+ * sub-field -- the intersection of the piece with the source shard and the
+ * destination shard, which for chunk layouts is chunk(n, dim)[k] on the
+ * sending side and cat(pieces, dim) in ascending piece order on the
+ * receiving side (Suika/migration.py:304-310, 536); ZERO pieces for the
+ * padding rows of vocab_pad shards; RECAST pieces where recast[f] = 1 (an
+ * f32 field also written as a bf16 copy, slot right after the field's).
+ * Peers are the source ranks, ascending.
+ *
+ * metas[n_metas] holds every meta the ops name (op.src_meta and
+ * op.dst_shard index it); specs[k * n_fields + f] is the source tensor of op
+ * k, field f, and must have the op's source shard shape (get_send_tensor's
+ * check, migration.py:293-294).  Returns SR_EINVAL with a message naming the
+ * tensor (as "#<name id>") when the ops do not assemble their shards.
+ */
+int sr_lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops,
+             const sr_src_spec* specs, int64_t n_fields, const int64_t* recast,
+             sr_lowering** out);
+
+/* Release the tables of sr_lower.  NULL is ignored. */
+void sr_lowering_destroy(sr_lowering* lowering);
+
 #ifdef __cplusplus
 }
 #endif
 
-#endif /* SUIKA_SCHEDULE_H */
+#endif /* SUIKA_PLANNER_H */

@@ -1,5 +1,5 @@
 """ctypes binding of ``libsuika_reshard.so`` (C ABI in include/suika_reshard.h
-and include/suika_schedule.h).
+and include/suika_planner.h).
 
 The binding fails loudly: importing the package never falls back to a CPU or
 torch path.  If the library is missing, every entry point raises
@@ -62,6 +62,8 @@ EXPORTED_SYMBOLS = (
     "sr_gather",
     "sr_plan_destroy",
     "sr_schedule",
+    "sr_lower",
+    "sr_lowering_destroy",
 )
 
 ABI_VERSION = 3
@@ -156,9 +158,61 @@ class SrOp(ctypes.Structure):
     ]
 
 
-# Both records are all-int64, so tables are plain [n, k] int64 matrices.
+class SrSrcSpec(ctypes.Structure):
+    """The tensor a source slot binds to (sr_src_spec)."""
+    _fields_ = [
+        ("dtype", ctypes.c_int64),
+        ("ndim", ctypes.c_int64),
+        ("shape", ctypes.c_int64 * SR_MAX_DIMS),
+    ]
+
+
+class SrSlotKey(ctypes.Structure):
+    """What a tensor slot of a lowering holds (sr_slot_key)."""
+    _fields_ = [
+        ("op", ctypes.c_int64),
+        ("field", ctypes.c_int64),
+        ("recast", ctypes.c_int64),
+        ("dtype", ctypes.c_int64),
+        ("ndim", ctypes.c_int64),
+        ("shape", ctypes.c_int64 * SR_MAX_DIMS),
+    ]
+
+
+class SrLowering(ctypes.Structure):
+    """Tables of one sr_lower call (owned by the library)."""
+    _fields_ = [
+        ("n_src", ctypes.c_int64),
+        ("n_dst", ctypes.c_int64),
+        ("n_pieces", ctypes.c_int64),
+        ("n_peers", ctypes.c_int64),
+        ("n_empty", ctypes.c_int64),
+        ("src", ctypes.POINTER(SrTensor)),
+        ("src_key", ctypes.POINTER(SrSlotKey)),
+        ("dst", ctypes.POINTER(SrTensor)),
+        ("dst_key", ctypes.POINTER(SrSlotKey)),
+        ("pieces", ctypes.POINTER(SrPiece)),
+        ("peer_rank", ctypes.POINTER(ctypes.c_int64)),
+        ("empty", ctypes.POINTER(SrSlotKey)),
+    ]
+
+
+# These records are all-int64, so tables are plain [n, k] int64 matrices.
 SR_META_WORDS = ctypes.sizeof(SrMeta) // 8
 SR_OP_WORDS = ctypes.sizeof(SrOp) // 8
+SR_SPEC_WORDS = ctypes.sizeof(SrSrcSpec) // 8
+SR_KEY_WORDS = ctypes.sizeof(SrSlotKey) // 8
+
+
+def copy_table(ptr, n: int, dtype) -> "np.ndarray":
+    """A numpy copy of ``n`` records of ``dtype`` at a ctypes pointer."""
+    import numpy as np
+    dtype = np.dtype(dtype)
+    if n == 0:
+        return np.zeros(0, dtype=dtype)
+    addr = ctypes.cast(ptr, ctypes.c_void_p).value
+    raw = (ctypes.c_char * (n * dtype.itemsize)).from_address(addr)
+    return np.frombuffer(raw, dtype=dtype).copy()
 
 
 def as_int64_ptr(arr) -> "ctypes.c_void_p":
@@ -242,6 +296,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     i64 = ctypes.c_int64
     lib.sr_schedule.restype = ctypes.c_int
     lib.sr_schedule.argtypes = [vp, i64, i64, vp, i64, i64, i64, vp, i64, ctypes.POINTER(i64)]
+    lib.sr_lower.restype = ctypes.c_int
+    lib.sr_lower.argtypes = [vp, i64, vp, i64, vp, i64, vp, ctypes.POINTER(ctypes.POINTER(SrLowering))]
+    lib.sr_lowering_destroy.restype = None
+    lib.sr_lowering_destroy.argtypes = [ctypes.POINTER(SrLowering)]
 
 
 def lib() -> ctypes.CDLL:

@@ -3,8 +3,9 @@
 The library is compiled with ``hipcc`` directly (no torch extension
 machinery) so that it stays a plain C-ABI shared object that ``ctypes`` -- or
 any other FFI -- can load.  hipcc cross-compiles for gfx950 without a GPU
-present.  Sources: ``reshard.hip`` (plan builder and kernels) and
-``schedule.cpp`` (the host-only transfer scheduler).
+present.  Sources: ``reshard.hip`` (plan builder and kernels),
+``schedule.cpp`` and ``lower.cpp`` (the host-only planner: transfer schedule
+and its lowering to region moves).
 """
 from __future__ import annotations
 
@@ -16,7 +17,8 @@ from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
-SOURCES = [PKG_DIR / "csrc" / "reshard.hip", PKG_DIR / "csrc" / "schedule.cpp"]
+SOURCES = [PKG_DIR / "csrc" / "reshard.hip", PKG_DIR / "csrc" / "schedule.cpp",
+           PKG_DIR / "csrc" / "lower.cpp"]
 INCLUDE = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "lib"
 LIB = LIB_DIR / "libsuika_reshard.so"

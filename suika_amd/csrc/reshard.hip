@@ -67,6 +67,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -711,6 +712,8 @@ struct Phase {
   // the tables, one pinned host buffer for their uploads
   bool ready = false;
   void* d_mem = nullptr;
+  size_t d_cap = 0;                     // bytes of d_mem / h_staging as allocated
+  size_t h_cap = 0;
   DevRel* d_rel = nullptr;
   DevItem* d_items = nullptr;
   DevTile* d_tiles = nullptr;
@@ -746,6 +749,8 @@ struct sr_plan {
   bool offsets_ready = false;
   void* d_offmem = nullptr;             // carved: offsets, payloads, peer lists
   unsigned char* h_offmem = nullptr;    // pinned upload of payloads and peer lists
+  size_t d_offcap = 0;
+  size_t h_offcap = 0;
   uint64_t* d_offset = nullptr;
   uint32_t* d_peer_begin = nullptr;
   uint32_t* d_peer_list = nullptr;
@@ -920,6 +925,111 @@ std::vector<uint32_t> item_order(const Phase& ph, bool by_src) {
   return order;
 }
 
+// ---------------------------------------------------------------- table memory
+//
+// One drop-in call builds and destroys several short-lived plans.  Their
+// table memory (a device block and a pinned block per phase, one of each for
+// the buffer offsets) and their events are kept for reuse instead of being
+// freed: each allocation or free costs tens of microseconds on the host and
+// hipFree synchronizes the device, and the last launch group of a call waits
+// for them.  Blocks come in power-of-two sizes (at least 64 KiB) so plans of
+// different sizes share them; at most kCacheDeviceBytes / kCacheHostBytes
+// stay cached per process and the rest is freed as before.  A block goes back
+// only after the events of the launches that used it have completed.
+constexpr size_t kCacheDeviceBytes = size_t(256) << 20;
+constexpr size_t kCacheHostBytes = size_t(64) << 20;
+constexpr size_t kCacheEvents = 256;
+
+size_t block_class(size_t bytes) {
+  size_t c = size_t(64) << 10;
+  while (c < bytes) c <<= 1;
+  return c;
+}
+
+class TableCache {
+ public:
+  int get(bool pinned, int device, size_t bytes, void** out, size_t* cap) {
+    const size_t want = block_class(bytes);
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      std::vector<Block>& list = pinned ? host_ : dev_;
+      for (size_t i = 0; i < list.size(); ++i)
+        if (list[i].device == device && list[i].bytes == want) {
+          *out = list[i].p;
+          *cap = want;
+          (pinned ? host_bytes_ : dev_bytes_) -= want;
+          list[i] = list.back();
+          list.pop_back();
+          return SR_OK;
+        }
+    }
+    if (pinned) SR_HIP_TRY(hipHostMalloc(out, want, hipHostMallocDefault));
+    else SR_HIP_TRY(hipMalloc(out, want));
+    *cap = want;
+    return SR_OK;
+  }
+
+  void put(bool pinned, int device, void* p, size_t cap) {
+    if (!p) return;
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      size_t& held = pinned ? host_bytes_ : dev_bytes_;
+      if (held + cap <= (pinned ? kCacheHostBytes : kCacheDeviceBytes)) {
+        (pinned ? host_ : dev_).push_back(Block{p, cap, device});
+        held += cap;
+        return;
+      }
+    }
+    if (pinned) (void)hipHostFree(p);
+    else (void)hipFree(p);
+  }
+
+  // Events are created on the current device, which must be `device`.
+  int get_event(int device, hipEvent_t* ev) {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      for (size_t i = events_.size(); i-- > 0;)
+        if (events_[i].first == device) {
+          *ev = events_[i].second;
+          events_.erase(events_.begin() + i);
+          return SR_OK;
+        }
+    }
+    SR_HIP_TRY(hipEventCreateWithFlags(ev, hipEventDisableTiming));
+    return SR_OK;
+  }
+
+  void put_event(int device, hipEvent_t ev) {
+    if (!ev) return;
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      if (events_.size() < kCacheEvents) {
+        events_.emplace_back(device, ev);
+        return;
+      }
+    }
+    (void)hipEventDestroy(ev);
+  }
+
+ private:
+  struct Block {
+    void* p;
+    size_t bytes;
+    int device;
+  };
+  std::mutex mu_;
+  std::vector<Block> dev_, host_;
+  std::vector<std::pair<int, hipEvent_t>> events_;
+  size_t dev_bytes_ = 0, host_bytes_ = 0;
+};
+
+// Never destroyed: cached blocks live until the process exits, so no HIP call
+// runs from a static destructor after the runtime may have shut down.
+TableCache& table_cache() {
+  static TableCache* cache = new TableCache();
+  return *cache;
+}
+
 int ensure_device(sr_plan* p) {
   int dev = -1;
   SR_HIP_TRY(hipGetDevice(&dev));
@@ -945,7 +1055,8 @@ size_t carve(size_t& end, size_t bytes) {
 // never waits for earlier work on the stream.
 int setup_offsets(sr_plan* p, hipStream_t stream) {
   if (p->offsets_ready) return SR_OK;
-  if (!p->ev_offsets) SR_HIP_TRY(hipEventCreateWithFlags(&p->ev_offsets, hipEventDisableTiming));
+  int rc;
+  if (!p->ev_offsets && (rc = table_cache().get_event(p->device, &p->ev_offsets)) != SR_OK) return rc;
   if (p->n_peers > 0 && !p->peer_list.empty()) {
     const size_t np = p->pieces.size();
     size_t in_end = 0;   // layout of the uploaded part: payloads, peer_begin, peer_list
@@ -955,9 +1066,12 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
     size_t dev_end = in_end;
     const size_t o_off = carve(dev_end, np * sizeof(uint64_t));
     // allocations survive a failed attempt and are reused by the retry
-    if (!p->d_offmem) SR_HIP_TRY(hipMalloc(&p->d_offmem, dev_end));
-    if (!p->h_offmem)
-      SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&p->h_offmem), in_end, hipHostMallocDefault));
+    if (!p->d_offmem && (rc = table_cache().get(false, p->device, dev_end, &p->d_offmem, &p->d_offcap)) != SR_OK)
+      return rc;
+    if (!p->h_offmem &&
+        (rc = table_cache().get(true, p->device, in_end, reinterpret_cast<void**>(&p->h_offmem),
+                                &p->h_offcap)) != SR_OK)
+      return rc;
     unsigned char* d = static_cast<unsigned char*>(p->d_offmem);
     p->d_payload = reinterpret_cast<uint64_t*>(d + o_pay);
     p->d_peer_begin = reinterpret_cast<uint32_t*>(d + o_beg);
@@ -980,9 +1094,10 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
 // the device, stream-ordered on `stream` (ev_setup marks completion).
 int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
   if (ph.ready) return SR_OK;
-  if (!ph.ev_setup) SR_HIP_TRY(hipEventCreateWithFlags(&ph.ev_setup, hipEventDisableTiming));
-  if (!ph.ev_staging) SR_HIP_TRY(hipEventCreateWithFlags(&ph.ev_staging, hipEventDisableTiming));
-  if (!ph.ev_kernel) SR_HIP_TRY(hipEventCreateWithFlags(&ph.ev_kernel, hipEventDisableTiming));
+  TableCache& cache = table_cache();
+  int rc;
+  for (hipEvent_t* ev : {&ph.ev_setup, &ph.ev_staging, &ph.ev_kernel})
+    if (!*ev && (rc = cache.get_event(p->device, ev)) != SR_OK) return rc;
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
@@ -993,10 +1108,12 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
     const size_t o_base = carve(end, (size_t(n) + 1) * sizeof(uint64_t));
     const size_t o_tiles = carve(end, ph.n_tiles * sizeof(DevTile));
     // allocations survive a failed attempt and are reused by the retry
-    if (!ph.d_mem) SR_HIP_TRY(hipMalloc(&ph.d_mem, end));
-    if (!ph.h_staging)   // descriptors + pointer table, the same layout as the device start
-      SR_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&ph.h_staging), o_ptr + nptr * sizeof(uint64_t),
-                               hipHostMallocDefault));
+    if (!ph.d_mem && (rc = cache.get(false, p->device, end, &ph.d_mem, &ph.d_cap)) != SR_OK) return rc;
+    // pinned: descriptors + pointer table, the same layout as the device start
+    if (!ph.h_staging &&
+        (rc = cache.get(true, p->device, o_ptr + nptr * sizeof(uint64_t),
+                        reinterpret_cast<void**>(&ph.h_staging), &ph.h_cap)) != SR_OK)
+      return rc;
     unsigned char* d = static_cast<unsigned char*>(ph.d_mem);
     ph.d_rel = reinterpret_cast<DevRel*>(d + o_rel);
     ph.d_ptrs = reinterpret_cast<uint64_t*>(d + o_ptr);
@@ -1009,7 +1126,7 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
     SR_HIP_TRY(hipMemcpyAsync(ph.d_rel, ph.h_staging + o_rel, n * sizeof(DevRel), hipMemcpyHostToDevice,
                               stream));
     if (needs_offsets) {
-      int rc = setup_offsets(p, stream);
+      rc = setup_offsets(p, stream);
       if (rc != SR_OK) return rc;
       SR_HIP_TRY(hipStreamWaitEvent(stream, p->ev_offsets, 0));
     }
@@ -1115,18 +1232,16 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   return SR_OK;
 }
 
-// Frees a phase's device tables.  Waits first for the last launches that
-// read them (bind, copy kernel, setup), so a plan can be destroyed right
-// after an asynchronous call.
-void free_phase(Phase& ph) {
-  if (ph.ev_kernel) (void)hipEventSynchronize(ph.ev_kernel);
-  if (ph.ev_staging) (void)hipEventSynchronize(ph.ev_staging);
-  if (ph.ev_setup) (void)hipEventSynchronize(ph.ev_setup);
-  if (ph.d_mem) (void)hipFree(ph.d_mem);
-  if (ph.h_staging) (void)hipHostFree(ph.h_staging);
-  if (ph.ev_setup) (void)hipEventDestroy(ph.ev_setup);
-  if (ph.ev_staging) (void)hipEventDestroy(ph.ev_staging);
-  if (ph.ev_kernel) (void)hipEventDestroy(ph.ev_kernel);
+// Releases a phase's device tables (to the table cache).  Waits first for
+// the last launches that read them (bind, copy kernel, setup), so a plan can
+// be destroyed right after an asynchronous call.
+void free_phase(Phase& ph, int device) {
+  TableCache& cache = table_cache();
+  for (hipEvent_t ev : {ph.ev_kernel, ph.ev_staging, ph.ev_setup})
+    if (ev) (void)hipEventSynchronize(ev);
+  cache.put(false, device, ph.d_mem, ph.d_cap);
+  cache.put(true, device, ph.h_staging, ph.h_cap);
+  for (hipEvent_t ev : {ph.ev_setup, ph.ev_staging, ph.ev_kernel}) cache.put_event(device, ev);
   ph = Phase();
 }
 
@@ -1570,13 +1685,14 @@ int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
 
 void sr_plan_destroy(sr_plan* plan) {
   if (!plan) return;
-  free_phase(plan->pack);
-  free_phase(plan->unpack);
-  free_phase(plan->gather);
+  free_phase(plan->pack, plan->device);
+  free_phase(plan->unpack, plan->device);
+  free_phase(plan->gather, plan->device);
+  TableCache& cache = table_cache();
   if (plan->ev_offsets) (void)hipEventSynchronize(plan->ev_offsets);
-  if (plan->d_offmem) (void)hipFree(plan->d_offmem);
-  if (plan->h_offmem) (void)hipHostFree(plan->h_offmem);
-  if (plan->ev_offsets) (void)hipEventDestroy(plan->ev_offsets);
+  cache.put(false, plan->device, plan->d_offmem, plan->d_offcap);
+  cache.put(true, plan->device, plan->h_offmem, plan->h_offcap);
+  cache.put_event(plan->device, plan->ev_offsets);
   delete plan;
 }
 

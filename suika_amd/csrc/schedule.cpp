@@ -1,4 +1,4 @@
-// schedule.cpp -- native transfer scheduler (include/suika_schedule.h).
+// schedule.cpp -- native transfer scheduler (sr_schedule, include/suika_planner.h).
 //
 // Restates, over flat sr_meta tables, the greedy planner of Suika's state
 // migration (paths relative to the Suika repository):
@@ -22,91 +22,18 @@
 #include <vector>
 
 #include "sr_internal.h"
+#include "sr_meta.h"
+#include "suika_planner.h"
 #include "suika_reshard.h"
-#include "suika_schedule.h"
 
 namespace {
 
-using sr_internal::fail;
-
-// A TensorMeta as the schedule sees it: a table row, or a piece derived from
-// one (another tp meta from scale_to_tp, or a row interval for vocab_pad).
-struct View {
-  const sr_meta* m;
-  int64_t tp_index;
-  int64_t tp_deg;    // 0: not tensor-parallel
-  int64_t row0;      // -1: no row interval
-  int64_t row1;
-  bool whole;        // the table row itself (scale_to_tp returned [self])
-};
-
-View of(const sr_meta& m) { return View{&m, m.tp_index, m.tp_deg, m.row0, m.row1, true}; }
-
-int64_t deg_of(const View& v) { return v.tp_deg > 0 ? v.tp_deg : 1; }
-
-bool mul(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out); }
-
-// Padded vocabulary rows at degree `deg`: a multiple of pad_multiple * deg.
-bool padded_rows(const View& v, int64_t* out) {
-  int64_t step;
-  if (!mul(v.m->kind_args[0], deg_of(v), &step) || step <= 0) return false;
-  const int64_t V = v.m->shape[0];
-  return mul((V + step - 1) / step, step, out);
-}
-
-// Global rows of a vocab_pad shard that hold data (TensorMeta.valid_rows).
-bool valid_rows(const View& v, int64_t* lo, int64_t* hi) {
-  if (v.row0 >= 0) {
-    *lo = v.row0;
-    *hi = v.row1;
-    return true;
-  }
-  int64_t padded;
-  if (!padded_rows(v, &padded)) return false;
-  const int64_t n = padded / deg_of(v);
-  int64_t end;
-  if (!mul(v.tp_index, n, lo) || __builtin_add_overflow(*lo, n, &end)) return false;
-  *hi = std::max(*lo, std::min(end, v.m->shape[0]));
-  return true;
-}
-
-// numel() of TensorMeta (migration.py:62-67 and the extensions): chunk
-// shards count prod(shape) / tp_deg, everything else its actual shape.
-bool numel(const View& v, int64_t* out) {
-  const sr_meta& m = *v.m;
-  int64_t dims[SR_MAX_DIMS];
-  for (int64_t d = 0; d < m.ndim; ++d) dims[d] = m.shape[d];
-  const bool plain_chunk = m.kind == SR_KIND_CHUNK && v.row0 < 0;
-  if (!plain_chunk) {
-    if (v.row0 >= 0) {
-      dims[0] = v.row1 - v.row0;
-    } else if (v.tp_deg > 0) {
-      if (m.kind == SR_KIND_VOCAB_PAD) {
-        int64_t padded;
-        if (!padded_rows(v, &padded)) return false;
-        dims[0] = padded / v.tp_deg;
-      } else {
-        const int64_t d = m.slice_dim < 0 ? m.slice_dim + m.ndim : m.slice_dim;
-        dims[d] /= v.tp_deg;
-      }
-    }
-  }
-  int64_t n = 1;
-  for (int64_t d = 0; d < m.ndim; ++d)
-    if (!mul(n, dims[d], &n)) return false;
-  *out = plain_chunk ? n / deg_of(v) : n;
-  return true;
-}
-
-bool volume(const View& v, int64_t* out) {
-  int64_t n;
-  return numel(v, &n) && mul(n, v.m->itemsize, out);
-}
+using namespace sr_internal;
 
 // is_tensor_tp_owned (migration.py:246-254): may `src` (a layout row) send
 // the piece `tgt`?  Returns 1 / 0, or a negative status.
 int owned(const sr_meta& src_row, const View& tgt) {
-  const View src = of(src_row);
+  const View src = view_of(src_row);
   if (tgt.m->kind == SR_KIND_VOCAB_PAD) {
     if (src_row.kind != SR_KIND_VOCAB_PAD)
       return fail(SR_EINVAL, "shard kind mismatch for #%lld", (long long)tgt.m->name);
@@ -128,35 +55,6 @@ int owned(const sr_meta& src_row, const View& tgt) {
     std::swap(d1, d2);
   }
   return i2 / (d2 / d1) == i1;
-}
-
-int check_meta(const sr_meta& m, int64_t n_names, const char* table, int64_t i) {
-  if (m.name < 0 || m.name >= n_names)
-    return fail(SR_EINVAL, "%s[%lld]: name id %lld outside [0, %lld)", table, (long long)i,
-                (long long)m.name, (long long)n_names);
-  if (m.ndim < 0 || m.ndim > SR_MAX_DIMS)
-    return fail(SR_EINVAL, "#%lld: ndim %lld outside [0, %d]", (long long)m.name, (long long)m.ndim,
-                SR_MAX_DIMS);
-  if (m.itemsize < 1)
-    return fail(SR_EINVAL, "#%lld: itemsize %lld", (long long)m.name, (long long)m.itemsize);
-  for (int64_t d = 0; d < m.ndim; ++d)
-    if (m.shape[d] < 0) return fail(SR_EINVAL, "#%lld: negative dim", (long long)m.name);
-  if (m.kind < SR_KIND_CHUNK || m.kind > SR_KIND_QKV_HEADS)
-    return fail(SR_EINVAL, "#%lld: unknown shard kind %lld", (long long)m.name, (long long)m.kind);
-  if (m.tp_deg < 0 || (m.tp_deg > 0 && m.tp_index < 0))
-    return fail(SR_EINVAL, "#%lld: tp meta (%lld, %lld, %lld)", (long long)m.name,
-                (long long)m.slice_dim, (long long)m.tp_index, (long long)m.tp_deg);
-  if (m.tp_deg > 0 && (m.ndim == 0 || m.slice_dim < -m.ndim || m.slice_dim >= m.ndim))
-    return fail(SR_EINVAL, "#%lld: slice_dim %lld of a %lld-D tensor", (long long)m.name,
-                (long long)m.slice_dim, (long long)m.ndim);
-  if (m.kind == SR_KIND_VOCAB_PAD &&
-      (m.tp_deg == 0 || (m.slice_dim != 0 && m.slice_dim != -m.ndim) || m.kind_args[0] < 1))
-    return fail(SR_EINVAL, "#%lld: vocab_pad is a TP layout sharded along dim 0 with a "
-                "positive pad multiple", (long long)m.name);
-  if ((m.row0 < 0) != (m.row1 < 0) || (m.row0 >= 0 && m.row1 < m.row0))
-    return fail(SR_EINVAL, "#%lld: row interval [%lld, %lld)", (long long)m.name, (long long)m.row0,
-                (long long)m.row1);
-  return SR_OK;
 }
 
 // Contiguous blocks of equal `rank`; a rank may not come back later, and a
@@ -216,7 +114,7 @@ int schedule(const sr_meta* src, int64_t n_src, int64_t R, const sr_meta* dst, i
     for (int64_t i = 0; i < n_src; ++i) name_rows[fill[src[i].name]++] = i;
   }
   int64_t max_tp = 1;
-  for (int64_t i = 0; i < n_src; ++i) max_tp = std::max(max_tp, deg_of(of(src[i])));
+  for (int64_t i = 0; i < n_src; ++i) max_tp = std::max(max_tp, deg_of(view_of(src[i])));
 
   std::vector<double> lat(R, 0.0);
   std::vector<char> est(R, 0);
@@ -229,7 +127,7 @@ int schedule(const sr_meta* src, int64_t n_src, int64_t R, const sr_meta* dst, i
     const int64_t dst_rank = dst[dblk[b]].rank;
     for (int64_t j = dblk[b]; j < dblk[b + 1]; ++j) {
       const sr_meta& dm = dst[j];
-      const View shard = of(dm);
+      const View shard = view_of(dm);
       const int64_t* rows_of = name_rows.data() + name_begin[dm.name];
       const int64_t n_rows = name_begin[dm.name + 1] - name_begin[dm.name];
       pieces.clear();
@@ -250,7 +148,7 @@ int schedule(const sr_meta* src, int64_t n_src, int64_t R, const sr_meta* dst, i
               return fail(SR_EINVAL, "vocab size mismatch for #%lld: %lld vs %lld",
                           (long long)dm.name, (long long)s.shape[0], (long long)dm.shape[0]);
             int64_t slo, shi;
-            if (!valid_rows(of(s), &slo, &shi))
+            if (!valid_rows(view_of(s), &slo, &shi))
               return fail(SR_EINVAL, "#%lld: vocabulary rows overflow", (long long)dm.name);
             for (int64_t e : {slo, shi})
               if (lo < e && e < hi) cuts.push_back(e);

@@ -1,4 +1,8 @@
-"""Shard geometry: which global elements a shard holds and where.
+"""Shard geometry on the host: which global elements a shard holds and where.
+
+Used to cut synthetic shards from global tensors (benchmark and smoke
+inputs) and to infer a destination shard from its pieces.  The plan's region
+moves are computed in the library (``sr_lower``) from the same definitions.
 
 Every tensor is viewed as a row-major 2-D matrix ``[R, C]``:
   * split along dim 0 (column-parallel weight/bias, embeddings, 1-D tensors):
@@ -9,12 +13,6 @@ A shard is a list of bands ``Seg``: a rectangle of the global matrix and the
 position of the same rectangle in the shard's local matrix.  Padding rows of a
 ``vocab_pad`` shard are listed separately (they hold zeros and have no global
 counterpart).
-
-``lower_op`` turns one ``TransferOp`` into region moves by intersecting the
-bands of the piece, of the source shard and of the destination shard.  For the
-reference's ``chunk`` layout this reproduces ``chunk(n, dim)[k]`` on the
-sending side (Suika/migration.py:304-310) and ``cat(pieces, dim=slice_dim)`` in
-ascending piece order on the receiving side (Suika/migration.py:536).
 """
 from __future__ import annotations
 
@@ -32,17 +30,6 @@ class Seg:
     l_col: int
     rows: int
     cols: int
-
-
-@dataclass(frozen=True)
-class Region:
-    """A move of ``rows x cols`` elements between local matrices."""
-    rows: int
-    cols: int
-    src_row: int
-    src_col: int
-    dst_row: int
-    dst_col: int
 
 
 @dataclass(frozen=True)
@@ -140,59 +127,6 @@ def segments(meta: TensorMeta, view: Optional[int] = None) -> Tuple[List[Seg], L
         return [Seg(idx * n, 0, 0, 0, n, C)], []
     n = _split(C, deg, f"{meta.name} cols")
     return [Seg(0, idx * n, 0, 0, R, n)], []
-
-
-def _intersect(a: Seg, b: Seg) -> Optional[Tuple[int, int, int, int]]:
-    r0 = max(a.g_row, b.g_row)
-    r1 = min(a.g_row + a.rows, b.g_row + b.rows)
-    c0 = max(a.g_col, b.g_col)
-    c1 = min(a.g_col + a.cols, b.g_col + b.cols)
-    if r1 <= r0 or c1 <= c0:
-        return None
-    return r0, r1, c0, c1
-
-
-def lower_op(op: TransferOp, dst_shard: TensorMeta) -> List[Region]:
-    """Region moves of one TransferOp, source local -> destination local."""
-    assert op.src_meta.kind == dst_shard.kind, \
-        f"{op.param_name}: shard kind {op.src_meta.kind} -> {dst_shard.kind}"
-    assert tuple(op.src_meta.shape) == tuple(dst_shard.shape), \
-        f"{op.param_name}: global shape {tuple(op.src_meta.shape)} -> {tuple(dst_shard.shape)}"
-    if op.src_meta.is_tp() and dst_shard.is_tp():
-        assert split_axis(op.src_meta) == split_axis(dst_shard), \
-            f"slice dim mismatch btw src {op.src_meta.slice_dim()} and dst {dst_shard.slice_dim()}"
-    view = view_axis(op.src_meta, dst_shard)
-    piece_segs, _ = segments(op.dst_meta, view)
-    src_segs, _ = segments(op.src_meta, view)
-    dst_segs, _ = segments(dst_shard, view)
-    regions: List[Region] = []
-    want = 0
-    got = 0
-    for pb in piece_segs:
-        want += pb.rows * pb.cols
-        for s in src_segs:
-            i = _intersect(pb, s)
-            if i is None:
-                continue
-            r0, r1, c0, c1 = i
-            part = Seg(r0, c0, 0, 0, r1 - r0, c1 - c0)
-            for d in dst_segs:
-                j = _intersect(part, d)
-                if j is None:
-                    continue
-                jr0, jr1, jc0, jc1 = j
-                regions.append(Region(
-                    rows=jr1 - jr0, cols=jc1 - jc0,
-                    src_row=s.l_row + jr0 - s.g_row, src_col=s.l_col + jc0 - s.g_col,
-                    dst_row=d.l_row + jr0 - d.g_row, dst_col=d.l_col + jc0 - d.g_col))
-                got += (jr1 - jr0) * (jc1 - jc0)
-    assert got == want, (f"{op.param_name}: source rank {op.src_rank} holds {got} of the "
-                         f"{want} elements of piece {op.dst_meta}")
-    return regions
-
-
-def pad_boxes(dst_shard: TensorMeta, view: Optional[int] = None) -> List[Box]:
-    return segments(dst_shard, view)[1]
 
 
 def infer_dst_shard(ops: List[TransferOp]) -> TensorMeta:

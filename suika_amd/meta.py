@@ -354,6 +354,15 @@ _NO_TP = (0, 0, 0)
 _NO_ROWS = (-1, -1)
 
 
+def meta_words(m: TensorMeta, rank: int, name_id: int) -> tuple:
+    """One sr_meta row (21 int64) of ``m``."""
+    shape, args = m.shape, m.kind_args
+    nd = len(shape)
+    assert nd <= 8 and len(args) <= 3, f"{m.name}: {nd}-D shape / {len(args)} kind args"
+    return (rank, name_id, m.dtype.itemsize, nd, *shape, *_SHAPE_PAD[nd], *(m.tp_meta or _NO_TP),
+            _KIND_CODE[m.kind], *args, *_ARGS_PAD[len(args)], *(m.rows or _NO_ROWS))
+
+
 def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta]):
     """A layout as an [n, 21] int64 sr_meta table, rank by rank in the
     layout's order; ``objs`` receives the TensorMeta of every row."""
@@ -366,11 +375,7 @@ def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta
             nid = names.get(name)
             if nid is None:
                 nid = names[name] = len(names)
-            shape, args = m.shape, m.kind_args
-            nd = len(shape)
-            assert nd <= 8 and len(args) <= 3, f"{name}: {nd}-D shape / {len(args)} kind args"
-            ext((rank, nid, m.dtype.itemsize, nd, *shape, *_SHAPE_PAD[nd], *(m.tp_meta or _NO_TP),
-                 _KIND_CODE[m.kind], *args, *_ARGS_PAD[len(args)], *(m.rows or _NO_ROWS)))
+            ext(meta_words(m, rank, nid))
             keep(m)
     return np.array(out, dtype=np.int64).reshape(-1, 21)
 

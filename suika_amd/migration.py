@@ -86,7 +86,7 @@ def execute_param_transfer(
     stream: Optional[torch.cuda.Stream] = None,
     route: str = "direct",
     arena: bool = False,
-    pipeline: int = 6,
+    pipeline: int = 8,
 ) -> StateDict:
     """Execute a transfer schedule for this rank; returns its target state.
 
@@ -136,17 +136,33 @@ def execute_param_transfer(
             f"[{rank}]: piece from rank {r} needs a cross-GPU exchange, which this one-GPU build "
             "does not implement; pass the peer shards as fake_source_state_dicts")
 
-    def source_specs(group: List[TransferOp]) -> Dict[Tuple[int, str, str], SlotSpec]:
+    dev_index = device.index
+
+    def source_specs(group: List[TransferOp]) -> Tuple[Dict[Tuple[int, str, str], SlotSpec],
+                                                       Dict[Tuple[int, str, str], int]]:
+        """Shape/dtype and device address of every source tensor the group
+        reads, each checked once (a CUDA tensor on ``device``, contiguous)."""
         specs: Dict[Tuple[int, str, str], SlotSpec] = {}
+        ptrs: Dict[Tuple[int, str, str], int] = {}
         for op in group:
             sd = source(op.src_rank)
-            assert op.param_name in sd, f"[{rank}]: param missing in source {op.param_name}"
-            entry = sd[op.param_name]
+            name = op.param_name
+            assert name in sd, f"[{rank}]: param missing in source {name}"
+            entry = sd[name]
             for f in normal:
-                assert f in entry, f"expected_sub_fields mismatch: {op.param_name} has no {f}"
+                key = (op.src_rank, name, f)
+                if key in specs:
+                    continue
+                assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
                 t = entry[f]
-                specs[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(t.shape), t.dtype)
-        return specs
+                assert isinstance(t, Tensor), f"source {name}/{f} of rank {op.src_rank}: not a tensor"
+                if not t.is_cuda or t.get_device() != dev_index:
+                    raise AssertionError(f"source {name}/{f} of rank {op.src_rank} is on {t.device}, "
+                                         f"not on {device}")
+                assert t.is_contiguous(), f"source {name}/{f} of rank {op.src_rank} is not contiguous"
+                specs[key] = SlotSpec(tuple(t.shape), t.dtype)
+                ptrs[key] = t.data_ptr()
+        return specs, ptrs
 
     # bytes per element over the moved fields, from the first op's sources
     # (only used to balance the launch groups)
@@ -171,38 +187,54 @@ def execute_param_transfer(
             # previous group's launch.
             for group in groups:
                 prof.start("execute schedule lowering")
-                plan = ReshardPlan(group, source_specs(group), normal, recast=recast,
-                                   options=plan_options)
+                specs, src_ptr = source_specs(group)
+                plan = ReshardPlan(group, specs, normal, recast=recast, options=plan_options)
                 prof.stop("execute schedule lowering")
                 plans.append(plan)
-                sources = {r: source(r) for r in plan.peers}
-                for r, sd in sources.items():
-                    for (sr, name, f) in plan.src_keys:
-                        t = sd[name][f] if sr == r else None
-                        if t is not None and t.device != device:
-                            raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, "
-                                                 f"not on {device}")
-                used_sources.update(sources)
+                used_sources.update((r, source(r)) for r in plan.peers)
+                src_ptrs = [src_ptr[key] for key in plan.src_keys]
                 if arena_views is None:
+                    # fresh tensors of the planned shapes: their addresses need no check
                     part = plan.alloc_dst(device)
+                    dst_ptrs = [part[name][f].data_ptr() for name, f in plan.dst_keys]
                 else:
                     part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
+                    dst_ptrs = plan.dst_pointers(part)
                 if route == "direct":
                     prof.start("execute gather")
-                    plan.gather(sources, part, stream)
+                    plan.gather_ptrs(src_ptrs, dst_ptrs, stream)
                     prof.stop("execute gather")
                 else:
                     bufs = plan.alloc_buffers(device)
                     buffers.append(bufs)
+                    buf_ptrs = [b.data_ptr() for b in bufs]
                     prof.start("execute pack")
-                    plan.pack(sources, bufs, stream)
+                    plan.pack_ptrs(src_ptrs, buf_ptrs, stream)
                     prof.stop("execute pack")
                     prof.start("execute unpack")
-                    plan.unpack(bufs, part, stream)
+                    plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
                     prof.stop("execute unpack")
                 target.update(part)
         log_func(f"=== reshard plan: {sum(p.n_pieces for p in plans)} pieces in {len(plans)} "
                  f"launch group(s), {sum(p.info.buffer_bytes for p in plans) / 1e6:.1f} MB of buffers ===")
+
+        # The rest of the host work runs while the last launches finish.
+        # 1-element sub-fields ride along whole; the first op's source wins,
+        # matching tensors[0].clone() of migration.py:538.
+        for f in scalars:
+            for op in ops:
+                entry = target.get(op.param_name)
+                if entry is None or f in entry:
+                    continue
+                src_entry = source(op.src_rank)[op.param_name]
+                if f in src_entry:
+                    entry[f] = src_entry[f].to(device).clone()
+
+        ordered: StateDict = {}
+        field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
+        for name in dict.fromkeys(op.param_name for op in ops):
+            entry = target[name]
+            ordered[name] = {f: entry[f] for f in field_order if f in entry}
     finally:
         # destroying a plan waits for its launches: buffers and sources may
         # be released afterwards whatever stream the kernels ran on
@@ -211,23 +243,6 @@ def execute_param_transfer(
         if gc_was_enabled:
             gc.enable()
     del buffers
-
-    # 1-element sub-fields ride along whole; the first op's source wins,
-    # matching tensors[0].clone() of migration.py:538.
-    for f in scalars:
-        for op in ops:
-            entry = target.get(op.param_name)
-            if entry is None or f in entry:
-                continue
-            src_entry = source(op.src_rank)[op.param_name]
-            if f in src_entry:
-                entry[f] = src_entry[f].to(device).clone()
-
-    ordered: StateDict = {}
-    field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
-    for name in dict.fromkeys(op.param_name for op in ops):
-        entry = target[name]
-        ordered[name] = {f: entry[f] for f in field_order if f in entry}
 
     if forcefully_free:
         for sd in used_sources.values():
@@ -239,10 +254,14 @@ def execute_param_transfer(
     return ordered
 
 
-# Bytes of piece data per launch group at least: a group's GPU time (about
-# 0.3 ms per GB at the measured rate) must cover the next group's host
-# planning for the overlap to pay; below 2 GB a single launch is faster.
+# Bytes of piece data per launch group on average at least: a group's GPU
+# time (about 0.3 ms per GB at the measured rate) must cover the next group's
+# host planning for the overlap to pay; below 2 GB a single launch is faster.
 PIPELINE_GROUP_BYTES = 2 << 30
+# Size ratio of consecutive launch groups: host planning runs at about 0.7x
+# the GPU time of the same pieces, so each group may be this much larger than
+# the one before it and still be planned before the GPU runs dry.
+PIPELINE_GROWTH = 1.3
 ARENA_ALIGN = 256
 
 
@@ -292,9 +311,11 @@ def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fiel
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:
     """Cut the ops into at most ``pipeline`` groups of whole tensors (all ops
     of a name stay together, so each group's plan covers its destinations
-    completely), contiguous in schedule order and of about equal bytes
-    (``elem_bytes``, bytes per element over all moved fields, only scales
-    the estimate)."""
+    completely), contiguous in schedule order, growing geometrically by
+    PIPELINE_GROWTH: the first group is small, so the GPU starts early, and
+    each group's GPU time covers the host planning of the next, larger one.
+    ``elem_bytes`` (bytes per element over all moved fields) only scales the
+    estimate."""
     by_name: Dict[str, List[TransferOp]] = {}
     for op in ops:
         by_name.setdefault(op.param_name, []).append(op)
@@ -302,16 +323,19 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
     for name_ops in by_name.values():
         n = 0
         for op in name_ops:
-            numel = 1
-            for d in op.dst_meta.actual_shape():
-                numel *= int(d)
-            n += numel
+            n += op.dst_meta.numel()
         sizes.append(n * elem_bytes)
     total = sum(sizes)
     k = max(1, min(int(pipeline), len(sizes), total // PIPELINE_GROUP_BYTES))
     if k == 1:
         return [list(ops)]
-    bounds = [total * (j + 1) / k for j in range(k - 1)]
+    weights = [PIPELINE_GROWTH ** j for j in range(k)]
+    scale = total / sum(weights)
+    bounds = []
+    acc_w = 0.0
+    for wgt in weights[:-1]:
+        acc_w += wgt
+        bounds.append(acc_w * scale)
     groups: List[List[TransferOp]] = [[]]
     acc = 0
     for name_ops, n in zip(by_name.values(), sizes):

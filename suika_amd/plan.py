@@ -12,6 +12,10 @@ Suika/migration.py:397-556) and the C ABI of ``libsuika_reshard.so``:
   shards become ZERO pieces, and a ``recast`` target field (bf16) is written by
   the unpack of its f32 source field.
 
+The lowering itself (regions, slots, pieces) runs in the library
+(``sr_lower``); this class encodes the ops, metas and source shapes as int64
+tables and maps the slots back to (rank, name, field) keys.
+
 The plan is built once from shapes and dtypes and can then be executed on any
 tensors of those shapes: ``pack`` and ``unpack`` are asynchronous on the
 current HIP stream.
@@ -19,6 +23,7 @@ current HIP stream.
 from __future__ import annotations
 
 import ctypes
+import re
 from dataclasses import dataclass
 from typing import Dict, List, Mapping, Optional, Sequence, Tuple
 
@@ -26,8 +31,8 @@ import numpy as np
 import torch
 
 from . import _lib
-from .geometry import infer_dst_shard, local_matrix, lower_op, pad_boxes, view_axis
-from .meta import TensorMeta, TransferOp
+from .geometry import infer_dst_shard
+from .meta import _SHAPE_PAD, TensorMeta, TransferOp, meta_words
 
 SrcKey = Tuple[int, str, str]   # (source rank, name, field)
 DstKey = Tuple[str, str]        # (name, field)
@@ -78,33 +83,11 @@ class SlotSpec:
     dtype: torch.dtype
 
 
-def _geometry_key(m: TensorMeta) -> tuple:
-    """What region lowering depends on: global shape, shard and kind (not
-    the name or dtype; TensorMeta's own equality ignores the shard index)."""
-    return (tuple(int(d) for d in m.shape), None if m.tp_meta is None else tuple(m.tp_meta),
-            m.kind, tuple(m.kind_args), m.rows)
-
-
 def _numel(shape: Sequence[int]) -> int:
     n = 1
     for s in shape:
         n *= int(s)
     return n
-
-
-def _matrix_of(shape: Sequence[int], view: int) -> Tuple[int, int]:
-    shape = [int(s) for s in shape]
-    if not shape:
-        return 1, 1
-    if view == 1:
-        r = 1
-        for s in shape[:-1]:
-            r *= s
-        return r, shape[-1]
-    c = 1
-    for s in shape[1:]:
-        c *= s
-    return shape[0], c
 
 
 def _stream_handle(stream) -> ctypes.c_void_p:
@@ -136,133 +119,125 @@ class ReshardPlan:
         self.fields = list(fields)
         self.recast = recast
         self.options = options or PlanOptions()
-
-        by_name: Dict[str, List[TransferOp]] = {}
-        for op in ops:
-            by_name.setdefault(op.param_name, []).append(op)
+        ops = list(ops)
         dst_ranks = {op.dst_rank for op in ops}
         assert len(dst_ranks) <= 1, f"ops target several ranks {sorted(dst_ranks)}"
         self.dst_rank = dst_ranks.pop() if dst_ranks else None
-
-        self.peers: List[int] = sorted({op.src_rank for op in ops})
-        peer_index = {r: i for i, r in enumerate(self.peers)}
-
-        self.src_keys: List[SrcKey] = []
-        src_index: Dict[SrcKey, int] = {}
-        self.src_specs: Dict[SrcKey, SlotSpec] = {}
-        self.dst_keys: List[DstKey] = []
-        dst_index: Dict[DstKey, int] = {}
-        self.dst_specs: Dict[DstKey, SlotSpec] = {}
-        self.dst_metas: Dict[str, TensorMeta] = {}
-
-        # rows of the C tables (sr_tensor / sr_piece field order), converted
-        # to arrays in one step: thousands of ctypes records cost milliseconds
-        c_src: List[tuple] = []
-        c_dst: List[tuple] = []
-        c_pieces: List[tuple] = []
-
-        # Slots are made once per (tensor, field); the 2-D view ``rc`` is the
-        # same for every field of a tensor and is computed by the caller.
-        def src_slot(key: SrcKey, rc: Tuple[int, int]) -> int:
-            if key not in src_index:
-                spec = src_specs[key]
-                src_index[key] = len(self.src_keys)
-                self.src_keys.append(key)
-                self.src_specs[key] = spec
-                c_src.append((rc[0], rc[1], sr_dtype(spec.dtype), 0))
-            return src_index[key]
-
-        def dst_slot(key: DstKey, shape: Tuple[int, ...], rc: Tuple[int, int], dtype: torch.dtype) -> int:
-            if key not in dst_index:
-                dst_index[key] = len(self.dst_keys)
-                self.dst_keys.append(key)
-                self.dst_specs[key] = SlotSpec(shape, dtype)
-                c_dst.append((rc[0], rc[1], sr_dtype(dtype), 0))
-            else:
-                assert self.dst_specs[key].dtype == dtype, \
-                    f"{key}: sources disagree on dtype ({self.dst_specs[key].dtype} vs {dtype})"
-            return dst_index[key]
-
         recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
 
-        self.empty_dst: Dict[DstKey, SlotSpec] = {}   # zero-element destinations (no pieces)
-        lowered: Dict[tuple, list] = {}
-        self.piece_owner: List[Tuple[str, int]] = []   # (name, peer) per piece
+        # the destination shard of every tensor: attached by the schedule, else
+        # inferred from the tensor's pieces
+        by_name: Dict[str, List[TransferOp]] = {}
+        for op in ops:
+            by_name.setdefault(op.param_name, []).append(op)
+        name_id = {name: i for i, name in enumerate(by_name)}
+        self.dst_metas: Dict[str, TensorMeta] = {}
         for name, name_ops in by_name.items():
-            dst_shard = infer_dst_shard(name_ops)
-            self.dst_metas[name] = dst_shard
-            view = view_axis(dst_shard, *[op.src_meta for op in name_ops])
-            field_dtype: Dict[str, torch.dtype] = {}
-            for op in name_ops:
-                checked = set()
-                for f in self.fields:
-                    key = (op.src_rank, name, f)
-                    assert key in src_specs, f"[{op.src_rank}]: param missing in source {name}/{f}"
-                    shape = tuple(src_specs[key].shape)
-                    if shape not in checked:
-                        op.check_send(shape)
-                        checked.add(shape)
-                    field_dtype.setdefault(f, src_specs[key].dtype)
-                    assert field_dtype[f] == src_specs[key].dtype, \
-                        f"{name}/{f}: dtype differs between sources"
-            shape = tuple(int(d) for d in dst_shard.actual_shape())
-            if _numel(shape) == 0:
-                # nothing to move: an empty tensor per field, as clone() of an
-                # empty piece gives in the reference (migration.py:538)
-                for f in self.fields:
-                    self.empty_dst[(name, f)] = SlotSpec(shape, field_dtype[f])
-                    for tgt, sf in recast.items():
-                        if sf == f:
-                            self.empty_dst[(name, tgt)] = SlotSpec(shape, torch.bfloat16)
-                continue
-            # destination slots of every field, then the pieces that fill them
-            drc = local_matrix(dst_shard, view)
-            dslot: Dict[str, int] = {}
-            for f in self.fields:
-                dslot[f] = dst_slot((name, f), shape, drc, field_dtype[f])
-                tgt = recast_of.get(f)
-                if tgt is not None:
-                    assert field_dtype[f] == torch.float32, f"{name}/{f}: recast source must be float32"
-                    dslot[tgt] = dst_slot((name, tgt), shape, drc, torch.bfloat16)
-            for op in name_ops:
-                peer = peer_index[op.src_rank]
-                if not self.fields:
-                    continue
-                src_rc = _matrix_of(src_specs[(op.src_rank, name, self.fields[0])].shape, view)
-                sslot = {f: src_slot((op.src_rank, name, f), src_rc) for f in self.fields}
-                # regions depend only on the shard geometry, which repeats
-                # from layer to layer: lower each distinct geometry once
-                gkey = (_geometry_key(op.src_meta), _geometry_key(op.dst_meta), _geometry_key(dst_shard))
-                regions = lowered.get(gkey)
-                if regions is None:
-                    regions = lowered[gkey] = lower_op(op, dst_shard)
-                for reg in regions:
-                    for f in self.fields:
-                        s = sslot[f]
-                        tgt = recast_of.get(f)
-                        if tgt is not None:
-                            kind, d, d2 = _lib.SR_PIECE_RECAST, dslot[f], dslot[tgt]
-                        else:
-                            kind, d, d2 = _lib.SR_PIECE_COPY, dslot[f], -1
-                        c_pieces.append((kind, peer, s, d, d2, 0, reg.rows, reg.cols,
-                                         reg.src_row, reg.src_col, reg.dst_row, reg.dst_col))
-                        self.piece_owner.append((name, peer))
-            for box in pad_boxes(dst_shard, view):
-                for f, slot in dslot.items():
-                    c_pieces.append((_lib.SR_PIECE_ZERO, 0, -1, slot, -1, 0,
-                                     box.rows, box.cols, 0, 0, box.row, box.col))
-                    self.piece_owner.append((name, -1))
+            shard = name_ops[0].dst_shard_meta
+            self.dst_metas[name] = shard if shard is not None else infer_dst_shard(name_ops)
 
-        self.n_pieces = len(c_pieces)
-        self._src_arr = np.array(c_src, dtype=_lib.SR_TENSOR_DTYPE).reshape(-1)
-        self._dst_arr = np.array(c_dst, dtype=_lib.SR_TENSOR_DTYPE).reshape(-1)
-        self._piece_arr = np.array(c_pieces, dtype=_lib.SR_PIECE_DTYPE).reshape(-1)
-        self._pieces_view = self._c_src_view = self._c_dst_view = None
+        # sr_lower's tables: the metas the ops name, the ops, the source specs
         L = self._L = _lib.lib()
+        meta_row: Dict[tuple, int] = {}
+        meta_words_: List[int] = []
+        op_words: List[int] = []
+        spec_words: List[int] = []
+        field_dtype: Dict[DstKey, torch.dtype] = {}
+        nf = len(self.fields)
+
+        def row_of(m: TensorMeta, nid: int) -> int:
+            key = (id(m), nid)
+            r = meta_row.get(key)
+            if r is None:
+                r = meta_row[key] = len(meta_row)
+                meta_words_.extend(meta_words(m, 0, nid))
+            return r
+
+        for k, op in enumerate(ops):
+            name = op.param_name
+            nid = name_id[name]
+            shard = self.dst_metas[name]
+            m = op.dst_meta
+            if m is shard:
+                piece = (0, 0, -1, -1)
+            else:
+                # a piece is the shard's tensor at another degree or rows
+                assert m.kind == shard.kind and tuple(m.shape) == tuple(shard.shape), \
+                    f"{name}: piece {m} is not part of shard {shard}"
+                tp = m.tp_meta
+                if tp is None:   # an unsplit piece: the whole tensor
+                    idx, deg = (0, 1) if shard.tp_meta is not None else (0, 0)
+                else:
+                    assert shard.tp_meta is None or tp[0] == shard.tp_meta[0], \
+                        f"{name}: piece {m} is split along another dim than shard {shard}"
+                    idx, deg = tp[1], tp[2]
+                piece = (idx, deg, *(m.rows or (-1, -1)))
+            op_words.extend((nid, op.src_rank, op.dst_rank, row_of(op.src_meta, nid), row_of(shard, nid), *piece))
+            for f in self.fields:
+                key = (op.src_rank, name, f)
+                spec = src_specs.get(key)
+                assert spec is not None, f"[{op.src_rank}]: param missing in source {name}/{f}"
+                dt = field_dtype.setdefault((name, f), spec.dtype)
+                assert dt == spec.dtype, f"{name}/{f}: dtype differs between sources"
+                shape = tuple(spec.shape)
+                nd = len(shape)
+                assert nd <= _lib.SR_MAX_DIMS, f"{name}/{f}: {nd}-D source"
+                spec_words.extend((sr_dtype(spec.dtype), nd, *shape, *_SHAPE_PAD[nd]))
+        metas_arr = np.array(meta_words_, dtype=np.int64)
+        ops_arr = np.array(op_words, dtype=np.int64)
+        specs_arr = np.array(spec_words, dtype=np.int64)
+        recast_arr = np.array([1 if f in recast_of else 0 for f in self.fields] or [0], dtype=np.int64)
+        low = ctypes.POINTER(_lib.SrLowering)()
+        rc = L.sr_lower(_lib.as_int64_ptr(metas_arr), len(meta_row), _lib.as_int64_ptr(ops_arr), len(ops),
+                        _lib.as_int64_ptr(specs_arr), nf, _lib.as_int64_ptr(recast_arr), ctypes.byref(low))
+        if rc != _lib.SR_OK:
+            names = list(by_name)
+            msg = re.sub(r"#(\d+)", lambda g: names[int(g.group(1))], _lib.last_error(L))
+            raise _lib.PlanError(f"sr_lower: {_lib.STATUS_NAMES.get(rc, rc)}: {msg}")
+        try:
+            lw = low.contents
+            self._src_arr = _lib.copy_table(lw.src, lw.n_src, _lib.SR_TENSOR_DTYPE)
+            self._dst_arr = _lib.copy_table(lw.dst, lw.n_dst, _lib.SR_TENSOR_DTYPE)
+            self._piece_arr = _lib.copy_table(lw.pieces, lw.n_pieces, _lib.SR_PIECE_DTYPE)
+            self.peers: List[int] = _lib.copy_table(lw.peer_rank, lw.n_peers, np.int64).tolist()
+            src_keys = _lib.copy_table(lw.src_key, lw.n_src, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+            dst_keys = _lib.copy_table(lw.dst_key, lw.n_dst, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+            empty = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+        finally:
+            L.sr_lowering_destroy(low)
+
+        fields_ = self.fields
+        self.src_keys: List[SrcKey] = []
+        self.src_specs: Dict[SrcKey, SlotSpec] = {}
+        for k, f, *_ in src_keys:
+            op = ops[k]
+            key = (op.src_rank, op.param_name, fields_[f])
+            self.src_keys.append(key)
+            self.src_specs[key] = src_specs[key]
+
+        def dst_entry(row) -> Tuple[DstKey, SlotSpec]:
+            k, f, is_recast, _, nd = row[:5]
+            name = ops[k].param_name
+            field = fields_[f]
+            shape = tuple(row[5:5 + nd])
+            if is_recast:
+                return (name, recast_of[field]), SlotSpec(shape, torch.bfloat16)
+            return (name, field), SlotSpec(shape, field_dtype[(name, field)])
+
+        self.dst_keys: List[DstKey] = []
+        self.dst_specs: Dict[DstKey, SlotSpec] = {}
+        for row in dst_keys:
+            key, spec = dst_entry(row)
+            self.dst_keys.append(key)
+            self.dst_specs[key] = spec
+        self.empty_dst: Dict[DstKey, SlotSpec] = dict(dst_entry(row) for row in empty)
+
+        self.n_pieces = len(self._piece_arr)
+        self._pieces_view = self._c_src_view = self._c_dst_view = None
         opt = self.options.to_c()
-        rc = L.sr_plan_create(_lib.as_tensors(self._src_arr), len(c_src),
-                              _lib.as_tensors(self._dst_arr), len(c_dst), len(self.peers),
-                              _lib.as_pieces(self._piece_arr), len(c_pieces), ctypes.byref(opt),
+        rc = L.sr_plan_create(_lib.as_tensors(self._src_arr), len(self._src_arr),
+                              _lib.as_tensors(self._dst_arr), len(self._dst_arr), len(self.peers),
+                              _lib.as_pieces(self._piece_arr), self.n_pieces, ctypes.byref(opt),
                               ctypes.byref(self._handle))
         _lib.check(rc, "sr_plan_create", L)
         self.peer_bytes: List[int] = []

@@ -1,11 +1,11 @@
-/* A C11 caller of include/suika_reshard.h and include/suika_schedule.h:
+/* A C11 caller of include/suika_reshard.h and include/suika_planner.h:
  * scheduling, plan creation, buffer layout and error reporting (host-only
  * calls, no GPU needed).  Prints one line per check; the test compares them. */
 #include <stdio.h>
 #include <string.h>
 
 #include "suika_reshard.h"
-#include "suika_schedule.h"
+#include "suika_planner.h"
 
 /* one [4, 16] f32 row-parallel weight: rank `rank` holds column shard idx/deg */
 static sr_meta weight(int64_t rank, int64_t idx, int64_t deg) {

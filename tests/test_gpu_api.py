@@ -65,14 +65,24 @@ def test_execute_rejects_cpu_and_bad_shapes():
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     cpu = to_device(srcs, w, "cpu")
     fields = [(f, "normal") for f in w.src_fields]
-    with pytest.raises(AssertionError):
+    with pytest.raises(AssertionError, match="is on cpu, not on cuda"):
         execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
                                fake_source_state_dicts=cpu)
     gpu = to_device(srcs, w, "cuda")
     r = next(iter(gpu))
     name = next(iter(gpu[r]))
-    gpu[r][name]["param"] = gpu[r][name]["param"].reshape(-1)[:-1].clone()
-    with pytest.raises(AssertionError, match="shape"):
+    good = gpu[r][name]["param"]
+    gpu[r][name]["param"] = good.reshape(-1)[:-1].clone()
+    with pytest.raises(AssertionError, match=f"param {name} - src_tensor shape"):
+        execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                               fake_source_state_dicts=gpu)
+    gpu[r][name]["param"] = good
+    # a transposed view of the right shape: strided, so rejected by name
+    op2 = next(op for op in w.ops() if gpu[op.src_rank][op.param_name]["param"].dim() == 2
+               and min(gpu[op.src_rank][op.param_name]["param"].shape) > 1)
+    r2, name2 = op2.src_rank, op2.param_name
+    gpu[r2][name2]["param"] = gpu[r2][name2]["param"].t().contiguous().t()
+    with pytest.raises(AssertionError, match=f"source {name2}/param of rank {r2} is not contiguous"):
         execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
                                fake_source_state_dicts=gpu)
 

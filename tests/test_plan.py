@@ -4,7 +4,8 @@
   piece for every op as the oracle's restatement of the reference schedule;
 * executing a ``ReshardPlan``'s pieces with numpy (pack into the library's
   buffer layout, then unpack) reproduces the oracle bit for bit -- this pins
-  the lowering (geometry), the buffer offsets and the coverage check;
+  the lowering (the library's ``sr_lower``), the buffer offsets and the
+  coverage check;
 * the benchmark plans have the documented sizes (P, D, pieces).
 """
 import numpy as np
@@ -13,7 +14,6 @@ import torch
 
 from oracle import reshard_oracle as O
 from suika_amd import ParamLayout, TensorMeta, schedule_param_transfer
-from suika_amd.geometry import lower_op
 from suika_amd.plan import ReshardPlan, SlotSpec
 from suika_amd.workloads import CONFIG_ORDER, CONFIGS, fields_of
 from tests import cases
@@ -146,12 +146,25 @@ def test_benchmark_shortest_row_runs():
     assert min(shortest.values()) == 768 and shortest["gpt125m_tp2_tp4"] == 768, shortest
 
 
-def test_lower_op_rejects_uncovered_piece():
+def test_lowering_rejects_uncovered_piece():
+    """A source that does not hold its piece: the lowering names the tensor
+    and the missing elements instead of planning a wrong copy."""
     from suika_amd import TransferOp
     src = TensorMeta(name="a", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 1, 2))
     dst = TensorMeta(name="a", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
-    with pytest.raises(AssertionError, match="holds 0 of"):
-        lower_op(TransferOp("a", 1, 0, src, dst), dst)
+    specs = {(1, "a", "param"): SlotSpec((4, 4), torch.float32)}
+    with pytest.raises(AssertionError, match="a: source rank 1 holds 0 of the 16 elements"):
+        ReshardPlan([TransferOp("a", 1, 0, src, dst)], specs, ["param"])
+
+
+def test_lowering_rejects_wrong_source_shape():
+    """get_send_tensor's shape check (migration.py:293-294), by name."""
+    from suika_amd import TransferOp
+    src = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    dst = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    specs = {(0, "w", "param"): SlotSpec((4, 5), torch.float32)}
+    with pytest.raises(AssertionError, match=r"param w - src_tensor shape \(4, 5\) mismatch with src_meta \(4, 4\)"):
+        ReshardPlan([TransferOp("w", 0, 0, src, dst)], specs, ["param"])
 
 
 def test_arena_layout_and_views():
@@ -219,14 +232,14 @@ def test_zero_element_tensors_are_planned_as_empty():
 
 def test_pipeline_groups_keep_tensors_whole():
     """Launch groups of execute_param_transfer: contiguous in schedule order,
-    every op of a tensor in one group, at most ``pipeline`` groups, each
-    carrying at least PIPELINE_GROUP_BYTES unless it is the only one."""
+    every op of a tensor in one group, at most ``pipeline`` groups carrying
+    PIPELINE_GROUP_BYTES on average at least, growing from a small first one."""
     from suika_amd import migration
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         ops = w.ops()
         elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
-        for pipeline in (1, 3, 4, 100):
+        for pipeline in (1, 3, 4, 8, 100):
             groups = migration._pipeline_groups(ops, elem, pipeline)
             assert [op for g in groups for op in g] == ops
             assert 1 <= len(groups) <= pipeline
@@ -235,6 +248,10 @@ def test_pipeline_groups_keep_tensors_whole():
                 names = {op.param_name for op in g}
                 assert not names & seen, "a tensor split across groups"
                 seen |= names
+            sizes = [sum(op.dst_meta.numel() for op in g) * elem for g in groups]
+            assert len(groups) == 1 or sum(sizes) / len(groups) >= migration.PIPELINE_GROUP_BYTES
+            if len(groups) >= 3:
+                assert sizes[0] < sizes[-1], (key, pipeline, sizes)
     small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
     assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1

@@ -1,4 +1,4 @@
-"""The library's transfer scheduler (``sr_schedule``, include/suika_schedule.h)
+"""The library's transfer scheduler (``sr_schedule``, include/suika_planner.h)
 behind ``schedule_param_transfer``, checked on the CPU against the oracle's
 restatement of the reference schedule (Suika/migration.py:322-381):
 
