@@ -37,7 +37,7 @@ from .geometry import infer_dst_shard
 from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
                    schedule_param_transfer)
 from . import _lib
-from .plan import PlanOptions, ReshardPlan, SlotSpec
+from .plan import PlanOptions, ReshardPlan
 
 StateDict = Dict[str, Dict[str, Tensor]]
 
@@ -136,34 +136,6 @@ def execute_param_transfer(
             f"[{rank}]: piece from rank {r} needs a cross-GPU exchange, which this one-GPU build "
             "does not implement; pass the peer shards as fake_source_state_dicts")
 
-    dev_index = device.index
-
-    def source_specs(group: List[TransferOp]) -> Tuple[Dict[Tuple[int, str, str], SlotSpec],
-                                                       Dict[Tuple[int, str, str], int]]:
-        """Shape/dtype and device address of every source tensor the group
-        reads, each checked once (a CUDA tensor on ``device``, contiguous)."""
-        specs: Dict[Tuple[int, str, str], SlotSpec] = {}
-        ptrs: Dict[Tuple[int, str, str], int] = {}
-        for op in group:
-            sd = source(op.src_rank)
-            name = op.param_name
-            assert name in sd, f"[{rank}]: param missing in source {name}"
-            entry = sd[name]
-            for f in normal:
-                key = (op.src_rank, name, f)
-                if key in specs:
-                    continue
-                assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
-                t = entry[f]
-                assert isinstance(t, Tensor), f"source {name}/{f} of rank {op.src_rank}: not a tensor"
-                if not t.is_cuda or t.get_device() != dev_index:
-                    raise AssertionError(f"source {name}/{f} of rank {op.src_rank} is on {t.device}, "
-                                         f"not on {device}")
-                assert t.is_contiguous(), f"source {name}/{f} of rank {op.src_rank} is not contiguous"
-                specs[key] = SlotSpec(tuple(t.shape), t.dtype)
-                ptrs[key] = t.data_ptr()
-        return specs, ptrs
-
     # bytes per element over the moved fields, from the first op's sources
     # (only used to balance the launch groups)
     elem_bytes = 0
@@ -187,16 +159,16 @@ def execute_param_transfer(
             # previous group's launch.
             for group in groups:
                 prof.start("execute schedule lowering")
-                specs, src_ptr = source_specs(group)
-                plan = ReshardPlan(group, specs, normal, recast=recast, options=plan_options)
+                # shapes, dtypes and addresses read from the source tensors (each
+                # checked once: contiguous, on this device)
+                plan, src_ptrs = ReshardPlan.from_sources(group, source, normal, device, recast=recast,
+                                                          options=plan_options, rank=rank)
                 prof.stop("execute schedule lowering")
                 plans.append(plan)
                 used_sources.update((r, source(r)) for r in plan.peers)
-                src_ptrs = [src_ptr[key] for key in plan.src_keys]
                 if arena_views is None:
                     # fresh tensors of the planned shapes: their addresses need no check
-                    part = plan.alloc_dst(device)
-                    dst_ptrs = [part[name][f].data_ptr() for name, f in plan.dst_keys]
+                    part, dst_ptrs = plan.alloc_dst_ptrs(device)
                 else:
                     part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
                     dst_ptrs = plan.dst_pointers(part)

@@ -25,7 +25,7 @@ from __future__ import annotations
 import ctypes
 import re
 from dataclasses import dataclass
-from typing import Dict, List, Mapping, Optional, Sequence, Tuple
+from typing import Callable, Dict, List, Mapping, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -83,6 +83,13 @@ class SlotSpec:
     dtype: torch.dtype
 
 
+def _spec_words(out: List[int], shape: Tuple[int, ...], dtype: torch.dtype, name: str, field: str) -> None:
+    """Append one sr_src_spec row (dtype, ndim, shape[8])."""
+    nd = len(shape)
+    assert nd <= _lib.SR_MAX_DIMS, f"{name}/{field}: {nd}-D source"
+    out.extend((sr_dtype(dtype), nd, *shape, *_SHAPE_PAD[nd]))
+
+
 def _numel(shape: Sequence[int]) -> int:
     n = 1
     for s in shape:
@@ -110,6 +117,62 @@ class ReshardPlan:
         field) the ops read; ``fields`` are the normal sub-fields moved;
         ``recast`` maps a bf16 destination field to the f32 field it is
         rounded from (e.g. ``{"param": "master"}``)."""
+        self._setup(ops, fields, recast, options)
+        spec_words: List[int] = []
+        dtypes: List[torch.dtype] = []
+        for op in self._ops:
+            name = op.param_name
+            for f in self.fields:
+                spec = src_specs.get((op.src_rank, name, f))
+                assert spec is not None, f"[{op.src_rank}]: param missing in source {name}/{f}"
+                _spec_words(spec_words, tuple(spec.shape), spec.dtype, name, f)
+                dtypes.append(spec.dtype)
+        self._build(spec_words, dtypes)
+
+    @classmethod
+    def from_sources(cls, ops: Sequence[TransferOp], source: Callable[[int], Mapping],
+                     fields: Sequence[str], device: torch.device,
+                     recast: Optional[Mapping[str, str]] = None,
+                     options: Optional[PlanOptions] = None,
+                     rank: Optional[int] = None) -> Tuple["ReshardPlan", List[int]]:
+        """The plan of ``ops`` with shapes and dtypes read from the source
+        tensors themselves, and the device address of every source slot.
+
+        ``source(r)`` is rank ``r``'s state dict ``{name: {field: Tensor}}``.
+        Each tensor is read once: it must be a contiguous CUDA tensor on
+        ``device``.  ``rank`` (the executing rank) only prefixes messages.
+        """
+        self = cls.__new__(cls)
+        self._setup(ops, fields, recast, options)
+        dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        spec_words: List[int] = []
+        dtypes: List[torch.dtype] = []
+        ptrs: List[int] = []
+        who = f"[{rank}]" if rank is not None else ""
+        for op in self._ops:
+            r = op.src_rank
+            name = op.param_name
+            sd = source(r)
+            assert name in sd, f"{who}: param missing in source {name}"
+            entry = sd[name]
+            for f in self.fields:
+                assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
+                t = entry[f]
+                assert isinstance(t, torch.Tensor), f"source {name}/{f} of rank {r}: not a tensor"
+                if not t.is_cuda or t.get_device() != dev_index:
+                    raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, not on {device}")
+                assert t.is_contiguous(), f"source {name}/{f} of rank {r} is not contiguous"
+                dt = t.dtype
+                _spec_words(spec_words, tuple(t.shape), dt, name, f)
+                dtypes.append(dt)
+                ptrs.append(t.data_ptr())
+        self._build(spec_words, dtypes)
+        src_ptrs = np.array(ptrs, dtype=np.uint64)[self._src_index].tolist() if ptrs else []
+        return self, src_ptrs
+
+    def _setup(self, ops, fields, recast, options) -> None:
+        """Everything but the source specs: validation, destination shards and
+        the op / meta tables of sr_lower."""
         self._handle = ctypes.c_void_p()
         recast = dict(recast or {})
         for tgt, srcf in recast.items():
@@ -119,31 +182,27 @@ class ReshardPlan:
         self.fields = list(fields)
         self.recast = recast
         self.options = options or PlanOptions()
-        ops = list(ops)
+        ops = self._ops = list(ops)
         dst_ranks = {op.dst_rank for op in ops}
         assert len(dst_ranks) <= 1, f"ops target several ranks {sorted(dst_ranks)}"
         self.dst_rank = dst_ranks.pop() if dst_ranks else None
-        recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
+        self._recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
 
         # the destination shard of every tensor: attached by the schedule, else
         # inferred from the tensor's pieces
         by_name: Dict[str, List[TransferOp]] = {}
         for op in ops:
             by_name.setdefault(op.param_name, []).append(op)
-        name_id = {name: i for i, name in enumerate(by_name)}
+        self._names = list(by_name)
+        name_id = {name: i for i, name in enumerate(self._names)}
         self.dst_metas: Dict[str, TensorMeta] = {}
         for name, name_ops in by_name.items():
             shard = name_ops[0].dst_shard_meta
             self.dst_metas[name] = shard if shard is not None else infer_dst_shard(name_ops)
 
-        # sr_lower's tables: the metas the ops name, the ops, the source specs
-        L = self._L = _lib.lib()
         meta_row: Dict[tuple, int] = {}
         meta_words_: List[int] = []
         op_words: List[int] = []
-        spec_words: List[int] = []
-        field_dtype: Dict[DstKey, torch.dtype] = {}
-        nf = len(self.fields)
 
         def row_of(m: TensorMeta, nid: int) -> int:
             key = (id(m), nid)
@@ -153,7 +212,7 @@ class ReshardPlan:
                 meta_words_.extend(meta_words(m, 0, nid))
             return r
 
-        for k, op in enumerate(ops):
+        for op in ops:
             name = op.param_name
             nid = name_id[name]
             shard = self.dst_metas[name]
@@ -173,25 +232,32 @@ class ReshardPlan:
                     idx, deg = tp[1], tp[2]
                 piece = (idx, deg, *(m.rows or (-1, -1)))
             op_words.extend((nid, op.src_rank, op.dst_rank, row_of(op.src_meta, nid), row_of(shard, nid), *piece))
-            for f in self.fields:
-                key = (op.src_rank, name, f)
-                spec = src_specs.get(key)
-                assert spec is not None, f"[{op.src_rank}]: param missing in source {name}/{f}"
-                dt = field_dtype.setdefault((name, f), spec.dtype)
-                assert dt == spec.dtype, f"{name}/{f}: dtype differs between sources"
-                shape = tuple(spec.shape)
-                nd = len(shape)
-                assert nd <= _lib.SR_MAX_DIMS, f"{name}/{f}: {nd}-D source"
-                spec_words.extend((sr_dtype(spec.dtype), nd, *shape, *_SHAPE_PAD[nd]))
-        metas_arr = np.array(meta_words_, dtype=np.int64)
-        ops_arr = np.array(op_words, dtype=np.int64)
+        self._metas_arr = np.array(meta_words_, dtype=np.int64)
+        self._n_metas = len(meta_row)
+        self._ops_arr = np.array(op_words, dtype=np.int64)
+
+    def _build(self, spec_words: List[int], dtypes: List[torch.dtype]) -> None:
+        """sr_lower on the tables, then sr_plan_create on its output."""
+        L = self._L = _lib.lib()
+        ops, nf = self._ops, len(self.fields)
+        self._dtypes = dtypes   # torch dtype of the source of (op k, field f) at k * nf + f
+        # one torch dtype per (tensor, field) across sources (the library
+        # compares element types, which several torch dtypes share)
+        for f in range(nf):
+            if len(set(dtypes[f::nf])) > 1:
+                seen: Dict[str, torch.dtype] = {}
+                for k, op in enumerate(ops):
+                    dt = seen.setdefault(op.param_name, dtypes[k * nf + f])
+                    assert dt == dtypes[k * nf + f], \
+                        f"{op.param_name}/{self.fields[f]}: dtype differs between sources"
         specs_arr = np.array(spec_words, dtype=np.int64)
-        recast_arr = np.array([1 if f in recast_of else 0 for f in self.fields] or [0], dtype=np.int64)
+        recast_arr = np.array([1 if f in self._recast_of else 0 for f in self.fields] or [0], dtype=np.int64)
         low = ctypes.POINTER(_lib.SrLowering)()
-        rc = L.sr_lower(_lib.as_int64_ptr(metas_arr), len(meta_row), _lib.as_int64_ptr(ops_arr), len(ops),
-                        _lib.as_int64_ptr(specs_arr), nf, _lib.as_int64_ptr(recast_arr), ctypes.byref(low))
+        rc = L.sr_lower(_lib.as_int64_ptr(self._metas_arr), self._n_metas, _lib.as_int64_ptr(self._ops_arr),
+                        len(ops), _lib.as_int64_ptr(specs_arr), nf, _lib.as_int64_ptr(recast_arr),
+                        ctypes.byref(low))
         if rc != _lib.SR_OK:
-            names = list(by_name)
+            names = self._names
             msg = re.sub(r"#(\d+)", lambda g: names[int(g.group(1))], _lib.last_error(L))
             raise _lib.PlanError(f"sr_lower: {_lib.STATUS_NAMES.get(rc, rc)}: {msg}")
         try:
@@ -200,37 +266,15 @@ class ReshardPlan:
             self._dst_arr = _lib.copy_table(lw.dst, lw.n_dst, _lib.SR_TENSOR_DTYPE)
             self._piece_arr = _lib.copy_table(lw.pieces, lw.n_pieces, _lib.SR_PIECE_DTYPE)
             self.peers: List[int] = _lib.copy_table(lw.peer_rank, lw.n_peers, np.int64).tolist()
-            src_keys = _lib.copy_table(lw.src_key, lw.n_src, (np.int64, _lib.SR_KEY_WORDS)).tolist()
-            dst_keys = _lib.copy_table(lw.dst_key, lw.n_dst, (np.int64, _lib.SR_KEY_WORDS)).tolist()
-            empty = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+            src_rows = _lib.copy_table(lw.src_key, lw.n_src, (np.int64, _lib.SR_KEY_WORDS))
+            self._dst_rows = _lib.copy_table(lw.dst_key, lw.n_dst, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+            self._empty_rows = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS)).tolist()
         finally:
             L.sr_lowering_destroy(low)
-
-        fields_ = self.fields
-        self.src_keys: List[SrcKey] = []
-        self.src_specs: Dict[SrcKey, SlotSpec] = {}
-        for k, f, *_ in src_keys:
-            op = ops[k]
-            key = (op.src_rank, op.param_name, fields_[f])
-            self.src_keys.append(key)
-            self.src_specs[key] = src_specs[key]
-
-        def dst_entry(row) -> Tuple[DstKey, SlotSpec]:
-            k, f, is_recast, _, nd = row[:5]
-            name = ops[k].param_name
-            field = fields_[f]
-            shape = tuple(row[5:5 + nd])
-            if is_recast:
-                return (name, recast_of[field]), SlotSpec(shape, torch.bfloat16)
-            return (name, field), SlotSpec(shape, field_dtype[(name, field)])
-
-        self.dst_keys: List[DstKey] = []
-        self.dst_specs: Dict[DstKey, SlotSpec] = {}
-        for row in dst_keys:
-            key, spec = dst_entry(row)
-            self.dst_keys.append(key)
-            self.dst_specs[key] = spec
-        self.empty_dst: Dict[DstKey, SlotSpec] = dict(dst_entry(row) for row in empty)
+        # source slot -> (op, field) position in the per-(op, field) lists
+        self._src_index = src_rows[:, 0] * nf + src_rows[:, 1] if len(src_rows) else np.zeros(0, np.int64)
+        self._src_rows = src_rows.tolist()
+        self._views = None
 
         self.n_pieces = len(self._piece_arr)
         self._pieces_view = self._c_src_view = self._c_dst_view = None
@@ -248,6 +292,82 @@ class ReshardPlan:
         info = _lib.SrPlanInfo()
         _lib.check(L.sr_plan_info_get(self._handle, ctypes.byref(info)), "sr_plan_info_get", L)
         self.info = info
+
+    # ----------------------------------------------- slots as (rank, name, field)
+    def _dst_entry(self, row) -> Tuple[DstKey, SlotSpec]:
+        k, f, is_recast, _, nd = row[:5]
+        name = self._ops[k].param_name
+        field = self.fields[f]
+        shape = tuple(row[5:5 + nd])
+        if is_recast:
+            return (name, self._recast_of[field]), SlotSpec(shape, torch.bfloat16)
+        return (name, field), SlotSpec(shape, self._dtypes[k * len(self.fields) + f])
+
+    def _key_views(self):
+        """Slot keys and specs as dicts, built on first use."""
+        if self._views is None:
+            nf = len(self.fields)
+            src_keys: List[SrcKey] = []
+            src_specs: Dict[SrcKey, SlotSpec] = {}
+            for k, f, _, _, nd, *shape in self._src_rows:
+                op = self._ops[k]
+                key = (op.src_rank, op.param_name, self.fields[f])
+                src_keys.append(key)
+                src_specs[key] = SlotSpec(tuple(shape[:nd]), self._dtypes[k * nf + f])
+            dst_keys: List[DstKey] = []
+            dst_specs: Dict[DstKey, SlotSpec] = {}
+            for row in self._dst_rows:
+                key, spec = self._dst_entry(row)
+                dst_keys.append(key)
+                dst_specs[key] = spec
+            empty = dict(self._dst_entry(row) for row in self._empty_rows)
+            self._views = (src_keys, src_specs, dst_keys, dst_specs, empty)
+        return self._views
+
+    @property
+    def src_keys(self) -> List[SrcKey]:
+        """(source rank, name, field) of every source slot, in slot order."""
+        return self._key_views()[0]
+
+    @property
+    def src_specs(self) -> Dict[SrcKey, SlotSpec]:
+        return self._key_views()[1]
+
+    @property
+    def dst_keys(self) -> List[DstKey]:
+        """(name, field) of every destination slot, in slot order."""
+        return self._key_views()[2]
+
+    @property
+    def dst_specs(self) -> Dict[DstKey, SlotSpec]:
+        return self._key_views()[3]
+
+    @property
+    def empty_dst(self) -> Dict[DstKey, SlotSpec]:
+        """Zero-element destinations: no slot, no piece."""
+        return self._key_views()[4]
+
+    def alloc_dst_ptrs(self, device) -> Tuple[Dict[str, Dict[str, torch.Tensor]], List[int]]:
+        """Fresh destination tensors (as ``alloc_dst``) and the device
+        address of every destination slot, straight from the slot table."""
+        out: Dict[str, Dict[str, torch.Tensor]] = {}
+        ptrs: List[int] = []
+        ops, fields, nf, dtypes = self._ops, self.fields, len(self.fields), self._dtypes
+        empty = torch.empty
+        for rows, keep in ((self._dst_rows, True), (self._empty_rows, False)):
+            for k, f, is_recast, _, nd, *shape in rows:
+                if is_recast:
+                    field, dt = self._recast_of[fields[f]], torch.bfloat16
+                else:
+                    field, dt = fields[f], dtypes[k * nf + f]
+                t = empty(shape[:nd], dtype=dt, device=device)
+                entry = out.get(ops[k].param_name)
+                if entry is None:
+                    entry = out[ops[k].param_name] = {}
+                entry[field] = t
+                if keep:
+                    ptrs.append(t.data_ptr())
+        return out, ptrs
 
     # -------------------------------------------------------------- sizes
     @property
@@ -321,14 +441,11 @@ class ReshardPlan:
         they are views of one allocation laid out by ``arena_layout`` (one
         allocator call instead of one per tensor; a model adopting them with
         ``load_state_dict(assign=True)`` keeps them in place)."""
+        if not arena:
+            return self.alloc_dst_ptrs(device)[0]
         out: Dict[str, Dict[str, torch.Tensor]] = {}
         for (name, field), spec in self.empty_dst.items():
             out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
-        if not arena:
-            for (name, field) in self.dst_keys:
-                spec = self.dst_specs[(name, field)]
-                out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
-            return out
         total, offsets = self.arena_layout()
         buf = torch.empty(max(1, total), dtype=torch.uint8, device=device)
         for (name, field) in self.dst_keys:

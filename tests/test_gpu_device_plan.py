@@ -207,3 +207,51 @@ def test_two_plans_concurrently_on_two_streams():
     finally:
         for h in plans:
             L.sr_plan_destroy(h)
+
+
+@pytest.mark.gpu
+def test_plan_tables_reused_across_threads_and_sizes():
+    """Destroyed plans hand their table memory and events to a per-process
+    cache; new plans of other sizes reuse them.  Four host threads, each on
+    its own stream, create, run and destroy plans of different sizes
+    concurrently; every result stays exact."""
+    import threading
+    print("[gpu device-plan] table cache, 4 threads", flush=True)
+    L = _lib.lib()
+    errors = []
+
+    def worker(tid):
+        try:
+            stream = torch.cuda.Stream()
+            gen = torch.Generator("cpu").manual_seed(200 + tid)
+            for it in range(6):
+                rows = [ROWS, 700, 1500][(tid + it) % 3]
+                pcs = [p for p in _pieces(seed=50 + tid * 10 + it) if p.src_row + p.rows <= rows]
+                # keep the destination covered: whole rows of the kept pieces only
+                covered = {p.src_row + r for p in pcs for r in range(p.rows)}
+                pcs = [p for p in pcs if all(p.src_row + r in covered for r in range(p.rows))]
+                pcs += [_lib.SrPiece(_lib.SR_PIECE_COPY, 0, 0, 0, -1, 0, 1, COLS, r, 0, r, 0)
+                        for r in range(rows) if r not in covered]
+                t = (_lib.SrTensor * 1)(_lib.SrTensor(rows, COLS, _lib.SR_DT_U8, 0))
+                arr = (_lib.SrPiece * len(pcs))(*pcs)
+                h = ctypes.c_void_p()
+                _lib.check(L.sr_plan_create(t, 1, t, 1, N_PEERS, arr, len(pcs), None, ctypes.byref(h)), "create")
+                src_h = torch.randint(0, 256, (rows, COLS), dtype=torch.uint8, generator=gen)
+                with torch.cuda.stream(stream):
+                    src = src_h.cuda()
+                    dst = torch.full((rows, COLS), POISON, dtype=torch.uint8, device="cuda")
+                    _lib.check(L.sr_gather(h, _vp([src.data_ptr()]), _vp([dst.data_ptr()]), stream.cuda_stream),
+                               "gather")
+                L.sr_plan_destroy(h)
+                stream.synchronize()
+                if not torch.equal(dst.cpu(), src_h):
+                    errors.append((tid, it, rows))
+        except Exception as e:   # reported below with the thread and iteration
+            errors.append((tid, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
