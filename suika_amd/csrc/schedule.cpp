@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <new>
 #include <vector>
 
 #include "sr_internal.h"
@@ -240,5 +241,9 @@ int schedule(const sr_meta* src, int64_t n_src, int64_t R, const sr_meta* dst, i
 extern "C" int sr_schedule(const sr_meta* src, int64_t n_src, int64_t n_src_ranks, const sr_meta* dst,
                            int64_t n_dst, int64_t n_names, int64_t minimum_est_peers, sr_op* ops,
                            int64_t cap, int64_t* n_ops) {
-  return schedule(src, n_src, n_src_ranks, dst, n_dst, n_names, minimum_est_peers, ops, cap, n_ops);
+  try {
+    return schedule(src, n_src, n_src_ranks, dst, n_dst, n_names, minimum_est_peers, ops, cap, n_ops);
+  } catch (const std::bad_alloc&) {
+    return fail(SR_ENOMEM, "sr_schedule: out of host memory");
+  }
 }

@@ -149,23 +149,32 @@ class ReshardPlan:
         dtypes: List[torch.dtype] = []
         ptrs: List[int] = []
         who = f"[{rank}]" if rank is not None else ""
+        fields = self.fields
+        words, keep_dtype, keep_ptr = spec_words.extend, dtypes.append, ptrs.append
+        Tensor = torch.Tensor
         for op in self._ops:
             r = op.src_rank
             name = op.param_name
             sd = source(r)
             assert name in sd, f"{who}: param missing in source {name}"
             entry = sd[name]
-            for f in self.fields:
-                assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
-                t = entry[f]
-                assert isinstance(t, torch.Tensor), f"source {name}/{f} of rank {r}: not a tensor"
+            for f in fields:
+                t = entry.get(f)
+                if t is None or not isinstance(t, Tensor):
+                    assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
+                    raise AssertionError(f"source {name}/{f} of rank {r}: not a tensor")
                 if not t.is_cuda or t.get_device() != dev_index:
                     raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, not on {device}")
                 assert t.is_contiguous(), f"source {name}/{f} of rank {r} is not contiguous"
+                shape = t.shape
+                nd = len(shape)
                 dt = t.dtype
-                _spec_words(spec_words, tuple(t.shape), dt, name, f)
-                dtypes.append(dt)
-                ptrs.append(t.data_ptr())
+                code = _DTYPES.get(dt)
+                assert code is not None and nd <= 8, \
+                    f"source {name}/{f}: {dt}, {nd}-D is not supported by the reshard engine"
+                words((code, nd, *shape, *_SHAPE_PAD[nd]))
+                keep_dtype(dt)
+                keep_ptr(t.data_ptr())
         self._build(spec_words, dtypes)
         src_ptrs = np.array(ptrs, dtype=np.uint64)[self._src_index].tolist() if ptrs else []
         return self, src_ptrs

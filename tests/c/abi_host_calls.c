@@ -67,5 +67,33 @@ int main(void) {
   for (int64_t k = 0; k < n_ops; ++k)
     printf("op %lld -> %lld piece %lld/%lld\n", (long long)ops[k].src_rank, (long long)ops[k].dst_rank,
            (long long)ops[k].piece_tp_index, (long long)ops[k].piece_tp_deg);
+
+  /* ... lowered to the engine's tables and planned, still without Python:
+     one meta table (sources, then the target), the ops' shard rows shifted */
+  sr_meta metas[3] = {from[0], from[1], to[0]};
+  sr_src_spec specs[2];
+  for (int64_t k = 0; k < n_ops; ++k) {
+    ops[k].dst_shard += 2;
+    memset(&specs[k], 0, sizeof(specs[k]));
+    specs[k].dtype = SR_DT_F32;
+    specs[k].ndim = 2;
+    specs[k].shape[0] = 4;   /* each source shard: [4, 8] */
+    specs[k].shape[1] = 8;
+  }
+  const int64_t no_recast[1] = {0};
+  sr_lowering* low = NULL;
+  rc = sr_lower(metas, 3, ops, n_ops, specs, 1, no_recast, &low);
+  printf("lower %d src %lld dst %lld pieces %lld peers %lld\n", rc, (long long)low->n_src, (long long)low->n_dst,
+         (long long)low->n_pieces, (long long)low->n_peers);
+  for (int64_t k = 0; k < low->n_pieces; ++k)
+    printf("piece peer %d src %d cols %llu dst_col %llu\n", low->pieces[k].peer, low->pieces[k].src,
+           (unsigned long long)low->pieces[k].cols, (unsigned long long)low->pieces[k].dst_col);
+  sr_plan* lowered = NULL;
+  rc = sr_plan_create(low->src, (int32_t)low->n_src, low->dst, (int32_t)low->n_dst, (int32_t)low->n_peers,
+                      low->pieces, (int32_t)low->n_pieces, NULL, &lowered);
+  sr_plan_peer_bytes(lowered, 1, &b1);
+  printf("planned %d peer1_bytes %llu\n", rc, (unsigned long long)b1);
+  sr_plan_destroy(lowered);
+  sr_lowering_destroy(low);
   return 0;
 }

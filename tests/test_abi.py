@@ -238,6 +238,10 @@ def test_c_caller(tmp_path):
         "schedule 0 ops 2",
         "op 0 -> 0 piece 0/2",
         "op 1 -> 0 piece 1/2",
+        "lower 0 src 2 dst 1 pieces 2 peers 2",
+        "piece peer 0 src 0 cols 8 dst_col 0",   # column halves of the row-parallel merge
+        "piece peer 1 src 1 cols 8 dst_col 8",
+        "planned 0 peer1_bytes 128",
     ], out.stdout
 
 

@@ -255,3 +255,26 @@ def test_pipeline_groups_keep_tensors_whole():
     small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
     assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1
+
+
+def test_from_sources_rejects_bad_sources_by_name():
+    """ReshardPlan.from_sources (the drop-in operator's planner) reads the
+    source tensors themselves; what it cannot use is rejected with the
+    tensor's name before anything reaches a GPU."""
+    from suika_amd import TransferOp
+    src = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    dst = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    ops = [TransferOp("w", 3, 0, src, dst)]
+    dev = torch.device("cuda", 0)
+
+    def plan(sd):
+        return ReshardPlan.from_sources(ops, lambda r: sd, ["param"], dev, rank=0)
+
+    with pytest.raises(AssertionError, match=r"source w/param of rank 3 is on cpu, not on cuda:0"):
+        plan({"w": {"param": torch.zeros(4, 4)}})
+    with pytest.raises(AssertionError, match=r"\[0\]: param missing in source w"):
+        plan({})
+    with pytest.raises(AssertionError, match="expected_sub_fields mismatch: w has no param"):
+        plan({"w": {"exp_avg": torch.zeros(4, 4)}})
+    with pytest.raises(AssertionError, match="source w/param of rank 3: not a tensor"):
+        plan({"w": {"param": [0.0] * 16}})
