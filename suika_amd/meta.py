@@ -336,6 +336,40 @@ class TransferOp:
         """Receive buffer of the piece's shape (Suika/migration.py:285-287)."""
         return torch.empty(self.dst_meta.actual_shape(), dtype=self.dst_meta.dtype, device=device)
 
+    def get_send_tensor(self, src_tensor: Tensor) -> Tensor:
+        """The contiguous part of ``src_tensor`` this op sends (migration.py:290-312).
+
+        A source shard at least as fine as the piece is sent whole (the tensor
+        itself); otherwise the piece -- the reference's
+        ``chunk(dst_deg / src_deg, slice_dim)[k].contiguous()``, or the rows
+        of a vocab_pad piece -- is cut into a new tensor by the reshard
+        engine on the tensor's GPU.  The copy is complete when this returns.
+        """
+        self.check_send(src_tensor.shape)
+        src, piece = self.src_meta, self.dst_meta
+        if piece.rows is None and src.tp_deg() >= piece.tp_deg():
+            return src_tensor
+        assert src_tensor.is_cuda, \
+            (f"get_send_tensor: param {self.param_name} - the reshard engine runs on the GPU; "
+             f"src_tensor is on {src_tensor.device}")
+        from .plan import ReshardPlan
+        name = self.param_name
+        op = TransferOp(name, self.src_rank, self.dst_rank, src, piece, dst_shard_meta=piece)
+        device = src_tensor.device
+        with torch.cuda.device(device):
+            plan, src_ptrs = ReshardPlan.from_sources([op], lambda r: {name: {"x": src_tensor}}, ["x"], device)
+            try:
+                out, dst_ptrs = plan.alloc_dst_ptrs(device)
+                if dst_ptrs:
+                    plan.gather_ptrs(src_ptrs, dst_ptrs)
+            finally:
+                plan.close()   # waits for the launch
+        send = out[name]["x"]
+        assert send.shape == piece.actual_shape(), \
+            (f"get_send_tensor: param {name} - send_tensor shape {send.shape} mismatch with dst_meta "
+             f"{piece.actual_shape()}")
+        return send
+
     def check_send(self, src_shape) -> None:
         """The reference's preconditions of get_send_tensor (migration.py:293-294)."""
         assert torch.Size(src_shape) == self.src_meta.actual_shape(), \

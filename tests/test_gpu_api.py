@@ -170,3 +170,52 @@ def test_zero_element_tensors(route):
         torch.cuda.synchronize()
         assert torch.equal(out["w"]["param"].cpu(), w)
         assert tuple(out["none"]["param"].shape) == (0,) and tuple(out["none2d"]["param"].shape) == (0, 4)
+
+
+def _send_case(case):
+    """(source meta, piece meta, expected piece from the source tensor)."""
+    from oracle import reshard_oracle as O
+    from tests.harness import to_ometa
+    f32 = torch.float32
+    if case in ("rows", "cols"):
+        dim = 0 if case == "rows" else -1
+        src = TensorMeta(name="w", dtype=f32, shape=(12, 16), tp_meta=(dim, 1, 2))
+        piece = TensorMeta(name="w", dtype=f32, shape=(12, 16), tp_meta=(dim, 3, 4))
+        # the reference: chunk(dst_deg // src_deg, dim)[dst_idx - src_idx * (dst_deg // src_deg)]
+        return src, piece, lambda t: t.chunk(2, dim=dim)[1].contiguous()
+    if case == "qkv":
+        src = TensorMeta(name="qkv", dtype=f32, shape=(24, 5), tp_meta=(0, 0, 1), kind="qkv_heads",
+                         kind_args=(4, 2, 3))
+        piece = TensorMeta(name="qkv", dtype=f32, shape=(24, 5), tp_meta=(0, 1, 2), kind="qkv_heads",
+                           kind_args=(4, 2, 3))
+    else:   # vocab: rows [2, 6) of rank 0's shard of a 10-row table padded to 16 at degree 2
+        src = TensorMeta(name="e", dtype=f32, shape=(10, 4), tp_meta=(0, 0, 2), kind="vocab_pad",
+                         kind_args=(4,))
+        piece = src.with_rows(2, 6)
+    G = np.arange(int(np.prod(src.shape)), dtype=np.float32).reshape(tuple(src.shape))
+    want = O.shard_of(G, to_ometa(piece)) if piece.rows is None else G[2:6]
+    return src, piece, lambda t: torch.from_numpy(np.ascontiguousarray(want)).to(t.device)
+
+
+@pytest.mark.parametrize("case", ["rows", "cols", "qkv", "vocab"])
+def test_get_send_tensor_cuts_the_piece(case):
+    """TransferOp.get_send_tensor (migration.py:290-312) on the engine: the
+    reference's chunk(...)[k].contiguous() for chunk shards, the closed-form
+    piece for the head-granular and vocabulary kinds; a shard at least as
+    fine as the piece is sent as the tensor itself."""
+    from oracle import reshard_oracle as O
+    from tests.harness import to_ometa
+    print(f"[gpu api] get_send_tensor {case}", flush=True)
+    src, piece, expect = _send_case(case)
+    G = np.arange(int(np.prod(src.shape)), dtype=np.float32).reshape(tuple(src.shape))
+    t = torch.from_numpy(np.ascontiguousarray(O.shard_of(G, to_ometa(src)))).cuda()
+    op = TransferOp(src.name, 0, 1, src, piece)
+    got = op.get_send_tensor(t)
+    assert got.is_contiguous() and got.data_ptr() != t.data_ptr()
+    assert torch.equal(got, expect(t)), case
+    assert tuple(got.shape) == tuple(piece.actual_shape())
+    # the reverse direction: the finer source is sent whole, without a copy
+    if piece.rows is None:
+        back = TransferOp(src.name, 0, 1, piece, src)
+        t2 = got.clone()
+        assert back.get_send_tensor(t2) is t2

@@ -278,3 +278,18 @@ def test_from_sources_rejects_bad_sources_by_name():
         plan({"w": {"exp_avg": torch.zeros(4, 4)}})
     with pytest.raises(AssertionError, match="source w/param of rank 3: not a tensor"):
         plan({"w": {"param": [0.0] * 16}})
+
+
+def test_get_send_tensor_host_rules():
+    """get_send_tensor's host side (migration.py:293-300): the reference's
+    shape assertion, the whole-tensor case without any GPU, and no CPU
+    fallback for a piece that needs cutting."""
+    from suika_amd import TransferOp
+    coarse = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 1))
+    fine = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    t = torch.zeros(4, 4)
+    assert TransferOp("w", 0, 1, fine, coarse).get_send_tensor(t) is t
+    with pytest.raises(AssertionError, match=r"src_tensor shape \(4, 4\) mismatch with src_meta"):
+        TransferOp("w", 0, 1, coarse, fine).get_send_tensor(t)
+    with pytest.raises(AssertionError, match="runs on the GPU; src_tensor is on cpu"):
+        TransferOp("w", 0, 1, coarse, fine).get_send_tensor(torch.zeros(8, 4))
