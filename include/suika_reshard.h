@@ -213,7 +213,10 @@ int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
 /*
  * Release a plan and its device tables.  Waits for the plan's own launches
  * still in flight (it may follow an asynchronous call directly); does not
- * synchronize anything else.  NULL is ignored.
+ * synchronize anything else.  NULL is ignored.  The table memory and events
+ * are kept for reuse by later plans instead of being freed (hipFree
+ * synchronizes the device): at most 256 MiB of device memory and 64 MiB of
+ * pinned host memory per process, held until the process exits.
  */
 void sr_plan_destroy(sr_plan* plan);
 
