@@ -14,6 +14,7 @@ from pathlib import Path
 from typing import Optional
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsuika_reshard.so"
+HOST_PATH = Path(__file__).resolve().parent / "lib" / "_suika_host.so"
 
 SR_OK = 0
 SR_EINVAL = -1
@@ -317,6 +318,29 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"{path}: ABI {handle.sr_abi_version()} != expected {ABI_VERSION}")
         _lib = handle
     return _lib
+
+
+_host = None
+
+
+def host():
+    """Load (once) and return the host extension (per-tensor work of the
+    drop-in operator, on torch's C++ API); raise if it is missing."""
+    global _host
+    if _host is None:
+        import importlib.util
+
+        import torch  # noqa: F401  (its libraries back the extension)
+        path = Path(os.environ.get("SUIKA_HOST_LIB", str(HOST_PATH)))
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python suika_amd/build.py`; there is no fallback path")
+        spec = importlib.util.spec_from_file_location("_suika_host", str(path))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _host = mod
+    return _host
 
 
 def last_error(handle: Optional[ctypes.CDLL] = None) -> str:

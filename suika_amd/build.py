@@ -6,6 +6,10 @@ any other FFI -- can load.  hipcc cross-compiles for gfx950 without a GPU
 present.  Sources: ``reshard.hip`` (plan builder and kernels),
 ``schedule.cpp`` and ``lower.cpp`` (the host-only planner: transfer schedule
 and its lowering to region moves).
+
+``build_host`` compiles ``host_bind.cpp`` into ``suika_amd/lib/_suika_host.so``,
+the CPython extension (on torch's C++ API) that does the drop-in operator's
+per-tensor host work; it is a plain ``g++`` line against the installed torch.
 """
 from __future__ import annotations
 
@@ -22,6 +26,8 @@ SOURCES = [PKG_DIR / "csrc" / "reshard.hip", PKG_DIR / "csrc" / "schedule.cpp",
 INCLUDE = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "lib"
 LIB = LIB_DIR / "libsuika_reshard.so"
+HOST_SRC = PKG_DIR / "csrc" / "host_bind.cpp"
+HOST_LIB = LIB_DIR / "_suika_host.so"
 
 ARCH = "gfx950"
 
@@ -69,5 +75,33 @@ def build(verbose: bool = False, out: Path = LIB, defines=()) -> Path:
     return out
 
 
+def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
+    """Compile the torch-facing host extension (always recompiles)."""
+    import sysconfig
+
+    import torch
+    from torch.utils.cpp_extension import include_paths, library_paths
+    out = Path(out)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_suffix(".so.tmp")
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    libdirs = library_paths()
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wno-unused-function",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-DTORCH_EXTENSION_NAME=_suika_host",
+           *[f"-I{p}" for p in include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           str(HOST_SRC), *[f"-L{p}" for p in libdirs], *[f"-Wl,-rpath,{p}" for p in libdirs],
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("host extension build failed:\n" + (res.stdout + res.stderr)[-6000:])
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_host(verbose="-v" in sys.argv))

@@ -127,7 +127,7 @@ class ReshardPlan:
                 assert spec is not None, f"[{op.src_rank}]: param missing in source {name}/{f}"
                 _spec_words(spec_words, tuple(spec.shape), spec.dtype, name, f)
                 dtypes.append(spec.dtype)
-        self._build(spec_words, dtypes)
+        self._build(np.array(spec_words, dtype=np.int64), dtypes)
 
     @classmethod
     def from_sources(cls, ops: Sequence[TransferOp], source: Callable[[int], Mapping],
@@ -145,39 +145,10 @@ class ReshardPlan:
         self = cls.__new__(cls)
         self._setup(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
-        spec_words: List[int] = []
-        dtypes: List[torch.dtype] = []
-        ptrs: List[int] = []
         who = f"[{rank}]" if rank is not None else ""
-        fields = self.fields
-        words, keep_dtype, keep_ptr = spec_words.extend, dtypes.append, ptrs.append
-        Tensor = torch.Tensor
-        for op in self._ops:
-            r = op.src_rank
-            name = op.param_name
-            sd = source(r)
-            assert name in sd, f"{who}: param missing in source {name}"
-            entry = sd[name]
-            for f in fields:
-                t = entry.get(f)
-                if t is None or not isinstance(t, Tensor):
-                    assert f in entry, f"expected_sub_fields mismatch: {name} has no {f}"
-                    raise AssertionError(f"source {name}/{f} of rank {r}: not a tensor")
-                if not t.is_cuda or t.get_device() != dev_index:
-                    raise AssertionError(f"source {name}/{f} of rank {r} is on {t.device}, not on {device}")
-                assert t.is_contiguous(), f"source {name}/{f} of rank {r} is not contiguous"
-                shape = t.shape
-                nd = len(shape)
-                dt = t.dtype
-                code = _DTYPES.get(dt)
-                assert code is not None and nd <= 8, \
-                    f"source {name}/{f}: {dt}, {nd}-D is not supported by the reshard engine"
-                words((code, nd, *shape, *_SHAPE_PAD[nd]))
-                keep_dtype(dt)
-                keep_ptr(t.data_ptr())
-        self._build(spec_words, dtypes)
-        src_ptrs = np.array(ptrs, dtype=np.uint64)[self._src_index].tolist() if ptrs else []
-        return self, src_ptrs
+        specs, dtypes, ptrs = _lib.host().collect_sources(self._ops, source, self.fields, dev_index, who)
+        self._build(specs, dtypes)
+        return self, ptrs[self._src_index].tolist()
 
     def _setup(self, ops, fields, recast, options) -> None:
         """Everything but the source specs: validation, destination shards and
@@ -192,6 +163,7 @@ class ReshardPlan:
         self.recast = recast
         self.options = options or PlanOptions()
         ops = self._ops = list(ops)
+        self._op_names = [op.param_name for op in ops]
         dst_ranks = {op.dst_rank for op in ops}
         assert len(dst_ranks) <= 1, f"ops target several ranks {sorted(dst_ranks)}"
         self.dst_rank = dst_ranks.pop() if dst_ranks else None
@@ -245,7 +217,7 @@ class ReshardPlan:
         self._n_metas = len(meta_row)
         self._ops_arr = np.array(op_words, dtype=np.int64)
 
-    def _build(self, spec_words: List[int], dtypes: List[torch.dtype]) -> None:
+    def _build(self, specs_arr: np.ndarray, dtypes: List[torch.dtype]) -> None:
         """sr_lower on the tables, then sr_plan_create on its output."""
         L = self._L = _lib.lib()
         ops, nf = self._ops, len(self.fields)
@@ -259,7 +231,6 @@ class ReshardPlan:
                     dt = seen.setdefault(op.param_name, dtypes[k * nf + f])
                     assert dt == dtypes[k * nf + f], \
                         f"{op.param_name}/{self.fields[f]}: dtype differs between sources"
-        specs_arr = np.array(spec_words, dtype=np.int64)
         recast_arr = np.array([1 if f in self._recast_of else 0 for f in self.fields] or [0], dtype=np.int64)
         low = ctypes.POINTER(_lib.SrLowering)()
         rc = L.sr_lower(_lib.as_int64_ptr(self._metas_arr), self._n_metas, _lib.as_int64_ptr(self._ops_arr),
@@ -276,8 +247,8 @@ class ReshardPlan:
             self._piece_arr = _lib.copy_table(lw.pieces, lw.n_pieces, _lib.SR_PIECE_DTYPE)
             self.peers: List[int] = _lib.copy_table(lw.peer_rank, lw.n_peers, np.int64).tolist()
             src_rows = _lib.copy_table(lw.src_key, lw.n_src, (np.int64, _lib.SR_KEY_WORDS))
-            self._dst_rows = _lib.copy_table(lw.dst_key, lw.n_dst, (np.int64, _lib.SR_KEY_WORDS)).tolist()
-            self._empty_rows = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS)).tolist()
+            self._dst_rows = _lib.copy_table(lw.dst_key, lw.n_dst, (np.int64, _lib.SR_KEY_WORDS))
+            self._empty_rows = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS))
         finally:
             L.sr_lowering_destroy(low)
         # source slot -> (op, field) position in the per-(op, field) lists
@@ -325,11 +296,11 @@ class ReshardPlan:
                 src_specs[key] = SlotSpec(tuple(shape[:nd]), self._dtypes[k * nf + f])
             dst_keys: List[DstKey] = []
             dst_specs: Dict[DstKey, SlotSpec] = {}
-            for row in self._dst_rows:
+            for row in self._dst_rows.tolist():
                 key, spec = self._dst_entry(row)
                 dst_keys.append(key)
                 dst_specs[key] = spec
-            empty = dict(self._dst_entry(row) for row in self._empty_rows)
+            empty = dict(self._dst_entry(row) for row in self._empty_rows.tolist())
             self._views = (src_keys, src_specs, dst_keys, dst_specs, empty)
         return self._views
 
@@ -359,24 +330,14 @@ class ReshardPlan:
     def alloc_dst_ptrs(self, device) -> Tuple[Dict[str, Dict[str, torch.Tensor]], List[int]]:
         """Fresh destination tensors (as ``alloc_dst``) and the device
         address of every destination slot, straight from the slot table."""
-        out: Dict[str, Dict[str, torch.Tensor]] = {}
-        ptrs: List[int] = []
-        ops, fields, nf, dtypes = self._ops, self.fields, len(self.fields), self._dtypes
-        empty = torch.empty
-        for rows, keep in ((self._dst_rows, True), (self._empty_rows, False)):
-            for k, f, is_recast, _, nd, *shape in rows:
-                if is_recast:
-                    field, dt = self._recast_of[fields[f]], torch.bfloat16
-                else:
-                    field, dt = fields[f], dtypes[k * nf + f]
-                t = empty(shape[:nd], dtype=dt, device=device)
-                entry = out.get(ops[k].param_name)
-                if entry is None:
-                    entry = out[ops[k].param_name] = {}
-                entry[field] = t
-                if keep:
-                    ptrs.append(t.data_ptr())
-        return out, ptrs
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        recast_names = [self._recast_of.get(f) for f in self.fields]
+        out, ptrs = _lib.host().alloc_dst(self._dst_rows.reshape(-1, _lib.SR_KEY_WORDS),
+                                          self._empty_rows.reshape(-1, _lib.SR_KEY_WORDS),
+                                          self._op_names, self.fields, recast_names, self._dtypes, device)
+        return out, ptrs.tolist()
 
     # -------------------------------------------------------------- sizes
     @property

@@ -270,3 +270,29 @@ def test_overlapping_objects_rejected_before_launch():
     assert L.sr_pack(h, src, bufs, None) == _lib.SR_EOVERLAP
     assert "peer_bufs[0] and peer_bufs[1]" in _lib.last_error()
     L.sr_plan_destroy(h)
+
+
+def test_host_extension_loads():
+    """The host extension (per-tensor work of the drop-in operator) is built
+    in-tree and exposes its two entry points."""
+    mod = _lib.host()
+    assert callable(mod.collect_sources) and callable(mod.alloc_dst)
+    assert Path(mod.__file__).resolve() == _lib.HOST_PATH.resolve()
+
+
+def test_missing_host_extension_raises(tmp_path):
+    """No fallback: without the host extension the planner raises."""
+    import os
+    import subprocess
+    import sys
+    code = ("from suika_amd import _lib\n"
+            "try:\n"
+            "    _lib.host()\n"
+            "except RuntimeError as e:\n"
+            "    assert 'missing' in str(e) and 'no fallback' in str(e), e\n"
+            "    print('raised')\n")
+    env = dict(os.environ, SUIKA_HOST_LIB=str(tmp_path / "absent.so"))
+    root = Path(__file__).resolve().parents[1]
+    out = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0 and "raised" in out.stdout, out.stderr[-2000:]

@@ -293,3 +293,25 @@ def test_get_send_tensor_host_rules():
         TransferOp("w", 0, 1, coarse, fine).get_send_tensor(t)
     with pytest.raises(AssertionError, match="runs on the GPU; src_tensor is on cpu"):
         TransferOp("w", 0, 1, coarse, fine).get_send_tensor(torch.zeros(8, 4))
+
+
+def test_from_sources_reports_errors_in_op_order():
+    """Source state dicts are fetched rank by rank in op order, so the first
+    op decides the error, as in the reference's loop (migration.py:426-494):
+    a missing own parameter is an AssertionError, a remote rank without a
+    local copy the caller's own error."""
+    from suika_amd import TransferOp
+    m = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    m1 = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 1, 2))
+    dst = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 1))
+
+    def source(r):
+        if r == 0:
+            return {}
+        raise NotImplementedError("remote rank")
+
+    own_first = [TransferOp("w", 0, 0, m, m, dst), TransferOp("w", 1, 0, m1, m1, dst)]
+    with pytest.raises(AssertionError, match="param missing in source w"):
+        ReshardPlan.from_sources(own_first, source, ["param"], torch.device("cuda", 0), rank=0)
+    with pytest.raises(NotImplementedError, match="remote rank"):
+        ReshardPlan.from_sources(own_first[::-1], source, ["param"], torch.device("cuda", 0), rank=0)
