@@ -12,7 +12,10 @@
 //                    (sr_src_spec rows), dtypes and device addresses, with
 //                    the same checks and messages as the Python host;
 //   alloc_dst:       destination slot rows (sr_slot_key) -> fresh tensors in
-//                    {name: {field: tensor}} and their addresses.
+//                    {name: {field: tensor}} and their addresses;
+//   bind_dst:        caller-provided destinations (an arena's views) checked
+//                    against the slot rows -> their addresses;
+//   arena_views:     the same dict of typed views into one allocation.
 //
 // No device work happens here; the tensors come from torch's caching
 // allocator on the device's current stream, as torch.empty would.
@@ -184,6 +187,86 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
   return py::make_tuple(out, ptrs);
 }
 
+// Addresses of caller-provided destination tensors for the slot rows, each
+// checked against its slot: a contiguous tensor of the slot's shape and
+// dtype on `device`.
+py::array_t<uint64_t> bind_dst(py::dict part, const RowTable& rows, py::list names, py::list fields,
+                               py::list recast_names, py::list dtypes, at::Device device) {
+  const int64_t nf = int64_t(fields.size());
+  const int64_t n = rows.ndim() == 2 ? rows.shape(0) : 0;
+  if (n && rows.shape(1) != kKeyWords) throw py::value_error("slot rows must have 13 columns");
+  py::array_t<uint64_t> ptrs({n});
+  uint64_t* pp = ptrs.mutable_data();
+  const int64_t* r = rows.data();
+  for (int64_t i = 0; i < n; ++i, r += kKeyWords) {
+    const int64_t k = r[0], f = r[1], is_recast = r[2], nd = r[4];
+    if (k < 0 || k >= int64_t(names.size()) || f < 0 || f >= nf || nd < 0 || nd > 8)
+      throw py::value_error("malformed slot row");
+    py::handle name = names[k];
+    py::handle field = is_recast ? recast_names[f] : fields[f];
+    at::ScalarType st = at::kBFloat16;
+    if (!is_recast) {
+      py::handle dt = dtypes[k * nf + f];
+      if (!THPDtype_Check(dt.ptr())) throw py::type_error("dtypes must hold torch.dtype objects");
+      st = reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type;
+    }
+    const std::string what = "(" + py::repr(name).cast<std::string>() + ", " +
+                             py::repr(field).cast<std::string>() + ")";
+    py::object entry = lookup(part.ptr(), name.ptr());
+    py::object obj = entry ? lookup(entry.ptr(), field.ptr()) : py::object();
+    if (!obj) assertion(what + ": no destination tensor");
+    if (!THPVariable_Check(obj.ptr())) assertion(what + ": not a tensor");
+    const at::Tensor& t = THPVariable_Unpack(obj.ptr());
+    if (t.device() != device)
+      assertion(what + ": tensor is on " + t.device().str() + ", the kernels run on " + device.str());
+    if (!t.is_contiguous()) assertion(what + ": tensor is not contiguous");
+    if (t.scalar_type() != st) assertion(what + ": dtype differs from the planned one");
+    bool same = t.dim() == nd;
+    for (int64_t d = 0; same && d < nd; ++d) same = t.size(d) == r[5 + d];
+    if (!same) assertion(what + ": shape differs from the planned one");
+    pp[i] = reinterpret_cast<uint64_t>(t.data_ptr());
+  }
+  return ptrs;
+}
+
+// Typed views of one byte buffer (a destination arena): row i is
+// (byte offset, ndim, shape[8]); out[names[i]][fields[i]] is the view.
+py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, const RowTable& rows,
+                     py::list dtypes) {
+  const int64_t n = rows.ndim() == 2 ? rows.shape(0) : 0;
+  if (n && rows.shape(1) != 10) throw py::value_error("arena rows must have 10 columns");
+  if (int64_t(names.size()) != n || int64_t(fields.size()) != n || int64_t(dtypes.size()) != n)
+    throw py::value_error("one name, field and dtype per arena row");
+  if (buf.scalar_type() != at::kByte || buf.dim() != 1 || !buf.is_contiguous())
+    throw py::value_error("the arena must be a contiguous 1-D uint8 tensor");
+  py::dict out;
+  const int64_t* r = rows.data();
+  for (int64_t i = 0; i < n; ++i, r += 10) {
+    py::handle dt = dtypes[i];
+    if (!THPDtype_Check(dt.ptr())) throw py::type_error("dtypes must hold torch.dtype objects");
+    const at::ScalarType st = reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type;
+    const int64_t nd = r[1];
+    if (nd < 0 || nd > 8) throw py::value_error("malformed arena row");
+    int64_t numel = 1;
+    for (int64_t d = 0; d < nd; ++d) numel *= r[2 + d];
+    const int64_t bytes = numel * int64_t(c10::elementSize(st));
+    if (r[0] < 0 || r[0] + bytes > buf.size(0) || r[0] % int64_t(c10::elementSize(st)) != 0)
+      throw py::value_error("arena row outside the buffer or misaligned");
+    at::Tensor v = buf.narrow(0, r[0], bytes).view(st).view(at::IntArrayRef(r + 2, size_t(nd)));
+    py::handle name = names[i];
+    PyObject* entry = PyDict_GetItemWithError(out.ptr(), name.ptr());
+    if (!entry) {
+      if (PyErr_Occurred()) throw py::error_already_set();
+      py::dict fresh;
+      out[name] = fresh;
+      entry = fresh.ptr();
+    }
+    py::object wrapped = py::reinterpret_steal<py::object>(THPVariable_Wrap(v));
+    if (PyDict_SetItem(entry, fields[i].ptr(), wrapped.ptr()) != 0) throw py::error_already_set();
+  }
+  return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_suika_host, m) {
@@ -192,4 +275,8 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("device_index"), py::arg("who"));
   m.def("alloc_dst", &alloc_dst, py::arg("rows"), py::arg("empty_rows"), py::arg("names"), py::arg("fields"),
         py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
+  m.def("bind_dst", &bind_dst, py::arg("part"), py::arg("rows"), py::arg("names"), py::arg("fields"),
+        py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
+  m.def("arena_views", &arena_views, py::arg("buf"), py::arg("names"), py::arg("fields"), py::arg("rows"),
+        py::arg("dtypes"));
 }

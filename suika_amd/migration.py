@@ -27,6 +27,7 @@ from __future__ import annotations
 import gc
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
@@ -171,7 +172,7 @@ def execute_param_transfer(
                     part, dst_ptrs = plan.alloc_dst_ptrs(device)
                 else:
                     part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
-                    dst_ptrs = plan.dst_pointers(part)
+                    dst_ptrs = plan.bind_dst_ptrs(part, device)
                 if route == "direct":
                     prof.start("execute gather")
                     plan.gather_ptrs(src_ptrs, dst_ptrs, stream)
@@ -270,14 +271,15 @@ def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fiel
                 n *= d
             end += n * dtypes[(name, f)].itemsize
     buf = torch.empty(max(1, end), dtype=torch.uint8, device=device)
-    out: StateDict = {}
+    names, fields_, rows, dts = [], [], [], []
     for (name, f), off in offsets.items():
-        dt = dtypes[(name, f)]
-        n = 1
-        for d in shapes[name]:
-            n *= d
-        out.setdefault(name, {})[f] = buf[off:off + n * dt.itemsize].view(dt).view(shapes[name])
-    return out
+        shape = shapes[name]
+        names.append(name)
+        fields_.append(f)
+        rows.extend((off, len(shape), *shape, *(0,) * (8 - len(shape))))
+        dts.append(dtypes[(name, f)])
+    table = np.array(rows, dtype=np.int64).reshape(-1, 10)
+    return _lib.host().arena_views(buf, names, fields_, table, dts)
 
 
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:

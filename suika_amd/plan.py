@@ -339,6 +339,17 @@ class ReshardPlan:
                                           self._op_names, self.fields, recast_names, self._dtypes, device)
         return out, ptrs.tolist()
 
+    def bind_dst_ptrs(self, dst: Mapping[str, Mapping[str, torch.Tensor]], device) -> List[int]:
+        """Addresses of caller-provided destination tensors in slot order,
+        each checked against its slot (contiguous, planned shape and dtype,
+        on ``device``)."""
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        recast_names = [self._recast_of.get(f) for f in self.fields]
+        return _lib.host().bind_dst(dst, self._dst_rows.reshape(-1, _lib.SR_KEY_WORDS), self._op_names,
+                                    self.fields, recast_names, self._dtypes, device).tolist()
+
     # -------------------------------------------------------------- sizes
     @property
     def pack_bytes(self) -> int:
@@ -418,11 +429,17 @@ class ReshardPlan:
             out.setdefault(name, {})[field] = torch.empty(spec.shape, dtype=spec.dtype, device=device)
         total, offsets = self.arena_layout()
         buf = torch.empty(max(1, total), dtype=torch.uint8, device=device)
+        names, fields, rows, dtypes = [], [], [], []
         for (name, field) in self.dst_keys:
             spec = self.dst_specs[(name, field)]
-            off = offsets[(name, field)]
-            n = _numel(spec.shape) * spec.dtype.itemsize
-            out.setdefault(name, {})[field] = buf[off:off + n].view(spec.dtype).view(spec.shape)
+            names.append(name)
+            fields.append(field)
+            rows.extend((offsets[(name, field)], len(spec.shape), *spec.shape, *_SHAPE_PAD[len(spec.shape)]))
+            dtypes.append(spec.dtype)
+        views = _lib.host().arena_views(buf, names, fields, np.array(rows, dtype=np.int64).reshape(-1, 10),
+                                        dtypes)
+        for name, entry in views.items():
+            out.setdefault(name, {}).update(entry)
         return out
 
     # ---------------------------------------------------------- execution
@@ -447,9 +464,7 @@ class ReshardPlan:
         return ptrs
 
     def dst_pointers(self, dst: Mapping[str, Mapping[str, torch.Tensor]]):
-        dev = torch.cuda.current_device()
-        return [self._check_tensor(dst[name][field], self.dst_specs[(name, field)], (name, field), dev)
-                for (name, field) in self.dst_keys]
+        return self.bind_dst_ptrs(dst, torch.device("cuda", torch.cuda.current_device()))
 
     def buf_pointers(self, buffers: Sequence[torch.Tensor]):
         assert len(buffers) == len(self.peers), f"{len(buffers)} buffers for {len(self.peers)} peers"

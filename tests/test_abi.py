@@ -296,3 +296,21 @@ def test_missing_host_extension_raises(tmp_path):
     out = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True,
                          text=True, timeout=300)
     assert out.returncode == 0 and "raised" in out.stdout, out.stderr[-2000:]
+
+
+def test_host_arena_views_checks_rows():
+    """arena_views builds typed views of one byte buffer and rejects rows
+    outside it or misaligned for their dtype."""
+    import numpy as np
+    import torch
+    mod = _lib.host()
+    buf = torch.arange(64, dtype=torch.uint8)
+    rows = np.array([[0, 2, 2, 4] + [0] * 6, [32, 1, 8] + [0] * 7], dtype=np.int64)
+    out = mod.arena_views(buf, ["a", "b"], ["f32", "u8"], rows, [torch.float32, torch.uint8])
+    assert out["a"]["f32"].shape == (2, 4) and out["a"]["f32"].dtype == torch.float32
+    assert out["a"]["f32"].untyped_storage().data_ptr() == buf.untyped_storage().data_ptr()
+    assert out["b"]["u8"].tolist() == list(range(32, 40))
+    with pytest.raises(ValueError, match="outside the buffer or misaligned"):
+        mod.arena_views(buf, ["a"], ["f"], np.array([[60, 1, 2] + [0] * 7], dtype=np.int64), [torch.float32])
+    with pytest.raises(ValueError, match="outside the buffer or misaligned"):
+        mod.arena_views(buf, ["a"], ["f"], np.array([[2, 1, 2] + [0] * 7], dtype=np.int64), [torch.float32])

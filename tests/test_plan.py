@@ -315,3 +315,31 @@ def test_from_sources_reports_errors_in_op_order():
         ReshardPlan.from_sources(own_first, source, ["param"], torch.device("cuda", 0), rank=0)
     with pytest.raises(NotImplementedError, match="remote rank"):
         ReshardPlan.from_sources(own_first[::-1], source, ["param"], torch.device("cuda", 0), rank=0)
+
+
+def test_bind_dst_checks_every_destination():
+    """Caller-provided destinations (an arena's views, or any dict) are
+    bound slot by slot and rejected by name when they do not match."""
+    ops = [o for o in _empty_case(2, 1) if o.dst_rank == 0]
+    specs = {(o.src_rank, o.param_name, f): SlotSpec(tuple(o.src_meta.actual_shape()), torch.float32)
+             for o in ops for f in ("master", "exp_avg")}
+    plan = ReshardPlan(ops, specs, ["master", "exp_avg"], recast={"param": "master"})
+    cpu = torch.device("cpu")
+    dst = plan.alloc_dst(cpu)
+    ptrs = plan.bind_dst_ptrs(dst, cpu)
+    assert ptrs == [dst[n][f].data_ptr() for n, f in plan.dst_keys]
+    arena = plan.alloc_dst(cpu, arena=True)
+    assert plan.bind_dst_ptrs(arena, cpu) == [arena[n][f].data_ptr() for n, f in plan.dst_keys]
+    bad = {n: dict(e) for n, e in dst.items()}
+    bad["w"]["param"] = torch.empty(8, 4)                 # f32 where bf16 is planned
+    with pytest.raises(AssertionError, match=r"\('w', 'param'\): dtype differs"):
+        plan.bind_dst_ptrs(bad, cpu)
+    bad["w"]["param"] = torch.empty(4, 8, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match=r"\('w', 'param'\): shape differs"):
+        plan.bind_dst_ptrs(bad, cpu)
+    del bad["w"]["param"]
+    with pytest.raises(AssertionError, match=r"\('w', 'param'\): no destination tensor"):
+        plan.bind_dst_ptrs(bad, cpu)
+    with pytest.raises(AssertionError, match="tensor is on cpu, the kernels run on cuda:0"):
+        plan.bind_dst_ptrs(dst, torch.device("cuda", 0))
+    plan.close()
