@@ -1,4 +1,4 @@
-// host_bind.cpp -- per-tensor host work of the drop-in operator, native
+// host_bind.cpp -- per-tensor and per-meta host work of the drop-in operators, native
 // (suika_amd/lib/_suika_host.so, a CPython extension on torch's C++ API).
 //
 // execute_param_transfer (Suika/migration.py:397-556) touches every source
@@ -15,7 +15,11 @@
 //                    {name: {field: tensor}} and their addresses;
 //   bind_dst:        caller-provided destinations (an arena's views) checked
 //                    against the slot rows -> their addresses;
-//   arena_views:     the same dict of typed views into one allocation.
+//   arena_views:     the same dict of typed views into one allocation;
+//   encode_layout:   a ParamLayout as an sr_meta table (sr_schedule's input);
+//   make_ops:        sr_schedule's op table as TransferOp objects;
+//   encode_ops:      one rank's TransferOps as sr_lower's op and meta tables;
+//   piece_numels:    elements per op's piece (launch-group balancing).
 //
 // No device work happens here; the tensors come from torch's caching
 // allocator on the device's current stream, as torch.empty would.
@@ -27,6 +31,7 @@
 
 #include <cstdint>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace py = pybind11;
@@ -267,6 +272,313 @@ py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, con
   return out;
 }
 
+// ------------------------------------------------------------ layouts and ops
+
+constexpr int64_t kMetaWords = 21;   // sr_meta: rank, name, itemsize, ndim, shape[8], tp[3], kind, args[3], rows[2]
+
+int64_t as_int(PyObject* o) {
+  const long long v = PyLong_AsLongLong(o);
+  if (v == -1 && PyErr_Occurred()) throw py::error_already_set();
+  return int64_t(v);
+}
+
+// Interned attribute names (created once, never released).
+struct Names {
+  PyObject *dtype, *shape, *kind_args, *tp_meta, *kind, *rows, *name, *dict;
+  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta;
+  PyObject *chunk, *vocab_pad, *qkv_heads;
+  Names() {
+    auto in = [](const char* s) { return PyUnicode_InternFromString(s); };
+    dtype = in("dtype"); shape = in("shape"); kind_args = in("kind_args"); tp_meta = in("tp_meta");
+    kind = in("kind"); rows = in("rows"); name = in("name"); dict = in("__dict__");
+    param_name = in("param_name"); src_rank = in("src_rank"); dst_rank = in("dst_rank");
+    src_meta = in("src_meta"); dst_meta = in("dst_meta"); dst_shard_meta = in("dst_shard_meta");
+    chunk = in("chunk"); vocab_pad = in("vocab_pad"); qkv_heads = in("qkv_heads");
+  }
+};
+
+const Names& names_() {
+  static Names* n = new Names();
+  return *n;
+}
+
+py::object attr(PyObject* o, PyObject* key) {
+  PyObject* v = PyObject_GetAttr(o, key);
+  if (!v) throw py::error_already_set();
+  return py::reinterpret_steal<py::object>(v);
+}
+
+// One sr_meta row of a TensorMeta (the attributes its constructor sets).
+void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
+  const Names& N = names_();
+  std::fill(row, row + kMetaWords, 0);
+  row[0] = rank;
+  row[1] = name_id;
+  py::object dt = attr(m, N.dtype);
+  if (!THPDtype_Check(dt.ptr())) throw py::type_error("TensorMeta.dtype is not a torch.dtype");
+  row[2] = int64_t(c10::elementSize(reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type));
+  py::object shape = attr(m, N.shape), args = attr(m, N.kind_args);
+  if (!PyTuple_Check(shape.ptr()) || !PyTuple_Check(args.ptr()))
+    throw py::type_error("TensorMeta.shape and kind_args must be tuples");
+  const int64_t nd = int64_t(PyTuple_GET_SIZE(shape.ptr())), na = int64_t(PyTuple_GET_SIZE(args.ptr()));
+  if (nd > 8 || na > 3)
+    assertion(py::str(attr(m, N.name)).cast<std::string>() + ": " + std::to_string(nd) + "-D shape / " +
+              std::to_string(na) + " kind args");
+  row[3] = nd;
+  for (int64_t d = 0; d < nd; ++d) row[4 + d] = as_int(PyTuple_GET_ITEM(shape.ptr(), d));
+  py::object tp = attr(m, N.tp_meta);
+  if (tp.ptr() != Py_None) {
+    if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3)
+      throw py::value_error("tp_meta must be (slice_dim, tp_index, tp_deg)");
+    for (int i = 0; i < 3; ++i) row[12 + i] = as_int(PyTuple_GET_ITEM(tp.ptr(), i));
+  }
+  py::object kind = attr(m, N.kind);
+  if (!PyUnicode_Check(kind.ptr())) throw py::type_error("TensorMeta.kind must be a str");
+  if (PyUnicode_Compare(kind.ptr(), N.chunk) == 0) row[15] = 0;
+  else if (PyUnicode_Compare(kind.ptr(), N.vocab_pad) == 0) row[15] = 1;
+  else if (PyUnicode_Compare(kind.ptr(), N.qkv_heads) == 0) row[15] = 2;
+  else throw py::value_error("unknown shard kind " + py::str(kind).cast<std::string>());
+  if (PyErr_Occurred()) throw py::error_already_set();
+  for (int64_t i = 0; i < na; ++i) row[16 + i] = as_int(PyTuple_GET_ITEM(args.ptr(), i));
+  py::object rows = attr(m, N.rows);
+  if (rows.ptr() == Py_None) {
+    row[19] = row[20] = -1;
+  } else {
+    if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2)
+      throw py::value_error("rows must be (first, end)");
+    row[19] = as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
+    row[20] = as_int(PyTuple_GET_ITEM(rows.ptr(), 1));
+  }
+}
+
+// A ParamLayout's {rank: {name: TensorMeta}} as an [n, 21] sr_meta table,
+// rank by rank in dict order; `names` maps names to ids (extended in first-
+// seen order) and `objs` receives each row's TensorMeta.
+py::array_t<int64_t> encode_layout(py::dict layout, py::dict names, py::list objs) {
+  int64_t n = 0;
+  for (auto kv : layout) {
+    if (!PyDict_Check(kv.second.ptr())) throw py::type_error("a layout maps ranks to dicts of TensorMeta");
+    n += int64_t(PyDict_GET_SIZE(kv.second.ptr()));
+  }
+  py::array_t<int64_t> out({n, kMetaWords});
+  int64_t* row = out.mutable_data();
+  for (auto kv : layout) {
+    const int64_t rank = as_int(kv.first.ptr());
+    PyObject *key, *value;
+    Py_ssize_t pos = 0;
+    while (PyDict_Next(kv.second.ptr(), &pos, &key, &value)) {
+      PyObject* id = PyDict_GetItemWithError(names.ptr(), key);
+      int64_t nid;
+      if (id) {
+        nid = as_int(id);
+      } else {
+        if (PyErr_Occurred()) throw py::error_already_set();
+        nid = int64_t(PyDict_GET_SIZE(names.ptr()));
+        py::int_ v(nid);
+        if (PyDict_SetItem(names.ptr(), key, v.ptr()) != 0) throw py::error_already_set();
+      }
+      meta_row(value, rank, nid, row);
+      if (PyList_Append(objs.ptr(), value) != 0) throw py::error_already_set();
+      row += kMetaWords;
+    }
+  }
+  return out;
+}
+
+// A new instance of a plain Python class without running its __init__, and
+// its (fresh) instance dict.
+py::object bare_instance(PyObject* cls, PyObject** dict_out) {
+  static PyObject* empty = PyTuple_New(0);
+  PyTypeObject* type = reinterpret_cast<PyTypeObject*>(cls);
+  PyObject* obj = type->tp_new(type, empty, nullptr);
+  if (!obj) throw py::error_already_set();
+  py::object o = py::reinterpret_steal<py::object>(obj);
+  PyObject* d = PyObject_GenericGetDict(obj, nullptr);   // new reference
+  if (!d) throw py::error_already_set();
+  Py_DECREF(d);   // the instance keeps its dict
+  *dict_out = d;
+  return o;
+}
+
+void set(PyObject* d, PyObject* key, PyObject* value) {
+  if (PyDict_SetItem(d, key, value) != 0) throw py::error_already_set();
+}
+
+// A piece of `shard`: the same TensorMeta with another tp meta or a row
+// interval, built without running the constructor.
+py::object derived(PyObject* meta_cls, PyObject* shard, PyObject* tp_meta, PyObject* rows) {
+  const Names& N = names_();
+  PyObject* d;
+  py::object m = bare_instance(meta_cls, &d);
+  py::object src = attr(shard, N.dict);
+  if (PyDict_Update(d, src.ptr()) != 0) throw py::error_already_set();
+  set(d, N.tp_meta, tp_meta);
+  set(d, N.rows, rows);
+  return m;
+}
+
+// TransferOps of an sr_op table (sr_schedule's output): source metas and
+// destination shards are the layouts' own objects, pieces derived from the
+// shards.
+py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::list dst_objs, py::handle op_cls,
+                  py::handle meta_cls) {
+  const Names& N = names_();
+  if (!PyType_Check(op_cls.ptr()) || !PyType_Check(meta_cls.ptr())) throw py::type_error("classes expected");
+  const int64_t n = ops.ndim() == 2 ? ops.shape(0) : 0;
+  if (n && ops.shape(1) != 9) throw py::value_error("op rows must have 9 columns");
+  py::list out(n);
+  const int64_t* r = ops.data();
+  for (int64_t i = 0; i < n; ++i, r += 9) {
+    const int64_t nid = r[0], s_row = r[3], d_row = r[4], p_idx = r[5], p_deg = r[6], r0 = r[7], r1 = r[8];
+    if (nid < 0 || nid >= int64_t(names.size()) || s_row < 0 || s_row >= int64_t(src_objs.size()) ||
+        d_row < 0 || d_row >= int64_t(dst_objs.size()))
+      throw py::value_error("malformed op row");
+    PyObject* shard = PyList_GET_ITEM(dst_objs.ptr(), d_row);
+    py::object piece;
+    if (r0 >= 0) {
+      py::object tp = attr(shard, N.tp_meta);
+      piece = derived(meta_cls.ptr(), shard, tp.ptr(), py::make_tuple(r0, r1).ptr());
+    } else if (p_deg) {
+      py::object tp = attr(shard, N.tp_meta);
+      if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("shard has no tp_meta");
+      py::tuple ptp = py::make_tuple(py::reinterpret_borrow<py::object>(PyTuple_GET_ITEM(tp.ptr(), 0)), p_idx, p_deg);
+      piece = derived(meta_cls.ptr(), shard, ptp.ptr(), Py_None);
+    } else {
+      piece = py::reinterpret_borrow<py::object>(shard);
+    }
+    PyObject* d;
+    py::object op = bare_instance(op_cls.ptr(), &d);
+    set(d, N.param_name, PyList_GET_ITEM(names.ptr(), nid));
+    set(d, N.src_rank, py::int_(r[1]).ptr());
+    set(d, N.dst_rank, py::int_(r[2]).ptr());
+    set(d, N.src_meta, PyList_GET_ITEM(src_objs.ptr(), s_row));
+    set(d, N.dst_meta, piece.ptr());
+    set(d, N.dst_shard_meta, shard);
+    PyList_SET_ITEM(out.ptr(), i, op.release().ptr());
+  }
+  return out;
+}
+
+// sr_lower's op and meta tables for one destination rank's TransferOps:
+// `shards` maps each name to its destination shard, `name_ids` to its id.
+// Metas are numbered in first-use order (each object once per name); a piece
+// is encoded relative to its shard: (0, 0) for the shard itself, else its tp
+// index and degree (an unsplit piece of a split shard: (0, 1)) and rows.
+py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
+  const Names& N = names_();
+  const int64_t n = int64_t(ops.size());
+  py::array_t<int64_t> op_rows({n, int64_t(9)});
+  int64_t* orow = op_rows.mutable_data();
+  std::vector<int64_t> metas;
+  struct KeyHash {
+    size_t operator()(const std::pair<PyObject*, int64_t>& k) const {
+      return std::hash<PyObject*>()(k.first) * 31u + std::hash<int64_t>()(k.second);
+    }
+  };
+  std::unordered_map<std::pair<PyObject*, int64_t>, int64_t, KeyHash> meta_of;   // (object, name id) -> row
+  auto row_of = [&](PyObject* m, int64_t nid) -> int64_t {
+    const std::pair<PyObject*, int64_t> key(m, nid);
+    auto it = meta_of.find(key);
+    if (it != meta_of.end()) return it->second;
+    const int64_t row = int64_t(metas.size() / kMetaWords);
+    metas.resize(metas.size() + kMetaWords);
+    meta_row(m, 0, nid, metas.data() + row * kMetaWords);
+    meta_of.emplace(key, row);
+    return row;
+  };
+  for (int64_t k = 0; k < n; ++k, orow += 9) {
+    PyObject* op = PyList_GET_ITEM(ops.ptr(), k);
+    py::object name = attr(op, N.param_name);
+    PyObject* nid_obj = PyDict_GetItemWithError(name_ids.ptr(), name.ptr());
+    PyObject* shard = PyDict_GetItemWithError(shards.ptr(), name.ptr());
+    if (!nid_obj || !shard) {
+      if (PyErr_Occurred()) throw py::error_already_set();
+      throw py::key_error("no shard for " + py::str(name).cast<std::string>());
+    }
+    const int64_t nid = as_int(nid_obj);
+    py::object m = attr(op, N.dst_meta);
+    int64_t idx = 0, deg = 0, r0 = -1, r1 = -1;
+    if (m.ptr() != shard) {
+      const std::string nm = py::str(name).cast<std::string>();
+      py::object mk = attr(m.ptr(), N.kind), sk = attr(shard, N.kind);
+      py::object ms = attr(m.ptr(), N.shape), ss = attr(shard, N.shape);
+      const int same_kind = PyObject_RichCompareBool(mk.ptr(), sk.ptr(), Py_EQ);
+      const int same_shape = PyObject_RichCompareBool(ms.ptr(), ss.ptr(), Py_EQ);
+      if (same_kind < 0 || same_shape < 0) throw py::error_already_set();
+      if (!same_kind || !same_shape)
+        assertion(nm + ": piece " + py::str(m).cast<std::string>() + " is not part of shard " +
+                  py::str(py::handle(shard)).cast<std::string>());
+      py::object tp = attr(m.ptr(), N.tp_meta), stp = attr(shard, N.tp_meta);
+      if (tp.ptr() == Py_None) {   // an unsplit piece: the whole tensor
+        deg = stp.ptr() != Py_None ? 1 : 0;
+      } else {
+        if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("malformed tp_meta");
+        if (stp.ptr() != Py_None) {
+          const int same_dim = PyObject_RichCompareBool(PyTuple_GET_ITEM(tp.ptr(), 0),
+                                                        PyTuple_GET_ITEM(stp.ptr(), 0), Py_EQ);
+          if (same_dim < 0) throw py::error_already_set();
+          if (!same_dim)
+            assertion(nm + ": piece " + py::str(m).cast<std::string>() + " is split along another dim than shard " +
+                      py::str(py::handle(shard)).cast<std::string>());
+        }
+        idx = as_int(PyTuple_GET_ITEM(tp.ptr(), 1));
+        deg = as_int(PyTuple_GET_ITEM(tp.ptr(), 2));
+      }
+      py::object rows = attr(m.ptr(), N.rows);
+      if (rows.ptr() != Py_None) {
+        if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2) throw py::value_error("malformed rows");
+        r0 = as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
+        r1 = as_int(PyTuple_GET_ITEM(rows.ptr(), 1));
+      }
+    }
+    py::object src = attr(op, N.src_meta);
+    orow[0] = nid;
+    orow[1] = as_int(attr(op, N.src_rank).ptr());
+    orow[2] = as_int(attr(op, N.dst_rank).ptr());
+    orow[3] = row_of(src.ptr(), nid);
+    orow[4] = row_of(shard, nid);
+    orow[5] = idx;
+    orow[6] = deg;
+    orow[7] = r0;
+    orow[8] = r1;
+  }
+  const int64_t n_metas = int64_t(metas.size() / kMetaWords);
+  py::array_t<int64_t> meta_arr({n_metas, kMetaWords});
+  std::copy(metas.begin(), metas.end(), meta_arr.mutable_data());
+  return py::make_tuple(meta_arr, op_rows);
+}
+
+// Elements of every op's piece (op.dst_meta): a row interval times the
+// other dims, else the global size over the tp degree (TensorMeta.numel of
+// a chunk piece).  Used to balance launch groups.
+py::array_t<int64_t> piece_numels(py::list ops) {
+  const Names& N = names_();
+  const int64_t n = int64_t(ops.size());
+  py::array_t<int64_t> out({n});
+  int64_t* o = out.mutable_data();
+  for (int64_t k = 0; k < n; ++k) {
+    py::object m = attr(PyList_GET_ITEM(ops.ptr(), k), N.dst_meta);
+    py::object shape = attr(m.ptr(), N.shape), tp = attr(m.ptr(), N.tp_meta), rows = attr(m.ptr(), N.rows);
+    if (!PyTuple_Check(shape.ptr())) throw py::type_error("TensorMeta.shape must be a tuple");
+    const Py_ssize_t nd = PyTuple_GET_SIZE(shape.ptr());
+    int64_t v = 1;
+    if (rows.ptr() != Py_None) {
+      if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2) throw py::value_error("malformed rows");
+      v = as_int(PyTuple_GET_ITEM(rows.ptr(), 1)) - as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
+      for (Py_ssize_t d = 1; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
+    } else {
+      for (Py_ssize_t d = 0; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
+      if (tp.ptr() != Py_None) {
+        if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("malformed tp_meta");
+        const int64_t deg = as_int(PyTuple_GET_ITEM(tp.ptr(), 2));
+        if (deg > 0) v /= deg;
+      }
+    }
+    o[k] = v;
+  }
+  return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_suika_host, m) {
@@ -279,4 +591,9 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
   m.def("arena_views", &arena_views, py::arg("buf"), py::arg("names"), py::arg("fields"), py::arg("rows"),
         py::arg("dtypes"));
+  m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
+  m.def("piece_numels", &piece_numels, py::arg("ops"));
+  m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
+  m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
+        py::arg("op_cls"), py::arg("meta_cls"));
 }

@@ -381,47 +381,15 @@ class TransferOp:
              f"{self.src_meta.slice_dim()} and dst {self.dst_meta.slice_dim()}")
 
 
-_KIND_CODE = {CHUNK: 0, VOCAB_PAD: 1, QKV_HEADS: 2}
 _SHAPE_PAD = [(0,) * (8 - n) for n in range(9)]
-_ARGS_PAD = [(0,) * (3 - n) for n in range(4)]
-_NO_TP = (0, 0, 0)
-_NO_ROWS = (-1, -1)
-
-
-def meta_words(m: TensorMeta, rank: int, name_id: int) -> tuple:
-    """One sr_meta row (21 int64) of ``m``."""
-    shape, args = m.shape, m.kind_args
-    nd = len(shape)
-    assert nd <= 8 and len(args) <= 3, f"{m.name}: {nd}-D shape / {len(args)} kind args"
-    return (rank, name_id, m.dtype.itemsize, nd, *shape, *_SHAPE_PAD[nd], *(m.tp_meta or _NO_TP),
-            _KIND_CODE[m.kind], *args, *_ARGS_PAD[len(args)], *(m.rows or _NO_ROWS))
 
 
 def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta]):
     """A layout as an [n, 21] int64 sr_meta table, rank by rank in the
-    layout's order; ``objs`` receives the TensorMeta of every row."""
-    import numpy as np
-    out: List[int] = []
-    ext = out.extend
-    keep = objs.append
-    for rank, metas in pl.layout.items():
-        for name, m in metas.items():
-            nid = names.get(name)
-            if nid is None:
-                nid = names[name] = len(names)
-            ext(meta_words(m, rank, nid))
-            keep(m)
-    return np.array(out, dtype=np.int64).reshape(-1, 21)
-
-
-def _derived(shard: TensorMeta, tp_meta: Optional[TPMeta], rows: Optional[Tuple[int, int]]) -> TensorMeta:
-    """A piece of ``shard``: the same tensor with another tp meta or a row
-    interval (what scale_to_tp / with_rows build), without re-validating."""
-    m = TensorMeta.__new__(TensorMeta)
-    m.__dict__.update(shard.__dict__)
-    m.tp_meta = tp_meta
-    m.rows = rows
-    return m
+    layout's order; ``names`` maps tensor names to ids and ``objs`` receives
+    the TensorMeta of every row (the host extension walks the dicts)."""
+    from . import _lib
+    return _lib.host().encode_layout(pl.layout, names, objs)
 
 
 def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layout: ParamLayout,
@@ -463,26 +431,9 @@ def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layou
         msg = re.sub(r"#(\d+)", lambda g: by_id[int(g.group(1))], _lib.last_error(L))
         raise _lib.PlanError(f"schedule_param_transfer: {msg}")
 
-    schedule: List[TransferOp] = []
-    append = schedule.append
-    by_id = list(names)
-    new_op = TransferOp.__new__
-    for nid, s_rank, d_rank, s_row, d_row, p_idx, p_deg, r0, r1 in ops[:n_ops.value].tolist():
-        shard = dst_objs[d_row]
-        if r0 >= 0:
-            piece = _derived(shard, shard.tp_meta, (r0, r1))
-        elif p_deg:
-            piece = _derived(shard, (shard.tp_meta[0], p_idx, p_deg), None)
-        else:
-            piece = shard
-        op = new_op(TransferOp)
-        op.param_name = by_id[nid]
-        op.src_rank = s_rank
-        op.dst_rank = d_rank
-        op.src_meta = src_objs[s_row]
-        op.dst_meta = piece
-        op.dst_shard_meta = shard
-        append(op)
+    # TransferOps over the layouts' own metas; a piece is its shard with
+    # another tp meta (scale_to_tp) or a row interval (vocab_pad)
+    schedule = _lib.host().make_ops(ops[:n_ops.value], list(names), src_objs, dst_objs, TransferOp, TensorMeta)
     if log_func is not None:
         for op in schedule:
             if op.src_rank != op.dst_rank:

@@ -291,14 +291,11 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
     ``elem_bytes`` (bytes per element over all moved fields) only scales the
     estimate."""
     by_name: Dict[str, List[TransferOp]] = {}
-    for op in ops:
+    numel: Dict[str, int] = {}
+    for op, n in zip(ops, _lib.host().piece_numels(ops).tolist()):
         by_name.setdefault(op.param_name, []).append(op)
-    sizes = []
-    for name_ops in by_name.values():
-        n = 0
-        for op in name_ops:
-            n += op.dst_meta.numel()
-        sizes.append(n * elem_bytes)
+        numel[op.param_name] = numel.get(op.param_name, 0) + n
+    sizes = [numel[name] * elem_bytes for name in by_name]
     total = sum(sizes)
     k = max(1, min(int(pipeline), len(sizes), total // PIPELINE_GROUP_BYTES))
     if k == 1:

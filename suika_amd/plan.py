@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from .geometry import infer_dst_shard
-from .meta import _SHAPE_PAD, TensorMeta, TransferOp, meta_words
+from .meta import _SHAPE_PAD, TensorMeta, TransferOp
 
 SrcKey = Tuple[int, str, str]   # (source rank, name, field)
 DstKey = Tuple[str, str]        # (name, field)
@@ -181,41 +181,9 @@ class ReshardPlan:
             shard = name_ops[0].dst_shard_meta
             self.dst_metas[name] = shard if shard is not None else infer_dst_shard(name_ops)
 
-        meta_row: Dict[tuple, int] = {}
-        meta_words_: List[int] = []
-        op_words: List[int] = []
-
-        def row_of(m: TensorMeta, nid: int) -> int:
-            key = (id(m), nid)
-            r = meta_row.get(key)
-            if r is None:
-                r = meta_row[key] = len(meta_row)
-                meta_words_.extend(meta_words(m, 0, nid))
-            return r
-
-        for op in ops:
-            name = op.param_name
-            nid = name_id[name]
-            shard = self.dst_metas[name]
-            m = op.dst_meta
-            if m is shard:
-                piece = (0, 0, -1, -1)
-            else:
-                # a piece is the shard's tensor at another degree or rows
-                assert m.kind == shard.kind and tuple(m.shape) == tuple(shard.shape), \
-                    f"{name}: piece {m} is not part of shard {shard}"
-                tp = m.tp_meta
-                if tp is None:   # an unsplit piece: the whole tensor
-                    idx, deg = (0, 1) if shard.tp_meta is not None else (0, 0)
-                else:
-                    assert shard.tp_meta is None or tp[0] == shard.tp_meta[0], \
-                        f"{name}: piece {m} is split along another dim than shard {shard}"
-                    idx, deg = tp[1], tp[2]
-                piece = (idx, deg, *(m.rows or (-1, -1)))
-            op_words.extend((nid, op.src_rank, op.dst_rank, row_of(op.src_meta, nid), row_of(shard, nid), *piece))
-        self._metas_arr = np.array(meta_words_, dtype=np.int64)
-        self._n_metas = len(meta_row)
-        self._ops_arr = np.array(op_words, dtype=np.int64)
+        # sr_lower's op and meta tables (the host extension reads the ops)
+        self._metas_arr, self._ops_arr = _lib.host().encode_ops(ops, self.dst_metas, name_id)
+        self._n_metas = len(self._metas_arr)
 
     def _build(self, specs_arr: np.ndarray, dtypes: List[torch.dtype]) -> None:
         """sr_lower on the tables, then sr_plan_create on its output."""

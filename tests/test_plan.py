@@ -343,3 +343,19 @@ def test_bind_dst_checks_every_destination():
     with pytest.raises(AssertionError, match="tensor is on cpu, the kernels run on cuda:0"):
         plan.bind_dst_ptrs(dst, torch.device("cuda", 0))
     plan.close()
+
+
+def test_pieces_must_belong_to_their_shard():
+    """A hand-built op whose piece is not a part of its destination shard
+    (another tensor shape, or split along another dim) is rejected by name
+    when the plan's tables are encoded."""
+    from suika_amd import TransferOp
+    src = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 2))
+    shard = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 1))
+    specs = {(0, "w", "param"): SlotSpec((4, 4), torch.float32)}
+    other_shape = TensorMeta(name="w", dtype=torch.float32, shape=(8, 8), tp_meta=(0, 0, 2))
+    with pytest.raises(AssertionError, match="w: piece .* is not part of shard"):
+        ReshardPlan([TransferOp("w", 0, 0, src, other_shape, shard)], specs, ["param"])
+    other_dim = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(-1, 0, 2))
+    with pytest.raises(AssertionError, match="w: piece .* is split along another dim than shard"):
+        ReshardPlan([TransferOp("w", 0, 0, src, other_dim, shard)], specs, ["param"])
