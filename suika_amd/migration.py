@@ -64,6 +64,17 @@ def forcefully_free_tensor(tensor: Tensor) -> None:
             tensor.data = torch.empty(0, device="meta")
 
 
+def cuda_gc() -> None:
+    """Collect garbage and return cached device memory to the driver
+    (Suika/utils.py:248-253): Python's collector, then torch's cache, a
+    device synchronisation and the release of unused IPC handles."""
+    gc.collect()
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+        torch.cuda.synchronize()
+        torch.cuda.ipc_collect()
+
+
 def _current_rank(world) -> int:
     if dist.is_available() and dist.is_initialized():
         return dist.get_rank(world)

@@ -359,3 +359,15 @@ def test_pieces_must_belong_to_their_shard():
     other_dim = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(-1, 0, 2))
     with pytest.raises(AssertionError, match="w: piece .* is split along another dim than shard"):
         ReshardPlan([TransferOp("w", 0, 0, src, other_dim, shard)], specs, ["param"])
+
+
+def test_utils_helpers():
+    """forcefully_free_tensor releases a tensor's storage now and cuda_gc runs
+    without a GPU (Suika/utils.py:248-260)."""
+    from suika_amd import cuda_gc, forcefully_free_tensor
+    t = torch.ones(1024)
+    view = t[:8]
+    forcefully_free_tensor(t)
+    assert t.untyped_storage().nbytes() == 0 and view.untyped_storage().nbytes() == 0
+    forcefully_free_tensor("not a tensor")   # ignored, as in the reference
+    cuda_gc()
