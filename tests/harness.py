@@ -167,17 +167,29 @@ POISON = 0xA5
 @contextlib.contextmanager
 def poisoned_allocations():
     """Fill every destination tensor and peer buffer the plan allocates with
-    POISON bytes, so a byte the kernels never write cannot pass as correct
-    by holding a previous run's value."""
+    POISON bytes -- fresh destinations, arena views and buffers alike -- so a
+    byte the kernels never write cannot pass as correct by holding a previous
+    run's value."""
+    from suika_amd import migration
     from suika_amd.plan import ReshardPlan
-    alloc_dst, alloc_buffers = ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers
+    alloc_dst, alloc_dst_ptrs = ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs
+    alloc_buffers, arena_views = ReshardPlan.alloc_buffers, migration._arena_views
 
-    def dst(self, device, **kw):
-        out = alloc_dst(self, device, **kw)
+    poisoned = {"tensors": 0}
+
+    def poison(out):
         for ent in out.values():
             for t in ent.values():
                 t.view(torch.uint8).fill_(POISON)
+                poisoned["tensors"] += 1
         return out
+
+    def dst(self, device, **kw):
+        return poison(alloc_dst(self, device, **kw))
+
+    def dst_ptrs(self, device):
+        out, ptrs = alloc_dst_ptrs(self, device)
+        return poison(out), ptrs
 
     def buffers(self, device):
         out = alloc_buffers(self, device)
@@ -185,11 +197,16 @@ def poisoned_allocations():
             b.fill_(POISON)
         return out
 
-    ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers = dst, buffers
+    def arena(*a, **kw):
+        return poison(arena_views(*a, **kw))
+
+    ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = dst, dst_ptrs
+    ReshardPlan.alloc_buffers, migration._arena_views = buffers, arena
     try:
-        yield
+        yield poisoned
     finally:
-        ReshardPlan.alloc_dst, ReshardPlan.alloc_buffers = alloc_dst, alloc_buffers
+        ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = alloc_dst, alloc_dst_ptrs
+        ReshardPlan.alloc_buffers, migration._arena_views = alloc_buffers, arena_views
 
 
 def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers"):
@@ -199,11 +216,13 @@ def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="b
     ops = w.ops()
     fake = to_device(srcs_np, w, device)
     expected_sub_fields = [(f, "normal") for f in w.src_fields]
-    with poisoned_allocations():
+    with poisoned_allocations() as poisoned:
         out = execute_param_transfer(ops, {}, torch.device(device), expected_sub_fields,
                                      rank=w.dst_rank, fake_source_state_dicts=fake,
                                      recast=w.recast_map, plan_options=plan_options, route=route)
     torch.cuda.synchronize()
+    n_out = sum(len(e) for e in out.values())
+    assert poisoned["tensors"] >= n_out, "destinations were not poisoned before the kernels ran"
     return {n: {f: t2np(t) for f, t in e.items()} for n, e in out.items()}
 
 

@@ -87,10 +87,11 @@ def test_fullsize_index_coded(key):
     # the drop-in operator (launch groups planned while the GPU runs, poisoned
     # destinations) must agree bit for bit as well
     print(f"[gpu fullsize] {key}: execute_param_transfer", flush=True)
-    with poisoned_allocations():
+    with poisoned_allocations() as poisoned:
         out = execute_param_transfer(ops, {}, dev, [(f, "normal") for f in w.src_fields],
                                      rank=w.dst_rank, fake_source_state_dicts=sources, recast=recast)
     torch.cuda.synchronize()
+    assert poisoned["tensors"] >= sum(len(e) for e in out.values()), "destinations were not poisoned"
     for (name, f) in plan.dst_keys:
         if not torch.equal(dst[name][f].view(torch.uint8), out[name][f].view(torch.uint8)):
             bad.append((name, f, "execute_param_transfer"))
