@@ -209,7 +209,7 @@ def poisoned_allocations():
         ReshardPlan.alloc_buffers, migration._arena_views = alloc_buffers, arena_views
 
 
-def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers"):
+def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers", arena=False):
     """Product path: execute_param_transfer on the GPU with peer shards
     resident; destinations and buffers start as POISON bytes."""
     from suika_amd import execute_param_transfer
@@ -219,7 +219,8 @@ def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="b
     with poisoned_allocations() as poisoned:
         out = execute_param_transfer(ops, {}, torch.device(device), expected_sub_fields,
                                      rank=w.dst_rank, fake_source_state_dicts=fake,
-                                     recast=w.recast_map, plan_options=plan_options, route=route)
+                                     recast=w.recast_map, plan_options=plan_options, route=route,
+                                     arena=arena)
     torch.cuda.synchronize()
     n_out = sum(len(e) for e in out.values())
     assert poisoned["tensors"] >= n_out, "destinations were not poisoned before the kernels ran"

@@ -65,7 +65,7 @@ def random_case(seed: int) -> Workload:
 
 
 SEEDS = list(range(60))
-GPU_SEEDS = list(range(60, 90))
+GPU_SEEDS = list(range(60, 120))
 
 
 def _names(w):
@@ -100,7 +100,8 @@ def test_fuzz_gpu(seed):
     glob = index_state(w, _names(w))
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     want = oracle_dest(w, srcs)
-    got = gpu_execute(w, srcs, route="direct" if seed % 2 else "buffers")
+    # both routes, and every third case into one destination arena
+    got = gpu_execute(w, srcs, route="direct" if seed % 2 else "buffers", arena=seed % 3 == 0)
     assert set(got) == set(want)
     for name, ent in want.items():
         for f, a in ent.items():
