@@ -34,6 +34,9 @@
  *     caller.  The library owns only the plan and its descriptor tables.
  *   - Calls that take a hipStream_t are asynchronous and stream-ordered; the
  *     caller synchronizes.  A plan may be used from one host thread at a time.
+ *     A phase's first call builds its device tables on a library stream of
+ *     the device (they read none of the caller's data); the copy kernel on the
+ *     caller's stream waits for them through an event.
  *   - Device pointers must be aligned to their element size; peer buffers
  *     to 16 bytes (torch allocations are 512-byte aligned).
  *   - Status codes: SR_OK (0) on success, a negative sr_status otherwise.

@@ -999,6 +999,24 @@ class TableCache {
     return SR_OK;
   }
 
+  // One stream per device for the first-use setup of plans (table uploads,
+  // tile scan/emit, first bind): default priority, non-blocking, kept for
+  // the process.  It lets a launch group's setup run while the previous
+  // group's copy kernel still occupies the caller's stream.
+  int setup_stream(int device, hipStream_t* out) {
+    std::lock_guard<std::mutex> lock(mu_);
+    for (const auto& ds : streams_)
+      if (ds.first == device) {
+        *out = ds.second;
+        return SR_OK;
+      }
+    hipStream_t s = nullptr;
+    SR_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    streams_.emplace_back(device, s);
+    *out = s;
+    return SR_OK;
+  }
+
   void put_event(int device, hipEvent_t ev) {
     if (!ev) return;
     {
@@ -1020,6 +1038,7 @@ class TableCache {
   std::mutex mu_;
   std::vector<Block> dev_, host_;
   std::vector<std::pair<int, hipEvent_t>> events_;
+  std::vector<std::pair<int, hipStream_t>> streams_;
   size_t dev_bytes_ = 0, host_bytes_ = 0;
 };
 
@@ -1188,9 +1207,16 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   if (rebind && (rc = check_disjoint(ph, ptrs)) != SR_OK) return rc;
   rc = ensure_device(p);
   if (rc != SR_OK) return rc;
-  rc = setup_phase(p, ph, kind != kGather, stream);
+  // A phase's first use builds its tables and binds the pointers on the
+  // device's setup stream: they are the library's own memory and read no
+  // caller data, so they may run while earlier work on `stream` (such as the
+  // previous launch group's copy) is still going.  Later rebinds stay on
+  // `stream`, ordered after the phase's previous launch.
+  const bool first = !ph.ready;
+  hipStream_t setup = stream;
+  if (first && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
+  rc = setup_phase(p, ph, kind != kGather, setup);
   if (rc != SR_OK) return rc;
-  SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
 
   const uint32_t n = uint32_t(ph.rel.size());
   if (rebind) {
@@ -1198,18 +1224,21 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
     // may still be read by the previous launch of this phase.
     SR_HIP_TRY(hipEventSynchronize(ph.ev_staging));
     std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
-    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_kernel, 0));
+    if (!first) {   // here setup == stream: after the tables and the last launch
+      SR_HIP_TRY(hipStreamWaitEvent(setup, ph.ev_setup, 0));
+      SR_HIP_TRY(hipStreamWaitEvent(setup, ph.ev_kernel, 0));
+    }
     SR_HIP_TRY(hipMemcpyAsync(ph.d_ptrs, ph.h_ptrs, ptrs.size() * sizeof(uint64_t),
-                              hipMemcpyHostToDevice, stream));
+                              hipMemcpyHostToDevice, setup));
     hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0,
-                       stream, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
+                       setup, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
     SR_HIP_TRY(hipGetLastError());
-    SR_HIP_TRY(hipEventRecord(ph.ev_staging, stream));
+    SR_HIP_TRY(hipEventRecord(ph.ev_staging, setup));
     ph.bound = ptrs;
     ph.bound_valid = true;
-  } else {
-    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_staging, 0));
   }
+  SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
+  SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_staging, 0));
 
   const uint32_t n_tiles = uint32_t(ph.n_tiles);
   uint32_t grid = n_tiles;
