@@ -83,11 +83,6 @@ def global_matrix(meta: TensorMeta, view: Optional[int] = None) -> Tuple[int, in
     return _matrix(meta.shape, view_axis(meta) if view is None else view)
 
 
-def local_matrix(meta: TensorMeta, view: Optional[int] = None) -> Tuple[int, int]:
-    """``[rows, cols]`` of the shard as stored (``actual_shape``)."""
-    return _matrix(meta.actual_shape(), view_axis(meta) if view is None else view)
-
-
 def _split(n: int, deg: int, what: str) -> int:
     assert n % deg == 0, f"{what}: {n} is not divisible by tp degree {deg}"
     return n // deg

@@ -371,3 +371,17 @@ def test_utils_helpers():
     assert t.untyped_storage().nbytes() == 0 and view.untyped_storage().nbytes() == 0
     forcefully_free_tensor("not a tensor")   # ignored, as in the reference
     cuda_gc()
+
+
+def test_reference_meta_accessors():
+    """TensorMeta.numel / volumn / __eq__ and TransferOp.get_recv_tensor keep
+    the reference's meaning (migration.py:62-67, 120-127, 285-287)."""
+    from suika_amd import TransferOp
+    shard = TensorMeta(name="w", dtype=torch.bfloat16, shape=(8, 6), tp_meta=(-1, 1, 2))
+    assert shard.numel() == 24 and shard.volumn() == 48
+    assert tuple(shard.actual_shape()) == (8, 3)
+    # equality ignores the shard index, as the reference's does
+    assert shard == TensorMeta(name="x", dtype=torch.bfloat16, shape=(8, 6), tp_meta=(-1, 0, 2))
+    assert shard != TensorMeta(name="w", dtype=torch.float32, shape=(8, 6), tp_meta=(-1, 1, 2))
+    recv = TransferOp("w", 0, 1, shard, shard).get_recv_tensor(torch.device("cpu"))
+    assert tuple(recv.shape) == (8, 3) and recv.dtype == torch.bfloat16
