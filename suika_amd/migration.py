@@ -113,11 +113,13 @@ def execute_param_transfer(
     buffers, then unpack: the path an exchange between GPUs goes through);
     ``arena`` places every destination tensor in one allocation (field by
     field over all tensors, schedule order within a field, 256-byte
-    aligned), for a
-    model that adopts them with ``load_state_dict(assign=True)``;
-    ``pipeline`` cuts the transfer into up to that many launch groups of
-    whole tensors, each planned on the host while the GPU runs the previous
-    one (groups of at least 2 GB of pieces).
+    aligned), for a model that adopts them with
+    ``load_state_dict(assign=True)``; ``pipeline`` cuts the transfer into up
+    to that many launch groups of whole tensors, each planned on the host
+    while the GPU runs the previous one (2 GB per group on average at least,
+    growing from a small first one); ``stream`` runs the kernels on that
+    stream, after the work already queued on the current stream (which may
+    be producing the sources).  The call returns when the kernels are done.
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     _lib.lib()   # raises when the HIP library is missing: there is no other path
@@ -163,6 +165,12 @@ def execute_param_transfer(
     # A full pass of Python's cyclic collector over a large heap (tens of ms)
     # would stall the host between launch groups and idle the GPU; it is
     # paused for the call (reference counting still frees memory).
+    if stream is not None:
+        # the sources (and memory the allocator hands out) may still be in
+        # use by work queued on the current stream
+        cur = torch.cuda.current_stream(device)
+        if stream != cur:
+            stream.wait_stream(cur)
     gc_was_enabled = gc.isenabled()
     gc.disable()
     try:

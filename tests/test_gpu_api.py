@@ -219,3 +219,31 @@ def test_get_send_tensor_cuts_the_piece(case):
         back = TransferOp(src.name, 0, 1, piece, src)
         t2 = got.clone()
         assert back.get_send_tensor(t2) is t2
+
+
+def test_execute_on_a_side_stream_waits_for_current_work():
+    """stream=...: the kernels run on the given stream but after the work
+    already queued on the current stream.  Here the sources are filled by
+    device copies queued behind a bounded sleep kernel on the current stream,
+    so a gather that did not wait would read the zeros they replace."""
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] side stream {w.key}", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    real = to_device(srcs, w, "cuda")
+    fake = {r: {n: {f: torch.zeros_like(t) for f, t in e.items()} for n, e in sd.items()}
+            for r, sd in real.items()}
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    torch.cuda._sleep(50_000_000)   # ~20 ms of spinning on the current stream
+    for r, sd in fake.items():
+        for n, e in sd.items():
+            for f, t in e.items():
+                t.copy_(real[r][n][f])
+    out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                 rank=w.dst_rank, fake_source_state_dicts=fake, stream=side)
+    torch.cuda.synchronize()
+    for name, e in want.items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
