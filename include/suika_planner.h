@@ -35,6 +35,8 @@ extern "C" {
 #endif
 
 #define SR_MAX_DIMS 8
+#define SR_MAX_TP_DEG 65536       /* largest tensor-parallel degree accepted */
+#define SR_MAX_SCHEDULE (1 << 26) /* largest schedule sr_schedule produces */
 
 /* Shard kinds: the reference's torch.chunk layout and two extensions. */
 typedef enum sr_shard_kind {
@@ -99,8 +101,9 @@ typedef struct sr_op {
  *
  * Writes at most `cap` ops; *n_ops receives the schedule's length.  Returns
  * SR_EINVAL (nothing usable written) when cap is too small, when a piece
- * has no owner ("illegal transfer"), or on malformed tables; the message
- * names the tensor.
+ * has no owner ("illegal transfer"), on malformed tables (a tp degree above
+ * SR_MAX_TP_DEG among them), or when the schedule would exceed
+ * SR_MAX_SCHEDULE pieces; the message names the tensor.
  */
 int sr_schedule(const sr_meta* src, int64_t n_src, int64_t n_src_ranks,
                 const sr_meta* dst, int64_t n_dst,

@@ -251,7 +251,8 @@ int lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops
     }
     if (op.dst_rank != ops[0].dst_rank)
       return fail(SR_EINVAL, "ops target several ranks (%lld and %lld)", ll(ops[0].dst_rank), ll(op.dst_rank));
-    if (op.piece_tp_deg < 0 || (op.piece_tp_deg > 0 && op.piece_tp_index < 0) || (op.row0 < 0) != (op.row1 < 0) ||
+    if (op.piece_tp_deg < 0 || op.piece_tp_deg > SR_MAX_TP_DEG || (op.piece_tp_deg > 0 && op.piece_tp_index < 0) ||
+        (op.row0 < 0) != (op.row1 < 0) ||
         (op.row0 >= 0 && (op.row1 < op.row0 || op.piece_tp_deg == 0)))
       return fail(SR_EINVAL, "#%lld: malformed piece of op %lld", ll(op.name), ll(k));
     for (int64_t f = 0; f < n_fields; ++f) {

@@ -164,12 +164,14 @@ int schedule(const sr_meta* src, int64_t n_src, int64_t R, const sr_meta* dst, i
         if (max_tp % dm.tp_deg != 0)
           return fail(SR_EINVAL, "scale_to_tp: target degree %lld is not a multiple of %lld (#%lld)",
                       (long long)max_tp, (long long)dm.tp_deg, (long long)dm.name);
-        const int64_t scale = max_tp / dm.tp_deg;
+        const int64_t scale = max_tp / dm.tp_deg;   // <= SR_MAX_TP_DEG (checked degrees)
         for (int64_t i = 0; i < scale; ++i)
           pieces.push_back(View{&dm, scale * dm.tp_index + i, max_tp, -1, -1, false});
       } else {
         pieces.push_back(shard);
       }
+      if (count + int64_t(pieces.size()) > SR_MAX_SCHEDULE)
+        return fail(SR_EINVAL, "sr_schedule: more than %d pieces", SR_MAX_SCHEDULE);
       for (const View& p : pieces) {
         owner_rows.clear();
         bool self_owner = false;

@@ -116,9 +116,9 @@ inline int check_meta(const sr_meta& m, int64_t n_names, const char* table, int6
     if (m.shape[d] < 0) return fail(SR_EINVAL, "#%lld: negative dim", (long long)m.name);
   if (m.kind < SR_KIND_CHUNK || m.kind > SR_KIND_QKV_HEADS)
     return fail(SR_EINVAL, "#%lld: unknown shard kind %lld", (long long)m.name, (long long)m.kind);
-  if (m.tp_deg < 0 || (m.tp_deg > 0 && m.tp_index < 0))
-    return fail(SR_EINVAL, "#%lld: tp meta (%lld, %lld, %lld)", (long long)m.name,
-                (long long)m.slice_dim, (long long)m.tp_index, (long long)m.tp_deg);
+  if (m.tp_deg < 0 || m.tp_deg > SR_MAX_TP_DEG || (m.tp_deg > 0 && m.tp_index < 0))
+    return fail(SR_EINVAL, "#%lld: tp meta (%lld, %lld, %lld) (degree at most %d)", (long long)m.name,
+                (long long)m.slice_dim, (long long)m.tp_index, (long long)m.tp_deg, SR_MAX_TP_DEG);
   if (m.tp_deg > 0 && (m.ndim == 0 || m.slice_dim < -m.ndim || m.slice_dim >= m.ndim))
     return fail(SR_EINVAL, "#%lld: slice_dim %lld of a %lld-D tensor", (long long)m.name,
                 (long long)m.slice_dim, (long long)m.ndim);
@@ -126,6 +126,15 @@ inline int check_meta(const sr_meta& m, int64_t n_names, const char* table, int6
       (m.tp_deg == 0 || (m.slice_dim != 0 && m.slice_dim != -m.ndim) || m.kind_args[0] < 1))
     return fail(SR_EINVAL, "#%lld: vocab_pad is a TP layout sharded along dim 0 with a "
                 "positive pad multiple", (long long)m.name);
+  if (m.kind == SR_KIND_QKV_HEADS) {
+    // rows == (n_q + 2 n_kv) * head_dim, as TensorMeta's constructor asserts
+    int64_t heads, rows;
+    const int64_t n_q = m.kind_args[0], n_kv = m.kind_args[1], hd = m.kind_args[2];
+    if (m.ndim < 1 || n_q < 1 || n_kv < 1 || hd < 1 || !mul(n_kv, 2, &heads) ||
+        __builtin_add_overflow(heads, n_q, &heads) || !mul(heads, hd, &rows) || rows != m.shape[0])
+      return fail(SR_EINVAL, "#%lld: qkv_heads rows %lld != (n_q + 2 n_kv) * head_dim", (long long)m.name,
+                  (long long)(m.ndim ? m.shape[0] : 0));
+  }
   if ((m.row0 < 0) != (m.row1 < 0) || (m.row0 >= 0 && m.row1 < m.row0))
     return fail(SR_EINVAL, "#%lld: row interval [%lld, %lld)", (long long)m.name, (long long)m.row0,
                 (long long)m.row1);

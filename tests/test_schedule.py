@@ -175,6 +175,7 @@ def test_raw_call_reports_the_needed_table_size():
     ({"kind": 3}, "unknown shard kind"),
     ({"slice_dim": 2}, "slice_dim 2 of a 2-D tensor"),
     ({"row0": 3}, "row interval"),
+    ({"tp_deg": 1 << 40}, "degree at most 65536"),
 ])
 def test_malformed_tables_are_rejected(bad, match):
     spl = ParamLayout.from_metas({0: {"a": _m("a", (8, 4), (0, 0, 2))}, 1: {"a": _m("a", (8, 4), (0, 1, 2))}})
@@ -182,7 +183,7 @@ def test_malformed_tables_are_rejected(bad, match):
     names = {}
     src = _encode_layout(spl, names, [])
     dst = _encode_layout(tpl, names, [])
-    col = {"rank": 0, "name": 1, "ndim": 3, "slice_dim": 12, "kind": 15, "row0": 19}
+    col = {"rank": 0, "name": 1, "ndim": 3, "slice_dim": 12, "tp_deg": 14, "kind": 15, "row0": 19}
     src[1, col[next(iter(bad))]] = next(iter(bad.values()))
     L = _lib.lib()
     n = ctypes.c_int64()
@@ -191,3 +192,90 @@ def test_malformed_tables_are_rejected(bad, match):
                        _lib.as_int64_ptr(ops), 8, ctypes.byref(n))
     assert rc == _lib.SR_EINVAL
     assert match in _lib.last_error()
+
+
+def _corrupt(table, rng, n_cells):
+    t = table.copy()
+    for _ in range(n_cells):
+        i = rng.randrange(t.shape[0])
+        j = rng.randrange(t.shape[1])
+        t[i, j] = rng.choice([-(1 << 62), -7, -1, 0, 1, 2, 3, 9, 1 << 20, 1 << 62, int(t[i, j]) + 1])
+    return t
+
+
+@pytest.mark.parametrize("seed", range(120))
+def test_planner_rejects_corrupted_tables_without_crashing(seed):
+    """Random cells of valid sr_meta / sr_op / sr_src_spec tables replaced by
+    extreme or off-by-one values: sr_schedule and sr_lower return a status
+    (and the tables they accept still lower), never crash or read outside the
+    tables."""
+    rng = random.Random(seed)
+    w = random_case(seed)
+    spl, tpl = w.layouts()
+    names = {}
+    src = _encode_layout(spl, names, [])
+    dst = _encode_layout(tpl, names, [])
+    L = _lib.lib()
+    n = ctypes.c_int64()
+    cap = 4 * len(dst) * 16
+    ops = np.zeros((cap, _lib.SR_OP_WORDS), dtype=np.int64)
+    for trial in range(10):
+        s2 = _corrupt(src, rng, rng.randint(1, 3))
+        d2 = _corrupt(dst, rng, rng.randint(0, 2))
+        rc = L.sr_schedule(_lib.as_int64_ptr(s2), len(s2), len(spl.layout), _lib.as_int64_ptr(d2), len(d2),
+                           len(names), 1, _lib.as_int64_ptr(ops), cap, ctypes.byref(n))
+        assert rc in (_lib.SR_OK, _lib.SR_EINVAL, _lib.SR_ENOMEM)
+    # lower one rank's valid schedule with corrupted ops / specs
+    rc = L.sr_schedule(_lib.as_int64_ptr(src), len(src), len(spl.layout), _lib.as_int64_ptr(dst), len(dst),
+                       len(names), 1, _lib.as_int64_ptr(ops), cap, ctypes.byref(n))
+    assert rc == _lib.SR_OK
+    sched = ops[:n.value].copy()
+    sched = sched[sched[:, 2] == sched[0, 2]]
+    metas = np.concatenate([src, dst])
+    sched[:, 4] += len(src)
+    nf = 2
+    specs = np.zeros((len(sched) * nf, _lib.SR_SPEC_WORDS), dtype=np.int64)
+    for k, row in enumerate(sched):
+        m = src[row[3]]
+        nd = int(m[3])
+        shape = m[4:4 + nd].copy()
+        if m[14] > 0 and m[15] == 0:
+            d = int(m[12]) % nd
+            shape[d] //= m[14]
+        for f in range(nf):
+            specs[k * nf + f, :2] = (_lib.SR_DT_F32, nd)
+            specs[k * nf + f, 2:2 + nd] = shape
+    recast = np.array([0, 0], dtype=np.int64)
+    low = ctypes.POINTER(_lib.SrLowering)()
+    for trial in range(10):
+        o2 = _corrupt(sched, rng, rng.randint(1, 3))
+        m2 = _corrupt(metas, rng, rng.randint(0, 2))
+        s2 = _corrupt(specs, rng, rng.randint(0, 2))
+        rc = L.sr_lower(_lib.as_int64_ptr(m2), len(m2), _lib.as_int64_ptr(o2), len(o2), _lib.as_int64_ptr(s2),
+                        nf, _lib.as_int64_ptr(recast), ctypes.byref(low))
+        assert rc in (_lib.SR_OK, _lib.SR_EINVAL, _lib.SR_ENOMEM), rc
+        if rc == _lib.SR_OK:
+            lw = low.contents
+            h = ctypes.c_void_p()
+            rc2 = L.sr_plan_create(lw.src, lw.n_src, lw.dst, lw.n_dst, lw.n_peers, lw.pieces, lw.n_pieces, None,
+                                   ctypes.byref(h))
+            assert rc2 <= 0
+            L.sr_plan_destroy(h)
+            L.sr_lowering_destroy(low)
+
+
+def test_qkv_rows_must_match_heads():
+    """A qkv_heads row whose rows are not (n_q + 2 n_kv) * head_dim is
+    rejected, as TensorMeta's constructor does for Python callers."""
+    m = _m("qkv", (24, 5), (0, 0, 2), kind="qkv_heads", kind_args=(4, 2, 3))
+    names = {}
+    spl = ParamLayout.from_metas({0: {"qkv": m}})
+    src = _encode_layout(spl, names, [])
+    dst = src.copy()
+    src[0, 16] = 5            # n_q 5: (5 + 4) * 3 = 27 rows, not 24
+    L = _lib.lib()
+    n = ctypes.c_int64()
+    ops = np.zeros((8, _lib.SR_OP_WORDS), dtype=np.int64)
+    rc = L.sr_schedule(_lib.as_int64_ptr(src), 1, 1, _lib.as_int64_ptr(dst), 1, 1, 1, _lib.as_int64_ptr(ops), 8,
+                       ctypes.byref(n))
+    assert rc == _lib.SR_EINVAL and "qkv_heads rows 24" in _lib.last_error()
