@@ -314,3 +314,51 @@ def test_host_arena_views_checks_rows():
         mod.arena_views(buf, ["a"], ["f"], np.array([[60, 1, 2] + [0] * 7], dtype=np.int64), [torch.float32])
     with pytest.raises(ValueError, match="outside the buffer or misaligned"):
         mod.arena_views(buf, ["a"], ["f"], np.array([[2, 1, 2] + [0] * 7], dtype=np.int64), [torch.float32])
+
+
+@pytest.mark.parametrize("seed", range(100))
+def test_plan_create_rejects_corrupted_tables_without_crashing(seed):
+    """Real lowerings with random fields of their sr_piece / sr_tensor tables
+    replaced by extreme or off-by-one values: sr_plan_create returns a status
+    in bounded time and never crashes or reads outside its tables."""
+    import random
+    import time
+
+    import numpy as np
+    import torch
+    from suika_amd.plan import ReshardPlan, SlotSpec
+    from tests.test_fuzz import random_case
+    rng = random.Random(seed)
+    w = random_case(seed)
+    ops = w.ops()
+    dt = w.dtypes
+    specs = {(op.src_rank, op.param_name, f): SlotSpec(tuple(op.src_meta.actual_shape()), dt[f])
+             for op in ops for f in w.src_fields}
+    plan = ReshardPlan(ops, specs, list(w.src_fields), recast=w.recast_map)
+    pieces, src, dst = plan._piece_arr.copy(), plan._src_arr.copy(), plan._dst_arr.copy()
+    n_peers = len(plan.peers)
+    plan.close()
+    L = _lib.lib()
+    extremes = [0, 1, 2, 7, (1 << 31) - 1, (1 << 62), (1 << 64) - 1]
+    for trial in range(20):
+        p2, s2, d2 = pieces.copy(), src.copy(), dst.copy()
+        for _ in range(rng.randint(1, 3)):
+            table = rng.choice([p2, p2, s2, d2]) if len(s2) else p2
+            if not len(table):
+                continue
+            i = rng.randrange(len(table))
+            field = rng.choice(table.dtype.names)
+            if np.issubdtype(table.dtype[field], np.signedinteger):
+                table[field][i] = rng.choice([-1, 0, 1, 3, 1 << 30, int(table[field][i]) + 1])
+            else:
+                table[field][i] = rng.choice(extremes + [(int(table[field][i]) + 1) % (1 << 64)])
+        h = ctypes.c_void_p()
+        t0 = time.perf_counter()
+        rc = L.sr_plan_create(_lib.as_tensors(s2), len(s2), _lib.as_tensors(d2), len(d2), n_peers,
+                              _lib.as_pieces(p2), len(p2), None, ctypes.byref(h))
+        assert time.perf_counter() - t0 < 5.0
+        assert rc <= 0
+        if rc == 0:
+            L.sr_plan_destroy(h)
+        else:
+            assert not h.value
