@@ -75,6 +75,27 @@ def build(verbose: bool = False, out: Path = LIB, defines=()) -> Path:
     return out
 
 
+C_GPU_SRC = REPO_DIR / "tests" / "c" / "abi_gpu_reshard.c"
+C_GPU_BIN = LIB_DIR / "abi_gpu_reshard"
+
+
+def build_c_check(verbose: bool = False, out: Path = C_GPU_BIN) -> Path:
+    """Compile the C11 program that drives the whole native path on the GPU
+    (tests/c/abi_gpu_reshard.c) against the library; its GPU test runs it."""
+    out = Path(out)
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    cc = os.environ.get("CC") or shutil.which("gcc") or "gcc"
+    cmd = [cc, "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}",
+           f"-I{rocm / 'include'}", str(C_GPU_SRC), f"-L{LIB_DIR}", "-lsuika_reshard", f"-L{rocm / 'lib'}",
+           "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{LIB_DIR}", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(out)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("C check build failed:\n" + (res.stdout + res.stderr)[-4000:])
+    return out
+
+
 def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
     """Compile the torch-facing host extension (always recompiles)."""
     import sysconfig
@@ -105,3 +126,4 @@ def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
     print(build_host(verbose="-v" in sys.argv))
+    print(build_c_check(verbose="-v" in sys.argv))
