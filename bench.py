@@ -47,6 +47,9 @@ def parse_args(argv=None):
     ap.add_argument("--temporal", action="store_true",
                     help="ordinary cached loads/stores instead of streaming ones")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--host-sources", action="store_true",
+                    help="also time the direct route with sources copied from pinned host memory "
+                         "(PCIe-inclusive; pins the share's source bytes on the host)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum timed CPU work per thread count")
     ap.add_argument("--cpu-layers", type=int, default=0,
@@ -193,6 +196,50 @@ def api_latency(w, sources, dev, repeats: int = 3) -> dict:
                         "allocator), device-side tile/offset/item tables, gather launch, synchronize"}
 
 
+def host_sources_leg(plan, sources, sp, dp, stream, repeats: int = 3) -> dict:
+    """PCIe-inclusive rate of the direct route: the share's sources start in
+    pinned host memory (as after a checkpoint read), are copied into their HBM
+    tensors (one host-to-device copy per tensor, from one pinned allocation),
+    and one gather follows on the same stream.  Not the headline value: the
+    C ABI takes device pointers, so this adds the host link in front of it."""
+    import torch
+    tensors = [sources[r][n][f] for (r, n, f) in plan.src_keys]
+    offs, total = [], 0
+    for t in tensors:
+        total = (total + 255) // 256 * 256
+        offs.append(total)
+        total += t.numel() * t.element_size()
+    print(f"[bench] host sources: pinning {total / 1e9:.2f} GB", file=sys.stderr, flush=True)
+    host = torch.empty(total, dtype=torch.uint8, pin_memory=True)
+    views = [host[o:o + t.numel() * t.element_size()].view(t.dtype).view(t.shape)
+             for o, t in zip(offs, tensors)]
+    for v, t in zip(views, tensors):
+        v.copy_(t)
+    torch.cuda.synchronize()
+    h2d, gat = [], []
+    for _ in range(repeats + 1):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record(stream)
+        for v, t in zip(views, tensors):
+            t.copy_(v, non_blocking=True)
+        e[1].record(stream)
+        plan.gather_ptrs(sp, dp, stream)
+        e[2].record(stream)
+        torch.cuda.synchronize()
+        h2d.append(e[0].elapsed_time(e[1]))
+        gat.append(e[1].elapsed_time(e[2]))
+    h2d, gat = h2d[1:], gat[1:]
+    del views, host
+    h_ms = sum(h2d) / len(h2d)
+    g_ms = sum(gat) / len(gat)
+    b_gather = plan.gather_bytes
+    return {"source_bytes": total, "tensors": len(tensors), "runs": repeats,
+            "h2d_ms": round(h_ms, 2), "h2d_GBps": round(total / (h_ms * 1e-3) / 1e9, 1),
+            "gather_ms": round(g_ms, 3), "total_ms": round(h_ms + g_ms, 2),
+            "pcie_inclusive_GBps": round(b_gather / ((h_ms + g_ms) * 1e-3) / 1e9, 1),
+            "note": "gather bytes (P + D) over host-to-device copies + gather; not the headline value"}
+
+
 def cpu_model() -> str:
     try:
         import subprocess
@@ -290,6 +337,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     gather_ms = g0.elapsed_time(g1) / K
     b_gather = plan.gather_bytes
+    host_leg = host_sources_leg(plan, sources, sp, dp, stream) if args.host_sources else None
 
     # End to end through the drop-in operator: execute_param_transfer with
     # every source resident on this GPU (route "direct").  Host wall time from
@@ -356,6 +404,7 @@ def main(argv=None) -> int:
                           "GBps": round(b_gather / (gather_ms * 1e-3) / 1e9, 1),
                           "pct_of_peak": round(100 * b_gather / (gather_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)},
         "api": api,
+        "host_sources": host_leg,
         "roofline": {
             "bound": "hbm",
             "kernel": dom,

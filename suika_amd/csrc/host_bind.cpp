@@ -245,6 +245,7 @@ py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, con
   if (buf.scalar_type() != at::kByte || buf.dim() != 1 || !buf.is_contiguous())
     throw py::value_error("the arena must be a contiguous 1-D uint8 tensor");
   py::dict out;
+  const c10::Storage& storage = buf.storage();
   const int64_t* r = rows.data();
   for (int64_t i = 0; i < n; ++i, r += 10) {
     py::handle dt = dtypes[i];
@@ -255,9 +256,17 @@ py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, con
     int64_t numel = 1;
     for (int64_t d = 0; d < nd; ++d) numel *= r[2 + d];
     const int64_t bytes = numel * int64_t(c10::elementSize(st));
-    if (r[0] < 0 || r[0] + bytes > buf.size(0) || r[0] % int64_t(c10::elementSize(st)) != 0)
+    const int64_t esize = int64_t(c10::elementSize(st));
+    if (r[0] < 0 || r[0] + bytes > buf.size(0) || (buf.storage_offset() + r[0]) % esize != 0)
       throw py::value_error("arena row outside the buffer or misaligned");
-    at::Tensor v = buf.narrow(0, r[0], bytes).view(st).view(at::IntArrayRef(r + 2, size_t(nd)));
+    // One tensor on the arena's storage at the row's offset (what
+    // narrow().view(dtype).view(shape) gives, without the three dispatched
+    // ops and two intermediate tensors per view).
+    auto impl = c10::make_intrusive<c10::TensorImpl>(c10::Storage(storage), buf.key_set(),
+                                                     c10::scalarTypeToTypeMeta(st));
+    impl->set_storage_offset((buf.storage_offset() + r[0]) / esize);
+    impl->set_sizes_contiguous(at::IntArrayRef(r + 2, size_t(nd)));
+    at::Tensor v(std::move(impl));
     py::handle name = names[i];
     PyObject* entry = PyDict_GetItemWithError(out.ptr(), name.ptr());
     if (!entry) {

@@ -266,38 +266,39 @@ def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fiel
     by_name: Dict[str, List[TransferOp]] = {}
     for op in ops:
         by_name.setdefault(op.param_name, []).append(op)
-    shapes: Dict[str, Tuple[int, ...]] = {}
-    dtypes: Dict[Tuple[str, str], torch.dtype] = {}
+    # recast targets (bf16 of a moved field) first, then the moved fields
+    targets = [t for t, sf in recast.items() if sf in fields]
+    order = targets + [f for f in fields if f not in recast]
+    n_names, n_fields = len(by_name), len(order)
+    # one row per name: ndim, shape[8]; one dtype per (field, name)
+    geom: List[Tuple[int, ...]] = []
+    numel: List[int] = []
+    field_dts: List[List[torch.dtype]] = [[] for _ in order]
     for name, name_ops in by_name.items():
-        shapes[name] = tuple(int(d) for d in infer_dst_shard(name_ops).actual_shape())
+        shape = tuple(int(d) for d in infer_dst_shard(name_ops).actual_shape())
+        geom.append((len(shape),) + shape + (0,) * (8 - len(shape)))
+        n = 1
+        for d in shape:
+            n *= d
+        numel.append(n)
         entry = source(name_ops[0].src_rank)[name]
-        for f in fields:
-            dtypes[(name, f)] = entry[f].dtype
-        for tgt, sf in recast.items():
-            if sf in fields:
-                dtypes[(name, tgt)] = torch.bfloat16
-    order = list(recast) + [f for f in fields if f not in recast]
-    offsets: Dict[Tuple[str, str], int] = {}
-    end = 0
-    for f in order:
-        for name in by_name:
-            if (name, f) not in dtypes:
-                continue
-            end = (end + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
-            offsets[(name, f)] = end
-            n = 1
-            for d in shapes[name]:
-                n *= d
-            end += n * dtypes[(name, f)].itemsize
+        dt = {f: entry[f].dtype for f in fields}
+        dt.update((t, torch.bfloat16) for t in targets)
+        for k, f in enumerate(order):
+            field_dts[k].append(dt[f])
+    dts = [d for row in field_dts for d in row]
+    itemsize = np.array([d.itemsize for d in dts], dtype=np.int64).reshape(n_fields, n_names)
+    # field by field, names in schedule order, each start 256-byte aligned
+    size = (itemsize * np.array(numel, dtype=np.int64)).reshape(-1)
+    step = (size + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
+    offset = np.zeros_like(size)
+    np.cumsum(step[:-1], out=offset[1:])
+    end = int(offset[-1] + size[-1]) if size.size else 0
     buf = torch.empty(max(1, end), dtype=torch.uint8, device=device)
-    names, fields_, rows, dts = [], [], [], []
-    for (name, f), off in offsets.items():
-        shape = shapes[name]
-        names.append(name)
-        fields_.append(f)
-        rows.extend((off, len(shape), *shape, *(0,) * (8 - len(shape))))
-        dts.append(dtypes[(name, f)])
-    table = np.array(rows, dtype=np.int64).reshape(-1, 10)
+    table = np.concatenate([offset[:, None], np.tile(np.array(geom, dtype=np.int64).reshape(n_names, 9),
+                                                      (n_fields, 1))], axis=1)
+    names = list(by_name) * n_fields
+    fields_ = [f for f in order for _ in range(n_names)]
     return _lib.host().arena_views(buf, names, fields_, table, dts)
 
 

@@ -203,6 +203,53 @@ def test_arena_layout_and_views():
     plan.close()
 
 
+def _arena_restated(ops, dtypes, fields, recast):
+    """execute_param_transfer's arena layout placed tensor by tensor: recast
+    targets first, then the moved fields; names in schedule order within a
+    field; each start rounded up to 256 bytes."""
+    from suika_amd.geometry import infer_dst_shard
+    names = list(dict.fromkeys(op.param_name for op in ops))
+    order = [t for t, sf in recast.items() if sf in fields] + [f for f in fields if f not in recast]
+    end, want = 0, {}
+    for f in order:
+        for name in names:
+            shape = tuple(infer_dst_shard([op for op in ops if op.param_name == name]).actual_shape())
+            dtype = torch.bfloat16 if f in recast else dtypes[f]
+            end = -(-end // 256) * 256
+            want[(name, f)] = (end, shape, dtype)
+            end += int(np.prod(shape, dtype=np.int64)) * dtype.itemsize
+    return want, end
+
+
+@pytest.mark.parametrize("case", ["qwen7b_tp2_tp4", "llama7b_tp4pp2_tp2pp2", "empty"])
+def test_execute_arena_views_layout(case):
+    """The drop-in call's destination arena (built before any plan, then
+    filled by the launch groups) against the placement restated tensor by
+    tensor; a recast target whose source field is not moved gets no slot."""
+    from suika_amd import migration
+    if case == "empty":
+        ops, fields, recast, dtypes = _empty_case(2, 1), ["param"], {}, {"param": torch.float32}
+    else:
+        w = cases.scaled_configs()[case]
+        ops, fields, dtypes = w.ops(), list(w.src_fields), w.dtypes
+        recast = dict(w.recast_map, extra_bf16="not_moved")
+    src = {}
+    for op in ops:
+        src.setdefault(op.src_rank, {})[op.param_name] = {f: torch.empty(0, dtype=dtypes[f]) for f in fields}
+    views = migration._arena_views(ops, src.__getitem__, fields, recast, torch.device("cpu"))
+    want, end = _arena_restated(ops, dtypes, fields, recast)
+    got_keys = {(n, f) for n, e in views.items() for f in e}
+    assert got_keys == set(want)
+    base = next(iter(next(iter(views.values())).values())).untyped_storage()
+    assert base.nbytes() == max(1, end)
+    for (name, f), (off, shape, dtype) in want.items():
+        t = views[name][f]
+        assert t.untyped_storage().data_ptr() == base.data_ptr(), (name, f)
+        # (data_ptr() of a zero-element tensor is 0; its storage offset still counts)
+        assert t.storage_offset() * t.element_size() == off, (name, f)
+        assert tuple(t.shape) == shape and t.dtype == dtype and t.is_contiguous(), (name, f)
+
+
 def _empty_case(tp_src, tp_dst):
     def metas(tp):
         return ParamLayout.from_metas({r: {
