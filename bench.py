@@ -56,6 +56,9 @@ def parse_args(argv=None):
                     help="time a sample with this many destination-stage layers (0: the full share)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a flat copy of BYTES through the library (counter calibration)")
+    ap.add_argument("--row-sweep", type=int, default=0, metavar="BYTES",
+                    help="strided dim -1 pieces (cat / split) of several row widths against a flat "
+                         "copy, BYTES read and written per case, then exit")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -154,6 +157,73 @@ def calibrate_copy(nbytes: int, steps: int) -> dict:
     return {"calibration": "flat copy through sr_pack_kernel", "bytes_read": rows * cols * 4,
             "bytes_written": rows * cols * 4, "ms": round(ms, 4),
             "GBps": round(2 * rows * cols * 4 / ms / 1e6, 1)}
+
+
+ROW_SWEEP_BYTES = (256, 512, 768, 1024, 2048, 4096, 16384)
+
+
+def row_sweep(nbytes: int, steps: int) -> list:
+    """Bandwidth of strided pieces against a flat copy of the same bytes,
+    through sr_gather.  "cat": two [R, C] f32 sources written as the column
+    halves of one [R, 2C] destination (the dim -1 merge: strided writes).
+    "split": one [R, 2C] source read as two [R, C] destinations (the dim -1
+    split: strided reads).  A row of C f32 is the row width swept; every case
+    reads and writes ``nbytes``."""
+    import ctypes
+    import torch
+    from suika_amd import _lib
+    L = _lib.lib()
+    dev = torch.device("cuda", 0)
+    s = torch.cuda.current_stream()
+    F32 = _lib.SR_DT_F32
+
+    def run(src_shapes, dst_shapes, pieces):
+        src = (_lib.SrTensor * len(src_shapes))(*[_lib.SrTensor(r, c, F32, 0) for r, c in src_shapes])
+        dst = (_lib.SrTensor * len(dst_shapes))(*[_lib.SrTensor(r, c, F32, 0) for r, c in dst_shapes])
+        pcs = (_lib.SrPiece * len(pieces))(*[_lib.SrPiece(_lib.SR_PIECE_COPY, 0, si, di, -1, 0, r, c, 0, sc, 0, dc)
+                                             for si, di, r, c, sc, dc in pieces])
+        h = ctypes.c_void_p()
+        _lib.check(L.sr_plan_create(src, len(src_shapes), dst, len(dst_shapes), 1, pcs, len(pieces), None,
+                                    ctypes.byref(h)), "sr_plan_create", L)
+        a = [torch.ones((r, c), dtype=torch.float32, device=dev) for r, c in src_shapes]
+        b = [torch.empty((r, c), dtype=torch.float32, device=dev) for r, c in dst_shapes]
+        vp = ctypes.c_void_p
+        sp = (vp * len(a))(*[t.data_ptr() for t in a])
+        dp = (vp * len(b))(*[t.data_ptr() for t in b])
+        sh = vp(s.cuda_stream)
+        for _ in range(2):
+            _lib.check(L.sr_gather(h, sp, dp, sh), "sr_gather", L)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(s)
+        for _ in range(steps):
+            _lib.check(L.sr_gather(h, sp, dp, sh), "sr_gather", L)
+        e1.record(s)
+        torch.cuda.synchronize()
+        L.sr_plan_destroy(h)
+        del a, b
+        return e0.elapsed_time(e1) / steps
+
+    out = []
+    for width in ROW_SWEEP_BYTES:
+        c = width // 4
+        r = nbytes // (2 * width)
+        cases = {
+            "flat": ([(r, 2 * c)], [(r, 2 * c)], [(0, 0, r, 2 * c, 0, 0)]),
+            "cat": ([(r, c), (r, c)], [(r, 2 * c)], [(0, 0, r, c, 0, 0), (1, 0, r, c, 0, c)]),
+            "split": ([(r, 2 * c)], [(r, c), (r, c)], [(0, 0, r, c, 0, 0), (0, 1, r, c, c, 0)]),
+        }
+        for name, (ss, ds, pcs) in cases.items():
+            if name == "flat" and width != ROW_SWEEP_BYTES[0]:
+                continue
+            ms = run(ss, ds, pcs)
+            moved = 2 * r * 2 * width
+            print(f"[bench] row sweep {name} row {width} B: {ms:.3f} ms", file=sys.stderr, flush=True)
+            out.append({"pattern": name, "row_bytes": width if name != "flat" else None, "rows": r,
+                        "bytes_moved": moved, "ms": round(ms, 4),
+                        "GBps": round(moved / (ms * 1e-3) / 1e9, 1),
+                        "pct_of_peak": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)})
+    return out
 
 
 def api_latency(w, sources, dev, repeats: int = 3) -> dict:
@@ -266,6 +336,11 @@ def main(argv=None) -> int:
     if args.calibrate_copy:
         torch.cuda.set_device(0)
         print(json.dumps(calibrate_copy(args.calibrate_copy, args.steps)), flush=True)
+        return 0
+    if args.row_sweep:
+        torch.cuda.set_device(0)
+        for rec in row_sweep(args.row_sweep, args.steps):
+            print(json.dumps(rec), flush=True)
         return 0
 
     key = args.config or BENCH_CONFIG
