@@ -168,7 +168,8 @@ def row_sweep(nbytes: int, steps: int) -> list:
     halves of one [R, 2C] destination (the dim -1 merge: strided writes).
     "split": one [R, 2C] source read as two [R, C] destinations (the dim -1
     split: strided reads).  A row of C f32 is the row width swept; every case
-    reads and writes ``nbytes``."""
+    reads and writes ``nbytes``.  Two contiguous RECAST cases (the fused
+    fp32 -> bf16 unpack) come first."""
     import ctypes
     import torch
     from suika_amd import _lib
@@ -177,16 +178,25 @@ def row_sweep(nbytes: int, steps: int) -> list:
     s = torch.cuda.current_stream()
     F32 = _lib.SR_DT_F32
 
-    def run(src_shapes, dst_shapes, pieces):
-        src = (_lib.SrTensor * len(src_shapes))(*[_lib.SrTensor(r, c, F32, 0) for r, c in src_shapes])
-        dst = (_lib.SrTensor * len(dst_shapes))(*[_lib.SrTensor(r, c, F32, 0) for r, c in dst_shapes])
-        pcs = (_lib.SrPiece * len(pieces))(*[_lib.SrPiece(_lib.SR_PIECE_COPY, 0, si, di, -1, 0, r, c, 0, sc, 0, dc)
-                                             for si, di, r, c, sc, dc in pieces])
+    BF16 = _lib.SR_DT_BF16
+    tdt = {F32: torch.float32, BF16: torch.bfloat16}
+
+    def run(src_shapes, dst_shapes, pieces, kind=_lib.SR_PIECE_COPY):
+        # shapes are (rows, cols) of f32, or (rows, cols, sr dtype)
+        src_shapes = [s3 if len(s3) == 3 else (*s3, F32) for s3 in src_shapes]
+        dst_shapes = [s3 if len(s3) == 3 else (*s3, F32) for s3 in dst_shapes]
+        src = (_lib.SrTensor * len(src_shapes))(*[_lib.SrTensor(r, c, d, 0) for r, c, d in src_shapes])
+        dst = (_lib.SrTensor * len(dst_shapes))(*[_lib.SrTensor(r, c, d, 0) for r, c, d in dst_shapes])
+        if kind == _lib.SR_PIECE_COPY:
+            recs = [_lib.SrPiece(kind, 0, si, di, -1, 0, r, c, 0, sc, 0, dc) for si, di, r, c, sc, dc in pieces]
+        else:   # RECAST: (src, f32 dst or -1, bf16 dst2, rows, cols)
+            recs = [_lib.SrPiece(kind, 0, si, di, d2, 0, r, c, 0, 0, 0, 0) for si, di, d2, r, c in pieces]
+        pcs = (_lib.SrPiece * len(recs))(*recs)
         h = ctypes.c_void_p()
-        _lib.check(L.sr_plan_create(src, len(src_shapes), dst, len(dst_shapes), 1, pcs, len(pieces), None,
+        _lib.check(L.sr_plan_create(src, len(src_shapes), dst, len(dst_shapes), 1, pcs, len(recs), None,
                                     ctypes.byref(h)), "sr_plan_create", L)
-        a = [torch.ones((r, c), dtype=torch.float32, device=dev) for r, c in src_shapes]
-        b = [torch.empty((r, c), dtype=torch.float32, device=dev) for r, c in dst_shapes]
+        a = [torch.ones((r, c), dtype=tdt[d], device=dev) for r, c, d in src_shapes]
+        b = [torch.empty((r, c), dtype=tdt[d], device=dev) for r, c, d in dst_shapes]
         vp = ctypes.c_void_p
         sp = (vp * len(a))(*[t.data_ptr() for t in a])
         dp = (vp * len(b))(*[t.data_ptr() for t in b])
@@ -205,6 +215,18 @@ def row_sweep(nbytes: int, steps: int) -> list:
         return e0.elapsed_time(e1) / steps
 
     out = []
+    # the fused fp32 -> bf16 recast of unpack, contiguous: f32 + bf16 copies
+    # (4 bytes read, 6 written per element) and the bf16 copy alone (4 read, 2
+    # written), each reading ``nbytes``
+    r, c = nbytes // 4 // 4096, 4096
+    for name, dshapes, pcs in (("recast", [(r, c), (r, c, BF16)], [(0, 0, 1, r, c)]),
+                               ("recast_bf16_only", [(r, c, BF16)], [(0, -1, 0, r, c)])):
+        ms = run([(r, c)], dshapes, pcs, kind=_lib.SR_PIECE_RECAST)
+        moved = r * c * (4 + 2 + (4 if name == "recast" else 0))
+        print(f"[bench] row sweep {name}: {ms:.3f} ms", file=sys.stderr, flush=True)
+        out.append({"pattern": name, "row_bytes": None, "rows": r, "bytes_moved": moved, "ms": round(ms, 4),
+                    "GBps": round(moved / (ms * 1e-3) / 1e9, 1),
+                    "pct_of_peak": round(100 * moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)})
     for width in ROW_SWEEP_BYTES:
         c = width // 4
         r = nbytes // (2 * width)

@@ -119,6 +119,14 @@ constexpr uint64_t kBufAlign = 256;
 #endif
 constexpr uint32_t kXcds = SR_INTERLEAVE_WAYS;
 constexpr uint32_t kMaxGrid = 0xffffffffu / kBlock;    // grid work-items stay below 2^32
+// A RECAST item that writes the f32 copy and the bf16 copy moves 2.5x its
+// source bytes (a COPY item 2x); its tiles hold tile_bytes >> this many
+// source bytes, so a workgroup's pass stays near a copy tile's traffic.
+#ifndef SR_RECAST_TILE_SHIFT
+#define SR_RECAST_TILE_SHIFT 1
+#endif
+constexpr uint32_t kRecastTileShift = SR_RECAST_TILE_SHIFT;
+static_assert(kRecastTileShift <= 2, "RECAST tiles of at least tile_bytes / 4 (>= 1 KiB)");
 
 // ---------------------------------------------------------------- errors
 
@@ -467,7 +475,13 @@ __global__ __launch_bounds__(kBlock) void sr_gather_kernel(const DevItem* __rest
 enum : uint32_t {
   kRelSrcBuf = 1u << 16,   // source side is a peer buffer at the piece's offset
   kRelDstBuf = 1u << 17,   // destination side is a peer buffer at the piece's offset
+  kRelTileShiftBit = 20,   // bits 20-23: the item's tiles are tile_bytes >> this
 };
+
+// log2 of an item's tile size in source bytes.
+__host__ __device__ inline uint32_t item_tile_shift(uint32_t kind, uint32_t tile_shift) {
+  return tile_shift - ((kind >> kRelTileShiftBit) & 0xfu);
+}
 
 struct alignas(8) DevRel {
   uint64_t src_off;        // byte offset of the region origin in its object
@@ -480,7 +494,8 @@ struct alignas(8) DevRel {
   uint32_t row_bytes;      // 0 = contiguous
   uint32_t magic;
   uint32_t shifts;
-  uint32_t kind;           // bits 0-7 kind, 8-15 element bytes, kRelSrcBuf / kRelDstBuf
+  uint32_t kind;           // bits 0-7 kind, 8-15 element bytes, kRelSrcBuf / kRelDstBuf,
+                           // bits 20-23 tile size reduction (kRelTileShiftBit)
   int32_t src_slot;        // index into the phase's pointer table, -1 = none
   int32_t dst_slot;
   int32_t dst2_slot;
@@ -547,11 +562,14 @@ __global__ __launch_bounds__(kSetupBlock) void sr_offsets_kernel(
 __global__ __launch_bounds__(kScanBlock) void sr_tile_scan_kernel(const DevRel* __restrict__ rel,
                                                                   uint32_t n, uint32_t tile_shift,
                                                                   uint64_t* __restrict__ tile_base) {
-  const uint64_t tile = uint64_t(1) << tile_shift;
   uint64_t carry = 0;
   for (uint32_t base = 0; base < n; base += kScanBlock) {
     const uint32_t k = base + threadIdx.x;
-    const uint64_t v = k < n ? (rel[k].total + tile - 1) >> tile_shift : 0;
+    uint64_t v = 0;
+    if (k < n) {
+      const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
+      v = (rel[k].total + (uint64_t(1) << sh) - 1) >> sh;
+    }
     uint64_t total;
     const uint64_t ex = block_exclusive_scan<kScanBlock>(v, total);
     if (k < n) tile_base[k] = carry + ex;
@@ -583,6 +601,7 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
   for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
     const uint64_t total = rel[k].total;
     const uint32_t width = rel[k].row_bytes;
+    const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
     const uint64_t cnt = tile_base[k + 1] - tile_base[k];
     // Items of a group have equal tile counts; tile j of member m goes to
     // group_start + j*M + m, so the members' tiles over the same rows are
@@ -591,11 +610,11 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
     const uint64_t gsize = rel[k].group_size;
     const uint64_t b = tile_base[k] - gm * cnt + gm;
     for (uint64_t j = threadIdx.x; j < cnt; j += kSetupBlock) {
-      const uint64_t start = j << tile_shift;
+      const uint64_t start = j << sh;
       const uint64_t left = total - start;
       DevTile t;
       t.item = k;
-      t.nbytes = uint32_t(left < (uint64_t(1) << tile_shift) ? left : (uint64_t(1) << tile_shift));
+      t.nbytes = uint32_t(left < (uint64_t(1) << sh) ? left : (uint64_t(1) << sh));
       t.pad = 0;
       if (width == 0) {
         t.start = start;
@@ -830,6 +849,11 @@ int check_coverage(const std::vector<std::vector<Box>>& boxes, const std::vector
 // block.  A destination row assembled from several pieces (a dim -1 `cat`)
 // is then written by adjacent tiles instead of once per piece, far apart in
 // time, so each DRAM page is opened once rather than once per piece.
+// Tile size reduction of an item (log2): RECAST items writing both copies.
+uint32_t tile_reduce(const HostItem& h) {
+  return (h.kind == kKindRecast && h.dst_slot >= 0) ? kRecastTileShift : 0;
+}
+
 void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_bytes, bool buf_src,
                bool buf_dst, bool group_by_src, bool row_groups) {
   ph.rel.clear();
@@ -856,6 +880,8 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     r.kind = h.kind | (h.esize << 8);
     if (buf_src && h.src_slot >= 0) r.kind |= kRelSrcBuf;
     if (buf_dst && h.dst_slot >= 0) r.kind |= kRelDstBuf;
+    const uint32_t reduce = tile_reduce(h);
+    r.kind |= reduce << kRelTileShiftBit;
     r.src_slot = h.src_slot;
     r.dst_slot = h.dst_slot >= 0 ? int32_t(ph.n_src_base) + h.dst_slot : -1;
     r.dst2_slot = h.dst2_slot >= 0 ? int32_t(ph.n_src_base) + h.dst2_slot : -1;
@@ -867,7 +893,8 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     r.group_size = 1;
     r.group_index = 0;
     ph.rel.push_back(r);
-    ph.n_tiles += (r.total + tile_bytes - 1) / tile_bytes;
+    const uint64_t item_tile = uint64_t(tile_bytes) >> reduce;
+    ph.n_tiles += (r.total + item_tile - 1) / item_tile;
   }
   if (!row_groups) return;
   struct Side {
@@ -886,7 +913,8 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
       const HostItem& a = ph.items[order[i - 1]];
       const HostItem& b = ph.items[order[i]];
       const Side sa = side(a), sb = side(b);
-      chain = !a.contiguous && !b.contiguous && a.kind == b.kind && a.rows == b.rows &&
+      chain = !a.contiguous && !b.contiguous && a.kind == b.kind && tile_reduce(a) == tile_reduce(b) &&
+              a.rows == b.rows &&
               a.row_bytes == b.row_bytes && sa.slot >= 0 && sa.slot == sb.slot &&
               sa.stride == sb.stride && sb.off == sa.off + sa.width;
     }

@@ -181,6 +181,29 @@ def test_tile_counts():
     _lib.lib().sr_plan_destroy(h)
 
 
+def test_tile_counts_recast():
+    """A RECAST item that writes the f32 and the bf16 copy moves 2.5x its
+    source bytes and is cut into tiles of half the tile size; a bf16-only
+    RECAST item (2 + 4 bytes per element moved, less than a copy's 8) keeps
+    the full tile."""
+    tile = 4096
+    # [64, 1000] f32 master -> f32 copy + bf16 copy; [64, 700] f32 -> bf16 only
+    src = [(64, 1000, F32), (64, 700, F32)]
+    dst = [(64, 1000, F32), (64, 1000, _lib.SR_DT_BF16), (64, 700, _lib.SR_DT_BF16)]
+    pcs = [piece(kind=_lib.SR_PIECE_RECAST, src=0, peer=0, dst=0, dst2=1, rows=64, cols=1000),
+           piece(kind=_lib.SR_PIECE_RECAST, src=1, peer=0, dst=-1, dst2=2, rows=64, cols=700)]
+    rc, h = _plan(src, dst, 1, pcs, options=_lib.SrPlanOptions(tile, 0, 0, 0))
+    assert rc == _lib.SR_OK, _lib.last_error()
+    info = _lib.SrPlanInfo()
+    assert _lib.lib().sr_plan_info_get(h, ctypes.byref(info)) == 0
+    ceil = lambda n, t: -(-n // t)  # noqa: E731
+    assert info.pack_tiles == ceil(64 * 1000 * 4, tile) + ceil(64 * 700 * 4, tile)
+    want = ceil(64 * 1000 * 4, tile // 2) + ceil(64 * 700 * 4, tile)
+    assert info.unpack_tiles == want
+    assert info.gather_tiles == want
+    _lib.lib().sr_plan_destroy(h)
+
+
 def test_python_errors_are_assertion_errors():
     with pytest.raises(AssertionError):
         _lib.check(_lib.SR_EBOUNDS, "x")
