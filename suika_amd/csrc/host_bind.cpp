@@ -13,9 +13,9 @@
 //                    the same checks and messages as the Python host;
 //   alloc_dst:       destination slot rows (sr_slot_key) -> fresh tensors in
 //                    {name: {field: tensor}} and their addresses;
-//   bind_dst:        caller-provided destinations (an arena's views) checked
+//   bind_dst:        caller-provided destinations (e.g. an arena's tensors) checked
 //                    against the slot rows -> their addresses;
-//   arena_views:     the same dict of typed views into one allocation;
+//   arena_views:     the same dict of typed tensors on one allocation's storage;
 //   encode_layout:   a ParamLayout as an sr_meta table (sr_schedule's input);
 //   make_ops:        sr_schedule's op table as TransferOp objects;
 //   encode_ops:      one rank's TransferOps as sr_lower's op and meta tables;
@@ -234,8 +234,8 @@ py::array_t<uint64_t> bind_dst(py::dict part, const RowTable& rows, py::list nam
   return ptrs;
 }
 
-// Typed views of one byte buffer (a destination arena): row i is
-// (byte offset, ndim, shape[8]); out[names[i]][fields[i]] is the view.
+// Typed tensors on the storage of one byte buffer (a destination arena): row i is
+// (byte offset, ndim, shape[8]); out[names[i]][fields[i]] is its tensor.
 py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, const RowTable& rows,
                      py::list dtypes) {
   const int64_t n = rows.ndim() == 2 ? rows.shape(0) : 0;

@@ -259,7 +259,7 @@ ARENA_ALIGN = 256
 
 def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fields: List[str],
                  recast: Mapping[str, str], device: torch.device) -> StateDict:
-    """Every destination tensor of the transfer as a view of one allocation,
+    """Every destination tensor of the transfer on the storage of one allocation,
     laid out before any plan is built: field by field (bf16 recast targets
     first, then the moved fields), tensors in schedule order within a field,
     each at a 256-byte aligned offset.  Launch groups then write into it."""

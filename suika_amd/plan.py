@@ -387,7 +387,7 @@ class ReshardPlan:
 
     def alloc_dst(self, device, arena: bool = False) -> Dict[str, Dict[str, torch.Tensor]]:
         """Fresh destination tensors, one per (name, field).  With ``arena``
-        they are views of one allocation laid out by ``arena_layout`` (one
+        they share the storage of one allocation laid out by ``arena_layout`` (one
         allocator call instead of one per tensor; a model adopting them with
         ``load_state_dict(assign=True)`` keeps them in place)."""
         if not arena:
