@@ -112,6 +112,9 @@ def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
            f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H",
            "-DTORCH_EXTENSION_NAME=_suika_host",
            *[f"-I{p}" for p in include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           # the library's TensorMeta arithmetic (sr_meta.h) and the headers it uses
+           "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{HOST_SRC.parent}",
+           f"-I{Path(os.environ.get('ROCM_PATH', '/opt/rocm')) / 'include'}",
            str(HOST_SRC), *[f"-L{p}" for p in libdirs], *[f"-Wl,-rpath,{p}" for p in libdirs],
            "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-o", str(tmp)]
     if verbose:

@@ -16,6 +16,8 @@
 //   bind_dst:        caller-provided destinations (e.g. an arena's tensors) checked
 //                    against the slot rows -> their addresses;
 //   arena_views:     the same dict of typed tensors on one allocation's storage;
+//   arena_tensors:   the drop-in call's destination arena: every (name, field)
+//                    of a transfer laid out and allocated in one go;
 //   encode_layout:   a ParamLayout as an sr_meta table (sr_schedule's input);
 //   make_ops:        sr_schedule's op table as TransferOp objects;
 //   encode_ops:      one rank's TransferOps as sr_lower's op and meta tables;
@@ -29,10 +31,13 @@
 #include <torch/csrc/DynamicTypes.h>
 #include <pybind11/numpy.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <string>
 #include <unordered_map>
 #include <vector>
+
+#include "sr_meta.h"
 
 namespace py = pybind11;
 
@@ -590,6 +595,132 @@ py::array_t<int64_t> piece_numels(py::list ops) {
 
 }  // namespace
 
+// The drop-in call's destination arena (an extension of
+// execute_param_transfer): every destination tensor of `ops` in one
+// allocation, field by field in `order`, names in schedule order within a
+// field, each at a 256-byte aligned offset.  A name's shape is the actual
+// shape of its destination shard: dst_shard_meta when attached, else the
+// pieces' tp indices merged at the piece degree (infer_dst_shard).  A field
+// in `targets` is bf16 (a recast target); any other takes the dtype of the
+// name's source tensor.  Returns {name: {field: tensor}}.
+py::dict arena_tensors(py::list ops, py::function source, py::list order, py::list targets, at::Device device) {
+  const Names& N = names_();
+  py::dict index;                          // name -> position in `groups`
+  std::vector<std::vector<PyObject*>> groups;
+  std::vector<py::object> names;
+  for (py::handle op : ops) {
+    py::object name = attr(op.ptr(), N.param_name);
+    PyObject* at = PyDict_GetItemWithError(index.ptr(), name.ptr());
+    if (!at && PyErr_Occurred()) throw py::error_already_set();
+    size_t g;
+    if (at) {
+      g = size_t(PyLong_AsSize_t(at));
+    } else {
+      g = groups.size();
+      index[name] = py::int_(g);
+      groups.emplace_back();
+      names.push_back(name);
+    }
+    groups[g].push_back(op.ptr());
+  }
+  const size_t n_names = names.size(), n_fields = order.size();
+  std::vector<bool> is_target(n_fields, false);
+  for (size_t k = 0; k < n_fields; ++k)
+    for (py::handle t : targets)
+      if (PyObject_RichCompareBool(order[k].ptr(), t.ptr(), Py_EQ) == 1) is_target[k] = true;
+  std::vector<int64_t> ndim(n_names), numel(n_names, 1), dims(n_names * SR_MAX_DIMS, 0);
+  std::vector<at::ScalarType> st(n_fields * n_names);
+  py::dict sources;
+  for (size_t i = 0; i < n_names; ++i) {
+    PyObject* first = groups[i][0];
+    const std::string nm = py::str(names[i]).cast<std::string>();
+    sr_meta m;
+    int64_t* row = reinterpret_cast<int64_t*>(&m);
+    sr_internal::View v;
+    py::object shard = attr(first, N.dst_shard_meta);
+    if (shard.ptr() != Py_None) {
+      meta_row(shard.ptr(), 0, 0, row);
+      v = sr_internal::view_of(m);
+    } else {
+      meta_row(attr(first, N.dst_meta).ptr(), 0, 0, row);
+      if (m.row0 >= 0) assertion(nm + ": vocab pieces need dst_shard_meta");
+      v = sr_internal::view_of(m);
+      if (m.tp_deg > 0 && groups[i].size() > 1) {
+        std::vector<int64_t> idx;
+        for (PyObject* op : groups[i]) {
+          py::object tp = attr(attr(op, N.dst_meta).ptr(), N.tp_meta);
+          if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3)
+            throw py::value_error("tp_meta must be (slice_dim, tp_index, tp_deg)");
+          idx.push_back(as_int(PyTuple_GET_ITEM(tp.ptr(), 1)));
+        }
+        std::sort(idx.begin(), idx.end());
+        const int64_t cnt = int64_t(idx.size()), T = m.tp_deg;
+        bool ok = T % cnt == 0 && idx[0] % cnt == 0;
+        for (int64_t j = 0; ok && j < cnt; ++j) ok = idx[j] == idx[0] + j;
+        if (!ok) {
+          std::string list = "[";
+          for (int64_t j = 0; j < cnt; ++j) list += (j ? ", " : "") + std::to_string(idx[j]);
+          assertion(nm + ": pieces " + list + "] at degree " + std::to_string(T) + " do not form one shard");
+        }
+        v.tp_index = idx[0] / cnt;
+        v.tp_deg = T / cnt;
+        v.whole = false;
+      }
+    }
+    if (!sr_internal::actual_shape(v, &dims[i * SR_MAX_DIMS]))
+      assertion(nm + ": destination shard shape overflows");
+    ndim[i] = m.ndim;
+    for (int64_t d = 0; d < m.ndim; ++d) {
+      const int64_t e = dims[i * SR_MAX_DIMS + d];
+      if (e < 0 || __builtin_mul_overflow(numel[i], e, &numel[i])) assertion(nm + ": bad destination shape");
+    }
+    // dtypes: bf16 for recast targets, else the source tensor's
+    py::object rank = attr(first, N.src_rank);
+    py::object sd = lookup(sources.ptr(), rank.ptr());
+    if (!sd) {
+      sd = source(rank);
+      sources[rank] = sd;
+    }
+    py::object entry = lookup(sd.ptr(), names[i].ptr());
+    if (!entry) assertion("param missing in source " + nm);
+    for (size_t k = 0; k < n_fields; ++k) {
+      if (is_target[k]) {
+        st[k * n_names + i] = at::kBFloat16;
+        continue;
+      }
+      py::object t = lookup(entry.ptr(), order[k].ptr());
+      if (!t || !THPVariable_Check(t.ptr()))
+        assertion("expected_sub_fields mismatch: " + nm + " has no tensor " + py::str(order[k]).cast<std::string>());
+      st[k * n_names + i] = THPVariable_Unpack(t.ptr()).scalar_type();
+    }
+  }
+  // field by field, names in schedule order, each start 256-byte aligned
+  std::vector<int64_t> offset(n_fields * n_names);
+  int64_t end = 0;
+  for (size_t j = 0; j < n_fields * n_names; ++j) {
+    const int64_t bytes = numel[j % n_names] * int64_t(c10::elementSize(st[j]));
+    end = (end + 255) / 256 * 256;
+    offset[j] = end;
+    end += bytes;
+  }
+  at::Tensor buf = at::empty({std::max<int64_t>(1, end)}, at::TensorOptions().dtype(at::kByte).device(device));
+  const c10::Storage& storage = buf.storage();
+  std::vector<py::dict> entries(n_names);
+  py::dict out;
+  for (size_t i = 0; i < n_names; ++i) out[names[i]] = entries[i];
+  for (size_t k = 0; k < n_fields; ++k)
+    for (size_t i = 0; i < n_names; ++i) {
+      const size_t j = k * n_names + i;
+      auto impl = c10::make_intrusive<c10::TensorImpl>(c10::Storage(storage), buf.key_set(),
+                                                       c10::scalarTypeToTypeMeta(st[j]));
+      impl->set_storage_offset(offset[j] / int64_t(c10::elementSize(st[j])));
+      impl->set_sizes_contiguous(at::IntArrayRef(&dims[i * SR_MAX_DIMS], size_t(ndim[i])));
+      py::object wrapped = py::reinterpret_steal<py::object>(THPVariable_Wrap(at::Tensor(std::move(impl))));
+      if (PyDict_SetItem(entries[i].ptr(), order[k].ptr(), wrapped.ptr()) != 0) throw py::error_already_set();
+    }
+  return out;
+}
+
 PYBIND11_MODULE(_suika_host, m) {
   m.doc() = "Per-tensor host work of execute_param_transfer (source checks, destination allocation)";
   m.def("collect_sources", &collect_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
@@ -600,6 +731,8 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
   m.def("arena_views", &arena_views, py::arg("buf"), py::arg("names"), py::arg("fields"), py::arg("rows"),
         py::arg("dtypes"));
+  m.def("arena_tensors", &arena_tensors, py::arg("ops"), py::arg("source"), py::arg("order"), py::arg("targets"),
+        py::arg("device"));
   m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
   m.def("piece_numels", &piece_numels, py::arg("ops"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));

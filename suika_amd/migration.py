@@ -27,14 +27,12 @@ from __future__ import annotations
 import gc
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
-import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
 from torch.nn import Module
 from torch.optim import Optimizer
 
-from .geometry import infer_dst_shard
 from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
                    schedule_param_transfer)
 from . import _lib
@@ -254,52 +252,19 @@ PIPELINE_GROUP_BYTES = 2 << 30
 # the GPU time of the same pieces, so each group may be this much larger than
 # the one before it and still be planned before the GPU runs dry.
 PIPELINE_GROWTH = 1.3
-ARENA_ALIGN = 256
 
 
 def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fields: List[str],
                  recast: Mapping[str, str], device: torch.device) -> StateDict:
-    """Every destination tensor of the transfer on the storage of one allocation,
-    laid out before any plan is built: field by field (bf16 recast targets
-    first, then the moved fields), tensors in schedule order within a field,
-    each at a 256-byte aligned offset.  Launch groups then write into it."""
-    by_name: Dict[str, List[TransferOp]] = {}
-    for op in ops:
-        by_name.setdefault(op.param_name, []).append(op)
-    # recast targets (bf16 of a moved field) first, then the moved fields
+    """Every destination tensor of the transfer on the storage of one
+    allocation, laid out before any plan is built: field by field (bf16
+    recast targets first, then the moved fields), tensors in schedule order
+    within a field, each at a 256-byte aligned offset.  Launch groups then
+    write into it.  The shapes (the destination shards'), dtypes, layout and
+    tensors are computed by the host extension in one pass."""
     targets = [t for t, sf in recast.items() if sf in fields]
     order = targets + [f for f in fields if f not in recast]
-    n_names, n_fields = len(by_name), len(order)
-    # one row per name: ndim, shape[8]; one dtype per (field, name)
-    geom: List[Tuple[int, ...]] = []
-    numel: List[int] = []
-    field_dts: List[List[torch.dtype]] = [[] for _ in order]
-    for name, name_ops in by_name.items():
-        shape = tuple(int(d) for d in infer_dst_shard(name_ops).actual_shape())
-        geom.append((len(shape),) + shape + (0,) * (8 - len(shape)))
-        n = 1
-        for d in shape:
-            n *= d
-        numel.append(n)
-        entry = source(name_ops[0].src_rank)[name]
-        dt = {f: entry[f].dtype for f in fields}
-        dt.update((t, torch.bfloat16) for t in targets)
-        for k, f in enumerate(order):
-            field_dts[k].append(dt[f])
-    dts = [d for row in field_dts for d in row]
-    itemsize = np.array([d.itemsize for d in dts], dtype=np.int64).reshape(n_fields, n_names)
-    # field by field, names in schedule order, each start 256-byte aligned
-    size = (itemsize * np.array(numel, dtype=np.int64)).reshape(-1)
-    step = (size + ARENA_ALIGN - 1) // ARENA_ALIGN * ARENA_ALIGN
-    offset = np.zeros_like(size)
-    np.cumsum(step[:-1], out=offset[1:])
-    end = int(offset[-1] + size[-1]) if size.size else 0
-    buf = torch.empty(max(1, end), dtype=torch.uint8, device=device)
-    table = np.concatenate([offset[:, None], np.tile(np.array(geom, dtype=np.int64).reshape(n_names, 9),
-                                                      (n_fields, 1))], axis=1)
-    names = list(by_name) * n_fields
-    fields_ = [f for f in order for _ in range(n_names)]
-    return _lib.host().arena_views(buf, names, fields_, table, dts)
+    return _lib.host().arena_tensors(ops, source, order, targets, device)
 
 
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:

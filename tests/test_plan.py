@@ -221,7 +221,7 @@ def _arena_restated(ops, dtypes, fields, recast):
     return want, end
 
 
-@pytest.mark.parametrize("case", ["qwen7b_tp2_tp4", "llama7b_tp4pp2_tp2pp2", "empty"])
+@pytest.mark.parametrize("case", list(cases.scaled_configs()) + ["empty"])
 def test_execute_arena_views_layout(case):
     """The drop-in call's destination arena (built before any plan, then
     filled by the launch groups) against the placement restated tensor by
@@ -248,6 +248,23 @@ def test_execute_arena_views_layout(case):
         # (data_ptr() of a zero-element tensor is 0; its storage offset still counts)
         assert t.storage_offset() * t.element_size() == off, (name, f)
         assert tuple(t.shape) == shape and t.dtype == dtype and t.is_contiguous(), (name, f)
+
+
+def test_execute_arena_errors():
+    """The arena builder's checks: pieces that do not form one destination
+    shard, and a source entry without a moved field."""
+    from suika_amd import TransferOp, migration
+    src = TensorMeta(name="w", dtype=torch.float32, shape=(8, 4), tp_meta=(0, 0, 4))
+    pieces = [TransferOp("w", 0, 0, src, TensorMeta(name="w", dtype=torch.float32, shape=(8, 4),
+                                                    tp_meta=(0, i, 4))) for i in (0, 2)]
+    sd = {0: {"w": {"param": torch.empty(0)}}}
+    with pytest.raises(AssertionError, match=r"w: pieces \[0, 2\] at degree 4 do not form one shard"):
+        migration._arena_views(pieces, sd.__getitem__, ["param"], {}, torch.device("cpu"))
+    ok = pieces[:1]
+    with pytest.raises(AssertionError, match="w has no tensor exp_avg"):
+        migration._arena_views(ok, sd.__getitem__, ["param", "exp_avg"], {}, torch.device("cpu"))
+    with pytest.raises(AssertionError, match="param missing in source w"):
+        migration._arena_views(ok, {0: {}}.__getitem__, ["param"], {}, torch.device("cpu"))
 
 
 def _empty_case(tp_src, tp_dst):
