@@ -313,12 +313,37 @@ def test_pipeline_groups_keep_tensors_whole():
                 assert not names & seen, "a tensor split across groups"
                 seen |= names
             sizes = [sum(op.dst_meta.numel() for op in g) * elem for g in groups]
-            assert len(groups) == 1 or sum(sizes) / len(groups) >= migration.PIPELINE_GROUP_BYTES
+            names_bytes = {}
+            for op in ops:
+                names_bytes[op.param_name] = names_bytes.get(op.param_name, 0) + op.dst_meta.numel() * elem
+            _, growth, min_bytes = migration._pipeline_shape(list(names_bytes.values()), pipeline)
+            assert len(groups) == 1 or sum(sizes) / len(groups) >= min_bytes
             if len(groups) >= 3:
                 assert sizes[0] < sizes[-1], (key, pipeline, sizes)
     small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
     assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1
+
+
+def test_pipeline_shape_by_tensor_size():
+    """Large tensors on average: at most 4 groups growing 2.5x; small ones:
+    up to ``pipeline`` groups growing 1.3x (the measured optima)."""
+    from suika_amd import migration
+    shapes = {}
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        ops = w.ops()
+        elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+        per_name = {}
+        for op in ops:
+            per_name[op.param_name] = per_name.get(op.param_name, 0) + op.dst_meta.numel() * elem
+        shapes[key] = migration._pipeline_shape(list(per_name.values()), 8)[:2]
+    assert shapes["llama7b_tp4pp2_tp2pp2"] == (4, 2.5)
+    assert shapes["llama13b_tp8_tp4pp2"] == (4, 2.5)
+    assert shapes["qwen7b_tp2_tp4"] == (4, 2.5)
+    assert shapes["gpt6.7b_tp1pp4_tp8"] == (5, 1.3)      # 12.1 GB // 2 GiB
+    assert shapes["gpt125m_tp2_tp4"][0] == 1
+    assert migration._pipeline_shape([], 8)[0] == 1
 
 
 def test_from_sources_rejects_bad_sources_by_name():
