@@ -27,6 +27,7 @@ from __future__ import annotations
 import gc
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
@@ -298,12 +299,23 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
     next, larger one.
     ``elem_bytes`` (bytes per element over all moved fields) only scales the
     estimate."""
-    by_name: Dict[str, List[TransferOp]] = {}
-    numel: Dict[str, int] = {}
-    for op, n in zip(ops, _lib.host().piece_numels(ops).tolist()):
-        by_name.setdefault(op.param_name, []).append(op)
-        numel[op.param_name] = numel.get(op.param_name, 0) + n
-    sizes = [numel[name] * elem_bytes for name in by_name]
+    numel = _lib.host().piece_numels(ops)
+    names = [op.param_name for op in ops]
+    # runs of consecutive ops of one tensor (the schedule emits a tensor's
+    # pieces together); a name that comes back later joins its first run
+    starts = [0] + [i for i in range(1, len(names)) if names[i] != names[i - 1]]
+    if len(starts) == len(set(names)):
+        runs = [(a, b) for a, b in zip(starts, starts[1:] + [len(ops)])] if ops else []
+        sizes = (np.add.reduceat(numel, starts) * elem_bytes).tolist() if ops else []
+        by_name = [ops[a:b] for a, b in runs]
+    else:
+        grouped: Dict[str, List[TransferOp]] = {}
+        count: Dict[str, int] = {}
+        for op, name, n in zip(ops, names, numel.tolist()):
+            grouped.setdefault(name, []).append(op)
+            count[name] = count.get(name, 0) + n
+        by_name = list(grouped.values())
+        sizes = [count[name] * elem_bytes for name in grouped]
     total = sum(sizes)
     k, growth, _ = _pipeline_shape(sizes, pipeline)
     if k == 1:
@@ -317,7 +329,7 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
         bounds.append(acc_w * scale)
     groups: List[List[TransferOp]] = [[]]
     acc = 0
-    for name_ops, n in zip(by_name.values(), sizes):
+    for name_ops, n in zip(by_name, sizes):
         if groups[-1] and len(groups) < k and acc >= bounds[len(groups) - 1]:
             groups.append([])
         groups[-1].extend(name_ops)
