@@ -323,6 +323,18 @@ def test_pipeline_groups_keep_tensors_whole():
     small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
     assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1
+    # a tensor whose ops are not consecutive still lands whole in one group,
+    # at the place of its first op
+    w = CONFIGS["llama7b_tp4pp2_tp2pp2"]
+    ops = list(w.ops())
+    ops = ops[1:] + ops[:1]                  # the first tensor's first op moves to the end
+    groups = migration._pipeline_groups(ops, 14, 8)
+    owner = {}
+    for gi, g in enumerate(groups):
+        for op in g:
+            assert owner.setdefault(op.param_name, gi) == gi
+    assert sorted(map(id, (op for g in groups for op in g))) == sorted(map(id, ops))
+    assert groups[0][0] is ops[0]
 
 
 def test_pipeline_shape_by_tensor_size():
