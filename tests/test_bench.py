@@ -1,0 +1,58 @@
+"""bench.py's contract: one GPU only, the CPU baseline sampler, and the JSON
+line's keys and arithmetic."""
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_more_than_one_gpu_is_refused():
+    out = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], cwd=ROOT, capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 2, out.stdout + out.stderr
+    assert "--gpus 2 is not supported" in out.stderr and out.stdout == ""
+
+
+def test_cpu_baseline_sample():
+    """The torch-CPU leg on a one-layer sample of the GPT-125M share: one
+    untimed run, then timed runs; bytes are the sample's algorithmic bytes."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+    from suika_amd.workloads import CONFIGS
+    t, nbytes, runs, layers = bench.cpu_baseline(CONFIGS["gpt125m_tp2_tp4"], 2, 0.0, layers=1)
+    assert t > 0 and runs >= 1 and layers == 1
+    assert 0 < nbytes < 4 * 0.835e9       # below the full share's B_alg
+
+
+@pytest.mark.gpu
+def test_bench_json_line(tmp_path):
+    """A short run on the smallest workload prints one JSON line with every
+    key the driver reads, self-consistent figures and no CPU baseline when
+    it is switched off."""
+    out_file = tmp_path / "b.json"
+    print("[bench test] gpt125m_tp2_tp4", flush=True)
+    res = subprocess.run([sys.executable, "bench.py", "--config", "gpt125m_tp2_tp4", "--steps", "3", "--warmup", "1",
+                          "--no-cpu-baseline", "--json-out", str(out_file)], cwd=ROOT, capture_output=True,
+                         text=True, timeout=240)
+    assert res.returncode == 0, res.stderr[-3000:]
+    lines = [l for l in res.stdout.splitlines() if l.strip()]
+    assert len(lines) == 1, res.stdout
+    d = json.loads(lines[0])
+    assert json.loads(out_file.read_text()) == d
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+              "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert k in d, k
+    assert d["n_gpus"] == 1 and d["steps"] == 3 and d["warmup"] == 1 and d["unit"] == "GB/s"
+    assert d["higher_is_better"] is True and d["vs_baseline"] is None and d["cpu_baseline"] is None
+    assert d["config"]["key"] == "gpt125m_tp2_tp4" and "workload" in d["config"]
+    b_alg = d["config"]["B_alg_bytes"]
+    assert abs(d["value"] - b_alg / (d["ms_per_step"] * 1e-3) / 1e9) <= 0.1 + 1e-3 * d["value"]
+    r = d["roofline"]
+    assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
+    assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
+    assert r["kernel"] in ("sr_pack_kernel", "sr_unpack_kernel")
+    assert 0.2 < r["frac"] < 1.0
