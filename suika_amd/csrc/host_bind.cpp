@@ -289,6 +289,7 @@ py::dict arena_views(const at::Tensor& buf, py::list names, py::list fields, con
 // ------------------------------------------------------------ layouts and ops
 
 constexpr int64_t kMetaWords = 21;   // sr_meta: rank, name, itemsize, ndim, shape[8], tp[3], kind, args[3], rows[2]
+static_assert(sizeof(sr_meta) == kMetaWords * sizeof(int64_t), "an sr_meta row is 21 int64 words");
 
 int64_t as_int(PyObject* o) {
   const long long v = PyLong_AsLongLong(o);
