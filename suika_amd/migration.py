@@ -27,7 +27,6 @@ from __future__ import annotations
 import gc
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
-import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
@@ -135,7 +134,7 @@ def execute_param_transfer(
     if rank is None:
         rank = _current_rank(world)
 
-    ops = [op for op in transfer_ops if op.dst_rank == rank]
+    ops = _lib.host().ops_of_rank(list(transfer_ops), int(rank))
     normal = [f for f, t in expected_sub_fields if not _is_meta_field(t)]
     scalars = [f for f, t in expected_sub_fields if _is_meta_field(t)]
     recast = dict(recast or {})
@@ -299,21 +298,20 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> L
     next, larger one.
     ``elem_bytes`` (bytes per element over all moved fields) only scales the
     estimate."""
-    numel = _lib.host().piece_numels(ops)
-    names = [op.param_name for op in ops]
+    ops = list(ops)
     # runs of consecutive ops of one tensor (the schedule emits a tensor's
     # pieces together); a name that comes back later joins its first run
-    starts = [0] + [i for i in range(1, len(names)) if names[i] != names[i - 1]]
-    if len(starts) == len(set(names)):
-        runs = [(a, b) for a, b in zip(starts, starts[1:] + [len(ops)])] if ops else []
-        sizes = (np.add.reduceat(numel, starts) * elem_bytes).tolist() if ops else []
-        by_name = [ops[a:b] for a, b in runs]
+    starts, run_numel, single = _lib.host().tensor_runs(ops)
+    if single:
+        ends = starts.tolist()[1:] + [len(ops)]
+        by_name = [ops[a:b] for a, b in zip(starts.tolist(), ends)]
+        sizes = (run_numel * elem_bytes).tolist()
     else:
         grouped: Dict[str, List[TransferOp]] = {}
         count: Dict[str, int] = {}
-        for op, name, n in zip(ops, names, numel.tolist()):
-            grouped.setdefault(name, []).append(op)
-            count[name] = count.get(name, 0) + n
+        for op, n in zip(ops, _lib.host().piece_numels(ops).tolist()):
+            grouped.setdefault(op.param_name, []).append(op)
+            count[op.param_name] = count.get(op.param_name, 0) + n
         by_name = list(grouped.values())
         sizes = [count[name] * elem_bytes for name in grouped]
     total = sum(sizes)
