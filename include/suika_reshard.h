@@ -113,7 +113,10 @@ typedef struct sr_piece {
 /* Plan tuning; pass NULL to sr_plan_create for the defaults. */
 typedef struct sr_plan_options {
   uint32_t tile_bytes;   /* bytes of source data per work tile; power of two in
-                            [4096, 16 MiB]; 0 = default (16384) */
+                            [4096, 16 MiB]; 0 = default (16384).  A RECAST
+                            piece that writes both the f32 and the bf16 copy
+                            moves 2.5x its source bytes and is cut at half
+                            this size */
   uint32_t max_blocks;   /* cap on workgroups per launch (grid-stride beyond;
                             rounded down to a multiple of 8 when the tile list
                             is XCD-interleaved); 0 = one workgroup per tile */
