@@ -61,13 +61,17 @@ EXPORTED_SYMBOLS = (
     "sr_pack",
     "sr_unpack",
     "sr_gather",
+    "sr_gather_noalloc",
     "sr_plan_destroy",
     "sr_schedule",
     "sr_lower",
     "sr_lowering_destroy",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
+
+# Device bytes per GPU that sr_gather_noalloc keeps its tables in (SR_SCRATCH_BYTES).
+SCRATCH_BYTES = 64 << 20
 
 
 class SrTensor(ctypes.Structure):
@@ -292,6 +296,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_unpack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.sr_gather.restype = ctypes.c_int
     lib.sr_gather.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_gather_noalloc.restype = ctypes.c_int
+    lib.sr_gather_noalloc.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
     i64 = ctypes.c_int64

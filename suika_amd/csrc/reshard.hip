@@ -1323,6 +1323,69 @@ int check_ptrs(const void* const* ptrs, size_t n, const std::vector<uint32_t>& a
   return SR_OK;
 }
 
+// Alignment each pointer of a gather must satisfy: its element size; 0 =
+// the slot is not used by the phase.
+void gather_alignment(const sr_plan* plan, std::vector<uint32_t>& sal, std::vector<uint32_t>& dal) {
+  sal.assign(plan->src.size(), 0);
+  dal.assign(plan->dst.size(), 0);
+  for (const sr_piece& pc : plan->pieces) {
+    if (pc.src >= 0) sal[pc.src] = dtype_size(plan->src[pc.src].dtype);
+    if (pc.dst >= 0) dal[pc.dst] = dtype_size(plan->dst[pc.dst].dtype);
+    if (pc.dst2 >= 0) dal[pc.dst2] = dtype_size(plan->dst[pc.dst2].dtype);
+  }
+}
+
+}  // namespace
+
+// ------------------------------------------------------- allocation-free gather
+// The device tables of sr_gather_noalloc live in this array, one copy per GPU,
+// allocated with the code object when the library is loaded on a device and
+// held until the process exits.  On the host, `scratch` names a stand-in, not
+// device memory: host code never passes it to a kernel or a copy, only the
+// per-device address that hipGetSymbolAddress returns (scratch_base below).
+static __device__ __align__(256) unsigned char scratch[SR_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 256;
+std::mutex g_scratch_mu;
+uint64_t g_scratch_addr[kMaxScratchDevices];   // 0 = not looked up yet
+
+// Address of `scratch` on the current device `device`, looked up once per
+// device (with that device current, as hipGetSymbolAddress requires).
+int scratch_base(int device, unsigned char** out) {
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(SR_EINVAL, "device %d out of range for the scratch table", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[device] == 0) {
+    void* p = nullptr;
+    SR_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr) return fail(SR_EHIP, "hipGetSymbolAddress(scratch) returned null on device %d", device);
+    g_scratch_addr[device] = reinterpret_cast<uintptr_t>(p);
+  }
+  *out = reinterpret_cast<unsigned char*>(g_scratch_addr[device]);
+  return SR_OK;
+}
+
+// Where the gather phase's tables sit in the scratch, and how much it needs.
+struct ScratchLayout {
+  size_t rel, ptrs, items, base, tiles, end;
+};
+
+ScratchLayout scratch_layout(const Phase& ph) {
+  const size_t n = ph.rel.size();
+  const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
+  ScratchLayout L{};
+  size_t end = 0;
+  L.rel = carve(end, n * sizeof(DevRel));
+  L.ptrs = carve(end, nptr * sizeof(uint64_t));
+  L.items = carve(end, n * sizeof(DevItem));
+  L.base = carve(end, (n + 1) * sizeof(uint64_t));
+  L.tiles = carve(end, size_t(ph.n_tiles) * sizeof(DevTile));
+  L.end = end;
+  return L;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ C ABI
@@ -1726,18 +1789,78 @@ int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs
 
 int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs, hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
-  std::vector<uint32_t> sal(plan->src.size(), 0), dal(plan->dst.size(), 0);
-  for (const sr_piece& pc : plan->pieces) {
-    if (pc.src >= 0) sal[pc.src] = dtype_size(plan->src[pc.src].dtype);
-    if (pc.dst >= 0) dal[pc.dst] = dtype_size(plan->dst[pc.dst].dtype);
-    if (pc.dst2 >= 0) dal[pc.dst2] = dtype_size(plan->dst[pc.dst2].dtype);
-  }
+  std::vector<uint32_t> sal, dal;
+  gather_alignment(plan, sal, dal);
   int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
   if (rc != SR_OK) return rc;
   rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
   if (rc != SR_OK) return rc;
   return run_phase(plan, plan->gather, kGather,
                    pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size()), stream);
+}
+
+int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
+                      hipStream_t stream) {
+  if (!plan) return fail(SR_EINVAL, "plan is null");
+  const Phase& ph = plan->gather;
+  // The size check comes first: it needs neither the pointers nor a device.
+  const ScratchLayout L = scratch_layout(ph);
+  if (L.end > size_t(SR_SCRATCH_BYTES))
+    return fail(SR_ENOMEM,
+                "sr_gather_noalloc: the plan's gather tables need %zu bytes (%zu items, %llu tiles) but "
+                "the scratch holds %zu; create the plan with a larger tile_bytes or split the transfer",
+                L.end, ph.rel.size(), (unsigned long long)ph.n_tiles, size_t(SR_SCRATCH_BYTES));
+  std::vector<uint32_t> sal, dal;
+  gather_alignment(plan, sal, dal);
+  int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
+  if (rc != SR_OK) return rc;
+  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
+  if (rc != SR_OK) return rc;
+  if (ph.rel.empty()) return SR_OK;
+  const std::vector<uint64_t> ptrs = pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size());
+  if ((rc = check_disjoint(ph, ptrs)) != SR_OK) return rc;
+
+  int dev = -1;
+  SR_HIP_TRY(hipGetDevice(&dev));
+  unsigned char* s = nullptr;
+  if ((rc = scratch_base(dev, &s)) != SR_OK) return rc;
+  DevRel* d_rel = reinterpret_cast<DevRel*>(s + L.rel);
+  uint64_t* d_ptrs = reinterpret_cast<uint64_t*>(s + L.ptrs);
+  DevItem* d_items = reinterpret_cast<DevItem*>(s + L.items);
+  uint64_t* d_base = reinterpret_cast<uint64_t*>(s + L.base);
+  DevTile* d_tiles = reinterpret_cast<DevTile*>(s + L.tiles);
+  const uint32_t n = uint32_t(ph.rel.size());
+
+  // Descriptors and pointers come from pageable host memory, which HIP copies
+  // synchronously: each copy waits for the work queued on `stream` before it
+  // (a previous call may still read the scratch) and the host buffers may be
+  // released on return.  Every table is then written whole on the device --
+  // tile_base by the scan, each tile position by the emit (the interleave is
+  // a permutation), each item by the bind -- so nothing needs clearing.
+  SR_HIP_TRY(hipMemcpyAsync(d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice, stream));
+  SR_HIP_TRY(hipMemcpyAsync(d_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice,
+                            stream));
+  const uint32_t shift = log2u(plan->opt.tile_bytes);
+  hipLaunchKernelGGL(sr_tile_scan_kernel, dim3(1), dim3(kScanBlock), 0, stream, d_rel, n, shift, d_base);
+  SR_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0, stream,
+                     d_rel, d_base, n, shift, ph.n_tiles, ph.interleave ? kXcds : 1u, d_tiles);
+  SR_HIP_TRY(hipGetLastError());
+  // gather items read no buffer offsets (no side is a peer buffer)
+  hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0, stream,
+                     d_rel, n, d_ptrs, static_cast<const uint64_t*>(nullptr), d_items);
+  SR_HIP_TRY(hipGetLastError());
+
+  const uint32_t n_tiles = uint32_t(ph.n_tiles);
+  uint32_t grid = n_tiles;
+  if (plan->opt.max_blocks != 0) grid = std::min(grid, plan->opt.max_blocks);
+  grid = std::min(grid, kMaxGrid);
+  if (ph.interleave && grid < n_tiles && grid >= kXcds) grid -= grid % kXcds;
+  const bool nt = (plan->opt.flags & SR_OPT_TEMPORAL) == 0;
+  hipLaunchKernelGGL(nt ? sr_gather_kernel<true> : sr_gather_kernel<false>, dim3(grid), dim3(kBlock), 0,
+                     stream, d_items, d_tiles, n_tiles);
+  SR_HIP_TRY(hipGetLastError());
+  return SR_OK;
 }
 
 void sr_plan_destroy(sr_plan* plan) {

@@ -466,6 +466,14 @@ class ReshardPlan:
                                _stream_handle(stream))
         _lib.check(rc, "sr_gather", self._L)
 
+    def gather_noalloc_ptrs(self, src_ptrs: List[int], dst_ptrs: List[int], stream=None) -> None:
+        """``sr_gather_noalloc``: the same gather with its device tables in
+        the library's static per-GPU scratch (no device allocation); calls
+        that overlap on one GPU race for it."""
+        rc = self._L.sr_gather_noalloc(self._handle, self._carray(src_ptrs), self._carray(dst_ptrs),
+                                       _stream_handle(stream))
+        _lib.check(rc, "sr_gather_noalloc", self._L)
+
     def gather(self, sources, dst, stream=None) -> None:
         """Source shards -> destination shards directly (async on ``stream``)."""
         self.gather_ptrs(self.src_pointers(sources), self.dst_pointers(dst), stream)

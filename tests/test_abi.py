@@ -21,7 +21,7 @@ def header_functions():
 
 def test_library_loads_and_version():
     L = _lib.lib()
-    assert L.sr_abi_version() == _lib.ABI_VERSION == 3
+    assert L.sr_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_every_declared_symbol_is_exported():
@@ -385,3 +385,29 @@ def test_plan_create_rejects_corrupted_tables_without_crashing(seed):
             L.sr_plan_destroy(h)
         else:
             assert not h.value
+
+
+def test_gather_noalloc_rejects_plans_beyond_the_scratch():
+    """A plan whose gather tables exceed SR_SCRATCH_BYTES is refused with
+    SR_ENOMEM before any device call (so this runs without a GPU); a larger
+    tile size brings the same transfer within the limit."""
+    assert _lib.SCRATCH_BYTES == 64 << 20
+    L = _lib.lib()
+    rows, cols = 1 << 20, 4096            # 16 GiB of f32: 4 Mi tiles of 4 KiB = 96 MiB of tiles
+    small = _lib.SrPlanOptions(4096, 0, 0, 0)
+    rc, h = _plan([(rows, cols, F32)], [(rows, cols, F32)], 1, [piece(rows=rows, cols=cols)], small)
+    assert rc == 0, _lib.last_error()
+    null = (ctypes.c_void_p * 1)(None)
+    assert L.sr_gather_noalloc(h, null, null, None) == _lib.SR_ENOMEM
+    msg = _lib.last_error()
+    assert "scratch holds 67108864" in msg and "tile_bytes" in msg, msg
+    L.sr_plan_destroy(h)
+    # 64 KiB tiles: 256 Ki tiles = 6 MiB; past the size check, the null
+    # pointers are the next thing refused -- still before any device call
+    rc, h = _plan([(rows, cols, F32)], [(rows, cols, F32)], 1, [piece(rows=rows, cols=cols)],
+                  _lib.SrPlanOptions(65536, 0, 0, 0))
+    assert rc == 0, _lib.last_error()
+    assert L.sr_gather_noalloc(h, null, null, None) == _lib.SR_EINVAL
+    assert "src_ptrs[0] is null" in _lib.last_error()
+    L.sr_plan_destroy(h)
+    assert L.sr_gather_noalloc(None, null, null, None) == _lib.SR_EINVAL
