@@ -322,7 +322,12 @@ def execute_fake_source(ops: List[OOp], rank: int, fake_sources: Dict[int, Dict[
 # bf16 rounding (round half to even on the upper 16 bits; NaN -> 0x7FC0)
 
 def rne_bf16(f32: np.ndarray) -> np.ndarray:
-    """float32 (or its uint32 bits) -> bfloat16 bits (uint16)."""
+    """float32 (or its uint32 bits) -> bfloat16 bits (uint16).
+
+    Pinned to torch's CPU ``.to(torch.bfloat16)`` bit for bit on every
+    pattern, NaNs included, as torch converts element by element (a strided
+    or 0-dim tensor); its vectorised loop over a contiguous tensor writes
+    0xFFFF for a NaN instead of 0x7FC0."""
     u = np.ascontiguousarray(f32).view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)

@@ -325,6 +325,31 @@ py::object attr(PyObject* o, PyObject* key) {
   return py::reinterpret_steal<py::object>(v);
 }
 
+// An attribute the reference's own objects do not carry: TensorMeta has only
+// name, dtype, shape and tp_meta (Suika/migration.py:29-58; tp_meta is left
+// unset when built from dtype and shape alone) and TransferOp only
+// param_name, src_rank, dst_rank, src_meta and dst_meta (:257-282).  Such an
+// object reads as `fallback`: a chunk layout, no kind arguments, no row
+// interval, no attached destination shard.
+py::object opt_attr(PyObject* o, PyObject* key, PyObject* fallback) {
+  PyObject* v = PyObject_GetAttr(o, key);
+  if (v) return py::reinterpret_steal<py::object>(v);
+  if (!PyErr_ExceptionMatches(PyExc_AttributeError)) throw py::error_already_set();
+  PyErr_Clear();
+  return py::reinterpret_borrow<py::object>(fallback);
+}
+
+PyObject* empty_tuple() {
+  static PyObject* t = PyTuple_New(0);
+  return t;
+}
+
+py::object kind_of(PyObject* m) { return opt_attr(m, names_().kind, names_().chunk); }
+py::object kind_args_of(PyObject* m) { return opt_attr(m, names_().kind_args, empty_tuple()); }
+py::object tp_meta_of(PyObject* m) { return opt_attr(m, names_().tp_meta, Py_None); }
+py::object rows_of(PyObject* m) { return opt_attr(m, names_().rows, Py_None); }
+py::object shard_of(PyObject* op) { return opt_attr(op, names_().dst_shard_meta, Py_None); }
+
 // One sr_meta row of a TensorMeta (the attributes its constructor sets).
 void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
   const Names& N = names_();
@@ -334,7 +359,7 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
   py::object dt = attr(m, N.dtype);
   if (!THPDtype_Check(dt.ptr())) throw py::type_error("TensorMeta.dtype is not a torch.dtype");
   row[2] = int64_t(c10::elementSize(reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type));
-  py::object shape = attr(m, N.shape), args = attr(m, N.kind_args);
+  py::object shape = attr(m, N.shape), args = kind_args_of(m);
   if (!PyTuple_Check(shape.ptr()) || !PyTuple_Check(args.ptr()))
     throw py::type_error("TensorMeta.shape and kind_args must be tuples");
   const int64_t nd = int64_t(PyTuple_GET_SIZE(shape.ptr())), na = int64_t(PyTuple_GET_SIZE(args.ptr()));
@@ -343,13 +368,13 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
               std::to_string(na) + " kind args");
   row[3] = nd;
   for (int64_t d = 0; d < nd; ++d) row[4 + d] = as_int(PyTuple_GET_ITEM(shape.ptr(), d));
-  py::object tp = attr(m, N.tp_meta);
+  py::object tp = tp_meta_of(m);
   if (tp.ptr() != Py_None) {
     if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3)
       throw py::value_error("tp_meta must be (slice_dim, tp_index, tp_deg)");
     for (int i = 0; i < 3; ++i) row[12 + i] = as_int(PyTuple_GET_ITEM(tp.ptr(), i));
   }
-  py::object kind = attr(m, N.kind);
+  py::object kind = kind_of(m);
   if (!PyUnicode_Check(kind.ptr())) throw py::type_error("TensorMeta.kind must be a str");
   if (PyUnicode_Compare(kind.ptr(), N.chunk) == 0) row[15] = 0;
   else if (PyUnicode_Compare(kind.ptr(), N.vocab_pad) == 0) row[15] = 1;
@@ -357,7 +382,7 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
   else throw py::value_error("unknown shard kind " + py::str(kind).cast<std::string>());
   if (PyErr_Occurred()) throw py::error_already_set();
   for (int64_t i = 0; i < na; ++i) row[16 + i] = as_int(PyTuple_GET_ITEM(args.ptr(), i));
-  py::object rows = attr(m, N.rows);
+  py::object rows = rows_of(m);
   if (rows.ptr() == Py_None) {
     row[19] = row[20] = -1;
   } else {
@@ -431,6 +456,9 @@ py::object derived(PyObject* meta_cls, PyObject* shard, PyObject* tp_meta, PyObj
   if (PyDict_Update(d, src.ptr()) != 0) throw py::error_already_set();
   set(d, N.tp_meta, tp_meta);
   set(d, N.rows, rows);
+  // a shard of the reference's TensorMeta class lacks the extension fields
+  if (PyDict_SetDefault(d, N.kind, N.chunk) == nullptr) throw py::error_already_set();
+  if (PyDict_SetDefault(d, N.kind_args, empty_tuple()) == nullptr) throw py::error_already_set();
   return m;
 }
 
@@ -453,10 +481,10 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
     PyObject* shard = PyList_GET_ITEM(dst_objs.ptr(), d_row);
     py::object piece;
     if (r0 >= 0) {
-      py::object tp = attr(shard, N.tp_meta);
+      py::object tp = tp_meta_of(shard);
       piece = derived(meta_cls.ptr(), shard, tp.ptr(), py::make_tuple(r0, r1).ptr());
     } else if (p_deg) {
-      py::object tp = attr(shard, N.tp_meta);
+      py::object tp = tp_meta_of(shard);
       if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("shard has no tp_meta");
       py::tuple ptp = py::make_tuple(py::reinterpret_borrow<py::object>(PyTuple_GET_ITEM(tp.ptr(), 0)), p_idx, p_deg);
       piece = derived(meta_cls.ptr(), shard, ptp.ptr(), Py_None);
@@ -517,7 +545,7 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
     int64_t idx = 0, deg = 0, r0 = -1, r1 = -1;
     if (m.ptr() != shard) {
       const std::string nm = py::str(name).cast<std::string>();
-      py::object mk = attr(m.ptr(), N.kind), sk = attr(shard, N.kind);
+      py::object mk = kind_of(m.ptr()), sk = kind_of(shard);
       py::object ms = attr(m.ptr(), N.shape), ss = attr(shard, N.shape);
       const int same_kind = PyObject_RichCompareBool(mk.ptr(), sk.ptr(), Py_EQ);
       const int same_shape = PyObject_RichCompareBool(ms.ptr(), ss.ptr(), Py_EQ);
@@ -525,7 +553,7 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
       if (!same_kind || !same_shape)
         assertion(nm + ": piece " + py::str(m).cast<std::string>() + " is not part of shard " +
                   py::str(py::handle(shard)).cast<std::string>());
-      py::object tp = attr(m.ptr(), N.tp_meta), stp = attr(shard, N.tp_meta);
+      py::object tp = tp_meta_of(m.ptr()), stp = tp_meta_of(shard);
       if (tp.ptr() == Py_None) {   // an unsplit piece: the whole tensor
         deg = stp.ptr() != Py_None ? 1 : 0;
       } else {
@@ -541,7 +569,7 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
         idx = as_int(PyTuple_GET_ITEM(tp.ptr(), 1));
         deg = as_int(PyTuple_GET_ITEM(tp.ptr(), 2));
       }
-      py::object rows = attr(m.ptr(), N.rows);
+      py::object rows = rows_of(m.ptr());
       if (rows.ptr() != Py_None) {
         if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2) throw py::value_error("malformed rows");
         r0 = as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
@@ -575,7 +603,7 @@ py::array_t<int64_t> piece_numels(py::list ops) {
   int64_t* o = out.mutable_data();
   for (int64_t k = 0; k < n; ++k) {
     py::object m = attr(PyList_GET_ITEM(ops.ptr(), k), N.dst_meta);
-    py::object shape = attr(m.ptr(), N.shape), tp = attr(m.ptr(), N.tp_meta), rows = attr(m.ptr(), N.rows);
+    py::object shape = attr(m.ptr(), N.shape), tp = tp_meta_of(m.ptr()), rows = rows_of(m.ptr());
     if (!PyTuple_Check(shape.ptr())) throw py::type_error("TensorMeta.shape must be a tuple");
     const Py_ssize_t nd = PyTuple_GET_SIZE(shape.ptr());
     int64_t v = 1;
@@ -685,7 +713,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
     sr_meta m;
     int64_t* row = reinterpret_cast<int64_t*>(&m);
     sr_internal::View v;
-    py::object shard = attr(first, N.dst_shard_meta);
+    py::object shard = shard_of(first);
     if (shard.ptr() != Py_None) {
       meta_row(shard.ptr(), 0, 0, row);
       v = sr_internal::view_of(m);
@@ -696,7 +724,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
       if (m.tp_deg > 0 && groups[i].size() > 1) {
         std::vector<int64_t> idx;
         for (PyObject* op : groups[i]) {
-          py::object tp = attr(attr(op, N.dst_meta).ptr(), N.tp_meta);
+          py::object tp = tp_meta_of(attr(op, N.dst_meta).ptr());
           if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3)
             throw py::value_error("tp_meta must be (slice_dim, tp_index, tp_deg)");
           idx.push_back(as_int(PyTuple_GET_ITEM(tp.ptr(), 1)));

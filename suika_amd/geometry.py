@@ -129,18 +129,23 @@ def infer_dst_shard(ops: List[TransferOp]) -> TensorMeta:
 
     Pieces of a shard at degree t, cut at the source degree T >= t, are the
     T/t consecutive indices starting at idx*T/t (Suika/migration.py:103-118).
+    The reference's own TransferOp / TensorMeta objects (no ``dst_shard_meta``,
+    ``kind``, ``kind_args`` or ``rows``; Suika/migration.py:29-58, 257-282)
+    read as chunk layouts.
     """
     first = ops[0]
-    if first.dst_shard_meta is not None:
-        return first.dst_shard_meta
+    shard = getattr(first, "dst_shard_meta", None)
+    if shard is not None:
+        return shard
     m = first.dst_meta
-    assert m.rows is None, f"{first.param_name}: vocab pieces need dst_shard_meta"
-    if not m.is_tp() or len(ops) == 1:
+    assert getattr(m, "rows", None) is None, f"{first.param_name}: vocab pieces need dst_shard_meta"
+    tp = getattr(m, "tp_meta", None)
+    if tp is None or len(ops) == 1:
         return m
-    dim, _, T = m.tp_meta
-    idxs = sorted(op.dst_meta.tp_index() for op in ops)
+    dim, _, T = tp
+    idxs = sorted(getattr(op.dst_meta, "tp_meta")[1] for op in ops)
     s = len(idxs)
     assert T % s == 0 and idxs == list(range(idxs[0], idxs[0] + s)) and idxs[0] % s == 0, \
         f"{first.param_name}: pieces {idxs} at degree {T} do not form one shard"
     return TensorMeta(name=m.name, dtype=m.dtype, shape=m.shape, tp_meta=(dim, idxs[0] // s, T // s),
-                      kind=m.kind, kind_args=m.kind_args)
+                      kind=getattr(m, "kind", CHUNK), kind_args=getattr(m, "kind_args", ()))

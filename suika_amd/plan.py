@@ -178,7 +178,7 @@ class ReshardPlan:
         name_id = {name: i for i, name in enumerate(self._names)}
         self.dst_metas: Dict[str, TensorMeta] = {}
         for name, name_ops in by_name.items():
-            shard = name_ops[0].dst_shard_meta
+            shard = getattr(name_ops[0], "dst_shard_meta", None)
             self.dst_metas[name] = shard if shard is not None else infer_dst_shard(name_ops)
 
         # sr_lower's op and meta tables (the host extension reads the ops)

@@ -51,15 +51,23 @@ def test_rne_matches_torch_special_values():
     ours = O.rne_bf16(specials)
     finite = ~np.isnan(specials.view(np.float32))
     np.testing.assert_array_equal(ours[finite], ref_bits[finite])
-    # NaN: quiet NaN of any sign/payload; torch's CPU path gives a NaN too
+    # NaN: torch's element conversion (a strided tensor) gives the quiet NaN
+    # 0x7FC0 for every sign and payload, and so does the oracle; torch's
+    # vectorised loop over a contiguous tensor gives 0xFFFF, also a quiet NaN
     assert np.all(np.isnan(ref.float().numpy()[~finite]))
     assert np.all(ours[~finite] == 0x7FC0)
+    flat = torch.from_numpy(specials.view(np.float32).copy())
+    elementwise = t2np(torch.stack([flat, flat], 1)[:, 0].to(torch.bfloat16))
+    np.testing.assert_array_equal(ours, elementwise)
 
 
 def test_rne_matches_torch_random():
     rng = np.random.default_rng(0)
     bits = rng.integers(0, 2 ** 32, size=200_000, dtype=np.uint64).astype(np.uint32)
     f = bits.view(np.float32)
+    # every pattern, NaNs included, against torch's element conversion
+    flat = torch.from_numpy(f.copy())
+    np.testing.assert_array_equal(O.rne_bf16(bits), t2np(torch.stack([flat, flat], 1)[:, 0].to(torch.bfloat16)))
     keep = ~np.isnan(f)
     ref = t2np(torch.from_numpy(f[keep].copy()).to(torch.bfloat16))
     np.testing.assert_array_equal(O.rne_bf16(bits[keep]), ref)

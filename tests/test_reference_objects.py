@@ -1,0 +1,159 @@
+"""The drop-in operators on the reference's own plan objects (CPU side).
+
+The ops of every case recorded from the reference's ``schedule_param_transfer``
+(tests/golden/schedule_vectors.json.gz) are rebuilt as objects that carry only
+the reference's attributes (tests/refshaped.py): no ``kind``, ``kind_args``,
+``rows`` or ``dst_shard_meta``.  They must plan exactly like this build's own
+ops, and the plan executed by the numpy simulation must equal the oracle's
+reshard of the same seeded shards.  ``schedule_param_transfer`` must also take
+layouts of such metas and reproduce the recorded schedule.
+"""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from suika_amd import _lib, schedule_param_transfer
+from suika_amd.migration import _pipeline_groups
+from suika_amd.plan import ReshardPlan, SlotSpec
+from suika_amd.workloads import CONFIGS
+from tests import cases
+from tests.harness import global_state, load_schedule_vectors, oracle_dest, simulate_plan, source_shards
+from tests.refshaped import RefTensorMeta, RefTransferOp, ops_from_vector, ref_layout
+from tests.test_plan import _esize
+
+SCHED = load_schedule_vectors()
+SMALL = {w.key: w for w in cases.all_small_cases()}
+CASES = sorted(SCHED["cases"])
+
+
+def _ref_kinds(w):
+    return replace(w, model=replace(w.model, vocab_parallel=False, fused_qkv=False))
+
+
+def _workload(case):
+    key = case.split("|")[0]
+    return _ref_kinds(SMALL[key] if key in SMALL else CONFIGS[key])
+
+
+def _ref_ops(case, omit_tp=False):
+    w = _workload(case)
+    spl, tpl = w.layouts()
+    rspl, rtpl = ref_layout(spl, omit_tp), ref_layout(tpl, omit_tp)
+    return w, rspl, rtpl, ops_from_vector(SCHED["cases"][case], SCHED["names"], rspl, rtpl)
+
+
+def _specs(w, ops):
+    dt = w.dtypes
+    out = {}
+    for op in ops:
+        sm = op.src_meta
+        tp = getattr(sm, "tp_meta", None)
+        shape = list(sm.shape)
+        if tp is not None:
+            shape[tp[0]] //= tp[2]
+        for f in w.src_fields:
+            out[(op.src_rank, op.param_name, f)] = SlotSpec(tuple(shape), dt[f])
+    return out
+
+
+def test_stand_ins_carry_only_the_reference_attributes():
+    _, rspl, _, ops = _ref_ops(CASES[0], omit_tp=True)
+    assert set(vars(ops[0])) == {"param_name", "src_rank", "dst_rank", "src_meta", "dst_meta"}
+    metas = [m for metas in rspl.layout.values() for m in metas.values()]
+    assert {frozenset(vars(m)) for m in metas} <= {frozenset({"name", "dtype", "shape", "tp_meta"}),
+                                                   frozenset({"name", "dtype", "shape"})}
+    assert any(not hasattr(m, "tp_meta") for m in metas), "a replicated meta without tp_meta"
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_schedule_takes_reference_layouts(case, monkeypatch):
+    """schedule_param_transfer over layouts of reference-shaped metas
+    reproduces the reference's recorded schedule."""
+    monkeypatch.setenv("NCCL_IB_DISABLE", case.split("|")[1].split("=")[1])
+    w, rspl, rtpl, ref_ops = _ref_ops(case, omit_tp=True)
+    ours = schedule_param_transfer(rspl, rtpl)
+    if case.split("|")[0] in CONFIGS:   # recorded for the destination rank only
+        ours = [op for op in ours if op.dst_rank == w.dst_rank]
+    got = [(op.param_name, op.src_rank, op.dst_rank, getattr(op.dst_meta, "tp_meta", None)) for op in ours]
+    want = [(op.param_name, op.src_rank, op.dst_rank, getattr(op.dst_meta, "tp_meta", None)) for op in ref_ops]
+    assert got == want
+    # the schedule's ops keep the reference's objects as source metas and shards
+    assert all(isinstance(op.src_meta, RefTensorMeta) for op in ours)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_reference_ops_plan_like_own_ops(case, monkeypatch):
+    """The reference's ops for the workload's destination rank lower to the
+    same pieces, slots and buffer layout as this build's own schedule."""
+    monkeypatch.setenv("NCCL_IB_DISABLE", case.split("|")[1].split("=")[1])
+    w, _, _, ref_ops = _ref_ops(case)
+    ref_ops = [op for op in ref_ops if op.dst_rank == w.dst_rank]
+    own = w.ops()
+    plan_ref = ReshardPlan(ref_ops, _specs(w, ref_ops), list(w.src_fields), recast=w.recast_map)
+    plan_own = ReshardPlan(own, _specs(w, own), list(w.src_fields), recast=w.recast_map)
+    try:
+        assert plan_ref.dst_keys == plan_own.dst_keys
+        assert [plan_ref.dst_specs[k] for k in plan_ref.dst_keys] == \
+            [plan_own.dst_specs[k] for k in plan_own.dst_keys]
+        assert plan_ref.src_keys == plan_own.src_keys
+        a, b = plan_ref.pieces, plan_own.pieces
+        assert len(a) == len(b) and all(tuple(x) == tuple(y) for x, y in zip(a, b))
+        assert plan_ref.peer_bytes == plan_own.peer_bytes
+    finally:
+        plan_ref.close()
+        plan_own.close()
+    # launch grouping (the host extension's run and size helpers) reads them too
+    groups = _pipeline_groups(ref_ops, 14, 8)
+    assert [op for g in groups for op in g] == ref_ops
+    numels = _lib.host().piece_numels(ref_ops).tolist()
+    assert numels == _lib.host().piece_numels(own).tolist()
+
+
+SMALL_CASES = [c for c in CASES if c.split("|")[0] in SMALL and c.endswith("=0")]
+
+
+@pytest.mark.parametrize("case", SMALL_CASES)
+def test_reference_ops_reshard_matches_oracle(case):
+    """The plan of the reference's ops, executed by the numpy simulation,
+    equals the oracle's reshard of the seeded shards, byte for byte."""
+    w, _, _, ref_ops = _ref_ops(case, omit_tp=True)
+    ref_ops = [op for op in ref_ops if op.dst_rank == w.dst_rank]
+    spl, _ = w.layouts()
+    glob = global_state(w, {n for metas in spl.layout.values() for n in metas})
+    srcs = source_shards(w, sorted(spl.layout), glob)
+    want = oracle_dest(w, srcs)
+    plan = ReshardPlan(ref_ops, _specs(w, ref_ops), list(w.src_fields), recast=w.recast_map)
+    try:
+        got = simulate_plan(plan, srcs, _esize)
+    finally:
+        plan.close()
+    assert {k[0] for k in got} == set(want)
+    for (name, f), a in got.items():
+        np.testing.assert_array_equal(a, want[name][f], err_msg=f"{case}: {name}/{f}")
+
+
+def test_missing_source_is_the_reference_assertion():
+    case = SMALL_CASES[0]
+    w, _, _, ref_ops = _ref_ops(case)
+    ref_ops = [op for op in ref_ops if op.dst_rank == w.dst_rank]
+    specs = _specs(w, ref_ops)
+    specs.pop(next(iter(specs)))
+    with pytest.raises(AssertionError, match="param missing in source"):
+        ReshardPlan(ref_ops, specs, list(w.src_fields))
+
+
+def test_reference_op_without_tp_meta_on_a_split_piece_is_rejected():
+    """A piece of a split shard must say which part it is: a reference
+    TransferOp whose dst_meta lacks tp_meta reads as the whole tensor."""
+    case = SMALL_CASES[0]
+    w, _, _, ref_ops = _ref_ops(case)
+    ref_ops = [op for op in ref_ops if op.dst_rank == w.dst_rank]
+    split = next(op for op in ref_ops if getattr(op.dst_meta, "tp_meta", None) is not None
+                 and op.dst_meta.tp_meta[2] > 1)
+    bad = RefTransferOp(split.param_name, split.src_rank, split.dst_rank, split.src_meta,
+                        RefTensorMeta(split.param_name, split.dst_meta.dtype, tuple(split.dst_meta.shape)))
+    ops = [bad if op is split else op for op in ref_ops]
+    with pytest.raises(AssertionError):
+        plan = ReshardPlan(ops, _specs(w, ops), list(w.src_fields))
+        plan.close()
