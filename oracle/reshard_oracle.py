@@ -25,6 +25,12 @@ Pins (tests/test_oracle*.py, tests/test_golden.py):
                                   brute-force ownership / coverage invariants
   * ``rne_bf16``                  vs torch.Tensor.to(torch.bfloat16) on CPU,
                                   incl. ties, subnormals, inf and NaN
+  * ``REFERENCE_KINDS`` /         vs the tp meta the reference's own model
+    ``kind_of_name``              classes, ``parallelize_tp`` and
+                                  ``get_param_tensor_meta`` produce for
+                                  3404 recorded parameters (GPT / Llama /
+                                  Qwen2 stages at TP 1-8), planted table
+                                  mistakes shown to fail
   * index maps                    vs brute force on tiny shapes
 No function here is left unpinned.
 Extensions the reference lacks (vocab padding, head-granular fused QKV, bf16
