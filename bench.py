@@ -17,6 +17,12 @@ of the same workload on this host's cores, scaled to the same unit.
 applies when every source shard is resident on this GPU; ``api`` times the
 drop-in operator end to end (``schedule_param_transfer`` for every rank, then
 ``execute_param_transfer`` with the sources resident).
+
+``parity`` is checked outside the timed regions, tensor by tensor and byte
+for byte, against the pack + unpack result: the direct gather, the drop-in
+operator (fresh and arena destinations) and -- with the CPU baseline on --
+the torch-CPU reshard, which runs on host copies of the same seeded source
+shards the GPU resharded.
 """
 from __future__ import annotations
 
@@ -72,16 +78,21 @@ def to_ometa(m):
                    kind_args=tuple(m.kind_args), rows=m.rows)
 
 
-def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0):
+def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0, srcs=None, keep_output: bool = False):
     """Time the torch-CPU restatement of the reference's CPU reshard on the
     destination share of ``w`` (or, with ``layers`` > 0, on a sample whose
     destination stage holds that many decoder layers): one untimed run, then
-    timed runs until ``min_seconds`` have passed.  Returns (seconds per run,
-    algorithmic bytes of the share, runs, decoder layers of the share)."""
+    timed runs until ``min_seconds`` have passed.  ``srcs`` are the seeded
+    source shards as CPU tensors (``{rank: {name: {field: tensor}}}``, the
+    host copies of what the GPU resharded); without them (the sample) they
+    are generated with the workload's seed on the CPU.  Returns (seconds per
+    run, algorithmic bytes of the share, runs, decoder layers of the share,
+    the untimed run's output if ``keep_output``)."""
     import torch
     from oracle import reshard_oracle as O
     from oracle.torch_ref import execute_torch_cpu
     from suika_amd.inventory import layer_partition
+    from suika_amd.workloads import make_source_state
 
     ws = w
     if layers:
@@ -94,16 +105,13 @@ def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0):
     dt = ws.dtypes
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
+    kept = None
     try:
-        srcs = {}
-        for op in ops:
-            for f in ws.src_fields:
-                ent = srcs.setdefault(op.src, {}).setdefault(op.name, {})
-                if f not in ent:
-                    t = torch.empty(O.actual_shape(op.src_meta), dtype=dt[f])
-                    t.fill_(0.5)
-                    ent[f] = t
+        if srcs is None:
+            srcs = make_source_state(ws, sorted({op.src for op in ops}), "cpu")
         out = execute_torch_cpu(ops, ws.dst_rank, srcs, list(ws.src_fields), ws.recast_map)
+        if keep_output:
+            kept = out
         del out
         runs, total = 0, 0.0
         while total < min_seconds or runs == 0:
@@ -125,7 +133,22 @@ def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0):
     plan.close()
     dst_pp = ws.dst.coord(ws.dst_rank)[0]
     n_dst_layers = layer_partition(ws.model.n_layer, ws.dst.pp)[dst_pp]
-    return total / runs, b_alg, runs, n_dst_layers
+    return total / runs, b_alg, runs, n_dst_layers, kept
+
+
+def mismatches(keys, got, want, device=None) -> list:
+    """(name, field) of every destination tensor whose bytes differ between
+    two results (tensors moved to ``device`` one at a time to compare)."""
+    import torch
+    bad = []
+    for name, f in keys:
+        a, b = got[name][f], want[name][f]
+        if device is not None:
+            a, b = a.to(device), b.to(device)
+        if a.shape != b.shape or a.dtype != b.dtype or \
+                not torch.equal(a.reshape(-1).view(torch.uint8), b.reshape(-1).view(torch.uint8)):
+            bad.append(f"{name}/{f}")
+    return bad
 
 
 def calibrate_copy(nbytes: int, steps: int) -> dict:
@@ -248,7 +271,7 @@ def row_sweep(nbytes: int, steps: int) -> list:
     return out
 
 
-def api_latency(w, sources, dev, repeats: int = 3) -> dict:
+def api_latency(w, sources, dev, repeats: int = 3, check=None) -> dict:
     """Wall time of the drop-in path: schedule_param_transfer for every rank,
     then execute_param_transfer for this GPU's share with all sources
     resident (fake-source dicts), route "direct".  One untimed call first;
@@ -275,6 +298,8 @@ def api_latency(w, sources, dev, repeats: int = 3) -> dict:
                                          arena=arena)
             torch.cuda.synchronize()
             t3 = time.perf_counter()
+            if check is not None and i == repeats:
+                check(arena, out)
             del out, fake
             if i:
                 sched_ms.append((t1 - t0) * 1e3)
@@ -421,8 +446,28 @@ def main(argv=None) -> int:
     print(f"[bench] pack {pack_ms:.3f} ms  unpack {unpack_ms:.3f} ms  step {total_ms:.3f} ms  "
           f"wall {wall_s * 1e3 / K:.3f} ms/step", file=sys.stderr, flush=True)
 
+    # Parity, outside the timed region: the pack + unpack result is kept and
+    # every other route (gather, the drop-in operator) and the torch-CPU
+    # reshard of the same seeded shards must reproduce it byte for byte.
+    keys = list(plan.dst_keys)
+    ref = {}
+    for name, f in keys:
+        ref.setdefault(name, {})[f] = dst[name][f].clone()
+    parity = {"tensors": len(keys), "mismatched": 0, "routes": {}}
+
+    def record(route, bad):
+        parity["routes"][route] = len(bad)
+        parity["mismatched"] += len(bad)
+        if bad:
+            parity.setdefault("first_mismatches", {})[route] = bad[:5]
+            print(f"[bench] PARITY: {route} differs in {len(bad)} tensors, first {bad[:3]}",
+                  file=sys.stderr, flush=True)
+
     # The direct route (sources resident on this GPU, no buffers): one gather
     # launch per reshard, P read + D written.  Reported beside the main line.
+    for e in dst.values():
+        for t in e.values():
+            t.view(torch.uint8).fill_(0xA5)
     for _ in range(2):
         plan.gather_ptrs(sp, dp, stream)
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -434,6 +479,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     gather_ms = g0.elapsed_time(g1) / K
     b_gather = plan.gather_bytes
+    record("gather_vs_pack_unpack", mismatches(keys, dst, ref))
     host_leg = host_sources_leg(plan, sources, sp, dp, stream) if args.host_sources else None
 
     # End to end through the drop-in operator: execute_param_transfer with
@@ -441,7 +487,9 @@ def main(argv=None) -> int:
     # the call to the synchronised result: region lowering, sr_plan_create,
     # destination allocation, device-side table setup and the gather launch.
     del dst
-    api = api_latency(w, sources, dev, repeats=3)
+    api = api_latency(w, sources, dev, repeats=3,
+                      check=lambda arena, out: record("execute_param_transfer" + ("_arena" if arena else ""),
+                                                      mismatches(keys, out, ref)))
 
     value = b_alg / (total_ms * 1e-3) / 1e9
     pack_gbps = b_pack / (pack_ms * 1e-3) / 1e9
@@ -512,8 +560,15 @@ def main(argv=None) -> int:
             "traffic": traffic,
         },
         "cpu_baseline": None,
+        "parity": parity,
     }
 
+    # the CPU reshard runs on host copies of the same seeded shards
+    srcs_cpu = None
+    if not args.no_cpu_baseline and not args.cpu_layers:
+        print(f"[bench] copying {P / 1e9:.2f} GB of source shards to the host", file=sys.stderr, flush=True)
+        srcs_cpu = {r: {n: {f: t.cpu() for f, t in e.items()} for n, e in sd.items()}
+                    for r, sd in sources.items()}
     del sources, bufs
     torch.cuda.empty_cache()
 
@@ -521,8 +576,17 @@ def main(argv=None) -> int:
         threads = len(os.sched_getaffinity(0))
         print(f"[bench] CPU baseline: torch-CPU reshard, {threads} threads", file=sys.stderr,
               flush=True)
-        t_n, b_n, runs_n, nl = cpu_baseline(w, threads, args.cpu_seconds, args.cpu_layers)
-        t_1, b_1, runs_1, nl1 = cpu_baseline(w, 1, args.cpu_seconds, args.cpu_layers)
+        t_n, b_n, runs_n, nl, cpu_out = cpu_baseline(w, threads, args.cpu_seconds, args.cpu_layers,
+                                                     srcs=srcs_cpu, keep_output=srcs_cpu is not None)
+        if cpu_out is not None:
+            print("[bench] comparing every destination tensor with the torch-CPU reshard",
+                  file=sys.stderr, flush=True)
+            record("vs_torch_cpu_reference", mismatches(keys, cpu_out, ref, device=dev))
+            parity["cpu_reference"] = ("torch-CPU reshard (oracle/torch_ref.py: the reference's fake-source "
+                                       "chunk/contiguous/cat loop) of the same seeded source shards")
+            del cpu_out
+        t_1, b_1, runs_1, nl1, _ = cpu_baseline(w, 1, args.cpu_seconds, args.cpu_layers, srcs=srcs_cpu)
+        del srcs_cpu
         rate_n = b_n / t_n / 1e9
         rate_1 = b_1 / t_1 / 1e9
         full_ms = b_alg / (rate_n * 1e9) * 1e3
@@ -534,6 +598,7 @@ def main(argv=None) -> int:
             "cores": threads,
             "kind": "port",
             "sample": (f"torch-CPU chunk/contiguous/cat reshard (oracle/torch_ref.py) of {what}, "
+                       f"seeded source shards (host copies of the GPU's inputs), "
                        f"{b_n / 1e9:.2f} GB algorithmic, {runs_n} timed runs of {t_n:.3f} s"),
             "ms": round(full_ms, 1),
             "one_thread_GBps": round(rate_1, 2),
@@ -545,6 +610,7 @@ def main(argv=None) -> int:
         print(f"[bench] CPU {rate_n:.2f} GB/s ({threads} thr), 1 thr {rate_1:.2f} GB/s", file=sys.stderr,
               flush=True)
 
+    del ref
     plan.close()
     line = json.dumps(result)
     print(line, flush=True)

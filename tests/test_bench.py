@@ -23,9 +23,42 @@ def test_cpu_baseline_sample():
     sys.path.insert(0, str(ROOT))
     import bench
     from suika_amd.workloads import CONFIGS
-    t, nbytes, runs, layers = bench.cpu_baseline(CONFIGS["gpt125m_tp2_tp4"], 2, 0.0, layers=1)
+    t, nbytes, runs, layers, out = bench.cpu_baseline(CONFIGS["gpt125m_tp2_tp4"], 2, 0.0, layers=1,
+                                                      keep_output=True)
     assert t > 0 and runs >= 1 and layers == 1
     assert 0 < nbytes < 4 * 0.835e9       # below the full share's B_alg
+    # the sample's output is the oracle's reshard of the same seeded shards
+    from dataclasses import replace
+
+    from oracle import reshard_oracle as O
+    from suika_amd.workloads import make_source_state
+    from tests.harness import t2np, to_olayout
+    w = CONFIGS["gpt125m_tp2_tp4"]
+    ws = replace(w, model=replace(w.model, n_layer=1))
+    spl, tpl = ws.layouts()
+    ops = O.schedule(to_olayout(spl), to_olayout(tpl))
+    srcs = make_source_state(ws, sorted({op.src for op in ops if op.dst == ws.dst_rank}), "cpu")
+    srcs_np = {r: {n: {f: t2np(x) for f, x in e.items()} for n, e in sd.items()} for r, sd in srcs.items()}
+    want = O.execute_fake_source(ops, ws.dst_rank, srcs_np, list(ws.src_fields), recast=ws.recast_map)
+    assert set(out) == set(want)
+    for name, ent in want.items():
+        for f, a in ent.items():
+            assert (t2np(out[name][f]) == a).all(), f"{name}/{f}"
+
+
+def test_mismatch_counter():
+    sys.path.insert(0, str(ROOT))
+    import torch
+
+    import bench
+    a = {"x": {"p": torch.arange(6, dtype=torch.float32)}, "y": {"p": torch.zeros(3, dtype=torch.bfloat16)}}
+    b = {"x": {"p": torch.arange(6, dtype=torch.float32)}, "y": {"p": torch.zeros(3, dtype=torch.bfloat16)}}
+    keys = [("x", "p"), ("y", "p")]
+    assert bench.mismatches(keys, a, b) == []
+    b["y"]["p"][1] = -0.0             # equal as numbers, different bytes
+    assert bench.mismatches(keys, a, b) == ["y/p"]
+    b["x"]["p"] = b["x"]["p"].to(torch.float64)
+    assert bench.mismatches(keys, a, b) == ["x/p", "y/p"]
 
 
 @pytest.mark.gpu
@@ -56,3 +89,7 @@ def test_bench_json_line(tmp_path):
     assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
     assert r["kernel"] in ("sr_pack_kernel", "sr_unpack_kernel")
     assert 0.2 < r["frac"] < 1.0
+    p = d["parity"]
+    assert p["mismatched"] == 0 and p["tensors"] > 0, p
+    assert set(p["routes"]) == {"gather_vs_pack_unpack", "execute_param_transfer",
+                                "execute_param_transfer_arena"}
