@@ -33,8 +33,8 @@ from torch import Tensor
 from torch.nn import Module
 from torch.optim import Optimizer
 
-from .meta import (ParamLayout, TensorMeta, TransferOp, get_named_parameters_and_persistent_buffers,
-                   schedule_param_transfer)
+from .meta import (CHUNK, QKV_HEADS, ParamLayout, TensorMeta, TransferOp,
+                   get_named_parameters_and_persistent_buffers, schedule_param_transfer)
 from . import _lib
 from .plan import PlanOptions, ReshardPlan
 
@@ -159,7 +159,6 @@ def execute_param_transfer(
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
-    used_sources: Dict[int, StateDict] = {}
     # A full pass of Python's cyclic collector over a large heap (tens of ms)
     # would stall the host between launch groups and idle the GPU; it is
     # paused for the call (reference counting still frees memory).
@@ -183,7 +182,6 @@ def execute_param_transfer(
                                                           options=plan_options, rank=rank)
                 prof.stop("execute schedule lowering")
                 plans.append(plan)
-                used_sources.update((r, source(r)) for r in plan.peers)
                 if arena_views is None:
                     # fresh tensors of the planned shapes: their addresses need no check
                     part, dst_ptrs = plan.alloc_dst_ptrs(device)
@@ -235,13 +233,51 @@ def execute_param_transfer(
     del buffers
 
     if forcefully_free:
-        for sd in used_sources.values():
-            for entry in sd.values():
+        # the source tensors the reference's freed pieces share storage with
+        # (migration.py:539-541); the rest stays untouched
+        for op in ops:
+            entry = source(op.src_rank).get(op.param_name, {})
+            if _piece_aliases_source(op):
                 for f in normal:
                     if f in entry:
                         forcefully_free_tensor(entry[f])
+            for f in scalars:
+                t = entry.get(f)
+                if isinstance(t, Tensor) and t.device == device:
+                    forcefully_free_tensor(t)
     source_state_dict.clear()
     return ordered
+
+
+def _tp_deg(meta) -> int:
+    tp = getattr(meta, "tp_meta", None)
+    return 1 if tp is None else int(tp[2])
+
+
+def _piece_aliases_source(op: TransferOp) -> bool:
+    """Whether the reference's piece of ``op`` shares the source tensor's
+    storage, so that its ``forcefully_free`` (migration.py:539-541) releases
+    the source.  ``get_send_tensor`` (:290-312) sends the source itself when
+    it is at least as fine as the piece, and otherwise
+    ``chunk(n, slice_dim)[k].contiguous()``: a view of the source when the
+    chunk is contiguous (split along the first dimension of extent above 1),
+    a copy otherwise (a row-parallel split).  A vocabulary piece is a row
+    range (a view); a head-granular QKV piece concatenates three chunks (a
+    copy).  A 1-element field is sent as ``tensor.to(device)``: the tensor
+    itself when it is already on the device."""
+    src, piece = op.src_meta, op.dst_meta
+    if getattr(piece, "rows", None) is not None:
+        return True
+    if _tp_deg(src) >= _tp_deg(piece):
+        return True
+    if getattr(src, "kind", CHUNK) == QKV_HEADS:
+        return False
+    shape = [int(x) for x in src.shape]
+    tp = getattr(piece, "tp_meta", None) or getattr(src, "tp_meta", None)
+    dim = tp[0] % len(shape) if shape else 0
+    local = list(shape)
+    local[dim] //= max(1, _tp_deg(src))
+    return all(x == 1 for x in local[:dim])
 
 
 # Bytes of piece data per launch group on average at least: a group's GPU

@@ -247,3 +247,56 @@ def test_execute_on_a_side_stream_waits_for_current_work():
     for name, e in want.items():
         for f, a in e.items():
             np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
+@pytest.mark.parametrize("key", ["gpt_test_tp2pp1_tp4pp1_d0.3", "llama_test_tp4pp1_tp2pp1_d0.1",
+                                 "vocab_pad_tp2_tp4_d3"])
+def test_forcefully_free_releases_what_the_reference_frees(key):
+    """With forcefully_free the reference frees the pieces it received
+    (migration.py:539-541), which releases a source only where the piece is
+    that tensor or a view of it.  The expected set comes from torch itself:
+    the torch restatement of get_send_tensor (oracle/torch_ref.py) runs on
+    CPU copies of the sources and a source counts as freed when its piece
+    shares its storage.  A 1-element field on the device is freed (sent as
+    tensor.to(device), the tensor itself); one on the CPU is not."""
+    from oracle import reshard_oracle as O
+    from oracle.torch_ref import get_send
+    from tests.harness import to_olayout
+    w = {c.key: c for c in cases.all_small_cases()}[key]
+    print(f"[gpu forcefully_free] {key}", flush=True)
+    glob = global_state(w, _names(w))
+    spl, tpl = w.layouts()
+    srcs = source_shards(w, sorted(spl.layout), glob)
+    fake = to_device(srcs, w, "cuda")
+    cpu = to_device(srcs, w, "cpu")
+    want = set()
+    for op in O.schedule(to_olayout(spl), to_olayout(tpl)):
+        if op.dst != w.dst_rank:
+            continue
+        for f in w.src_fields:
+            t = cpu[op.src][op.name][f]
+            if get_send(op, t).untyped_storage().data_ptr() == t.untyped_storage().data_ptr():
+                want.add((op.src, op.name, f))
+    for r, sd in fake.items():
+        for name, e in sd.items():
+            e["step_dev"] = torch.tensor([float(r)], device="cuda")
+            e["step_cpu"] = torch.tensor([float(r)])
+    kept = {(r, n, f): t for r, sd in fake.items() for n, e in sd.items() for f, t in e.items()}
+    fields = [(f, "normal") for f in w.src_fields] + [("step_dev", TensorMeta(torch.tensor([1.0]))),
+                                                      ("step_cpu", TensorMeta(torch.tensor([1.0])))]
+    out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                                 fake_source_state_dicts=fake, forcefully_free=True)
+    torch.cuda.synchronize()
+    for name, e in oracle_dest(w, srcs).items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+    read = {(op.src_rank, op.param_name) for op in w.ops()}
+    freed = {k for k, t in kept.items() if t.untyped_storage().nbytes() == 0}
+    assert {k for k in freed if k[2] in w.src_fields} == want
+    n_read = len(read) * len(w.src_fields)
+    if key.startswith("llama"):     # a TP merge sends whole source shards: all are released
+        assert len(want) == n_read
+    else:                           # row-parallel splits are copies: their sources survive
+        assert 0 < len(want) < n_read
+    assert {k for k in freed if k[2] == "step_dev"} == {(r, n, "step_dev") for (r, n) in read}
+    assert not any(k[2] == "step_cpu" for k in freed)
