@@ -65,6 +65,9 @@ def parse_args(argv=None):
     ap.add_argument("--row-sweep", type=int, default=0, metavar="BYTES",
                     help="strided dim -1 pieces (cat / split) of several row widths against a flat "
                          "copy, BYTES read and written per case, then exit")
+    ap.add_argument("--handoff", action="store_true",
+                    help="only run the live migration of the workload between old and new processes on "
+                         "this GPU (migration_save / migration_load) and print its timings, then exit")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -357,6 +360,235 @@ def host_sources_leg(plan, sources, sp, dp, stream, repeats: int = 3) -> dict:
             "note": "gather bytes (P + D) over host-to-device copies + gather; not the headline value"}
 
 
+# ---------------------------------------------------------------- live hand-off leg
+
+def _state_optimizer(params):
+    """An optimizer that only holds mixed-precision state per parameter (an
+    f32 master copy and Adam moments next to a bf16 parameter) and keeps its
+    dtypes when loaded: torch's Optimizer.load_state_dict casts floating
+    state to the parameter's dtype."""
+    import torch
+
+    class MixedPrecisionState(torch.optim.Optimizer):
+        def __init__(self, ps):
+            super().__init__(ps, {})
+
+        def load_state_dict(self, state_dict):
+            params = [p for g in self.param_groups for p in g["params"]]
+            self.state.clear()
+            for idx, st in state_dict["state"].items():
+                p = params[idx]
+                self.state[p] = {k: (v.to(device=p.device) if torch.is_tensor(v) else v) for k, v in st.items()}
+
+        def step(self, closure=None):
+            raise NotImplementedError("state holder only")
+
+    return MixedPrecisionState(params)
+
+
+def _seeded_global(w, name: str, shape, device):
+    """Seeded global tensors of one name (per-name seed, so any process can
+    regenerate them): master ~ N(0, 0.02), exp_avg ~ N(0, 1e-3), exp_avg_sq =
+    |N(0, 1e-6)|, bf16 param = RNE(master)."""
+    import zlib
+
+    import torch
+    from suika_amd.workloads import FIELD_STD
+    gen = torch.Generator(device=device)
+    gen.manual_seed((w.seed * 1000003 + zlib.crc32(name.encode())) & 0x7FFFFFFFFFFFFFFF)
+    dt = w.dtypes
+    base = "master" if "master" in w.src_fields else "param"
+    out = {}
+    for f in (base, "exp_avg", "exp_avg_sq"):
+        if f not in w.src_fields:
+            continue
+        g = torch.randn(shape, generator=gen, dtype=torch.float32, device=device).mul_(FIELD_STD[f])
+        if f == "exp_avg_sq":
+            g.abs_()
+        out[f] = g
+    if base == "master" and "param" in w.src_fields:
+        out["param"] = out["master"].to(dt["param"])
+    return {f: t.to(dt[f]) for f, t in out.items()}
+
+
+def _timed_log(sink):
+    def log(msg):
+        sink.append((time.time(), msg))
+    return log
+
+
+def _handoff_old(rank, key, port, queues, events):
+    import traceback
+
+    import torch
+    import torch.distributed as dist
+    try:
+        os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
+        from suika_amd import migration_save
+        from suika_amd.inventory import build_module
+        from suika_amd.workloads import CONFIGS, shard_global
+        w = CONFIGS[key]
+        dist.init_process_group("gloo", rank=rank, world_size=w.src.world)
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        dt = w.dtypes
+        pfield = "param" if "param" in w.src_fields else "master"
+        model = build_module(w.model, w.src, rank, dt[pfield], device=dev)
+        opt = _state_optimizer(model.parameters())
+        metas = w.layouts()[0].layout[rank]
+        for name, p in model.named_parameters():
+            glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
+            with torch.no_grad():
+                p.copy_(shard_global(glob[pfield], metas[name]))
+            opt.state[p] = {f: shard_global(glob[f], metas[name]) for f in w.src_fields if f != pfield}
+            del glob
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        log = []
+        events.put(("ready", rank, None))
+        migration_save(queues[rank], model, opt, other_context={"iter": 1}, log_func=_timed_log(log))
+        events.put(("saved", rank, log))
+    except BaseException:
+        events.put(("error", rank, traceback.format_exc()))
+    finally:
+        import torch.distributed as dist
+        if dist.is_initialized():
+            dist.destroy_process_group()
+
+
+def _handoff_new(rank, key, port, queues, events):
+    import traceback
+
+    import torch
+    import torch.distributed as dist
+    try:
+        os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
+        from suika_amd import migration_load
+        from suika_amd.inventory import build_module
+        from suika_amd.workloads import CONFIGS, shard_global
+        w = CONFIGS[key]
+        dist.init_process_group("gloo", rank=rank, world_size=w.dst.world)
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        dt = w.dtypes
+        pfield = "param" if "param" in w.src_fields else "master"
+        model = build_module(w.model, w.dst, rank, dt[pfield], device="meta")
+        log = []
+        t0 = time.time()
+        opt, ctx = migration_load(queues[rank], model, lambda: _state_optimizer(model.parameters()),
+                                  log_func=_timed_log(log))
+        t1 = time.time()
+        # every received tensor against the same seeded state, cut for this rank
+        metas = w.layouts()[1].layout[rank]
+        state = opt.state_dict()["state"]
+        n, bad = 0, []
+        for idx, (name, p) in enumerate(model.named_parameters()):
+            glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
+            got = {pfield: p, **{f: state[idx][f] for f in w.src_fields if f != pfield}}
+            for f, t in got.items():
+                want = shard_global(glob[f], metas[name])
+                n += 1
+                if t.dtype != want.dtype or t.shape != want.shape or \
+                        not torch.equal(t.reshape(-1).view(torch.uint8), want.reshape(-1).view(torch.uint8)):
+                    bad.append(f"{name}/{f}")
+            del glob
+        nbytes = sum(p.numel() * p.element_size() for p in model.parameters()) + \
+            sum(t.numel() * t.element_size() for e in state.values() for t in e.values() if torch.is_tensor(t))
+        events.put(("loaded", rank, {"log": log, "t_call": t0, "t_return": t1, "tensors": n, "bad": bad[:5],
+                                     "mismatched": len(bad), "bytes": nbytes}))
+    except BaseException:
+        events.put(("error", rank, traceback.format_exc()))
+    finally:
+        import torch.distributed as dist
+        if dist.is_initialized():
+            dist.destroy_process_group()
+
+
+def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
+    """Live migration of workload ``key`` between processes on this GPU: the
+    old plan's ranks (seeded state) call migration_save, the new plan's ranks
+    migration_load; every received tensor is checked bit for bit."""
+    import multiprocessing as mp
+    import queue as _queue
+    import socket
+
+    from suika_amd.handoff import dummy_migration_IPC_state_dict
+    from suika_amd.workloads import CONFIGS
+    w = CONFIGS[key]
+    old_ws, new_ws = w.src.world, w.dst.world
+    assert old_ws + new_ws <= 16, "at most 16 processes on the GPU"
+    ctx = mp.get_context("spawn")
+    queues = [(ctx.Queue(), ctx.Queue()) for _ in range(max(old_ws, new_ws))]
+    for q in queues[old_ws:]:          # guards of new ranks without an old counterpart
+        q[0].put(dummy_migration_IPC_state_dict)
+    events = ctx.Queue()
+    results = {}
+    deadline = time.time() + timeout_s
+
+    def wait_for(kind, count):
+        while sum(1 for ev, _ in results if ev == kind) < count:
+            try:
+                ev, rank, payload = events.get(timeout=max(1.0, deadline - time.time()))
+            except _queue.Empty:
+                raise RuntimeError(f"hand-off leg: timed out waiting for {kind}; have {sorted(results)}")
+            if ev == "error":
+                raise RuntimeError(f"hand-off leg: rank {rank} failed:\n{payload}")
+            results[(ev, rank)] = payload
+            print(f"[bench] hand-off: {ev} {rank}", file=sys.stderr, flush=True)
+
+    def port():
+        with socket.socket() as s_:
+            s_.bind(("127.0.0.1", 0))
+            return s_.getsockname()[1]
+
+    procs = []
+    try:
+        p_old, p_new = port(), port()
+        for r in range(old_ws):
+            procs.append(ctx.Process(target=_handoff_old, args=(r, key, p_old, queues, events)))
+            procs[-1].start()
+        wait_for("ready", old_ws)
+        for r in range(new_ws):
+            procs.append(ctx.Process(target=_handoff_new, args=(r, key, p_new, queues, events)))
+            procs[-1].start()
+        wait_for("loaded", new_ws)
+        wait_for("saved", old_ws)
+        for p in procs:
+            p.join(timeout=max(1.0, deadline - time.time()))
+    finally:
+        for p in procs:
+            if p.is_alive():
+                p.kill()
+                p.join(10)
+
+    def at(log, text):
+        return next(t for t, m in log if text in m)
+
+    old_logs = [results[("saved", r)] for r in range(old_ws)]
+    new_recs = [results[("loaded", r)] for r in range(new_ws)]
+    start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done: packing begins
+    pack_ms = max((at(l, "packed") - at(l, "is_scale_up")) * 1e3 for l in old_logs)
+    end = max(rec["t_return"] for rec in new_recs)
+    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "mapped the state")) * 1e3 for rec in new_recs]
+    return {
+        "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
+        "state_bytes_received": sum(rec["bytes"] for rec in new_recs),
+        "pack_ms_max": round(pack_ms, 2),
+        "reshard_ms_max": round(max(reshard), 2),
+        "handoff_ms": round((end - start) * 1e3, 1),
+        "handoff_ms_note": ("wall time from the old world's handshake to the last new rank's return from "
+                            "migration_load: pack, queue messages, IPC mapping, reshard, load_state_dict; "
+                            "new processes are fresh (first HIP use included)"),
+        "parity": {"tensors": sum(rec["tensors"] for rec in new_recs),
+                   "mismatched": sum(rec["mismatched"] for rec in new_recs),
+                   "first_mismatches": [b for rec in new_recs for b in rec["bad"]][:5],
+                   "against": "the same seeded global tensors cut for each new rank (suika_amd.workloads.shard_global)"},
+        "per_new_rank_log_ms": [
+            {m.split(":", 1)[1].strip()[:40]: round((t - rec["t_call"]) * 1e3, 1) for t, m in rec["log"]}
+            for rec in new_recs],
+    }
+
+
 def cpu_model() -> str:
     try:
         import subprocess
@@ -391,6 +623,10 @@ def main(argv=None) -> int:
         return 0
 
     key = args.config or BENCH_CONFIG
+    if args.handoff:
+        rec = handoff_leg(key)
+        print(json.dumps({"handoff": rec}), flush=True)
+        return 0 if rec["parity"]["mismatched"] == 0 else 1
     w = CONFIGS[key]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

@@ -66,7 +66,19 @@ EXPORTED_SYMBOLS = (
     "sr_schedule",
     "sr_lower",
     "sr_lowering_destroy",
+    "sr_handoff_alloc",
+    "sr_handoff_free",
+    "sr_handoff_open",
+    "sr_handoff_close",
 )
+
+# Largest hand-off allocation (SR_HANDOFF_MAX_BYTES, include/suika_handoff.h).
+HANDOFF_MAX_BYTES = 2146435072
+
+
+class SrIpcHandle(ctypes.Structure):
+    """The 64 opaque bytes of an exported hand-off allocation (sr_ipc_handle)."""
+    _fields_ = [("bytes", ctypes.c_ubyte * 64)]
 
 ABI_VERSION = 4
 
@@ -307,6 +319,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_lower.argtypes = [vp, i64, vp, i64, vp, i64, vp, ctypes.POINTER(ctypes.POINTER(SrLowering))]
     lib.sr_lowering_destroy.restype = None
     lib.sr_lowering_destroy.argtypes = [ctypes.POINTER(SrLowering)]
+    lib.sr_handoff_alloc.restype = ctypes.c_int
+    lib.sr_handoff_alloc.argtypes = [ctypes.c_uint64, ctypes.POINTER(vp), ctypes.POINTER(SrIpcHandle)]
+    lib.sr_handoff_free.restype = ctypes.c_int
+    lib.sr_handoff_free.argtypes = [vp]
+    lib.sr_handoff_open.restype = ctypes.c_int
+    lib.sr_handoff_open.argtypes = [ctypes.POINTER(SrIpcHandle), ctypes.POINTER(vp)]
+    lib.sr_handoff_close.restype = ctypes.c_int
+    lib.sr_handoff_close.argtypes = [vp]
 
 
 def lib() -> ctypes.CDLL:

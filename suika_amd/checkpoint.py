@@ -205,34 +205,70 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
     return (optimizer, other_context) if optimizer_provider else other_context
 
 
+def _device(device) -> torch.device:
+    """The reference's device argument (migration.py:1367-1372): default the
+    current CUDA device, made current."""
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    elif not isinstance(device, torch.device):
+        device = torch.device(device)
+    if device.type == "cuda":
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        torch.cuda.set_device(device.index)
+    return device
+
+
 def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = None,
                    other_context: Any = None, device: Optional[torch.device] = None,
                    world: Optional[dist.ProcessGroup] = None, log_func: Optional[Callable] = None,
                    checkpoint_resume: Optional[str] = None):
     """Suika's save-side migration API (Suika/migration.py:1357-1486).
 
-    With ``checkpoint_resume`` it writes the checkpoint (as the reference
-    does at :1382-1392).  The live hand-off to a new process -- CUDA IPC of
-    every tensor plus a cross-GPU exchange -- is not part of this one-GPU
-    build and raises ``NotImplementedError``."""
+    With ``checkpoint_resume`` it writes the checkpoint (:1382-1392).
+    Otherwise it hands this rank's state to the new plan's processes on the
+    same GPU over ``IPC_queues`` (forward, backward), as
+    ``suika_amd.handoff.live_save`` describes: the world-size handshake, the
+    state packed into exported device allocations, and their release once
+    the new world has resharded from them."""
+    if log_func is None:
+        log_func = lambda msg: None  # noqa: E731
+    device = _device(device)
+    log_func("migration_save: begin")
     if checkpoint_resume is not None:
+        log_func(f"migration_save: checkpoint-resume={checkpoint_resume}")
         return checkpoint_save(model=model, optimizer=optimizer, other_context=other_context,
                                checkpoint_dir=checkpoint_resume, world=world, log_func=log_func)
-    raise NotImplementedError("live migration between processes (IPC hand-off and cross-GPU "
-                              "exchange) is not part of this build; use checkpoint_resume or "
-                              "execute_param_transfer with the shards resident on this GPU")
+    from .handoff import live_save
+    return live_save(IPC_queues, model, optimizer, other_context, device, world, log_func)
 
 
 def migration_load(IPC_queues, model: Module,
                    optimizer: Union[Optimizer, Callable[[], Optimizer], None] = None,
                    device: Optional[torch.device] = None, world: Optional[dist.ProcessGroup] = None,
                    log_func: Optional[Callable] = None, checkpoint_resume: Optional[str] = None):
-    """Suika's load-side migration API (Suika/migration.py:1546-1727); see
-    ``migration_save``.  With ``checkpoint_resume`` the checkpoint is
-    resharded into ``model`` on the GPU (:1566-1575)."""
+    """Suika's load-side migration API (Suika/migration.py:1546-1727).
+
+    With ``checkpoint_resume`` the checkpoint is resharded into ``model`` on
+    the GPU (:1566-1575).  Otherwise the old plan's processes on the same GPU
+    hand their state over ``IPC_queues`` and this rank reshards its share
+    straight from their memory (``suika_amd.handoff.live_load``).  Returns
+    ``other_context``, or ``(optimizer, other_context)`` for an optimizer
+    provider; a fresh launch (the launcher's placeholder on the queue)
+    returns ``None`` / ``(optimizer_provider(), None)``."""
+    if log_func is None:
+        log_func = lambda msg: None  # noqa: E731
+    device = _device(device)
+    log_func("migration_load: begin")
     if checkpoint_resume is not None:
+        log_func(f"migration_load: checkpoint_resume = {checkpoint_resume}")
         return checkpoint_load(model=model, optimizer=optimizer, checkpoint_dir=checkpoint_resume,
                                world=world, log_func=log_func, device=device)
-    raise NotImplementedError("live migration between processes (IPC hand-off and cross-GPU "
-                              "exchange) is not part of this build; use checkpoint_resume or "
-                              "execute_param_transfer with the shards resident on this GPU")
+    if callable(optimizer) and not isinstance(optimizer, Optimizer):
+        optimizer_provider, optimizer = optimizer, None
+    elif isinstance(optimizer, Optimizer) or optimizer is None:
+        optimizer_provider = None
+    else:
+        raise TypeError(f"optimizer should be Optimizer or Callable, but got {type(optimizer)}")
+    from .handoff import live_load
+    return live_load(IPC_queues, model, optimizer_provider, optimizer, device, world, log_func)

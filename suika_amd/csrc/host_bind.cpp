@@ -23,7 +23,8 @@
 //   encode_ops:      one rank's TransferOps as sr_lower's op and meta tables;
 //   piece_numels:    elements per op's piece (launch-group balancing);
 //   ops_of_rank:     the ops one destination rank executes;
-//   tensor_runs:     runs of a tensor's consecutive ops and their elements.
+//   tensor_runs:     runs of a tensor's consecutive ops and their elements;
+//   device_views:    tensors over a mapped hand-off allocation (no copy).
 //
 // No device work happens here; the tensors come from torch's caching
 // allocator on the device's current stream, as torch.empty would.
@@ -797,6 +798,30 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
   return out;
 }
 
+// Tensors over device memory this process does not own -- another process's
+// hand-off allocation mapped here: one tensor per (byte offset, shape, dtype)
+// of `views` at `base` on cuda:`device_index`.  The tensors never free the
+// memory and must not outlive its mapping.
+py::list device_views(uint64_t base, py::list views, int64_t device_index) {
+  py::list out;
+  const at::Device dev(at::kCUDA, c10::DeviceIndex(device_index));
+  for (py::handle v : views) {
+    if (!PyTuple_Check(v.ptr()) || PyTuple_GET_SIZE(v.ptr()) != 3)
+      throw py::value_error("a view is (byte offset, shape, dtype)");
+    const uint64_t off = py::reinterpret_borrow<py::object>(PyTuple_GET_ITEM(v.ptr(), 0)).cast<uint64_t>();
+    const std::vector<int64_t> shape =
+        py::reinterpret_borrow<py::object>(PyTuple_GET_ITEM(v.ptr(), 1)).cast<std::vector<int64_t>>();
+    PyObject* dt = PyTuple_GET_ITEM(v.ptr(), 2);
+    if (!THPDtype_Check(dt)) throw py::type_error("view dtype must be a torch.dtype");
+    const at::ScalarType st = reinterpret_cast<THPDtype*>(dt)->scalar_type;
+    if (off % c10::elementSize(st) != 0) throw py::value_error("view offset not aligned to its element size");
+    at::Tensor t = at::from_blob(reinterpret_cast<void*>(base + off), shape, [](void*) {},
+                                 at::TensorOptions().dtype(st).device(dev));
+    out.append(py::reinterpret_steal<py::object>(THPVariable_Wrap(std::move(t))));
+  }
+  return out;
+}
+
 PYBIND11_MODULE(_suika_host, m) {
   m.doc() = "Per-tensor host work of execute_param_transfer (source checks, destination allocation)";
   m.def("collect_sources", &collect_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
@@ -816,4 +841,5 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
         py::arg("op_cls"), py::arg("meta_cls"));
+  m.def("device_views", &device_views, py::arg("base"), py::arg("views"), py::arg("device_index"));
 }

@@ -1,0 +1,366 @@
+"""Live state migration between processes on one GPU.
+
+Suika's ``migration_save`` / ``migration_load`` (Suika/migration.py:1357-1727)
+hand a job's model and optimizer state from the processes of its old plan to
+the processes of its new plan.  The two sets of processes run side by side;
+each guard process owns a pair of queues shared by its old and new rank
+(``IPC_queues``: forward, backward).  The reference moves every tensor through
+the queue as a CUDA-IPC handle, one acknowledgement each, clones it on the
+receiving side, and reshards over NCCL in the old world (scale-down) or the
+new one (scale-up) (Suika/utils.py:325-406).
+
+Here, with every old and new rank on the same GPU:
+
+* the handshake on world sizes is the reference's (rank 0 of each side, over
+  the queues, :1395-1405 / :1587-1598);
+* each old rank packs its merged state (``merge_model_and_optimizer_state_dict``)
+  into a few device allocations of its own with one gather launch, exports
+  them (``sr_handoff_alloc``, at most 1 GiB each, always below 2 GiB), frees
+  its state tensors as the reference frees each sent tensor, and the old world
+  all-gathers the export records (handles, offsets, shapes: CPU objects);
+* old rank ``i`` sends the source layout, the context and every old rank's
+  record to new rank ``i`` over its forward queue; new ranks without an old
+  counterpart read the launcher's placeholder (``dummy_migration_IPC_state_dict``),
+  and the new world takes rank 0's message;
+* each new rank maps the allocations of the old ranks its pieces come from
+  (``sr_handoff_open``), views the state there as tensors without copying, and
+  runs ``execute_param_transfer`` (one gather per launch group) straight from
+  them into one destination arena that the model adopts with
+  ``load_state_dict(assign=True)``;
+* after the new world's barrier, new rank 0 acknowledges on rank 0's backward
+  queue; the old world then frees its allocations and returns.
+
+The packed allocations are the per-peer buffers of a pack -> unpack reshard:
+the old side reads and writes P bytes, the new side reads P and writes D, and
+nothing is cloned tensor by tensor.  The scale-up / scale-down distinction of
+the reference only decides which world reshards; here the new world always
+does, reading from the mapped memory.
+"""
+from __future__ import annotations
+
+import ctypes
+import time
+from collections import OrderedDict
+from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
+
+import torch
+import torch.distributed as dist
+from torch import Tensor
+
+from . import _lib
+
+# Bytes per hand-off allocation the packer fills before it opens the next;
+# a single larger tensor gets an allocation of its own (below 2 GiB).
+CHUNK_BYTES = 1 << 30
+ALIGN = 256
+
+# What the launcher puts on a new guard's forward queue when no old process
+# exists (Suika/migration.py:1314-1318, training.py:319-323): migration_load
+# then finds no source layout and returns without state.
+dummy_migration_IPC_state_dict = {
+    "source_param_layout": None,
+    "source_state_dict": {},
+    "other_context_dict": {},
+}
+
+DONE = "suika_amd: handoff complete"
+
+
+def pack_layout(nbytes: Sequence[int], chunk_bytes: int = CHUNK_BYTES) -> Tuple[List[Tuple[int, int]], List[int]]:
+    """(chunk, byte offset) of every tensor of ``nbytes`` bytes, in order, and
+    the size of every chunk: tensors follow each other at 256-byte aligned
+    offsets until the next would pass ``chunk_bytes``; a tensor larger than
+    that gets a chunk of its own.  No chunk exceeds the hand-off limit."""
+    where: List[Tuple[int, int]] = []
+    sizes: List[int] = []
+    for n in nbytes:
+        assert 0 < n <= _lib.HANDOFF_MAX_BYTES, \
+            f"a tensor of {n} bytes does not fit one hand-off allocation ({_lib.HANDOFF_MAX_BYTES} bytes)"
+        off = (sizes[-1] + ALIGN - 1) // ALIGN * ALIGN if sizes else 0
+        if sizes and off + n <= chunk_bytes:
+            sizes[-1] = off + n
+        else:
+            sizes.append(n)
+            off = 0
+        where.append((len(sizes) - 1, off))
+    return where, sizes
+
+
+def _dtype_of(name: str) -> torch.dtype:
+    dt = getattr(torch, name.replace("torch.", ""), None)
+    assert isinstance(dt, torch.dtype), f"unknown dtype {name}"
+    return dt
+
+
+class Handoff:
+    """An old rank's merged state packed into exported device allocations.
+
+    ``state`` is ``{name: {field: tensor}}``.  Non-empty tensors on
+    ``device`` are packed, in order, at 256-byte aligned offsets into
+    allocations of at most ``chunk_bytes`` (a larger tensor gets one of its
+    own); every other value (CPU tensors such as AdamW's ``step``, empty
+    tensors) rides along in the record as a CPU tensor.  The copies are done
+    when the constructor returns.
+    """
+
+    def __init__(self, state: Dict[str, Dict[str, Tensor]], device: torch.device, rank: int,
+                 chunk_bytes: int = CHUNK_BYTES):
+        L = self._L = _lib.lib()
+        self.rank = rank
+        self.device = device
+        self._ptrs: List[int] = []
+        moved: List[Tuple[str, str, Tensor]] = []
+        self.tensors: Dict[str, Dict[str, tuple]] = {}
+        self.host: Dict[str, Dict[str, Tensor]] = {}
+        for name, entry in state.items():
+            for f, t in entry.items():
+                if not (isinstance(t, Tensor) and t.is_cuda and t.device == device and t.numel() > 0):
+                    self.host.setdefault(name, {})[f] = t.detach().cpu() if isinstance(t, Tensor) else t
+                    continue
+                assert t.is_contiguous(), f"handoff: {name}/{f} is not contiguous"
+                moved.append((name, f, t))
+        where, sizes = pack_layout([t.numel() * t.element_size() for _, _, t in moved], chunk_bytes)
+        packed = [(name, f, t, c, off) for (name, f, t), (c, off) in zip(moved, where)]
+        for name, f, t, c, off in packed:
+            self.tensors.setdefault(name, {})[f] = (c, off, tuple(t.shape), str(t.dtype))
+        self.chunks: List[Tuple[bytes, int]] = []
+        try:
+            with torch.cuda.device(device):
+                for n in sizes:
+                    ptr, handle = ctypes.c_void_p(), _lib.SrIpcHandle()
+                    _lib.check(L.sr_handoff_alloc(n, ctypes.byref(ptr), ctypes.byref(handle)), "sr_handoff_alloc", L)
+                    self._ptrs.append(ptr.value)
+                    self.chunks.append((bytes(handle.bytes), n))
+                if packed:
+                    self._pack(packed, sizes)
+        except BaseException:
+            self.release()
+            raise
+        self.bytes = sum(sizes)
+
+    def _pack(self, packed, sizes) -> None:
+        """One gather launch: every tensor, as bytes, to its chunk offset."""
+        import numpy as np
+        L = self._L
+        src = np.zeros(len(packed), dtype=_lib.SR_TENSOR_DTYPE)
+        dst = np.zeros(len(sizes), dtype=_lib.SR_TENSOR_DTYPE)
+        pieces = np.zeros(len(packed), dtype=_lib.SR_PIECE_DTYPE)
+        for i, (_, _, t, chunk, off) in enumerate(packed):
+            nbytes = t.numel() * t.element_size()
+            src[i] = (1, nbytes, _lib.SR_DT_U8, 0)
+            pieces[i] = (_lib.SR_PIECE_COPY, 0, i, chunk, -1, 0, 1, nbytes, 0, 0, 0, off)
+        for c, n in enumerate(sizes):
+            dst[c] = (1, n, _lib.SR_DT_U8, 0)
+        opts = _lib.SrPlanOptions(0, 0, _lib.SR_OPT_SKIP_COVERAGE, 0)
+        plan = ctypes.c_void_p()
+        _lib.check(L.sr_plan_create(_lib.as_tensors(src), len(src), _lib.as_tensors(dst), len(dst), 1,
+                                    _lib.as_pieces(pieces), len(pieces), ctypes.byref(opts), ctypes.byref(plan)),
+                   "handoff pack: sr_plan_create", L)
+        try:
+            vp = ctypes.c_void_p
+            sp = (vp * len(packed))(*[t.data_ptr() for _, _, t, _, _ in packed])
+            dp = (vp * len(sizes))(*self._ptrs)
+            stream = torch.cuda.current_stream(self.device)
+            _lib.check(L.sr_gather(plan, sp, dp, vp(stream.cuda_stream)), "handoff pack: sr_gather", L)
+            stream.synchronize()
+        finally:
+            L.sr_plan_destroy(plan)
+
+    def record(self) -> Dict[str, Any]:
+        """What a new rank needs to map and view this state (CPU objects)."""
+        return {"rank": self.rank, "device": self.device.index, "chunks": list(self.chunks),
+                "tensors": self.tensors, "host": self.host}
+
+    def release(self) -> None:
+        """Free the allocations (after every new rank has closed them)."""
+        L = self._L
+        with torch.cuda.device(self.device):
+            while self._ptrs:
+                _lib.check(L.sr_handoff_free(ctypes.c_void_p(self._ptrs.pop())), "sr_handoff_free", L)
+
+
+class MappedSources:
+    """Old ranks' packed state mapped into this process: ``states`` is
+    ``{old rank: {name: {field: tensor}}}``, tensors viewing the mapped
+    allocations (no copy); CPU values of the records ride along.  ``close``
+    unmaps them; the views must be dropped first."""
+
+    def __init__(self, records: Sequence[Dict[str, Any]], ranks: Sequence[int], device: torch.device):
+        L = self._L = _lib.lib()
+        self.device = device
+        self._opened: List[int] = []
+        self.states: Dict[int, Dict[str, Dict[str, Tensor]]] = {}
+        by_rank = {rec["rank"]: rec for rec in records}
+        host = _lib.host()
+        try:
+            with torch.cuda.device(device):
+                for r in ranks:
+                    rec = by_rank[r]
+                    assert rec["device"] == device.index, \
+                        f"rank {r}'s state is on cuda:{rec['device']}, this rank runs on {device}"
+                    bases = []
+                    for handle, _ in rec["chunks"]:
+                        h = _lib.SrIpcHandle()
+                        ctypes.memmove(h.bytes, handle, len(handle))
+                        ptr = ctypes.c_void_p()
+                        _lib.check(L.sr_handoff_open(ctypes.byref(h), ctypes.byref(ptr)), "sr_handoff_open", L)
+                        self._opened.append(ptr.value)
+                        bases.append(ptr.value)
+                    state: Dict[str, Dict[str, Tensor]] = {}
+                    keys = [(n, f) for n, e in rec["tensors"].items() for f in e]
+                    per_chunk: Dict[int, List[Tuple[str, str]]] = {}
+                    for n, f in keys:
+                        per_chunk.setdefault(rec["tensors"][n][f][0], []).append((n, f))
+                    for c, members in per_chunk.items():
+                        views = [(rec["tensors"][n][f][1], list(rec["tensors"][n][f][2]),
+                                  _dtype_of(rec["tensors"][n][f][3])) for n, f in members]
+                        for (n, f), t in zip(members, host.device_views(bases[c], views, device.index)):
+                            state.setdefault(n, {})[f] = t
+                    for n, e in rec["host"].items():
+                        for f, v in e.items():
+                            state.setdefault(n, {})[f] = v
+                    self.states[r] = state
+        except BaseException:
+            self.states = {}
+            self.close()
+            raise
+
+    def close(self) -> None:
+        L = self._L
+        self.states = {}
+        with torch.cuda.device(self.device):
+            while self._opened:
+                _lib.check(L.sr_handoff_close(ctypes.c_void_p(self._opened.pop())), "sr_handoff_close", L)
+
+
+def _broadcast_objects(*objs, group=None):
+    """Rank 0's objects on every rank of ``group`` (Suika/utils.py:98-104)."""
+    lst = list(objs)
+    src = 0 if group is None else dist.get_global_rank(group, 0)
+    dist.broadcast_object_list(lst, src=src, group=group)
+    return lst[0] if len(lst) == 1 else lst
+
+
+def live_save(IPC_queues, model, optimizer, other_context, device: torch.device, world,
+              log_func: Callable[[str], None]) -> None:
+    """The old side of a live migration (Suika/migration.py:1394-1486)."""
+    from .meta import ParamLayout
+    from .migration import forcefully_free_tensor, merge_model_and_optimizer_state_dict
+
+    rank = dist.get_rank(world)
+    if rank == 0:
+        old_world_size = dist.get_world_size(world)
+        IPC_queues[0].put(old_world_size)
+        new_world_size = IPC_queues[1].get(block=True)
+        is_scale_up = new_world_size >= old_world_size
+    else:
+        is_scale_up = new_world_size = None
+    is_scale_up, new_world_size = _broadcast_objects(is_scale_up, new_world_size, group=world)
+    log_func(f"migration_save: is_scale_up = {is_scale_up} (new world size {new_world_size})")
+
+    param_layout = ParamLayout()
+    param_layout.gather(model, world)
+    source_state_dict, other_context_dict = merge_model_and_optimizer_state_dict(model, optimizer, other_context)
+
+    t0 = time.perf_counter()
+    handoff = Handoff(source_state_dict, device, rank)
+    t1 = time.perf_counter()
+    log_func(f"migration_save: packed {handoff.bytes / 1e9:.3f} GB into {len(handoff.chunks)} hand-off "
+             f"allocation(s) in {(t1 - t0) * 1e3:.2f} ms")
+    # the state now lives in the hand-off allocations; release it as the
+    # reference releases every tensor it has sent (utils.py:372-376)
+    for entry in source_state_dict.values():
+        for t in entry.values():
+            if isinstance(t, Tensor) and t.is_cuda:
+                forcefully_free_tensor(t)
+    del source_state_dict
+    # and return the memory to the device for the new plan's processes, as
+    # the reference's cuda_gc does after sending (utils.py:248-253, 385)
+    torch.cuda.empty_cache()
+    try:
+        records = [None] * dist.get_world_size(world)
+        dist.all_gather_object(records, handoff.record(), group=world)
+        log_func(f"migration_save: {len(records)} hand-off record(s) gathered")
+        if rank < new_world_size:
+            IPC_queues[0].put({"source_param_layout": param_layout, "source_state_dict": {},
+                               "other_context_dict": other_context_dict, "handoff": records})
+            log_func("migration_save: hand-off sent to the new rank")
+        # the new world maps these allocations until it has resharded
+        if rank == 0:
+            ack = IPC_queues[1].get(block=True)
+            assert ack == DONE, f"migration_save: unexpected acknowledgement {ack!r}"
+        dist.barrier(world)
+        log_func("migration_save: the new world is done with the hand-off")
+    finally:
+        handoff.release()
+    log_func("migration_save: end")
+
+
+def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.device, world,
+              log_func: Callable[[str], None]):
+    """The new side of a live migration (Suika/migration.py:1586-1727)."""
+    from .meta import ParamLayout, schedule_param_transfer
+    from .migration import execute_param_transfer, split_model_and_optimizer_state_dict
+
+    rank = dist.get_rank(world)
+    if rank == 0:
+        old_world_size = IPC_queues[0].get(block=True)
+        new_world_size = dist.get_world_size(world)
+        if old_world_size != 0:
+            IPC_queues[1].put(new_world_size)
+        is_scale_up = new_world_size >= old_world_size
+    else:
+        is_scale_up = None
+    is_scale_up = _broadcast_objects(is_scale_up, group=world)
+    log_func(f"migration_load: is_scale_up = {is_scale_up}")
+
+    target_param_layout = ParamLayout()
+    target_param_layout.gather(model, world)
+    # old rank i's message, or the launcher's placeholder when there is none
+    msg = IPC_queues[0].get(block=True)
+    log_func("migration_load: hand-off message received")
+    source_param_layout, other_context_dict, records = _broadcast_objects(
+        msg.get("source_param_layout"), msg.get("other_context_dict"), msg.get("handoff"), group=world)
+    del msg
+
+    if source_param_layout is None:
+        log_func("migration_load: no checkpoint received; skip loading")
+        if hasattr(model, "instantiate") and getattr(model, "on_meta", False):
+            model.instantiate()
+        return (optimizer_provider(), None) if optimizer_provider else None
+
+    t0 = time.perf_counter()
+    ops = schedule_param_transfer(source_param_layout, target_param_layout)
+    needed = sorted({op.src_rank for op in ops if op.dst_rank == rank})
+    mapped = MappedSources(records, needed, device)
+    log_func(f"migration_load: mapped the state of old rank(s) {needed}")
+    try:
+        t1 = time.perf_counter()
+        target_state_dict = execute_param_transfer(
+            transfer_ops=ops, source_state_dict={}, device=device,
+            expected_sub_fields=other_context_dict["expected_sub_fields"], world=world,
+            fake_source_state_dicts=mapped.states, log_func=log_func, rank=rank, arena=True)
+        torch.cuda.synchronize(device)
+        t2 = time.perf_counter()
+    finally:
+        mapped.close()
+    log_func(f"migration_load: mapped {len(needed)} old rank(s) in {(t1 - t0) * 1e3:.2f} ms, resharded in "
+             f"{(t2 - t1) * 1e3:.2f} ms")
+    dist.barrier(world)
+    if rank == 0:
+        IPC_queues[1].put(DONE)
+    log_func("migration_load: every new rank has resharded")
+
+    model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
+        model=model, merged_state_dict=target_state_dict, other_context_dict=other_context_dict)
+    model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
+    model.load_state_dict(model_state_dict, assign=True)
+    log_func("migration_load: model state adopted")
+    if optimizer_provider:
+        optimizer = optimizer_provider()
+    if optimizer:
+        # one parameter group, as the reference (migration.py:1712-1716)
+        optimizer_state_dict["param_groups"][0]["params"] = optimizer.state_dict()["param_groups"][0]["params"]
+        optimizer.load_state_dict(optimizer_state_dict)
+    log_func("migration_load: end")
+    return (optimizer, other_context) if optimizer_provider else other_context

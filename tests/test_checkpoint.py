@@ -110,12 +110,24 @@ def test_checkpoint_save_files(tmp_path):
             assert float(ent["step"]) == r + 3
 
 
-def test_migration_without_checkpoint_is_not_in_this_build():
-    mod = build_module(MODEL, Parallel(1), 0)
-    with pytest.raises(NotImplementedError):
-        migration_save(None, mod)
-    with pytest.raises(NotImplementedError):
-        migration_load(None, mod)
+def test_migration_api_matches_the_reference_signatures():
+    """migration_save / migration_load take the reference's parameters, in
+    its order and with its defaults (Suika/migration.py:1357-1366,
+    1546-1554); the launcher's placeholder has the reference's keys
+    (:1314-1318)."""
+    import inspect
+
+    from suika_amd import dummy_migration_IPC_state_dict
+    save = inspect.signature(migration_save).parameters
+    load = inspect.signature(migration_load).parameters
+    assert list(save) == ["IPC_queues", "model", "optimizer", "other_context", "device", "world", "log_func",
+                          "checkpoint_resume"]
+    assert list(load) == ["IPC_queues", "model", "optimizer", "device", "world", "log_func", "checkpoint_resume"]
+    for params in (save, load):
+        for name in list(params)[2:]:
+            assert params[name].default is None, name
+    assert dummy_migration_IPC_state_dict == {"source_param_layout": None, "source_state_dict": {},
+                                              "other_context_dict": {}}
 
 
 def _check_loaded(model, opt, par, rank, glob):
