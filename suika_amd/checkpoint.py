@@ -14,12 +14,26 @@ The reference reshards on the CPU (``execute_param_transfer`` with
 ``device="cpu"``, migration.py:1235-1244); here the source files are
 memory-mapped, only the tensors this rank's pieces read are copied to HBM,
 and the HIP engine reshards them (``route="direct"``: one gather launch).
-Files hold only tensors, numbers, strings and plain containers -- layouts
-are stored as dicts -- so they load with ``torch.load(weights_only=True)``.
+
+The files are the reference's: ``param_layout.pt`` is a pickled
+``Suika.migration.ParamLayout`` of ``Suika.migration.TensorMeta`` objects and
+``other_context.pt`` holds such metas in ``expected_sub_fields``
+(migration.py:1175-1177).  Both are read with ``torch.load(weights_only=True)``:
+the two class paths are allowlisted to attribute holders of this module
+(``ReferenceParamLayout`` / ``ReferenceTensorMeta``), so loading a file runs
+none of its code, and the holders are then turned into this build's
+``ParamLayout`` / ``TensorMeta``.  ``checkpoint_save`` writes the same two
+class paths, so the reference's ``checkpoint_load`` reads them into its own
+classes.  This build's extra shard kinds ride along as ``kind`` /
+``kind_args`` attributes, which the reference does not read.  Layout files of
+the plain-dict format written by earlier versions of this module are still
+read.
 """
 from __future__ import annotations
 
 import os
+import pickle
+import types
 from collections import OrderedDict
 from typing import Any, Callable, Dict, Optional, Union
 
@@ -28,7 +42,7 @@ import torch.distributed as dist
 from torch.nn import Module
 from torch.optim import Optimizer
 
-from .meta import ParamLayout, TensorMeta, schedule_param_transfer
+from .meta import CHUNK, ParamLayout, TensorMeta, schedule_param_transfer
 from .migration import (execute_param_transfer, merge_model_and_optimizer_state_dict,
                         split_model_and_optimizer_state_dict)
 
@@ -61,18 +75,103 @@ def layout_from_plain(d: Dict[int, Dict[str, Dict[str, Any]]]) -> ParamLayout:
                                    for r, metas in d.items()})
 
 
-def _context_to_plain(ctx: Dict[str, Any]) -> Dict[str, Any]:
+class ReferenceTensorMeta:
+    """What a checkpoint file stores for a ``Suika.migration.TensorMeta``
+    (migration.py:29-58): the attributes ``name``, ``dtype``, ``shape``,
+    ``tp_meta`` and, for this build's shard kinds, ``kind`` / ``kind_args``.
+    An attribute holder: nothing of it runs when a file is loaded."""
+
+
+class ReferenceParamLayout:
+    """What a checkpoint file stores for a ``Suika.migration.ParamLayout``
+    (migration.py:161-170): the attribute ``layout``, {rank: {name: meta}}."""
+
+
+_REFERENCE_NAMES = {ReferenceTensorMeta: ("Suika.migration", "TensorMeta"),
+                    ReferenceParamLayout: ("Suika.migration", "ParamLayout")}
+_SAFE_GLOBALS = [(cls, f"{mod}.{name}") for cls, (mod, name) in _REFERENCE_NAMES.items()]
+
+
+class _ReferencePickler(pickle._Pickler):
+    """Pickles the two holders under the reference's class paths (without
+    importing the reference): the reference's ``torch.load`` then builds its
+    own ``ParamLayout`` / ``TensorMeta`` from their attributes."""
+
+    def save_global(self, obj, name=None):
+        ref = _REFERENCE_NAMES.get(obj) if isinstance(obj, type) else None
+        if ref is None:
+            return super().save_global(obj, name)
+        module, qualname = ref
+        if self.proto >= 4:
+            self.save(module)
+            self.save(qualname)
+            self.write(pickle.STACK_GLOBAL)
+        else:
+            self.write(pickle.GLOBAL + f"{module}\n{qualname}\n".encode("utf-8"))
+        self.memoize(obj)
+
+
+_PICKLE_MODULE = types.ModuleType("suika_amd_reference_pickle")
+_PICKLE_MODULE.Pickler = _ReferencePickler
+
+
+def meta_to_reference(m: TensorMeta) -> ReferenceTensorMeta:
+    r = ReferenceTensorMeta()
+    r.dtype = m.dtype
+    r.shape = torch.Size(int(s) for s in m.shape)
+    r.tp_meta = None if m.tp_meta is None else tuple(int(v) for v in m.tp_meta)
+    r.name = m.name
+    if m.kind != CHUNK:
+        r.kind = m.kind
+        r.kind_args = tuple(int(v) for v in m.kind_args)
+    return r
+
+
+def meta_from_reference(r) -> TensorMeta:
+    tp = getattr(r, "tp_meta", None)
+    return TensorMeta(name=getattr(r, "name", None), dtype=r.dtype, shape=tuple(r.shape),
+                      tp_meta=None if tp is None else tuple(tp), kind=getattr(r, "kind", CHUNK),
+                      kind_args=tuple(getattr(r, "kind_args", ())))
+
+
+def layout_to_reference(pl: ParamLayout) -> ReferenceParamLayout:
+    out = ReferenceParamLayout()
+    out.layout = {int(r): {n: meta_to_reference(m) for n, m in metas.items()} for r, metas in pl.layout.items()}
+    return out
+
+
+def layout_from_reference(obj) -> ParamLayout:
+    if isinstance(obj, dict):                  # the plain-dict format of earlier versions
+        return layout_from_plain(obj)
+    return ParamLayout.from_metas({int(r): {n: meta_from_reference(m) for n, m in metas.items()}
+                                   for r, metas in obj.layout.items()})
+
+
+def _context_to_reference(ctx: Dict[str, Any]) -> Dict[str, Any]:
     out = dict(ctx)
-    out["expected_sub_fields"] = [[f, t if isinstance(t, str) else meta_to_plain(t)]
+    out["expected_sub_fields"] = [(f, t if isinstance(t, str) else meta_to_reference(t))
                                   for f, t in ctx["expected_sub_fields"]]
     return out
 
 
-def _context_from_plain(ctx: Dict[str, Any]) -> Dict[str, Any]:
+def _context_from_reference(ctx: Dict[str, Any]) -> Dict[str, Any]:
     out = dict(ctx)
-    out["expected_sub_fields"] = [(f, t if isinstance(t, str) else meta_from_plain(t))
-                                  for f, t in ctx["expected_sub_fields"]]
+    out["expected_sub_fields"] = [
+        (f, t if isinstance(t, str) else (meta_from_plain(t) if isinstance(t, dict) else meta_from_reference(t)))
+        for f, t in ctx["expected_sub_fields"]]
     return out
+
+
+def save_reference_object(obj, path: str) -> None:
+    """``torch.save`` with the holders written under the reference's class paths."""
+    torch.save(obj, path, pickle_module=_PICKLE_MODULE)
+
+
+def load_reference_object(path: str):
+    """``torch.load(weights_only=True)`` of a layout or context file, the
+    reference's class paths allowlisted to the attribute holders."""
+    with torch.serialization.safe_globals(_SAFE_GLOBALS):
+        return torch.load(path, weights_only=True, map_location="cpu")
 
 
 def _rank_and_world(world) -> tuple:
@@ -108,8 +207,8 @@ def checkpoint_save(model: Module, optimizer: Optional[Optimizer], other_context
     state_dict, other_context_dict = merge_model_and_optimizer_state_dict(model, optimizer, other_context)
     rank, _ = _rank_and_world(world)
     if rank == 0:
-        torch.save(layout_to_plain(layout), os.path.join(checkpoint_dir, LAYOUT_FILE))
-        torch.save(_context_to_plain(other_context_dict), os.path.join(checkpoint_dir, CONTEXT_FILE))
+        save_reference_object(layout_to_reference(layout), os.path.join(checkpoint_dir, LAYOUT_FILE))
+        save_reference_object(_context_to_reference(other_context_dict), os.path.join(checkpoint_dir, CONTEXT_FILE))
     torch.save(state_dict, os.path.join(checkpoint_dir, f"state_dict_{rank}.pt"))
     log_func("checkpoint_save: end")
 
@@ -144,10 +243,9 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
     rank, _ = _rank_and_world(world)
 
     try:
-        source_layout = layout_from_plain(
-            torch.load(os.path.join(checkpoint_dir, LAYOUT_FILE), weights_only=True, map_location="cpu"))
-        other_context_dict = _context_from_plain(
-            torch.load(os.path.join(checkpoint_dir, CONTEXT_FILE), weights_only=True, map_location="cpu"))
+        source_layout = layout_from_reference(load_reference_object(os.path.join(checkpoint_dir, LAYOUT_FILE)))
+        other_context_dict = _context_from_reference(
+            load_reference_object(os.path.join(checkpoint_dir, CONTEXT_FILE)))
     except FileNotFoundError as e:
         log_func(f"checkpoint_load: [warning] checkpoint file not found, skip loading\n{e}")
         return (optimizer_provider(), None) if optimizer_provider else None

@@ -17,7 +17,8 @@ import torch.multiprocessing as mp
 
 from oracle import reshard_oracle as O
 from suika_amd import checkpoint_load, checkpoint_save, migration_load, migration_save, schedule_param_transfer
-from suika_amd.checkpoint import layout_from_plain, layout_to_plain
+from suika_amd.checkpoint import (layout_from_plain, layout_from_reference, layout_to_plain,
+                                  load_reference_object)
 from suika_amd.inventory import ModelSpec, Parallel, build_layout, build_module
 from tests.harness import t2np, to_ometa
 
@@ -93,9 +94,10 @@ def test_checkpoint_save_files(tmp_path):
     holds the closed-form slice of the global state."""
     write_checkpoint(tmp_path)
     par = Parallel(*SAVE_PAR)
-    layout = torch.load(tmp_path / "param_layout.pt", weights_only=True)
-    assert layout == layout_to_plain(build_layout(MODEL, par, torch.float32))
-    ctx = torch.load(tmp_path / "other_context.pt", weights_only=True)
+    layout = layout_from_reference(load_reference_object(tmp_path / "param_layout.pt"))
+    want = build_layout(MODEL, par, torch.float32)
+    assert layout_to_plain(layout) == layout_to_plain(want)
+    ctx = load_reference_object(tmp_path / "other_context.pt")
     assert ctx["other_context"] == {"iteration": 7, "tag": "ckpt"}
     assert [f for f, _ in ctx["expected_sub_fields"]] == ["param", "step", "exp_avg", "exp_avg_sq"]
     glob = global_tensors()
