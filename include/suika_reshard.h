@@ -135,6 +135,8 @@ typedef struct sr_plan_options {
 #define SR_OPT_NO_ROW_GROUPS 0x10u /* keep each strided piece's tiles together instead
                                      of dealing out the tiles of side-by-side pieces
                                      (a dim -1 concatenation) row block by row block */
+#define SR_OPT_GATHER_ONLY 0x20u  /* build only the gather phase (the buffer layout is still
+                                     reported); sr_pack / sr_unpack then fail with SR_EINVAL */
 
 typedef struct sr_plan sr_plan;
 

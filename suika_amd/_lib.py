@@ -45,6 +45,7 @@ SR_OPT_SKIP_COVERAGE = 0x2
 SR_OPT_PIECE_ORDER = 0x4
 SR_OPT_NO_XCD_INTERLEAVE = 0x8
 SR_OPT_NO_ROW_GROUPS = 0x10
+SR_OPT_GATHER_ONLY = 0x20
 
 SR_MAX_DIMS = 8
 SR_KIND_CHUNK, SR_KIND_VOCAB_PAD, SR_KIND_QKV_HEADS = 0, 1, 2

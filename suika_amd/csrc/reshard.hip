@@ -1447,7 +1447,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
   if (options) opt = *options;
   if (opt.reserved != 0) return fail(SR_EINVAL, "options.reserved must be 0");
   if (opt.flags & ~(SR_OPT_TEMPORAL | SR_OPT_SKIP_COVERAGE | SR_OPT_PIECE_ORDER | SR_OPT_NO_XCD_INTERLEAVE |
-                    SR_OPT_NO_ROW_GROUPS))
+                    SR_OPT_NO_ROW_GROUPS | SR_OPT_GATHER_ONLY))
     return fail(SR_EINVAL, "unknown option flags 0x%x", opt.flags);
   if (opt.tile_bytes == 0) opt.tile_bytes = kDefaultTileBytes;
   if (opt.tile_bytes < 4096 || opt.tile_bytes > (16u << 20) ||
@@ -1473,6 +1473,12 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
 
   std::vector<std::vector<Box>> cover(n_dst);
   const uint64_t max_row = (uint64_t(1) << 31) - opt.tile_bytes;
+  const bool buffers = (opt.flags & SR_OPT_GATHER_ONLY) == 0;   // build the pack and unpack phases
+  if (buffers) {
+    p->pack.items.reserve(size_t(n_pieces));
+    p->unpack.items.reserve(size_t(n_pieces));
+  }
+  p->gather.items.reserve(size_t(n_pieces));
 
   for (int32_t k = 0; k < n_pieces; ++k) {
     const sr_piece& pc = pieces[k];
@@ -1511,7 +1517,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
         return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
                         (unsigned long long)it.row_bytes));
       }
-      p->unpack.items.push_back(it);
+      if (buffers) p->unpack.items.push_back(it);
       p->unpack.bytes_written += pc.rows * pc.cols * es;
       p->gather.items.push_back(it);
       p->gather.bytes_written += pc.rows * pc.cols * es;
@@ -1580,7 +1586,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
                       (unsigned long long)pk.row_bytes));
     }
-    p->pack.items.push_back(pk);
+    if (buffers) p->pack.items.push_back(pk);
     p->pack.bytes_read += payload;
     p->pack.bytes_written += payload;
 
@@ -1613,7 +1619,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       return bad(fail(SR_EINVAL, "piece %d: strided row of %llu bytes too wide", k,
                       (unsigned long long)up.row_bytes));
     }
-    p->unpack.items.push_back(up);
+    if (buffers) p->unpack.items.push_back(up);
     p->unpack.bytes_read += payload;
     if (dst >= 0) p->unpack.bytes_written += payload;
     if (dst2 >= 0) p->unpack.bytes_written += payload / 2;
@@ -1661,10 +1667,12 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
     p->gather.n_src_base = uint32_t(n_src);
     p->gather.n_dst_base = uint32_t(n_dst);
     const bool groups = !(opt.flags & SR_OPT_NO_ROW_GROUPS);
-    build_rel(p->pack, by_piece ? identity(p->pack.items.size()) : item_order(p->pack, true),
-              opt.tile_bytes, false, true, true, groups);
-    build_rel(p->unpack, by_piece ? identity(p->unpack.items.size()) : item_order(p->unpack, false),
-              opt.tile_bytes, true, false, false, groups);
+    if (buffers) {
+      build_rel(p->pack, by_piece ? identity(p->pack.items.size()) : item_order(p->pack, true),
+                opt.tile_bytes, false, true, true, groups);
+      build_rel(p->unpack, by_piece ? identity(p->unpack.items.size()) : item_order(p->unpack, false),
+                opt.tile_bytes, true, false, false, groups);
+    }
     build_rel(p->gather, by_piece ? identity(p->gather.items.size()) : item_order(p->gather, false),
               opt.tile_bytes, false, false, false, groups);
   }
@@ -1756,6 +1764,7 @@ int sr_plan_info_get(const sr_plan* plan, sr_plan_info* out) {
 
 int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs, hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
+  if (plan->opt.flags & SR_OPT_GATHER_ONLY) return fail(SR_EINVAL, "sr_pack: the plan was created gather-only");
   // Alignment each pointer must satisfy: its element size; 0 = not read.
   std::vector<uint32_t> sal(plan->src.size(), 0), bal(plan->n_peers, 0);
   for (const sr_piece& pc : plan->pieces) {
@@ -1773,6 +1782,7 @@ int sr_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs, 
 
 int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs, hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
+  if (plan->opt.flags & SR_OPT_GATHER_ONLY) return fail(SR_EINVAL, "sr_unpack: the plan was created gather-only");
   std::vector<uint32_t> bal(plan->n_peers, 0), dal(plan->dst.size(), 0);
   for (const sr_piece& pc : plan->pieces) {
     if (pc.kind != SR_PIECE_ZERO) bal[pc.peer] = 16;

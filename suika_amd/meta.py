@@ -360,7 +360,7 @@ class TransferOp:
             plan, src_ptrs = ReshardPlan.from_sources([op], lambda r: {name: {"x": src_tensor}}, ["x"], device)
             try:
                 out, dst_ptrs = plan.alloc_dst_ptrs(device)
-                if dst_ptrs:
+                if len(dst_ptrs):
                     plan.gather_ptrs(src_ptrs, dst_ptrs)
             finally:
                 plan.close()   # waits for the launch

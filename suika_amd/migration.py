@@ -25,6 +25,7 @@ intended ``cat`` in ascending piece order.
 from __future__ import annotations
 
 import gc
+from dataclasses import replace
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
 import torch
@@ -155,6 +156,8 @@ def execute_param_transfer(
         first = source(ops[0].src_rank).get(ops[0].param_name, {})
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
     groups = _pipeline_groups(ops, elem_bytes, pipeline)
+    if route == "direct":   # the plans only ever gather
+        plan_options = replace(plan_options or PlanOptions(), gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []

@@ -67,13 +67,15 @@ class PlanOptions:
     address_order: bool = True   # tiles ordered by tensor address (library default)
     xcd_order: bool = True       # tiles interleaved 8 ways, one eighth per XCD (default)
     row_groups: bool = True      # side-by-side strided pieces dealt out by row block (default)
+    gather_only: bool = False    # build only the gather phase (no pack / unpack)
 
     def to_c(self) -> _lib.SrPlanOptions:
         flags = (0 if self.nontemporal else _lib.SR_OPT_TEMPORAL) | \
                 (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0) | \
                 (0 if self.address_order else _lib.SR_OPT_PIECE_ORDER) | \
                 (0 if self.xcd_order else _lib.SR_OPT_NO_XCD_INTERLEAVE) | \
-                (0 if self.row_groups else _lib.SR_OPT_NO_ROW_GROUPS)
+                (0 if self.row_groups else _lib.SR_OPT_NO_ROW_GROUPS) | \
+                (_lib.SR_OPT_GATHER_ONLY if self.gather_only else 0)
         return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, flags, 0)
 
 
@@ -136,7 +138,8 @@ class ReshardPlan:
                      options: Optional[PlanOptions] = None,
                      rank: Optional[int] = None) -> Tuple["ReshardPlan", List[int]]:
         """The plan of ``ops`` with shapes and dtypes read from the source
-        tensors themselves, and the device address of every source slot.
+        tensors themselves, and the device address of every source slot (a
+        uint64 array).
 
         ``source(r)`` is rank ``r``'s state dict ``{name: {field: Tensor}}``.
         Each tensor is read once: it must be a contiguous CUDA tensor on
@@ -148,7 +151,7 @@ class ReshardPlan:
         who = f"[{rank}]" if rank is not None else ""
         specs, dtypes, ptrs = _lib.host().collect_sources(self._ops, source, self.fields, dev_index, who)
         self._build(specs, dtypes)
-        return self, ptrs[self._src_index].tolist()
+        return self, np.ascontiguousarray(ptrs[self._src_index])
 
     def _setup(self, ops, fields, recast, options) -> None:
         """Everything but the source specs: validation, destination shards and
@@ -297,7 +300,8 @@ class ReshardPlan:
 
     def alloc_dst_ptrs(self, device) -> Tuple[Dict[str, Dict[str, torch.Tensor]], List[int]]:
         """Fresh destination tensors (as ``alloc_dst``) and the device
-        address of every destination slot, straight from the slot table."""
+        address of every destination slot (a uint64 array), straight from
+        the slot table."""
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
@@ -305,7 +309,7 @@ class ReshardPlan:
         out, ptrs = _lib.host().alloc_dst(self._dst_rows.reshape(-1, _lib.SR_KEY_WORDS),
                                           self._empty_rows.reshape(-1, _lib.SR_KEY_WORDS),
                                           self._op_names, self.fields, recast_names, self._dtypes, device)
-        return out, ptrs.tolist()
+        return out, ptrs
 
     def bind_dst_ptrs(self, dst: Mapping[str, Mapping[str, torch.Tensor]], device) -> List[int]:
         """Addresses of caller-provided destination tensors in slot order,
@@ -316,7 +320,7 @@ class ReshardPlan:
             device = torch.device("cuda", torch.cuda.current_device())
         recast_names = [self._recast_of.get(f) for f in self.fields]
         return _lib.host().bind_dst(dst, self._dst_rows.reshape(-1, _lib.SR_KEY_WORDS), self._op_names,
-                                    self.fields, recast_names, self._dtypes, device).tolist()
+                                    self.fields, recast_names, self._dtypes, device)
 
     # -------------------------------------------------------------- sizes
     @property
@@ -448,7 +452,12 @@ class ReshardPlan:
         return ptrs
 
     @staticmethod
-    def _carray(ptrs: List[int]) -> ctypes.Array:
+    def _carray(ptrs):
+        """A pointer array for the C ABI: a uint64 numpy array is passed by
+        address (no copy); a list is converted."""
+        if isinstance(ptrs, np.ndarray):
+            assert ptrs.dtype == np.uint64 and ptrs.flags["C_CONTIGUOUS"], "address arrays are contiguous uint64"
+            return ptrs.ctypes.data_as(ctypes.POINTER(ctypes.c_void_p))
         return (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
 
     def pack_ptrs(self, src_ptrs: List[int], buf_ptrs: List[int], stream=None) -> None:

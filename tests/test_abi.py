@@ -148,14 +148,33 @@ def test_recast_and_zero_rules():
 
 def test_options_validation():
     for opt in (_lib.SrPlanOptions(3000, 0, 0, 0), _lib.SrPlanOptions(0, 0, 0x80, 0),
-                _lib.SrPlanOptions(0, 0, 0x20, 0), _lib.SrPlanOptions(0, 0, 0, 1)):
+                _lib.SrPlanOptions(0, 0, 0x40, 0), _lib.SrPlanOptions(0, 0, 0, 1)):
         rc, _ = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece()], options=opt)
         assert rc == _lib.SR_EINVAL
     every = (_lib.SR_OPT_TEMPORAL | _lib.SR_OPT_SKIP_COVERAGE | _lib.SR_OPT_PIECE_ORDER |
-             _lib.SR_OPT_NO_XCD_INTERLEAVE | _lib.SR_OPT_NO_ROW_GROUPS)
+             _lib.SR_OPT_NO_XCD_INTERLEAVE | _lib.SR_OPT_NO_ROW_GROUPS | _lib.SR_OPT_GATHER_ONLY)
     rc, h = _plan([(4, 8, F32)], [(4, 8, F32)], 1, [piece()], options=_lib.SrPlanOptions(0, 0, every, 0))
     assert rc == _lib.SR_OK, _lib.last_error()
     _lib.lib().sr_plan_destroy(h)
+
+
+def test_gather_only_plan_refuses_pack_and_unpack():
+    """A gather-only plan keeps the buffer layout it reports but builds no
+    pack / unpack phase; those calls fail before touching any pointer."""
+    L = _lib.lib()
+    rc, h = _plan([(4, 8, F32), (4, 8, F32)], [(4, 16, F32)], 2,
+                  [piece(src=0, peer=0, dc=0), piece(src=1, peer=1, dc=8)],
+                  options=_lib.SrPlanOptions(0, 0, _lib.SR_OPT_GATHER_ONLY, 0))
+    assert rc == _lib.SR_OK, _lib.last_error()
+    info = _lib.SrPlanInfo()
+    assert L.sr_plan_info_get(h, ctypes.byref(info)) == 0
+    assert info.gather_tiles > 0 and info.pack_tiles == 0 and info.unpack_tiles == 0
+    b = ctypes.c_uint64()
+    assert L.sr_plan_peer_bytes(h, 1, ctypes.byref(b)) == 0 and b.value == 4 * 8 * 4
+    null = (ctypes.c_void_p * 2)(None, None)
+    assert L.sr_pack(h, null, null, None) == _lib.SR_EINVAL and "gather-only" in _lib.last_error()
+    assert L.sr_unpack(h, null, null, None) == _lib.SR_EINVAL and "gather-only" in _lib.last_error()
+    L.sr_plan_destroy(h)
 
 
 def test_tile_counts():

@@ -300,3 +300,34 @@ def test_forcefully_free_releases_what_the_reference_frees(key):
         assert 0 < len(want) < n_read
     assert {k for k in freed if k[2] == "step_dev"} == {(r, n, "step_dev") for (r, n) in read}
     assert not any(k[2] == "step_cpu" for k in freed)
+
+
+def test_fresh_destinations_are_ordinary_independent_tensors():
+    """Destinations come from torch's caching allocator like torch.empty:
+    the same device, counted by torch's memory statistics, one storage each
+    (freeing one leaves the others intact, as Suika's forcefully_free_tensor
+    expects)."""
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] fresh destinations {w.key}", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    fake = to_device(srcs, w, "cuda")
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                 rank=w.dst_rank, fake_source_state_dicts=fake)
+    torch.cuda.synchronize()
+    ref = torch.empty(1, device="cuda")
+    tensors = [t for e in out.values() for t in e.values()]
+    total = sum(t.untyped_storage().nbytes() for t in tensors)
+    assert torch.cuda.memory_allocated() - before >= total > 0
+    assert all(t.device == ref.device and t.is_contiguous() for t in tensors)
+    assert len({t.untyped_storage().data_ptr() for t in tensors}) == len(tensors)
+    assert all(t.untyped_storage().nbytes() == t.numel() * t.element_size() for t in tensors)
+    victim = tensors[0]
+    victim.untyped_storage().resize_(0)
+    for name, e in want.items():
+        for f, a in e.items():
+            if out[name][f] is not victim:
+                np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")

@@ -450,9 +450,9 @@ def test_bind_dst_checks_every_destination():
     cpu = torch.device("cpu")
     dst = plan.alloc_dst(cpu)
     ptrs = plan.bind_dst_ptrs(dst, cpu)
-    assert ptrs == [dst[n][f].data_ptr() for n, f in plan.dst_keys]
+    assert ptrs.tolist() == [dst[n][f].data_ptr() for n, f in plan.dst_keys]
     arena = plan.alloc_dst(cpu, arena=True)
-    assert plan.bind_dst_ptrs(arena, cpu) == [arena[n][f].data_ptr() for n, f in plan.dst_keys]
+    assert plan.bind_dst_ptrs(arena, cpu).tolist() == [arena[n][f].data_ptr() for n, f in plan.dst_keys]
     bad = {n: dict(e) for n, e in dst.items()}
     bad["w"]["param"] = torch.empty(8, 4)                 # f32 where bf16 is planned
     with pytest.raises(AssertionError, match=r"\('w', 'param'\): dtype differs"):
