@@ -304,13 +304,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_plan_info_get.restype = ctypes.c_int
     lib.sr_plan_info_get.argtypes = [vp, ctypes.POINTER(SrPlanInfo)]
     lib.sr_pack.restype = ctypes.c_int
-    lib.sr_pack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_pack.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_unpack.restype = ctypes.c_int
-    lib.sr_unpack.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_unpack.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_gather.restype = ctypes.c_int
-    lib.sr_gather.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_gather.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_gather_noalloc.restype = ctypes.c_int
-    lib.sr_gather_noalloc.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), vp]
+    lib.sr_gather_noalloc.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
     i64 = ctypes.c_int64

@@ -10,7 +10,8 @@ allocations for the same-GPU state hand-off between processes).
 
 ``build_host`` compiles ``host_bind.cpp`` into ``suika_amd/lib/_suika_host.so``,
 the CPython extension (on torch's C++ API) that does the drop-in operator's
-per-tensor host work; it is a plain ``g++`` line against the installed torch.
+per-tensor host work; it is a plain ``g++`` line against the installed torch
+and the library (whose sr_lower and sr_plan_create it calls), found beside it.
 """
 from __future__ import annotations
 
@@ -117,7 +118,9 @@ def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
            "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{HOST_SRC.parent}",
            f"-I{Path(os.environ.get('ROCM_PATH', '/opt/rocm')) / 'include'}",
            str(HOST_SRC), *[f"-L{p}" for p in libdirs], *[f"-Wl,-rpath,{p}" for p in libdirs],
-           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-o", str(tmp)]
+           "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+           # the library itself (sr_lower, sr_plan_create), found beside the extension
+           f"-L{LIB_DIR}", "-lsuika_reshard", "-Wl,-rpath,$ORIGIN", "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -37,11 +37,15 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstring>
+#include <memory>
 #include <string>
 #include <unordered_map>
 #include <vector>
 
 #include "sr_meta.h"
+#include "suika_planner.h"
+#include "suika_reshard.h"
 
 namespace py = pybind11;
 
@@ -708,6 +712,152 @@ py::tuple tensor_runs(py::list ops) {
   return py::make_tuple(a, b, single);
 }
 
+// The ops grouped by tensor, tensors in order of first appearance: (op
+// indices tensor by tensor, where each tensor's indices start (one entry
+// per tensor plus the end), elements of each tensor's pieces, whether every
+// tensor's ops are already consecutive -- the order is then the identity).
+py::tuple name_runs(py::list ops) {
+  const Names& N = names_();
+  py::array_t<int64_t> numel = piece_numels(ops);
+  const int64_t* e = numel.data();
+  const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
+  py::dict ids;
+  std::vector<std::vector<int64_t>> members;
+  std::vector<int64_t> sums;
+  bool single = true;
+  size_t prev = SIZE_MAX;
+  for (Py_ssize_t k = 0; k < n; ++k) {
+    py::object name = attr(PyList_GET_ITEM(ops.ptr(), k), N.param_name);
+    PyObject* id = PyDict_GetItemWithError(ids.ptr(), name.ptr());
+    size_t nid;
+    if (id) {
+      nid = size_t(as_int(id));
+      if (nid != prev) single = false;
+    } else {
+      if (PyErr_Occurred()) throw py::error_already_set();
+      nid = members.size();
+      py::int_ v(nid);
+      if (PyDict_SetItem(ids.ptr(), name.ptr(), v.ptr()) != 0) throw py::error_already_set();
+      members.emplace_back();
+      sums.push_back(0);
+    }
+    members[nid].push_back(k);
+    sums[nid] += e[k];
+    prev = nid;
+  }
+  const int64_t m = int64_t(members.size());
+  py::array_t<int64_t> order({int64_t(n)}), starts({m + 1}), total({m});
+  int64_t* o = order.mutable_data();
+  int64_t* st = starts.mutable_data();
+  int64_t at = 0;
+  for (int64_t i = 0; i < m; ++i) {
+    st[i] = at;
+    for (int64_t k : members[size_t(i)]) o[at++] = k;
+  }
+  st[m] = at;
+  std::copy(sums.begin(), sums.end(), total.mutable_data());
+  return py::make_tuple(order, starts, total, single);
+}
+
+// Launch groups of one rank's ops: whole tensors per group, the largest
+// tensors first (a two-stage pipeline -- host planning, then GPU copy --
+// finishes soonest with the GPU-heavy jobs first), sized by the cost model
+// the caller passes: the first group carries `first_ns` of GPU work, each
+// next one as many tensors as the host plans in `share` of the previous
+// group's GPU time (`group_ns` + `tensor_ns` per tensor), at most
+// `max_groups` groups.  The rest goes into one last group as soon as a next
+// group would hold fewer than `min_tensors` tensors or less than `group_ns`
+// of GPU work.  A tensor's GPU time is its elements times
+// `ns_per_element`.  Within a group, ops keep their schedule order.
+py::list launch_groups(py::list ops, double ns_per_element, int64_t max_groups, double first_ns,
+                       double share, double group_ns, double tensor_ns, int64_t min_tensors) {
+  py::tuple runs = name_runs(ops);
+  py::array_t<int64_t> order = runs[0].cast<py::array_t<int64_t>>();
+  py::array_t<int64_t> starts = runs[1].cast<py::array_t<int64_t>>();
+  py::array_t<int64_t> numel = runs[2].cast<py::array_t<int64_t>>();
+  const int64_t n = int64_t(numel.size());
+  py::list out;
+  if (max_groups <= 1 || n <= 1) {
+    out.append(ops);
+    return out;
+  }
+  const int64_t* e = numel.data();
+  std::vector<int64_t> rank(static_cast<size_t>(n));
+  for (int64_t i = 0; i < n; ++i) rank[size_t(i)] = i;
+  std::stable_sort(rank.begin(), rank.end(), [&](int64_t a, int64_t b) { return e[a] > e[b]; });
+  std::vector<double> cum(static_cast<size_t>(n));
+  double acc = 0;
+  for (int64_t i = 0; i < n; ++i) cum[size_t(i)] = acc += double(e[rank[size_t(i)]]) * ns_per_element;
+  auto gpu = [&](int64_t a, int64_t b) { return cum[size_t(b - 1)] - (a ? cum[size_t(a - 1)] : 0.0); };
+  std::vector<int64_t> bounds{0};
+  int64_t end = 1;
+  while (end < n && cum[size_t(end - 1)] < first_ns) ++end;
+  bounds.push_back(end);
+  while (end < n) {
+    int64_t next = n;
+    if (int64_t(bounds.size()) < max_groups) {
+      const double fits = (gpu(bounds[bounds.size() - 2], end) * share - group_ns) / tensor_ns;
+      if (fits >= double(min_tensors)) next = std::min<int64_t>(n, end + int64_t(fits));
+      // a group that is not the last pays its planning overhead back only
+      // if the GPU runs it at least that long (while the host plans on)
+      if (next < n && gpu(end, next) < group_ns) next = n;
+    }
+    end = next;
+    bounds.push_back(end);
+  }
+  if (bounds.size() == 2) {
+    out.append(ops);
+    return out;
+  }
+  const size_t k = bounds.size() - 1;
+  std::vector<int64_t> group_of(static_cast<size_t>(n));
+  for (size_t g = 0; g < k; ++g)
+    for (int64_t i = bounds[g]; i < bounds[g + 1]; ++i) group_of[size_t(rank[size_t(i)])] = int64_t(g);
+  std::vector<py::list> lists(k);
+  const int64_t* o = order.data();
+  const int64_t* st = starts.data();
+  for (int64_t m = 0; m < n; ++m) {
+    py::list& dst = lists[size_t(group_of[size_t(m)])];
+    for (int64_t p = st[m]; p < st[m + 1]; ++p)
+      if (PyList_Append(dst.ptr(), PyList_GET_ITEM(ops.ptr(), o[p])) != 0) throw py::error_already_set();
+  }
+  for (py::list& l : lists) out.append(l);
+  return out;
+}
+
+// The drop-in call's result: {name: {field: tensor}} with the names in
+// order of first appearance in `ops` and each entry's fields in
+// `field_order` (those present), from `target`, filled launch group by
+// launch group.
+py::dict ordered_result(py::list ops, py::dict target, py::list field_order) {
+  const Names& N = names_();
+  py::dict out;
+  const Py_ssize_t n = PyList_GET_SIZE(ops.ptr()), nf = PyList_GET_SIZE(field_order.ptr());
+  for (Py_ssize_t k = 0; k < n; ++k) {
+    py::object name = attr(PyList_GET_ITEM(ops.ptr(), k), N.param_name);
+    const int have = PyDict_Contains(out.ptr(), name.ptr());
+    if (have < 0) throw py::error_already_set();
+    if (have) continue;
+    PyObject* entry = PyDict_GetItemWithError(target.ptr(), name.ptr());
+    if (!entry) {
+      if (PyErr_Occurred()) throw py::error_already_set();
+      throw py::key_error(py::str(name).cast<std::string>());
+    }
+    py::dict e;
+    for (Py_ssize_t f = 0; f < nf; ++f) {
+      PyObject* field = PyList_GET_ITEM(field_order.ptr(), f);
+      PyObject* t = PyDict_GetItemWithError(entry, field);
+      if (t) {
+        if (PyDict_SetItem(e.ptr(), field, t) != 0) throw py::error_already_set();
+      } else if (PyErr_Occurred()) {
+        throw py::error_already_set();
+      }
+    }
+    if (PyDict_SetItem(out.ptr(), name.ptr(), e.ptr()) != 0) throw py::error_already_set();
+  }
+  return out;
+}
+
 }  // namespace
 
 // The drop-in call's destination arena (an extension of
@@ -860,6 +1010,198 @@ py::list device_views(uint64_t base, py::list views, int64_t device_index) {
   return out;
 }
 
+// ------------------------------------------------------------ one launch group's plan
+// ReshardPlan.from_sources in one call: the ops grouped by tensor, each
+// tensor's destination shard (op.dst_shard_meta, else `infer_shard(ops of the
+// name)`), the op / meta tables (encode_ops), the source tensors
+// (collect_sources), then sr_lower and sr_plan_create of libsuika_reshard.so
+// on its tables, with nothing copied through Python in between.  Raises
+// suika_amd._lib.PlanError (or ReshardError for device and memory failures)
+// with the library's message, tensor ids replaced by names.
+
+namespace {
+
+PyObject* lib_exception(const char* name) {
+  py::object mod = py::module_::import("suika_amd._lib");
+  py::object cls = mod.attr(name);
+  return cls.release().ptr();   // a new reference, kept for the process
+}
+
+const char* status_name(int rc) {
+  switch (rc) {
+    case SR_OK: return "SR_OK";
+    case SR_EINVAL: return "SR_EINVAL";
+    case SR_EBOUNDS: return "SR_EBOUNDS";
+    case SR_EALIGN: return "SR_EALIGN";
+    case SR_EOVERLAP: return "SR_EOVERLAP";
+    case SR_EHIP: return "SR_EHIP";
+    case SR_ENOMEM: return "SR_ENOMEM";
+    case SR_EDTYPE: return "SR_EDTYPE";
+    default: return nullptr;
+  }
+}
+
+// "<what>: <status>: <message>", as suika_amd._lib.check words it.
+[[noreturn]] void raise_status(int rc, const char* what, const std::string& msg) {
+  static PyObject* plan_error = lib_exception("PlanError");
+  static PyObject* reshard_error = lib_exception("ReshardError");
+  const char* name = status_name(rc);
+  const std::string text = std::string(what) + ": " + (name ? name : std::to_string(rc)) + ": " + msg;
+  PyErr_SetString(rc == SR_EHIP || rc == SR_ENOMEM ? reshard_error : plan_error, text.c_str());
+  throw py::error_already_set();
+}
+
+// "#<id>" in a library message -> the tensor's name.
+std::string with_names(const char* msg, py::list names) {
+  std::string out;
+  for (const char* c = msg; *c; ++c) {
+    if (*c == '#' && c[1] >= '0' && c[1] <= '9') {
+      size_t id = 0;
+      while (c[1] >= '0' && c[1] <= '9') id = id * 10 + size_t(*++c - '0');
+      out += id < names.size() ? py::str(names[id]).cast<std::string>() : "#" + std::to_string(id);
+    } else {
+      out += *c;
+    }
+  }
+  return out;
+}
+
+template <typename T>
+py::array table(const T* rows, int64_t n, py::dtype dt) {
+  if (dt.itemsize() != py::ssize_t(sizeof(T))) throw py::value_error("record dtype does not match the library");
+  py::array out(dt, std::vector<py::ssize_t>{py::ssize_t(n)});
+  if (n) std::memcpy(out.mutable_data(), rows, size_t(n) * sizeof(T));
+  return out;
+}
+
+py::array_t<int64_t> key_table(const sr_slot_key* rows, int64_t n) {
+  py::array_t<int64_t> out({n, kKeyWords});
+  if (n) std::memcpy(out.mutable_data(), rows, size_t(n) * sizeof(sr_slot_key));
+  return out;
+}
+
+static_assert(sizeof(sr_slot_key) == kKeyWords * sizeof(int64_t), "an sr_slot_key row is 13 int64 words");
+static_assert(sizeof(sr_src_spec) == kSpecWords * sizeof(int64_t), "an sr_src_spec row is 10 int64 words");
+static_assert(sizeof(sr_op) == 9 * sizeof(int64_t), "an sr_op row is 9 int64 words");
+
+}  // namespace
+
+py::tuple plan_sources(py::list ops, py::function source, py::list fields, std::vector<int64_t> recast,
+                       py::function infer_shard, int64_t device_index, const std::string& who,
+                       uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
+                       py::dtype piece_dt) {
+  const Names& N = names_();
+  const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
+  const int64_t nf = int64_t(fields.size());
+  if (int64_t(recast.size()) != nf) throw py::value_error("one recast flag per field");
+  // tensors in order of first appearance, their ops, the destination rank
+  py::dict name_ids;
+  py::list names, op_names(n);
+  std::vector<std::vector<PyObject*>> by_name;
+  std::vector<size_t> op_nid(n);
+  std::vector<int64_t> ranks;
+  for (Py_ssize_t k = 0; k < n; ++k) {
+    PyObject* op = PyList_GET_ITEM(ops.ptr(), k);
+    py::object name = attr(op, N.param_name);
+    PyObject* id = PyDict_GetItemWithError(name_ids.ptr(), name.ptr());
+    size_t nid;
+    if (id) {
+      nid = size_t(as_int(id));
+    } else {
+      if (PyErr_Occurred()) throw py::error_already_set();
+      nid = by_name.size();
+      py::int_ v(nid);
+      if (PyDict_SetItem(name_ids.ptr(), name.ptr(), v.ptr()) != 0) throw py::error_already_set();
+      names.append(name);
+      by_name.emplace_back();
+    }
+    by_name[nid].push_back(op);
+    op_nid[k] = nid;
+    const int64_t r = as_int(attr(op, N.dst_rank).ptr());
+    if (std::find(ranks.begin(), ranks.end(), r) == ranks.end()) ranks.push_back(r);
+    op_names[k] = name;
+  }
+  if (ranks.size() > 1) {
+    std::sort(ranks.begin(), ranks.end());
+    std::string list;
+    for (int64_t r : ranks) list += (list.empty() ? "" : ", ") + std::to_string(r);
+    assertion("ops target several ranks [" + list + "]");
+  }
+  py::dict shards;
+  for (size_t i = 0; i < by_name.size(); ++i) {
+    py::object shard = shard_of(by_name[i][0]);
+    if (shard.ptr() == Py_None) {
+      py::list group;
+      for (PyObject* op : by_name[i]) group.append(py::handle(op));
+      shard = infer_shard(group);
+    }
+    shards[names[i]] = shard;
+  }
+  py::tuple enc = encode_ops(ops, shards, name_ids);
+  py::array_t<int64_t> metas = enc[0].cast<py::array_t<int64_t>>(), op_rows = enc[1].cast<py::array_t<int64_t>>();
+  py::tuple col = collect_sources(ops, source, fields, device_index, who);
+  py::array_t<int64_t> specs = col[0].cast<py::array_t<int64_t>>();
+  py::array_t<uint64_t> ptrs = col[2].cast<py::array_t<uint64_t>>();
+  // one torch dtype per (tensor, field) across its sources: the library
+  // compares element types, which several torch dtypes share
+  {
+    py::list dtypes = col[1].cast<py::list>();
+    std::vector<PyObject*> first(by_name.size() * size_t(nf), nullptr);
+    for (Py_ssize_t k = 0; k < n; ++k)
+      for (int64_t f = 0; f < nf; ++f) {
+        PyObject* dt = PyList_GET_ITEM(dtypes.ptr(), k * nf + f);
+        PyObject*& seen = first[op_nid[k] * size_t(nf) + size_t(f)];
+        if (!seen) seen = dt;
+        if (seen != dt)
+          assertion(py::str(names[op_nid[k]]).cast<std::string>() + "/" + py::str(fields[f]).cast<std::string>() +
+                    ": dtype differs between sources");
+      }
+  }
+  const int64_t no_recast = 0;
+
+  sr_lowering* low = nullptr;
+  int rc = sr_lower(reinterpret_cast<const sr_meta*>(metas.data()), metas.shape(0),
+                    reinterpret_cast<const sr_op*>(op_rows.data()), int64_t(n),
+                    reinterpret_cast<const sr_src_spec*>(specs.data()), nf, nf ? recast.data() : &no_recast, &low);
+  if (rc != SR_OK) raise_status(rc, "sr_lower", with_names(sr_last_error(), names));
+  std::unique_ptr<sr_lowering, void (*)(sr_lowering*)> hold(low, sr_lowering_destroy);
+  // source slot s reads (op, field) = src_key[s].op, .field
+  py::array_t<uint64_t> src_ptrs({low->n_src});
+  {
+    uint64_t* o = src_ptrs.mutable_data();
+    const uint64_t* in = ptrs.data();
+    for (int64_t s = 0; s < low->n_src; ++s) o[s] = in[low->src_key[s].op * nf + low->src_key[s].field];
+  }
+  if (low->n_src > INT32_MAX || low->n_dst > INT32_MAX || low->n_pieces > INT32_MAX || low->n_peers > INT32_MAX)
+    throw py::value_error("lowering too large");
+  sr_plan_options opt{tile_bytes, max_blocks, flags, 0};
+  sr_plan* plan = nullptr;
+  rc = sr_plan_create(low->src, int32_t(low->n_src), low->dst, int32_t(low->n_dst), int32_t(low->n_peers),
+                      low->pieces, int32_t(low->n_pieces), &opt, &plan);
+  if (rc != SR_OK) raise_status(rc, "sr_plan_create", sr_last_error());
+  std::unique_ptr<sr_plan, void (*)(sr_plan*)> plan_hold(plan, sr_plan_destroy);
+  py::list peers, peer_bytes;
+  for (int64_t i = 0; i < low->n_peers; ++i) {
+    uint64_t b = 0;
+    if ((rc = sr_plan_peer_bytes(plan, int32_t(i), &b)) != SR_OK)
+      raise_status(rc, "sr_plan_peer_bytes", sr_last_error());
+    peers.append(low->peer_rank[i]);
+    peer_bytes.append(b);
+  }
+  sr_plan_info info{};
+  if ((rc = sr_plan_info_get(plan, &info)) != SR_OK)
+    raise_status(rc, "sr_plan_info_get", sr_last_error());
+  py::bytes info_bytes(reinterpret_cast<const char*>(&info), sizeof(info));
+  py::tuple out = py::make_tuple(
+      reinterpret_cast<uintptr_t>(plan), names, shards, op_names,
+      ranks.empty() ? py::object(py::none()) : py::object(py::int_(ranks[0])), col[1], src_ptrs,
+      table(low->src, low->n_src, tensor_dt), table(low->dst, low->n_dst, tensor_dt),
+      table(low->pieces, low->n_pieces, piece_dt), peers, key_table(low->src_key, low->n_src),
+      key_table(low->dst_key, low->n_dst), key_table(low->empty, low->n_empty), peer_bytes, info_bytes);
+  plan_hold.release();   // owned by the caller from here on
+  return out;
+}
+
 PYBIND11_MODULE(_suika_host, m) {
   m.doc() = "Per-tensor host work of execute_param_transfer (source checks, destination allocation)";
   m.def("collect_sources", &collect_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
@@ -876,8 +1218,15 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("piece_numels", &piece_numels, py::arg("ops"));
   m.def("ops_of_rank", &ops_of_rank, py::arg("ops"), py::arg("rank"));
   m.def("tensor_runs", &tensor_runs, py::arg("ops"));
+  m.def("name_runs", &name_runs, py::arg("ops"));
+  m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
+  m.def("launch_groups", &launch_groups, py::arg("ops"), py::arg("ns_per_element"), py::arg("max_groups"),
+        py::arg("first_ns"), py::arg("share"), py::arg("group_ns"), py::arg("tensor_ns"), py::arg("min_tensors"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
         py::arg("op_cls"), py::arg("meta_cls"));
   m.def("device_views", &device_views, py::arg("base"), py::arg("views"), py::arg("device_index"));
+  m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"), py::arg("recast"),
+        py::arg("infer_shard"), py::arg("device_index"), py::arg("who"), py::arg("tile_bytes"),
+        py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"), py::arg("piece_dtype"));
 }

@@ -70,6 +70,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "suika_reshard.h"
@@ -460,18 +461,21 @@ __global__ __launch_bounds__(kBlock) void sr_gather_kernel(const DevItem* __rest
 }
 
 // ------------------------------------------------- device-side plan binding
-// The host keeps O(pieces) descriptors; the per-tile table, the per-peer
-// buffer offsets and the absolute-address item table are computed on the
-// GPU from them:
+// The host keeps O(pieces) descriptors and the prefix sum of their tile
+// counts; the per-tile table, the per-peer buffer offsets and the
+// absolute-address item table are computed on the GPU from them:
 //   sr_offsets_kernel   per peer: exclusive prefix sum of the 256-byte
 //                       rounded payloads of its pieces, in piece order;
-//   sr_tile_scan_kernel exclusive prefix sum of the items' tile counts;
 //   sr_tile_emit_kernel one workgroup per item writes its tiles, placed in
-//                       the XCD-interleaved order;
+//                       the XCD-interleaved order, and on a phase's first
+//                       launch binds the item as sr_bind_kernel does;
 //   sr_bind_kernel      one lane per item: caller pointers + offsets ->
-//                       DevItem (addresses, vector width).
+//                       DevItem (addresses, vector width); later launches
+//                       with other pointers.
 
-// Pointer-independent item descriptor (device resident, uploaded once).
+// Pointer-independent item descriptor (written once on the host, read in place
+// from pinned memory by the setup kernels; copied to the scratch by the
+// allocation-free gather).
 enum : uint32_t {
   kRelSrcBuf = 1u << 16,   // source side is a peer buffer at the piece's offset
   kRelDstBuf = 1u << 17,   // destination side is a peer buffer at the piece's offset
@@ -535,7 +539,6 @@ __device__ uint64_t block_exclusive_scan(uint64_t v, uint64_t& total) {
   return before + x - v;
 }
 
-constexpr int kScanBlock = 1024;
 constexpr int kSetupBlock = 256;
 
 // One workgroup per peer.  peer_begin[p]..peer_begin[p+1] indexes
@@ -558,78 +561,6 @@ __global__ __launch_bounds__(kSetupBlock) void sr_offsets_kernel(
   }
 }
 
-// Single workgroup: tile_base[k] = tiles of items 0..k-1; tile_base[n] = all.
-__global__ __launch_bounds__(kScanBlock) void sr_tile_scan_kernel(const DevRel* __restrict__ rel,
-                                                                  uint32_t n, uint32_t tile_shift,
-                                                                  uint64_t* __restrict__ tile_base) {
-  uint64_t carry = 0;
-  for (uint32_t base = 0; base < n; base += kScanBlock) {
-    const uint32_t k = base + threadIdx.x;
-    uint64_t v = 0;
-    if (k < n) {
-      const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
-      v = (rel[k].total + (uint64_t(1) << sh) - 1) >> sh;
-    }
-    uint64_t total;
-    const uint64_t ex = block_exclusive_scan<kScanBlock>(v, total);
-    if (k < n) tile_base[k] = carry + ex;
-    carry += total;
-  }
-  if (threadIdx.x == 0) tile_base[n] = carry;
-}
-
-// Tile i of the item-ordered list goes to position pos(i).  With `ways`
-// segments of seg = ceil(n/ways) tiles (q full segments and a last one of
-// r tiles), tile j of segment s is dispatched at j*q + min(j, r) + s: the
-// list is read column by column, so consecutive workgroups -- which the
-// hardware deals to the 8 XCDs in turn -- take one tile from each segment.
-__device__ __forceinline__ uint64_t xcd_position(uint64_t i, uint64_t seg, uint64_t q, uint64_t r) {
-  const uint64_t s = i / seg;
-  const uint64_t j = i - s * seg;
-  return j * q + (j < r ? j : r) + s;
-}
-
-__global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
-    const DevRel* __restrict__ rel, const uint64_t* __restrict__ tile_base, uint32_t n,
-    uint32_t tile_shift, uint64_t n_tiles, uint32_t ways, DevTile* __restrict__ tiles) {
-  uint64_t seg = 1, q = n_tiles, r = 0;
-  if (ways > 1) {
-    seg = (n_tiles + ways - 1) / ways;
-    q = n_tiles / seg;
-    r = n_tiles - q * seg;
-  }
-  for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
-    const uint64_t total = rel[k].total;
-    const uint32_t width = rel[k].row_bytes;
-    const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
-    const uint64_t cnt = tile_base[k + 1] - tile_base[k];
-    // Items of a group have equal tile counts; tile j of member m goes to
-    // group_start + j*M + m, so the members' tiles over the same rows are
-    // adjacent in the list.
-    const uint64_t gm = rel[k].group_index;
-    const uint64_t gsize = rel[k].group_size;
-    const uint64_t b = tile_base[k] - gm * cnt + gm;
-    for (uint64_t j = threadIdx.x; j < cnt; j += kSetupBlock) {
-      const uint64_t start = j << sh;
-      const uint64_t left = total - start;
-      DevTile t;
-      t.item = k;
-      t.nbytes = uint32_t(left < (uint64_t(1) << sh) ? left : (uint64_t(1) << sh));
-      t.pad = 0;
-      if (width == 0) {
-        t.start = start;
-        t.c_base = 0;
-      } else {
-        const uint64_t row = start / width;
-        t.start = row;
-        t.c_base = uint32_t(start - row * width);
-      }
-      const uint64_t i = b + j * gsize;
-      tiles[ways > 1 ? xcd_position(i, seg, q, r) : i] = t;
-    }
-  }
-}
-
 // Largest power-of-two vector width (<= 16, >= esize) dividing every value
 // OR-ed into `acc`.
 __host__ __device__ inline uint32_t pick_vb(uint64_t acc, uint32_t esize) {
@@ -644,16 +575,12 @@ __host__ __device__ inline uint32_t log2u(uint32_t v) {
   return l;
 }
 
-// ptrs: the phase's pointer table (source objects, then destination
-// objects); offset: per-piece buffer offsets from sr_offsets_kernel.
-__global__ __launch_bounds__(kSetupBlock) void sr_bind_kernel(const DevRel* __restrict__ rel,
-                                                              uint32_t n,
-                                                              const uint64_t* __restrict__ ptrs,
-                                                              const uint64_t* __restrict__ offset,
-                                                              DevItem* __restrict__ items) {
-  const uint32_t k = blockIdx.x * kSetupBlock + threadIdx.x;
-  if (k >= n) return;
-  const DevRel h = rel[k];
+// The item of descriptor `h`: its object addresses resolved from `ptrs`,
+// the phase's pointer table (source objects, then destination objects),
+// and `offset`, the per-piece buffer offsets from sr_offsets_kernel, and
+// the widest vector access its addresses and sizes allow.
+__device__ __forceinline__ DevItem bind_item(const DevRel& h, const uint64_t* __restrict__ ptrs,
+                                             const uint64_t* __restrict__ offset) {
   const uint32_t kind = h.kind & 0xffu;
   const uint32_t esize = (h.kind >> 8) & 0xffu;
   const bool contiguous = h.row_bytes == 0;
@@ -690,7 +617,76 @@ __global__ __launch_bounds__(kSetupBlock) void sr_bind_kernel(const DevRel* __re
     lv = wide ? 2 : 0;
   }
   d.flags = kind | (lv << 4) | ((kind == kKindRecast && h.dst_slot >= 0) ? (1u << 8) : 0u);
-  items[k] = d;
+  return d;
+}
+
+// Tile i of the item-ordered list goes to position pos(i).  With `ways`
+// segments of seg = ceil(n/ways) tiles (q full segments and a last one of
+// r tiles), tile j of segment s is dispatched at j*q + min(j, r) + s: the
+// list is read column by column, so consecutive workgroups -- which the
+// hardware deals to the 8 XCDs in turn -- take one tile from each segment.
+__device__ __forceinline__ uint64_t xcd_position(uint64_t i, uint64_t seg, uint64_t q, uint64_t r) {
+  const uint64_t s = i / seg;
+  const uint64_t j = i - s * seg;
+  return j * q + (j < r ? j : r) + s;
+}
+
+// One workgroup per item writes the item's tiles (tile_base[k] = tiles of
+// items 0..k-1, computed with the descriptors on the host).  With `items`
+// non-null, lane 0 also binds the item to the pointer table `ptrs` (and the
+// buffer offsets `offset`), as sr_bind_kernel does: a phase's first launch
+// builds both tables in one kernel.
+__global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
+    const DevRel* __restrict__ rel, const uint64_t* __restrict__ tile_base, uint32_t n,
+    uint32_t tile_shift, uint64_t n_tiles, uint32_t ways, DevTile* __restrict__ tiles,
+    const uint64_t* __restrict__ ptrs, const uint64_t* __restrict__ offset, DevItem* __restrict__ items) {
+  uint64_t seg = 1, q = n_tiles, r = 0;
+  if (ways > 1) {
+    seg = (n_tiles + ways - 1) / ways;
+    q = n_tiles / seg;
+    r = n_tiles - q * seg;
+  }
+  for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
+    const uint64_t total = rel[k].total;
+    const uint32_t width = rel[k].row_bytes;
+    const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
+    const uint64_t cnt = tile_base[k + 1] - tile_base[k];
+    // Items of a group have equal tile counts; tile j of member m goes to
+    // group_start + j*M + m, so the members' tiles over the same rows are
+    // adjacent in the list.
+    const uint64_t gm = rel[k].group_index;
+    const uint64_t gsize = rel[k].group_size;
+    const uint64_t b = tile_base[k] - gm * cnt + gm;
+    if (items != nullptr && threadIdx.x == 0) items[k] = bind_item(rel[k], ptrs, offset);
+    for (uint64_t j = threadIdx.x; j < cnt; j += kSetupBlock) {
+      const uint64_t start = j << sh;
+      const uint64_t left = total - start;
+      DevTile t;
+      t.item = k;
+      t.nbytes = uint32_t(left < (uint64_t(1) << sh) ? left : (uint64_t(1) << sh));
+      t.pad = 0;
+      if (width == 0) {
+        t.start = start;
+        t.c_base = 0;
+      } else {
+        const uint64_t row = start / width;
+        t.start = row;
+        t.c_base = uint32_t(start - row * width);
+      }
+      const uint64_t i = b + j * gsize;
+      tiles[ways > 1 ? xcd_position(i, seg, q, r) : i] = t;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSetupBlock) void sr_bind_kernel(const DevRel* __restrict__ rel,
+                                                              uint32_t n,
+                                                              const uint64_t* __restrict__ ptrs,
+                                                              const uint64_t* __restrict__ offset,
+                                                              DevItem* __restrict__ items) {
+  const uint32_t k = blockIdx.x * kSetupBlock + threadIdx.x;
+  if (k >= n) return;
+  items[k] = bind_item(rel[k], ptrs, offset);
 }
 
 // ----------------------------------------------------------- host structures
@@ -717,6 +713,7 @@ struct HostItem {
 struct Phase {
   std::vector<HostItem> items;          // in piece order while the plan is built
   std::vector<DevRel> rel;              // items in dispatch (tile) order
+  std::vector<uint64_t> tile_base;      // tiles of rel[0..k-1]; tile_base[n] = n_tiles
   uint64_t n_tiles = 0;
   uint32_t n_src_base = 0;              // pointer table: sources, then destinations
   uint32_t n_dst_base = 0;
@@ -728,23 +725,26 @@ struct Phase {
   uint64_t bytes_read = 0;
   uint64_t bytes_written = 0;
   // device state, created on first use: one device allocation carved into
-  // the tables, one pinned host buffer for their uploads
+  // the item and tile tables, one pinned host buffer holding the
+  // descriptors, tile prefix and pointer table, which kernels read in place
   bool ready = false;
   void* d_mem = nullptr;
   size_t d_cap = 0;                     // bytes of d_mem / h_staging as allocated
   size_t h_cap = 0;
-  DevRel* d_rel = nullptr;
-  DevItem* d_items = nullptr;
-  DevTile* d_tiles = nullptr;
+  DevRel* d_rel = nullptr;              // device addresses of the h_staging parts
   uint64_t* d_tile_base = nullptr;
   uint64_t* d_ptrs = nullptr;
-  unsigned char* h_staging = nullptr;   // pinned: descriptors, then the pointer table
+  DevItem* d_items = nullptr;           // in d_mem
+  DevTile* d_tiles = nullptr;
+  unsigned char* h_staging = nullptr;   // pinned: descriptors, tile prefix, pointer table
+  void* h_dev = nullptr;                // h_staging's device address
   uint64_t* h_ptrs = nullptr;           // the pointer-table part of h_staging
   std::vector<uint64_t> bound;          // pointer table of the last bind
   bool bound_valid = false;
-  hipEvent_t ev_setup = nullptr;        // tile table and offsets written
-  hipEvent_t ev_staging = nullptr;      // last copy out of h_staging
+  hipEvent_t ev_setup = nullptr;        // tile table, offsets and the first bind written
+  hipEvent_t ev_staging = nullptr;      // a later bind done
   hipEvent_t ev_kernel = nullptr;       // last kernel reading d_items
+  hipEvent_t ev_bound = nullptr;        // the latest bind: ev_setup or ev_staging (not owned)
 };
 
 }  // namespace
@@ -760,6 +760,9 @@ struct sr_plan {
   Phase pack;
   Phase unpack;
   Phase gather;   // direct source -> destination, no buffers
+  // alignment each gather pointer must satisfy: its element size; 0 = the
+  // slot is not used by the gather
+  std::vector<uint32_t> gather_src_align, gather_dst_align;
   int device = -1;
   // Buffer offsets recomputed on the device: per-peer piece lists (CSR).
   std::vector<uint32_t> peer_begin;
@@ -858,8 +861,11 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
                bool buf_dst, bool group_by_src, bool row_groups) {
   ph.rel.clear();
   ph.rel.reserve(order.size());
+  ph.tile_base.clear();
+  ph.tile_base.reserve(order.size() + 1);
   ph.n_tiles = 0;
   for (uint32_t k : order) {
+    ph.tile_base.push_back(ph.n_tiles);
     const HostItem& h = ph.items[k];
     DevRel r{};
     r.src_off = h.src_off;
@@ -896,6 +902,7 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     const uint64_t item_tile = uint64_t(tile_bytes) >> reduce;
     ph.n_tiles += (r.total + item_tile - 1) / item_tile;
   }
+  ph.tile_base.push_back(ph.n_tiles);
   if (!row_groups) return;
   struct Side {
     int64_t slot;
@@ -976,7 +983,9 @@ size_t block_class(size_t bytes) {
 
 class TableCache {
  public:
-  int get(bool pinned, int device, size_t bytes, void** out, size_t* cap) {
+  // A block of at least `bytes`; for pinned host memory `dev_addr` (if not
+  // null) receives its device address, looked up once per allocation.
+  int get(bool pinned, int device, size_t bytes, void** out, size_t* cap, void** dev_addr = nullptr) {
     const size_t want = block_class(bytes);
     {
       std::lock_guard<std::mutex> lock(mu_);
@@ -985,14 +994,28 @@ class TableCache {
         if (list[i].device == device && list[i].bytes == want) {
           *out = list[i].p;
           *cap = want;
+          if (dev_addr) *dev_addr = list[i].dev;
           (pinned ? host_bytes_ : dev_bytes_) -= want;
           list[i] = list.back();
           list.pop_back();
           return SR_OK;
         }
     }
-    if (pinned) SR_HIP_TRY(hipHostMalloc(out, want, hipHostMallocDefault));
-    else SR_HIP_TRY(hipMalloc(out, want));
+    if (pinned) {
+      SR_HIP_TRY(hipHostMalloc(out, want, hipHostMallocDefault));
+      void* dev = nullptr;
+      const hipError_t e = hipHostGetDevicePointer(&dev, *out, 0);
+      if (e != hipSuccess) {
+        (void)hipHostFree(*out);
+        *out = nullptr;
+        return fail(SR_EHIP, "hipHostGetDevicePointer failed: %s", hipGetErrorString(e));
+      }
+      if (dev_addr) *dev_addr = dev;
+      std::lock_guard<std::mutex> lock(mu_);
+      host_dev_[*out] = dev;
+    } else {
+      SR_HIP_TRY(hipMalloc(out, want));
+    }
     *cap = want;
     return SR_OK;
   }
@@ -1003,10 +1026,11 @@ class TableCache {
       std::lock_guard<std::mutex> lock(mu_);
       size_t& held = pinned ? host_bytes_ : dev_bytes_;
       if (held + cap <= (pinned ? kCacheHostBytes : kCacheDeviceBytes)) {
-        (pinned ? host_ : dev_).push_back(Block{p, cap, device});
+        (pinned ? host_ : dev_).push_back(Block{p, cap, device, pinned ? host_dev_[p] : nullptr});
         held += cap;
         return;
       }
+      if (pinned) host_dev_.erase(p);
     }
     if (pinned) (void)hipHostFree(p);
     else (void)hipFree(p);
@@ -1062,8 +1086,10 @@ class TableCache {
     void* p;
     size_t bytes;
     int device;
+    void* dev;   // pinned blocks: device address
   };
   std::mutex mu_;
+  std::unordered_map<void*, void*> host_dev_;   // pinned block -> device address
   std::vector<Block> dev_, host_;
   std::vector<std::pair<int, hipEvent_t>> events_;
   std::vector<std::pair<int, hipStream_t>> streams_;
@@ -1137,56 +1163,60 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
   return SR_OK;
 }
 
-// First use of a phase: upload its descriptors and build the tile table on
-// the device, stream-ordered on `stream` (ev_setup marks completion).
-int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, hipStream_t stream) {
+// First use of a phase: its descriptors, tile prefix and pointer table go
+// into a pinned host buffer that the kernels read in place (no copy to the
+// device: the CPU writes it before the launch that reads it, and pinned host
+// memory is coherent at launch boundaries); one kernel then builds the tile
+// table and binds the items to `ptrs`, stream-ordered on `stream` (ev_setup
+// marks completion).
+int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, const std::vector<uint64_t>& ptrs,
+                hipStream_t stream) {
   if (ph.ready) return SR_OK;
   TableCache& cache = table_cache();
   int rc;
-  for (hipEvent_t* ev : {&ph.ev_setup, &ph.ev_staging, &ph.ev_kernel})
+  for (hipEvent_t* ev : {&ph.ev_setup, &ph.ev_kernel})
     if (!*ev && (rc = cache.get_event(p->device, ev)) != SR_OK) return rc;
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
-    size_t end = 0;
-    const size_t o_rel = carve(end, n * sizeof(DevRel));
-    const size_t o_ptr = carve(end, nptr * sizeof(uint64_t));
-    const size_t o_items = carve(end, n * sizeof(DevItem));
-    const size_t o_base = carve(end, (size_t(n) + 1) * sizeof(uint64_t));
-    const size_t o_tiles = carve(end, ph.n_tiles * sizeof(DevTile));
+    size_t h_end = 0;   // pinned: descriptors, tile prefix, pointer table
+    const size_t o_rel = carve(h_end, n * sizeof(DevRel));
+    const size_t o_base = carve(h_end, (size_t(n) + 1) * sizeof(uint64_t));
+    const size_t o_ptr = carve(h_end, nptr * sizeof(uint64_t));
+    size_t d_end = 0;   // device: item and tile tables
+    const size_t o_items = carve(d_end, n * sizeof(DevItem));
+    const size_t o_tiles = carve(d_end, ph.n_tiles * sizeof(DevTile));
     // allocations survive a failed attempt and are reused by the retry
-    if (!ph.d_mem && (rc = cache.get(false, p->device, end, &ph.d_mem, &ph.d_cap)) != SR_OK) return rc;
-    // pinned: descriptors + pointer table, the same layout as the device start
-    if (!ph.h_staging &&
-        (rc = cache.get(true, p->device, o_ptr + nptr * sizeof(uint64_t),
-                        reinterpret_cast<void**>(&ph.h_staging), &ph.h_cap)) != SR_OK)
+    if (!ph.d_mem && (rc = cache.get(false, p->device, d_end, &ph.d_mem, &ph.d_cap)) != SR_OK) return rc;
+    if (!ph.h_staging && (rc = cache.get(true, p->device, h_end, reinterpret_cast<void**>(&ph.h_staging),
+                                         &ph.h_cap, &ph.h_dev)) != SR_OK)
       return rc;
+    unsigned char* h = static_cast<unsigned char*>(ph.h_dev);   // the staging buffer's device address
     unsigned char* d = static_cast<unsigned char*>(ph.d_mem);
-    ph.d_rel = reinterpret_cast<DevRel*>(d + o_rel);
-    ph.d_ptrs = reinterpret_cast<uint64_t*>(d + o_ptr);
+    ph.d_rel = reinterpret_cast<DevRel*>(h + o_rel);
+    ph.d_tile_base = reinterpret_cast<uint64_t*>(h + o_base);
+    ph.d_ptrs = reinterpret_cast<uint64_t*>(h + o_ptr);
     ph.d_items = reinterpret_cast<DevItem*>(d + o_items);
-    ph.d_tile_base = reinterpret_cast<uint64_t*>(d + o_base);
     ph.d_tiles = reinterpret_cast<DevTile*>(d + o_tiles);
     ph.h_ptrs = reinterpret_cast<uint64_t*>(ph.h_staging + o_ptr);
-    // the descriptors go up once, asynchronously on the caller's stream
     std::memcpy(ph.h_staging + o_rel, ph.rel.data(), n * sizeof(DevRel));
-    SR_HIP_TRY(hipMemcpyAsync(ph.d_rel, ph.h_staging + o_rel, n * sizeof(DevRel), hipMemcpyHostToDevice,
-                              stream));
+    std::memcpy(ph.h_staging + o_base, ph.tile_base.data(), (size_t(n) + 1) * sizeof(uint64_t));
+    std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
     if (needs_offsets) {
       rc = setup_offsets(p, stream);
       if (rc != SR_OK) return rc;
       SR_HIP_TRY(hipStreamWaitEvent(stream, p->ev_offsets, 0));
     }
     const uint32_t shift = log2u(p->opt.tile_bytes);
-    hipLaunchKernelGGL(sr_tile_scan_kernel, dim3(1), dim3(kScanBlock), 0, stream, ph.d_rel, n, shift,
-                       ph.d_tile_base);
-    SR_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0,
                        stream, ph.d_rel, ph.d_tile_base, n, shift, ph.n_tiles,
-                       ph.interleave ? kXcds : 1u, ph.d_tiles);
+                       ph.interleave ? kXcds : 1u, ph.d_tiles, ph.d_ptrs, p->d_offset, ph.d_items);
     SR_HIP_TRY(hipGetLastError());
   }
   SR_HIP_TRY(hipEventRecord(ph.ev_setup, stream));
+  ph.ev_bound = ph.ev_setup;
+  ph.bound = ptrs;
+  ph.bound_valid = true;
   ph.ready = true;
   return SR_OK;
 }
@@ -1235,38 +1265,38 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   if (rebind && (rc = check_disjoint(ph, ptrs)) != SR_OK) return rc;
   rc = ensure_device(p);
   if (rc != SR_OK) return rc;
-  // A phase's first use builds its tables and binds the pointers on the
-  // device's setup stream: they are the library's own memory and read no
-  // caller data, so they may run while earlier work on `stream` (such as the
-  // previous launch group's copy) is still going.  Later rebinds stay on
-  // `stream`, ordered after the phase's previous launch.
-  const bool first = !ph.ready;
-  hipStream_t setup = stream;
-  if (first && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
-  rc = setup_phase(p, ph, kind != kGather, setup);
-  if (rc != SR_OK) return rc;
-
   const uint32_t n = uint32_t(ph.rel.size());
-  if (rebind) {
-    // The staging buffer may still feed the previous bind; the item table
-    // may still be read by the previous launch of this phase.
-    SR_HIP_TRY(hipEventSynchronize(ph.ev_staging));
+  if (!ph.ready) {
+    // A phase's first use builds its tables and binds the pointers on the
+    // device's setup stream: they are the library's own memory and read no
+    // caller data, so they may run while earlier work on `stream` (such as
+    // the previous launch group's copy) is still going.
+    hipStream_t setup = nullptr;
+    if ((rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
+    rc = setup_phase(p, ph, kind != kGather, ptrs, setup);
+    if (rc != SR_OK) return rc;
+    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
+  } else if (rebind) {
+    // Later rebinds run on `stream`, after the latest bind (which reads the
+    // pointer table in the staging buffer: the host rewrites it only once
+    // that bind is done) and after the phase's previous launch (which may
+    // still read the item table).
+    if (!ph.ev_staging && (rc = table_cache().get_event(p->device, &ph.ev_staging)) != SR_OK) return rc;
+    SR_HIP_TRY(hipEventSynchronize(ph.ev_bound));
     std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
-    if (!first) {   // here setup == stream: after the tables and the last launch
-      SR_HIP_TRY(hipStreamWaitEvent(setup, ph.ev_setup, 0));
-      SR_HIP_TRY(hipStreamWaitEvent(setup, ph.ev_kernel, 0));
-    }
-    SR_HIP_TRY(hipMemcpyAsync(ph.d_ptrs, ph.h_ptrs, ptrs.size() * sizeof(uint64_t),
-                              hipMemcpyHostToDevice, setup));
+    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_bound, 0));
+    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_kernel, 0));
     hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0,
-                       setup, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
+                       stream, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
     SR_HIP_TRY(hipGetLastError());
-    SR_HIP_TRY(hipEventRecord(ph.ev_staging, setup));
+    SR_HIP_TRY(hipEventRecord(ph.ev_staging, stream));
+    ph.ev_bound = ph.ev_staging;
     ph.bound = ptrs;
     ph.bound_valid = true;
+  } else {
+    // the latest bind (which follows the tables on its stream)
+    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_bound, 0));
   }
-  SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
-  SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_staging, 0));
 
   const uint32_t n_tiles = uint32_t(ph.n_tiles);
   uint32_t grid = n_tiles;
@@ -1324,8 +1354,10 @@ int check_ptrs(const void* const* ptrs, size_t n, const std::vector<uint32_t>& a
 }
 
 // Alignment each pointer of a gather must satisfy: its element size; 0 =
-// the slot is not used by the phase.
-void gather_alignment(const sr_plan* plan, std::vector<uint32_t>& sal, std::vector<uint32_t>& dal) {
+// the slot is not used by the phase.  Computed once, when the plan is made.
+void gather_alignment(sr_plan* plan) {
+  std::vector<uint32_t>& sal = plan->gather_src_align;
+  std::vector<uint32_t>& dal = plan->gather_dst_align;
   sal.assign(plan->src.size(), 0);
   dal.assign(plan->dst.size(), 0);
   for (const sr_piece& pc : plan->pieces) {
@@ -1378,9 +1410,9 @@ ScratchLayout scratch_layout(const Phase& ph) {
   ScratchLayout L{};
   size_t end = 0;
   L.rel = carve(end, n * sizeof(DevRel));
+  L.base = carve(end, (n + 1) * sizeof(uint64_t));
   L.ptrs = carve(end, nptr * sizeof(uint64_t));
   L.items = carve(end, n * sizeof(DevItem));
-  L.base = carve(end, (n + 1) * sizeof(uint64_t));
   L.tiles = carve(end, size_t(ph.n_tiles) * sizeof(DevTile));
   L.end = end;
   return L;
@@ -1719,6 +1751,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
     for (int32_t k = 0; k < n_pieces; ++k)
       if (pieces[k].kind != SR_PIECE_ZERO) p->peer_list[fill[pieces[k].peer]++] = uint32_t(k);
   }
+  gather_alignment(p);
   // Item tables are rebuilt from the descriptors; the per-item host copies
   // are no longer needed.
   for (Phase* ph : {&p->pack, &p->unpack, &p->gather}) std::vector<HostItem>().swap(ph->items);
@@ -1799,11 +1832,10 @@ int sr_unpack(sr_plan* plan, const void* const* peer_bufs, void* const* dst_ptrs
 
 int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs, hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
-  std::vector<uint32_t> sal, dal;
-  gather_alignment(plan, sal, dal);
-  int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
+  int rc = check_ptrs(src_ptrs, plan->src.size(), plan->gather_src_align, "src_ptrs");
   if (rc != SR_OK) return rc;
-  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
+  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), plan->gather_dst_align,
+                  "dst_ptrs");
   if (rc != SR_OK) return rc;
   return run_phase(plan, plan->gather, kGather,
                    pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size()), stream);
@@ -1820,11 +1852,10 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
                 "sr_gather_noalloc: the plan's gather tables need %zu bytes (%zu items, %llu tiles) but "
                 "the scratch holds %zu; create the plan with a larger tile_bytes or split the transfer",
                 L.end, ph.rel.size(), (unsigned long long)ph.n_tiles, size_t(SR_SCRATCH_BYTES));
-  std::vector<uint32_t> sal, dal;
-  gather_alignment(plan, sal, dal);
-  int rc = check_ptrs(src_ptrs, plan->src.size(), sal, "src_ptrs");
+  int rc = check_ptrs(src_ptrs, plan->src.size(), plan->gather_src_align, "src_ptrs");
   if (rc != SR_OK) return rc;
-  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), dal, "dst_ptrs");
+  rc = check_ptrs(reinterpret_cast<const void* const*>(dst_ptrs), plan->dst.size(), plan->gather_dst_align,
+                  "dst_ptrs");
   if (rc != SR_OK) return rc;
   if (ph.rel.empty()) return SR_OK;
   const std::vector<uint64_t> ptrs = pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size());
@@ -1841,24 +1872,23 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
   DevTile* d_tiles = reinterpret_cast<DevTile*>(s + L.tiles);
   const uint32_t n = uint32_t(ph.rel.size());
 
-  // Descriptors and pointers come from pageable host memory, which HIP copies
-  // synchronously: each copy waits for the work queued on `stream` before it
-  // (a previous call may still read the scratch) and the host buffers may be
-  // released on return.  Every table is then written whole on the device --
-  // tile_base by the scan, each tile position by the emit (the interleave is
-  // a permutation), each item by the bind -- so nothing needs clearing.
+  // Descriptors, tile prefix and pointers come from pageable host memory,
+  // which HIP copies synchronously: each copy waits for the work queued on
+  // `stream` before it (a previous call may still read the scratch) and the
+  // host buffers may be released on return.  Every table is then written
+  // whole -- the uploaded ones by the copies, each tile position by the emit
+  // (the interleave is a permutation) and each item by the bind it folds in --
+  // so nothing needs clearing.
   SR_HIP_TRY(hipMemcpyAsync(d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice, stream));
+  SR_HIP_TRY(hipMemcpyAsync(d_base, ph.tile_base.data(), (size_t(n) + 1) * sizeof(uint64_t),
+                            hipMemcpyHostToDevice, stream));
   SR_HIP_TRY(hipMemcpyAsync(d_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice,
                             stream));
   const uint32_t shift = log2u(plan->opt.tile_bytes);
-  hipLaunchKernelGGL(sr_tile_scan_kernel, dim3(1), dim3(kScanBlock), 0, stream, d_rel, n, shift, d_base);
-  SR_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0, stream,
-                     d_rel, d_base, n, shift, ph.n_tiles, ph.interleave ? kXcds : 1u, d_tiles);
-  SR_HIP_TRY(hipGetLastError());
   // gather items read no buffer offsets (no side is a peer buffer)
-  hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0, stream,
-                     d_rel, n, d_ptrs, static_cast<const uint64_t*>(nullptr), d_items);
+  hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0, stream,
+                     d_rel, d_base, n, shift, ph.n_tiles, ph.interleave ? kXcds : 1u, d_tiles, d_ptrs,
+                     static_cast<const uint64_t*>(nullptr), d_items);
   SR_HIP_TRY(hipGetLastError());
 
   const uint32_t n_tiles = uint32_t(ph.n_tiles);

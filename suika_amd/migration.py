@@ -28,6 +28,7 @@ import gc
 from dataclasses import replace
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
@@ -115,10 +116,12 @@ def execute_param_transfer(
     aligned), for a model that adopts them with
     ``load_state_dict(assign=True)``; ``pipeline`` cuts the transfer into up
     to that many launch groups of whole tensors, each planned on the host
-    while the GPU runs the previous one (growing from a small first one;
-    fewer groups growing faster when the tensors are large on average); ``stream`` runs the kernels on that
-    stream, after the work already queued on the current stream (which may
-    be producing the sources).  The call returns when the kernels are done.
+    while the GPU runs the previous one (largest tensors first, sized by a
+    cost model of host planning and GPU copy time); ``stream`` runs the
+    kernels on that stream, after the work already queued on the current
+    stream (which may be producing the sources).  The returned dict lists
+    the tensors in schedule order whatever the launch order.  The call
+    returns when the kernels are done.
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     _lib.lib()   # raises when the HIP library is missing: there is no other path
@@ -155,7 +158,8 @@ def execute_param_transfer(
     if ops and normal:
         first = source(ops[0].src_rank).get(ops[0].param_name, {})
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
-    groups = _pipeline_groups(ops, elem_bytes, pipeline)
+    n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
+    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies)
     if route == "direct":   # the plans only ever gather
         plan_options = replace(plan_options or PlanOptions(), gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
@@ -221,11 +225,10 @@ def execute_param_transfer(
                 if f in src_entry:
                     entry[f] = src_entry[f].to(device).clone()
 
-        ordered: StateDict = {}
+        # names in schedule order (launch groups take the largest first),
+        # recast targets first, then the sub-fields in their order
         field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
-        for name in dict.fromkeys(op.param_name for op in ops):
-            entry = target[name]
-            ordered[name] = {f: entry[f] for f in field_order if f in entry}
+        ordered: StateDict = _lib.host().ordered_result(ops, target, field_order)
     finally:
         # destroying a plan waits for its launches: buffers and sources may
         # be released afterwards whatever stream the kernels ran on
@@ -283,36 +286,22 @@ def _piece_aliases_source(op: TransferOp) -> bool:
     return all(x == 1 for x in local[:dim])
 
 
-# Bytes of piece data per launch group on average at least: a group's GPU
-# time (about 0.3 ms per GB at the measured rate) must cover the next group's
-# host planning for the overlap to pay; below 2 GB a single launch is faster.
-PIPELINE_GROUP_BYTES = 2 << 30
-# Size ratio of consecutive launch groups: host planning runs at about 0.7x
-# the GPU time of the same pieces, so each group may be this much larger than
-# the one before it and still be planned before the GPU runs dry.
-PIPELINE_GROWTH = 1.3
-# Host planning costs per tensor, GPU time per byte.  When the tensors are
-# large on average (at least this many bytes per name, over all moved
-# fields) the host plans far ahead of the GPU, and fewer groups growing
-# faster pay: every launch has its own ramp-up and tail.  Measured on the
-# benchmark shares: 4 groups growing 2.5x took 0.1-0.25 ms off the Llama2-7B,
-# Llama2-13B and Qwen2-7B calls (63-163 MB per name), while GPT-6.7B (31 MB
-# per name, 1552 tensors) lost 0.8 ms with them.
-PIPELINE_FAST_NAME_BYTES = 48 << 20
-PIPELINE_FAST_GROUPS = 4
-PIPELINE_FAST_GROWTH = 2.5
-
-
-def _pipeline_shape(sizes: List[int], pipeline: int) -> Tuple[int, float, int]:
-    """(groups, growth, minimum average bytes per group) for tensors of
-    ``sizes`` bytes, at most ``pipeline`` groups."""
-    total = sum(sizes)
-    if sizes and total / len(sizes) >= PIPELINE_FAST_NAME_BYTES:
-        k_max, growth, min_bytes = min(int(pipeline), PIPELINE_FAST_GROUPS), PIPELINE_FAST_GROWTH, \
-            PIPELINE_GROUP_BYTES // 2
-    else:
-        k_max, growth, min_bytes = int(pipeline), PIPELINE_GROWTH, PIPELINE_GROUP_BYTES
-    return max(1, min(k_max, len(sizes), total // min_bytes)), growth, min_bytes
+# Cost model of a launch group, measured on MI355X: the host plans a group
+# (sources read, lowering, plan, destination tensors, launch) in about
+# PLAN_NS_PER_GROUP plus PLAN_NS_PER_TENSOR per destination tensor, and the
+# gather moves GATHER_BYTES_PER_NS algorithmic bytes (read + written) per ns.
+PLAN_NS_PER_GROUP = 60_000
+PLAN_NS_PER_TENSOR = 1_000
+GATHER_BYTES_PER_NS = 6_100
+# GPU work of the first launch group: the host then plans the second while
+# it runs.
+FIRST_GROUP_NS = 100_000
+# Share of a group's GPU time the next group's planning may take.
+PLAN_SHARE = 0.9
+# Fewest tensors of a group that is not the last: when the previous group's
+# GPU time covers the planning of fewer, the host is the bottleneck and the
+# rest is planned as one group.
+MIN_GROUP_TENSORS = 4
 
 
 def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fields: List[str],
@@ -328,50 +317,32 @@ def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fiel
     return _lib.host().arena_tensors(ops, source, order, targets, device)
 
 
-def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int) -> List[List[TransferOp]]:
-    """Cut the ops into at most ``pipeline`` groups of whole tensors (all ops
-    of a name stay together, so each group's plan covers its destinations
-    completely), contiguous in schedule order, growing geometrically (the
-    shape from ``_pipeline_shape``): the first group is small, so the GPU
-    starts early, and each group's GPU time covers the host planning of the
-    next, larger one.
-    ``elem_bytes`` (bytes per element over all moved fields) only scales the
-    estimate."""
+def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int,
+                     tensors_per_name: int = 1) -> List[List[TransferOp]]:
+    """Cut the ops into at most ``pipeline`` launch groups of whole tensors
+    (all ops of a name stay together, so each group's plan covers its
+    destinations completely), each planned on the host while the GPU runs
+    the previous one.
+
+    A two-stage pipeline (host planning, then GPU copy) finishes soonest
+    when the jobs heavy on the second stage go first (Johnson's rule): the
+    tensors are taken largest first, so the GPU starts on a large tensor
+    planned in little time, and the small tensors, cheap to copy but as
+    costly to plan as large ones, come last.  The first group carries
+    FIRST_GROUP_NS of GPU work; each next group holds as many tensors as the
+    host can plan in PLAN_SHARE of the previous group's GPU time (the cost
+    model above); the rest forms the last group once a next group would
+    hold fewer than MIN_GROUP_TENSORS tensors or less GPU time than its own
+    planning overhead (PLAN_NS_PER_GROUP), or at the ``pipeline``-th group.
+    Within a group the tensors keep their schedule order.
+
+    ``elem_bytes`` is the bytes per element over all moved fields,
+    ``tensors_per_name`` the destination tensors per name (fields and
+    recast copies)."""
     ops = list(ops)
-    # runs of consecutive ops of one tensor (the schedule emits a tensor's
-    # pieces together); a name that comes back later joins its first run
-    starts, run_numel, single = _lib.host().tensor_runs(ops)
-    if single:
-        ends = starts.tolist()[1:] + [len(ops)]
-        by_name = [ops[a:b] for a, b in zip(starts.tolist(), ends)]
-        sizes = (run_numel * elem_bytes).tolist()
-    else:
-        grouped: Dict[str, List[TransferOp]] = {}
-        count: Dict[str, int] = {}
-        for op, n in zip(ops, _lib.host().piece_numels(ops).tolist()):
-            grouped.setdefault(op.param_name, []).append(op)
-            count[op.param_name] = count.get(op.param_name, 0) + n
-        by_name = list(grouped.values())
-        sizes = [count[name] * elem_bytes for name in grouped]
-    total = sum(sizes)
-    k, growth, _ = _pipeline_shape(sizes, pipeline)
-    if k == 1:
-        return [list(ops)]
-    weights = [growth ** j for j in range(k)]
-    scale = total / sum(weights)
-    bounds = []
-    acc_w = 0.0
-    for wgt in weights[:-1]:
-        acc_w += wgt
-        bounds.append(acc_w * scale)
-    groups: List[List[TransferOp]] = [[]]
-    acc = 0
-    for name_ops, n in zip(by_name, sizes):
-        if groups[-1] and len(groups) < k and acc >= bounds[len(groups) - 1]:
-            groups.append([])
-        groups[-1].extend(name_ops)
-        acc += n
-    return groups
+    return _lib.host().launch_groups(ops, 2.0 * elem_bytes / GATHER_BYTES_PER_NS, int(pipeline), FIRST_GROUP_NS,
+                                     PLAN_SHARE, PLAN_NS_PER_GROUP, PLAN_NS_PER_TENSOR * max(1, tensors_per_name),
+                                     MIN_GROUP_TENSORS)
 
 
 def schedule_and_execute_param_transfer(

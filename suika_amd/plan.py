@@ -101,7 +101,8 @@ def _numel(shape: Sequence[int]) -> int:
 
 def _stream_handle(stream) -> ctypes.c_void_p:
     if stream is None:
-        stream = torch.cuda.current_stream()
+        # the current stream's handle, without building a Stream object
+        return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch.cuda.current_device()))
     if isinstance(stream, torch.cuda.Stream):
         return ctypes.c_void_p(stream.cuda_stream)
     return ctypes.c_void_p(int(stream))
@@ -146,16 +147,27 @@ class ReshardPlan:
         ``device``.  ``rank`` (the executing rank) only prefixes messages.
         """
         self = cls.__new__(cls)
-        self._setup(ops, fields, recast, options)
+        self._configure(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
         who = f"[{rank}]" if rank is not None else ""
-        specs, dtypes, ptrs = _lib.host().collect_sources(self._ops, source, self.fields, dev_index, who)
-        self._build(specs, dtypes)
-        return self, np.ascontiguousarray(ptrs[self._src_index])
+        opt = self.options.to_c()
+        self._L = _lib.lib()
+        # grouping, shards, tables, source checks, sr_lower and sr_plan_create
+        # in one native call
+        (handle, self._names, self.dst_metas, self._op_names, self.dst_rank, self._dtypes, src_ptrs,
+         self._src_arr, self._dst_arr, self._piece_arr, self.peers, self._src_rows, self._dst_rows,
+         self._empty_rows, self.peer_bytes, info) = _lib.host().plan_sources(
+            self._ops, source, self.fields, [1 if f in self._recast_of else 0 for f in self.fields],
+            infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE)
+        self._handle = ctypes.c_void_p(handle)
+        self.info = _lib.SrPlanInfo.from_buffer_copy(info)
+        self.n_pieces = len(self._piece_arr)
+        self._views = self._pieces_view = self._c_src_view = self._c_dst_view = None
+        return self, src_ptrs
 
-    def _setup(self, ops, fields, recast, options) -> None:
-        """Everything but the source specs: validation, destination shards and
-        the op / meta tables of sr_lower."""
+    def _configure(self, ops, fields, recast, options) -> None:
+        """Fields, recast map and options, validated."""
         self._handle = ctypes.c_void_p()
         recast = dict(recast or {})
         for tgt, srcf in recast.items():
@@ -165,12 +177,18 @@ class ReshardPlan:
         self.fields = list(fields)
         self.recast = recast
         self.options = options or PlanOptions()
-        ops = self._ops = list(ops)
+        self._ops = list(ops)
+        self._recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
+
+    def _setup(self, ops, fields, recast, options) -> None:
+        """Everything but the source specs: validation, destination shards and
+        the op / meta tables of sr_lower."""
+        self._configure(ops, fields, recast, options)
+        ops = self._ops
         self._op_names = [op.param_name for op in ops]
         dst_ranks = {op.dst_rank for op in ops}
         assert len(dst_ranks) <= 1, f"ops target several ranks {sorted(dst_ranks)}"
         self.dst_rank = dst_ranks.pop() if dst_ranks else None
-        self._recast_of = {sf: t for t, sf in recast.items()}   # f32 field -> its bf16 target
 
         # the destination shard of every tensor: attached by the schedule, else
         # inferred from the tensor's pieces
@@ -222,9 +240,7 @@ class ReshardPlan:
             self._empty_rows = _lib.copy_table(lw.empty, lw.n_empty, (np.int64, _lib.SR_KEY_WORDS))
         finally:
             L.sr_lowering_destroy(low)
-        # source slot -> (op, field) position in the per-(op, field) lists
-        self._src_index = src_rows[:, 0] * nf + src_rows[:, 1] if len(src_rows) else np.zeros(0, np.int64)
-        self._src_rows = src_rows.tolist()
+        self._src_rows = src_rows
         self._views = None
 
         self.n_pieces = len(self._piece_arr)
@@ -260,7 +276,7 @@ class ReshardPlan:
             nf = len(self.fields)
             src_keys: List[SrcKey] = []
             src_specs: Dict[SrcKey, SlotSpec] = {}
-            for k, f, _, _, nd, *shape in self._src_rows:
+            for k, f, _, _, nd, *shape in self._src_rows.tolist():
                 op = self._ops[k]
                 key = (op.src_rank, op.param_name, self.fields[f])
                 src_keys.append(key)
@@ -454,10 +470,11 @@ class ReshardPlan:
     @staticmethod
     def _carray(ptrs):
         """A pointer array for the C ABI: a uint64 numpy array is passed by
-        address (no copy); a list is converted."""
+        address (no copy; the caller keeps it alive for the call); a list is
+        converted."""
         if isinstance(ptrs, np.ndarray):
             assert ptrs.dtype == np.uint64 and ptrs.flags["C_CONTIGUOUS"], "address arrays are contiguous uint64"
-            return ptrs.ctypes.data_as(ctypes.POINTER(ctypes.c_void_p))
+            return ptrs.__array_interface__["data"][0]
         return (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
 
     def pack_ptrs(self, src_ptrs: List[int], buf_ptrs: List[int], stream=None) -> None:

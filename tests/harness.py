@@ -312,3 +312,18 @@ def load_schedule_vectors():
     import json as _json
     with gzip.open(GOLDEN / "schedule_vectors.json.gz", "rt") as fh:
         return _json.load(fh)
+
+
+def round_robin_groups(k: int):
+    """A launch grouping for tests: the tensors dealt round robin into ``k``
+    groups (whole tensors, not contiguous in schedule order), as a stand-in
+    for ``migration._pipeline_groups`` that forces several launch groups on
+    small cases."""
+    def groups(ops, elem_bytes, pipeline, tensors_per_name=1):
+        index: Dict[str, int] = {}
+        out: List[list] = [[] for _ in range(k)]
+        for op in ops:
+            g = index.setdefault(op.param_name, len(index) % k)
+            out[g].append(op)
+        return [g for g in out if g]
+    return groups

@@ -127,7 +127,8 @@ def test_arena_destinations_and_adoption(route, groups, monkeypatch):
     load_state_dict(assign=True) keeps them in place (no copy)."""
     if groups == "many":
         from suika_amd import migration
-        monkeypatch.setattr(migration, "PIPELINE_GROUP_BYTES", 1 << 10)
+        from tests.harness import round_robin_groups
+        monkeypatch.setattr(migration, "_pipeline_groups", round_robin_groups(4))
     from suika_amd.inventory import build_module
     from tests.cases import scaled_configs
     from tests.harness import index_state, oracle_dest, source_shards, t2np, to_device

@@ -40,6 +40,7 @@ def _check(w, payload="seeded", options=None, route="buffers"):
         assert set(got[name]) == set(want[name]), name
         for f in want[name]:
             np.testing.assert_array_equal(got[name][f], want[name][f], err_msg=f"{w.key}: {name}/{f}")
+    return got
 
 
 @pytest.mark.parametrize("route", ["buffers", "direct"])
@@ -55,10 +56,14 @@ PIPELINED = list(cases.scaled_configs().values()) + cases.dp_cases()[:2]
 @pytest.mark.parametrize("w", PIPELINED, ids=[w.key for w in PIPELINED])
 def test_gpu_pipelined_launch_groups_match_oracle(w, route, monkeypatch):
     """execute_param_transfer in several launch groups (each planned while
-    the previous one runs), forced on small cases by a tiny group size."""
+    the previous one runs), forced on small cases: tensors dealt round robin
+    into four groups, so no group is contiguous in schedule order."""
     from suika_amd import migration
-    monkeypatch.setattr(migration, "PIPELINE_GROUP_BYTES", 1 << 10)
-    _check(w, payload="index", route=route)
+    from tests.harness import round_robin_groups
+    monkeypatch.setattr(migration, "_pipeline_groups", round_robin_groups(4))
+    got = _check(w, payload="index", route=route)
+    # the result lists the tensors in schedule order, whatever the launch order
+    assert list(got) == list(dict.fromkeys(op.param_name for op in w.ops()))
 
 
 SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())

@@ -294,47 +294,98 @@ def test_zero_element_tensors_are_planned_as_empty():
     plan.close()
 
 
+def _group_costs(w, groups, elem, tpn):
+    """(plan ns, GPU ns) of each launch group under the migration module's
+    cost model."""
+    from suika_amd import migration as M
+    out = []
+    for g in groups:
+        names = {op.param_name for op in g}
+        numel = sum(op.dst_meta.numel() for op in g)
+        out.append((M.PLAN_NS_PER_GROUP + M.PLAN_NS_PER_TENSOR * tpn * len(names),
+                    numel * 2.0 * elem / M.GATHER_BYTES_PER_NS))
+    return out
+
+
 def test_pipeline_groups_keep_tensors_whole():
-    """Launch groups of execute_param_transfer: contiguous in schedule order,
-    every op of a tensor in one group, at most ``pipeline`` groups carrying
-    PIPELINE_GROUP_BYTES on average at least, growing from a small first one."""
+    """Launch groups of execute_param_transfer: every op in exactly one
+    group, every op of a tensor in the same group, at most ``pipeline``
+    groups, schedule order kept within a group, the largest tensor in the
+    first group."""
     from suika_amd import migration
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         ops = w.ops()
         elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
-        for pipeline in (1, 3, 4, 8, 100):
-            groups = migration._pipeline_groups(ops, elem, pipeline)
-            assert [op for g in groups for op in g] == ops
+        tpn = len(w.src_fields) + len(w.recast_map)
+        position = {id(op): i for i, op in enumerate(ops)}
+        for pipeline in (1, 2, 3, 4, 8, 100):
+            groups = migration._pipeline_groups(ops, elem, pipeline, tpn)
+            assert sorted(position[id(op)] for g in groups for op in g) == list(range(len(ops)))
             assert 1 <= len(groups) <= pipeline
             seen = set()
             for g in groups:
                 names = {op.param_name for op in g}
                 assert not names & seen, "a tensor split across groups"
                 seen |= names
-            sizes = [sum(op.dst_meta.numel() for op in g) * elem for g in groups]
-            names_bytes = {}
+                assert [position[id(op)] for op in g] == sorted(position[id(op)] for op in g)
+            if pipeline == 1:
+                assert groups == [ops]
+            per_name = {}
             for op in ops:
-                names_bytes[op.param_name] = names_bytes.get(op.param_name, 0) + op.dst_meta.numel() * elem
-            _, growth, min_bytes = migration._pipeline_shape(list(names_bytes.values()), pipeline)
-            assert len(groups) == 1 or sum(sizes) / len(groups) >= min_bytes
-            if len(groups) >= 3:
-                assert sizes[0] < sizes[-1], (key, pipeline, sizes)
-    small = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
-    elem = sum(small.dtypes[f].itemsize for f in small.src_fields)
-    assert len(migration._pipeline_groups(small.ops(), elem, 4)) == 1
-    # a tensor whose ops are not consecutive still lands whole in one group,
-    # at the place of its first op
+                per_name[op.param_name] = per_name.get(op.param_name, 0) + op.dst_meta.numel()
+            if len(groups) > 1:
+                assert max(per_name, key=per_name.get) in {op.param_name for op in groups[0]}
+    # a tensor whose ops are not consecutive still lands whole in one group
     w = CONFIGS["llama7b_tp4pp2_tp2pp2"]
     ops = list(w.ops())
     ops = ops[1:] + ops[:1]                  # the first tensor's first op moves to the end
-    groups = migration._pipeline_groups(ops, 14, 8)
+    groups = migration._pipeline_groups(ops, 14, 8, 5)
     owner = {}
     for gi, g in enumerate(groups):
         for op in g:
             assert owner.setdefault(op.param_name, gi) == gi
     assert sorted(map(id, (op for g in groups for op in g))) == sorted(map(id, ops))
-    assert groups[0][0] is ops[0]
+
+
+def test_pipeline_groups_follow_the_cost_model():
+    """The cut: the first group carries FIRST_GROUP_NS of GPU work (the
+    fewest largest tensors that do); each later group but the last is
+    planned within PLAN_SHARE of its predecessor's GPU time and holds at
+    least MIN_GROUP_TENSORS names; tensors go largest first, so no tensor of
+    a later group is larger than one of an earlier group."""
+    from suika_amd import migration as M
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        ops = w.ops()
+        elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+        tpn = len(w.src_fields) + len(w.recast_map)
+        groups = M._pipeline_groups(ops, elem, 8, tpn)
+        costs = _group_costs(w, groups, elem, tpn)
+        sizes = []
+        for g in groups:
+            per = {}
+            for op in g:
+                per[op.param_name] = per.get(op.param_name, 0) + op.dst_meta.numel()
+            sizes.append(sorted(per.values()))
+        for a, b in zip(sizes[:-1], sizes[1:]):
+            assert a[0] >= b[-1], (key, "a later group holds a larger tensor")
+        first_gpu = costs[0][1]
+        assert first_gpu >= M.FIRST_GROUP_NS or len(groups) == 1
+        assert first_gpu - sizes[0][0] * 2.0 * elem / M.GATHER_BYTES_PER_NS < M.FIRST_GROUP_NS
+        for j in range(1, len(groups) - 1):
+            names = len(sizes[j])
+            assert names >= M.MIN_GROUP_TENSORS
+            assert costs[j][0] <= costs[j - 1][1] * M.PLAN_SHARE + 1e-6, (key, j)
+            assert costs[j][1] >= M.PLAN_NS_PER_GROUP, (key, j)
+    # the benchmark shares pipeline in 3 or 4 groups; a single tensor or
+    # pipeline=1 runs as one
+    shapes = {key: len(M._pipeline_groups(CONFIGS[key].ops(), 14, 8, 5)) for key in CONFIG_ORDER}
+    assert all(2 <= k <= 8 for k in shapes.values()), shapes
+    w = CONFIGS["gpt125m_tp2_tp4"]
+    one = [op for op in w.ops() if op.param_name == w.ops()[0].param_name]
+    assert M._pipeline_groups(one, 12, 8, 3) == [one]
+    assert M._pipeline_groups([], 12, 8, 3) == [[]]
 
 
 def test_ops_of_rank_and_tensor_runs():
@@ -357,27 +408,6 @@ def test_ops_of_rank_and_tensor_runs():
     ops = host.ops_of_rank(schedule_param_transfer(*CONFIGS["gpt125m_tp2_tp4"].layouts()), 0)
     assert host.tensor_runs(ops + ops[:1])[2] is False          # a tensor whose ops come back later
     assert host.tensor_runs([])[0].size == 0
-
-
-def test_pipeline_shape_by_tensor_size():
-    """Large tensors on average: at most 4 groups growing 2.5x; small ones:
-    up to ``pipeline`` groups growing 1.3x (the measured optima)."""
-    from suika_amd import migration
-    shapes = {}
-    for key in CONFIG_ORDER:
-        w = CONFIGS[key]
-        ops = w.ops()
-        elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
-        per_name = {}
-        for op in ops:
-            per_name[op.param_name] = per_name.get(op.param_name, 0) + op.dst_meta.numel() * elem
-        shapes[key] = migration._pipeline_shape(list(per_name.values()), 8)[:2]
-    assert shapes["llama7b_tp4pp2_tp2pp2"] == (4, 2.5)
-    assert shapes["llama13b_tp8_tp4pp2"] == (4, 2.5)
-    assert shapes["qwen7b_tp2_tp4"] == (4, 2.5)
-    assert shapes["gpt6.7b_tp1pp4_tp8"] == (5, 1.3)      # 12.1 GB // 2 GiB
-    assert shapes["gpt125m_tp2_tp4"][0] == 1
-    assert migration._pipeline_shape([], 8)[0] == 1
 
 
 def test_from_sources_rejects_bad_sources_by_name():
