@@ -358,6 +358,9 @@ def host():
         import importlib.util
 
         import torch  # noqa: F401  (its libraries back the extension)
+        # the extension calls the library: it binds (by soname) to the copy
+        # loaded here, so both sides share one instance of its state
+        lib()
         path = Path(os.environ.get("SUIKA_HOST_LIB", str(HOST_PATH)))
         if not path.exists():
             raise RuntimeError(

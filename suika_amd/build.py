@@ -39,6 +39,9 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-shared",
+    # the host extension names the library by this soname, so it binds to
+    # whichever copy the process loaded first (the ctypes binding's)
+    "-Wl,-soname,libsuika_reshard.so",
     # packed-FP32 instructions stay disabled for all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",

@@ -759,72 +759,6 @@ py::tuple name_runs(py::list ops) {
   return py::make_tuple(order, starts, total, single);
 }
 
-// Launch groups of one rank's ops: whole tensors per group, the largest
-// tensors first (a two-stage pipeline -- host planning, then GPU copy --
-// finishes soonest with the GPU-heavy jobs first), sized by the cost model
-// the caller passes: the first group carries `first_ns` of GPU work, each
-// next one as many tensors as the host plans in `share` of the previous
-// group's GPU time (`group_ns` + `tensor_ns` per tensor), at most
-// `max_groups` groups.  The rest goes into one last group as soon as a next
-// group would hold fewer than `min_tensors` tensors or less than `group_ns`
-// of GPU work.  A tensor's GPU time is its elements times
-// `ns_per_element`.  Within a group, ops keep their schedule order.
-py::list launch_groups(py::list ops, double ns_per_element, int64_t max_groups, double first_ns,
-                       double share, double group_ns, double tensor_ns, int64_t min_tensors) {
-  py::tuple runs = name_runs(ops);
-  py::array_t<int64_t> order = runs[0].cast<py::array_t<int64_t>>();
-  py::array_t<int64_t> starts = runs[1].cast<py::array_t<int64_t>>();
-  py::array_t<int64_t> numel = runs[2].cast<py::array_t<int64_t>>();
-  const int64_t n = int64_t(numel.size());
-  py::list out;
-  if (max_groups <= 1 || n <= 1) {
-    out.append(ops);
-    return out;
-  }
-  const int64_t* e = numel.data();
-  std::vector<int64_t> rank(static_cast<size_t>(n));
-  for (int64_t i = 0; i < n; ++i) rank[size_t(i)] = i;
-  std::stable_sort(rank.begin(), rank.end(), [&](int64_t a, int64_t b) { return e[a] > e[b]; });
-  std::vector<double> cum(static_cast<size_t>(n));
-  double acc = 0;
-  for (int64_t i = 0; i < n; ++i) cum[size_t(i)] = acc += double(e[rank[size_t(i)]]) * ns_per_element;
-  auto gpu = [&](int64_t a, int64_t b) { return cum[size_t(b - 1)] - (a ? cum[size_t(a - 1)] : 0.0); };
-  std::vector<int64_t> bounds{0};
-  int64_t end = 1;
-  while (end < n && cum[size_t(end - 1)] < first_ns) ++end;
-  bounds.push_back(end);
-  while (end < n) {
-    int64_t next = n;
-    if (int64_t(bounds.size()) < max_groups) {
-      const double fits = (gpu(bounds[bounds.size() - 2], end) * share - group_ns) / tensor_ns;
-      if (fits >= double(min_tensors)) next = std::min<int64_t>(n, end + int64_t(fits));
-      // a group that is not the last pays its planning overhead back only
-      // if the GPU runs it at least that long (while the host plans on)
-      if (next < n && gpu(end, next) < group_ns) next = n;
-    }
-    end = next;
-    bounds.push_back(end);
-  }
-  if (bounds.size() == 2) {
-    out.append(ops);
-    return out;
-  }
-  const size_t k = bounds.size() - 1;
-  std::vector<int64_t> group_of(static_cast<size_t>(n));
-  for (size_t g = 0; g < k; ++g)
-    for (int64_t i = bounds[g]; i < bounds[g + 1]; ++i) group_of[size_t(rank[size_t(i)])] = int64_t(g);
-  std::vector<py::list> lists(k);
-  const int64_t* o = order.data();
-  const int64_t* st = starts.data();
-  for (int64_t m = 0; m < n; ++m) {
-    py::list& dst = lists[size_t(group_of[size_t(m)])];
-    for (int64_t p = st[m]; p < st[m + 1]; ++p)
-      if (PyList_Append(dst.ptr(), PyList_GET_ITEM(ops.ptr(), o[p])) != 0) throw py::error_already_set();
-  }
-  for (py::list& l : lists) out.append(l);
-  return out;
-}
-
 // The drop-in call's result: {name: {field: tensor}} with the names in
 // order of first appearance in `ops` and each entry's fields in
 // `field_order` (those present), from `target`, filled launch group by
@@ -1015,7 +949,9 @@ py::list device_views(uint64_t base, py::list views, int64_t device_index) {
 // tensor's destination shard (op.dst_shard_meta, else `infer_shard(ops of the
 // name)`), the op / meta tables (encode_ops), the source tensors
 // (collect_sources), then sr_lower and sr_plan_create of libsuika_reshard.so
-// on its tables, with nothing copied through Python in between.  Raises
+// on its tables, with nothing copied through Python in between.  With
+// `gather`, also the fresh destination tensors (alloc_dst) and sr_gather
+// into them on `stream` (the drop-in call's direct route).  Raises
 // suika_amd._lib.PlanError (or ReshardError for device and memory failures)
 // with the library's message, tensor ids replaced by names.
 
@@ -1086,14 +1022,16 @@ static_assert(sizeof(sr_op) == 9 * sizeof(int64_t), "an sr_op row is 9 int64 wor
 
 }  // namespace
 
-py::tuple plan_sources(py::list ops, py::function source, py::list fields, std::vector<int64_t> recast,
+py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::list recast_names,
                        py::function infer_shard, int64_t device_index, const std::string& who,
                        uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
-                       py::dtype piece_dt) {
+                       py::dtype piece_dt, bool gather, uint64_t stream) {
   const Names& N = names_();
   const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
   const int64_t nf = int64_t(fields.size());
-  if (int64_t(recast.size()) != nf) throw py::value_error("one recast flag per field");
+  if (int64_t(recast_names.size()) != nf) throw py::value_error("one recast name (or None) per field");
+  std::vector<int64_t> recast(static_cast<size_t>(nf));
+  for (int64_t f = 0; f < nf; ++f) recast[size_t(f)] = recast_names[f].is_none() ? 0 : 1;
   // tensors in order of first appearance, their ops, the destination rank
   py::dict name_ids;
   py::list names, op_names(n);
@@ -1192,12 +1130,24 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, std::
   if ((rc = sr_plan_info_get(plan, &info)) != SR_OK)
     raise_status(rc, "sr_plan_info_get", sr_last_error());
   py::bytes info_bytes(reinterpret_cast<const char*>(&info), sizeof(info));
+  py::array_t<int64_t> dst_rows = key_table(low->dst_key, low->n_dst), empty_rows = key_table(low->empty, low->n_empty);
+  py::object part = py::none();
+  if (gather) {
+    // fresh destinations, then the gather on `stream`
+    py::tuple fresh = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
+                                at::Device(at::kCUDA, c10::DeviceIndex(device_index)));
+    part = fresh[0];
+    py::array_t<uint64_t> dst_ptrs = fresh[1].cast<py::array_t<uint64_t>>();
+    rc = sr_gather(plan, reinterpret_cast<const void* const*>(src_ptrs.data()),
+                   reinterpret_cast<void* const*>(dst_ptrs.data()), reinterpret_cast<hipStream_t>(stream));
+    if (rc != SR_OK) raise_status(rc, "sr_gather", sr_last_error());
+  }
   py::tuple out = py::make_tuple(
       reinterpret_cast<uintptr_t>(plan), names, shards, op_names,
       ranks.empty() ? py::object(py::none()) : py::object(py::int_(ranks[0])), col[1], src_ptrs,
       table(low->src, low->n_src, tensor_dt), table(low->dst, low->n_dst, tensor_dt),
       table(low->pieces, low->n_pieces, piece_dt), peers, key_table(low->src_key, low->n_src),
-      key_table(low->dst_key, low->n_dst), key_table(low->empty, low->n_empty), peer_bytes, info_bytes);
+      dst_rows, empty_rows, peer_bytes, info_bytes, part);
   plan_hold.release();   // owned by the caller from here on
   return out;
 }
@@ -1220,13 +1170,12 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("tensor_runs", &tensor_runs, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
-  m.def("launch_groups", &launch_groups, py::arg("ops"), py::arg("ns_per_element"), py::arg("max_groups"),
-        py::arg("first_ns"), py::arg("share"), py::arg("group_ns"), py::arg("tensor_ns"), py::arg("min_tensors"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
         py::arg("op_cls"), py::arg("meta_cls"));
   m.def("device_views", &device_views, py::arg("base"), py::arg("views"), py::arg("device_index"));
-  m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"), py::arg("recast"),
-        py::arg("infer_shard"), py::arg("device_index"), py::arg("who"), py::arg("tile_bytes"),
-        py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"), py::arg("piece_dtype"));
+  m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
+        py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),
+        py::arg("tile_bytes"), py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"),
+        py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0);
 }

@@ -70,7 +70,6 @@
 #include <mutex>
 #include <new>
 #include <string>
-#include <unordered_map>
 #include <vector>
 
 #include "suika_reshard.h"
@@ -473,9 +472,7 @@ __global__ __launch_bounds__(kBlock) void sr_gather_kernel(const DevItem* __rest
 //                       DevItem (addresses, vector width); later launches
 //                       with other pointers.
 
-// Pointer-independent item descriptor (written once on the host, read in place
-// from pinned memory by the setup kernels; copied to the scratch by the
-// allocation-free gather).
+// Pointer-independent item descriptor (device resident, uploaded once).
 enum : uint32_t {
   kRelSrcBuf = 1u << 16,   // source side is a peer buffer at the piece's offset
   kRelDstBuf = 1u << 17,   // destination side is a peer buffer at the piece's offset
@@ -540,6 +537,15 @@ __device__ uint64_t block_exclusive_scan(uint64_t v, uint64_t& total) {
 }
 
 constexpr int kSetupBlock = 256;
+// Tiles one workgroup of the emit kernel writes at most (16 per lane): a
+// large item's tiles are spread over several workgroups.
+constexpr uint32_t kEmitTiles = 4096;
+
+struct EmitChunk {
+  uint32_t item;
+  uint32_t chunk;   // the item's tiles [chunk * kEmitTiles, (chunk + 1) * kEmitTiles)
+};
+static_assert(sizeof(EmitChunk) == 8, "EmitChunk layout");
 
 // One workgroup per peer.  peer_begin[p]..peer_begin[p+1] indexes
 // peer_list, the peer's pieces in piece order.
@@ -631,14 +637,16 @@ __device__ __forceinline__ uint64_t xcd_position(uint64_t i, uint64_t seg, uint6
   return j * q + (j < r ? j : r) + s;
 }
 
-// One workgroup per item writes the item's tiles (tile_base[k] = tiles of
-// items 0..k-1, computed with the descriptors on the host).  With `items`
-// non-null, lane 0 also binds the item to the pointer table `ptrs` (and the
+// One workgroup per emit chunk -- up to kEmitTiles consecutive tiles of one
+// item (chunks[c] = {item, chunk index}; every item has at least one) --
+// writes those tiles (tile_base[k] = tiles of items 0..k-1, computed with the
+// descriptors on the host).  With `items` non-null, lane 0 of an item's
+// first chunk also binds the item to the pointer table `ptrs` (and the
 // buffer offsets `offset`), as sr_bind_kernel does: a phase's first launch
 // builds both tables in one kernel.
 __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
-    const DevRel* __restrict__ rel, const uint64_t* __restrict__ tile_base, uint32_t n,
-    uint32_t tile_shift, uint64_t n_tiles, uint32_t ways, DevTile* __restrict__ tiles,
+    const DevRel* __restrict__ rel, const uint64_t* __restrict__ tile_base, const EmitChunk* __restrict__ chunks,
+    uint32_t n_chunks, uint32_t tile_shift, uint64_t n_tiles, uint32_t ways, DevTile* __restrict__ tiles,
     const uint64_t* __restrict__ ptrs, const uint64_t* __restrict__ offset, DevItem* __restrict__ items) {
   uint64_t seg = 1, q = n_tiles, r = 0;
   if (ways > 1) {
@@ -646,7 +654,9 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
     q = n_tiles / seg;
     r = n_tiles - q * seg;
   }
-  for (uint32_t k = blockIdx.x; k < n; k += gridDim.x) {
+  for (uint32_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    const uint32_t k = chunks[c].item;
+    const uint64_t j0 = uint64_t(chunks[c].chunk) * kEmitTiles;
     const uint64_t total = rel[k].total;
     const uint32_t width = rel[k].row_bytes;
     const uint32_t sh = item_tile_shift(rel[k].kind, tile_shift);
@@ -657,8 +667,9 @@ __global__ __launch_bounds__(kSetupBlock) void sr_tile_emit_kernel(
     const uint64_t gm = rel[k].group_index;
     const uint64_t gsize = rel[k].group_size;
     const uint64_t b = tile_base[k] - gm * cnt + gm;
-    if (items != nullptr && threadIdx.x == 0) items[k] = bind_item(rel[k], ptrs, offset);
-    for (uint64_t j = threadIdx.x; j < cnt; j += kSetupBlock) {
+    if (items != nullptr && j0 == 0 && threadIdx.x == 0) items[k] = bind_item(rel[k], ptrs, offset);
+    const uint64_t j1 = cnt < j0 + kEmitTiles ? cnt : j0 + kEmitTiles;
+    for (uint64_t j = j0 + threadIdx.x; j < j1; j += kSetupBlock) {
       const uint64_t start = j << sh;
       const uint64_t left = total - start;
       DevTile t;
@@ -714,6 +725,7 @@ struct Phase {
   std::vector<HostItem> items;          // in piece order while the plan is built
   std::vector<DevRel> rel;              // items in dispatch (tile) order
   std::vector<uint64_t> tile_base;      // tiles of rel[0..k-1]; tile_base[n] = n_tiles
+  std::vector<EmitChunk> emit_chunks;   // the emit kernel's work: every item's tiles in chunks
   uint64_t n_tiles = 0;
   uint32_t n_src_base = 0;              // pointer table: sources, then destinations
   uint32_t n_dst_base = 0;
@@ -725,24 +737,22 @@ struct Phase {
   uint64_t bytes_read = 0;
   uint64_t bytes_written = 0;
   // device state, created on first use: one device allocation carved into
-  // the item and tile tables, one pinned host buffer holding the
-  // descriptors, tile prefix and pointer table, which kernels read in place
+  // the tables, one pinned host buffer for their uploads
   bool ready = false;
   void* d_mem = nullptr;
   size_t d_cap = 0;                     // bytes of d_mem / h_staging as allocated
   size_t h_cap = 0;
-  DevRel* d_rel = nullptr;              // device addresses of the h_staging parts
+  DevRel* d_rel = nullptr;              // uploaded: descriptors, tile prefix, pointer table
   uint64_t* d_tile_base = nullptr;
   uint64_t* d_ptrs = nullptr;
-  DevItem* d_items = nullptr;           // in d_mem
+  DevItem* d_items = nullptr;           // built on the device
   DevTile* d_tiles = nullptr;
-  unsigned char* h_staging = nullptr;   // pinned: descriptors, tile prefix, pointer table
-  void* h_dev = nullptr;                // h_staging's device address
+  unsigned char* h_staging = nullptr;   // pinned: the uploaded part, in the same layout
   uint64_t* h_ptrs = nullptr;           // the pointer-table part of h_staging
   std::vector<uint64_t> bound;          // pointer table of the last bind
   bool bound_valid = false;
   hipEvent_t ev_setup = nullptr;        // tile table, offsets and the first bind written
-  hipEvent_t ev_staging = nullptr;      // a later bind done
+  hipEvent_t ev_staging = nullptr;      // a later bind done (its copy out of h_staging too)
   hipEvent_t ev_kernel = nullptr;       // last kernel reading d_items
   hipEvent_t ev_bound = nullptr;        // the latest bind: ev_setup or ev_staging (not owned)
 };
@@ -903,6 +913,11 @@ void build_rel(Phase& ph, const std::vector<uint32_t>& order, uint32_t tile_byte
     ph.n_tiles += (r.total + item_tile - 1) / item_tile;
   }
   ph.tile_base.push_back(ph.n_tiles);
+  ph.emit_chunks.clear();
+  for (size_t k = 0; k < ph.rel.size(); ++k) {
+    const uint64_t cnt = ph.tile_base[k + 1] - ph.tile_base[k];
+    for (uint64_t c = 0; c * kEmitTiles < cnt; ++c) ph.emit_chunks.push_back(EmitChunk{uint32_t(k), uint32_t(c)});
+  }
   if (!row_groups) return;
   struct Side {
     int64_t slot;
@@ -983,9 +998,7 @@ size_t block_class(size_t bytes) {
 
 class TableCache {
  public:
-  // A block of at least `bytes`; for pinned host memory `dev_addr` (if not
-  // null) receives its device address, looked up once per allocation.
-  int get(bool pinned, int device, size_t bytes, void** out, size_t* cap, void** dev_addr = nullptr) {
+  int get(bool pinned, int device, size_t bytes, void** out, size_t* cap) {
     const size_t want = block_class(bytes);
     {
       std::lock_guard<std::mutex> lock(mu_);
@@ -994,28 +1007,14 @@ class TableCache {
         if (list[i].device == device && list[i].bytes == want) {
           *out = list[i].p;
           *cap = want;
-          if (dev_addr) *dev_addr = list[i].dev;
           (pinned ? host_bytes_ : dev_bytes_) -= want;
           list[i] = list.back();
           list.pop_back();
           return SR_OK;
         }
     }
-    if (pinned) {
-      SR_HIP_TRY(hipHostMalloc(out, want, hipHostMallocDefault));
-      void* dev = nullptr;
-      const hipError_t e = hipHostGetDevicePointer(&dev, *out, 0);
-      if (e != hipSuccess) {
-        (void)hipHostFree(*out);
-        *out = nullptr;
-        return fail(SR_EHIP, "hipHostGetDevicePointer failed: %s", hipGetErrorString(e));
-      }
-      if (dev_addr) *dev_addr = dev;
-      std::lock_guard<std::mutex> lock(mu_);
-      host_dev_[*out] = dev;
-    } else {
-      SR_HIP_TRY(hipMalloc(out, want));
-    }
+    if (pinned) SR_HIP_TRY(hipHostMalloc(out, want, hipHostMallocDefault));
+    else SR_HIP_TRY(hipMalloc(out, want));
     *cap = want;
     return SR_OK;
   }
@@ -1026,11 +1025,10 @@ class TableCache {
       std::lock_guard<std::mutex> lock(mu_);
       size_t& held = pinned ? host_bytes_ : dev_bytes_;
       if (held + cap <= (pinned ? kCacheHostBytes : kCacheDeviceBytes)) {
-        (pinned ? host_ : dev_).push_back(Block{p, cap, device, pinned ? host_dev_[p] : nullptr});
+        (pinned ? host_ : dev_).push_back(Block{p, cap, device});
         held += cap;
         return;
       }
-      if (pinned) host_dev_.erase(p);
     }
     if (pinned) (void)hipHostFree(p);
     else (void)hipFree(p);
@@ -1086,10 +1084,8 @@ class TableCache {
     void* p;
     size_t bytes;
     int device;
-    void* dev;   // pinned blocks: device address
   };
   std::mutex mu_;
-  std::unordered_map<void*, void*> host_dev_;   // pinned block -> device address
   std::vector<Block> dev_, host_;
   std::vector<std::pair<int, hipEvent_t>> events_;
   std::vector<std::pair<int, hipStream_t>> streams_;
@@ -1164,11 +1160,9 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
 }
 
 // First use of a phase: its descriptors, tile prefix and pointer table go
-// into a pinned host buffer that the kernels read in place (no copy to the
-// device: the CPU writes it before the launch that reads it, and pinned host
-// memory is coherent at launch boundaries); one kernel then builds the tile
-// table and binds the items to `ptrs`, stream-ordered on `stream` (ev_setup
-// marks completion).
+// up in one copy from pinned memory, then one kernel builds the tile table
+// and binds the items to `ptrs`, stream-ordered on `stream` (ev_setup marks
+// completion).
 int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, const std::vector<uint64_t>& ptrs,
                 hipStream_t stream) {
   if (ph.ready) return SR_OK;
@@ -1179,38 +1173,42 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, const std::vector<uin
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
-    size_t h_end = 0;   // pinned: descriptors, tile prefix, pointer table
-    const size_t o_rel = carve(h_end, n * sizeof(DevRel));
-    const size_t o_base = carve(h_end, (size_t(n) + 1) * sizeof(uint64_t));
-    const size_t o_ptr = carve(h_end, nptr * sizeof(uint64_t));
-    size_t d_end = 0;   // device: item and tile tables
-    const size_t o_items = carve(d_end, n * sizeof(DevItem));
-    const size_t o_tiles = carve(d_end, ph.n_tiles * sizeof(DevTile));
+    size_t end = 0;   // the first three are uploaded (pinned staging, same layout)
+    const size_t o_rel = carve(end, n * sizeof(DevRel));
+    const size_t o_base = carve(end, (size_t(n) + 1) * sizeof(uint64_t));
+    const size_t o_chunk = carve(end, ph.emit_chunks.size() * sizeof(EmitChunk));
+    const size_t o_ptr = carve(end, nptr * sizeof(uint64_t));
+    const size_t up_end = o_ptr + nptr * sizeof(uint64_t);
+    const size_t o_items = carve(end, n * sizeof(DevItem));
+    const size_t o_tiles = carve(end, ph.n_tiles * sizeof(DevTile));
     // allocations survive a failed attempt and are reused by the retry
-    if (!ph.d_mem && (rc = cache.get(false, p->device, d_end, &ph.d_mem, &ph.d_cap)) != SR_OK) return rc;
-    if (!ph.h_staging && (rc = cache.get(true, p->device, h_end, reinterpret_cast<void**>(&ph.h_staging),
-                                         &ph.h_cap, &ph.h_dev)) != SR_OK)
+    if (!ph.d_mem && (rc = cache.get(false, p->device, end, &ph.d_mem, &ph.d_cap)) != SR_OK) return rc;
+    if (!ph.h_staging &&
+        (rc = cache.get(true, p->device, up_end, reinterpret_cast<void**>(&ph.h_staging), &ph.h_cap)) != SR_OK)
       return rc;
-    unsigned char* h = static_cast<unsigned char*>(ph.h_dev);   // the staging buffer's device address
     unsigned char* d = static_cast<unsigned char*>(ph.d_mem);
-    ph.d_rel = reinterpret_cast<DevRel*>(h + o_rel);
-    ph.d_tile_base = reinterpret_cast<uint64_t*>(h + o_base);
-    ph.d_ptrs = reinterpret_cast<uint64_t*>(h + o_ptr);
+    ph.d_rel = reinterpret_cast<DevRel*>(d + o_rel);
+    ph.d_tile_base = reinterpret_cast<uint64_t*>(d + o_base);
+    ph.d_ptrs = reinterpret_cast<uint64_t*>(d + o_ptr);
     ph.d_items = reinterpret_cast<DevItem*>(d + o_items);
     ph.d_tiles = reinterpret_cast<DevTile*>(d + o_tiles);
     ph.h_ptrs = reinterpret_cast<uint64_t*>(ph.h_staging + o_ptr);
     std::memcpy(ph.h_staging + o_rel, ph.rel.data(), n * sizeof(DevRel));
     std::memcpy(ph.h_staging + o_base, ph.tile_base.data(), (size_t(n) + 1) * sizeof(uint64_t));
+    std::memcpy(ph.h_staging + o_chunk, ph.emit_chunks.data(), ph.emit_chunks.size() * sizeof(EmitChunk));
     std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
+    SR_HIP_TRY(hipMemcpyAsync(ph.d_mem, ph.h_staging, up_end, hipMemcpyHostToDevice, stream));
     if (needs_offsets) {
       rc = setup_offsets(p, stream);
       if (rc != SR_OK) return rc;
       SR_HIP_TRY(hipStreamWaitEvent(stream, p->ev_offsets, 0));
     }
     const uint32_t shift = log2u(p->opt.tile_bytes);
-    hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0,
-                       stream, ph.d_rel, ph.d_tile_base, n, shift, ph.n_tiles,
-                       ph.interleave ? kXcds : 1u, ph.d_tiles, ph.d_ptrs, p->d_offset, ph.d_items);
+    const uint32_t n_chunks = uint32_t(ph.emit_chunks.size());
+    hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n_chunks, 65535u)), dim3(kSetupBlock), 0,
+                       stream, ph.d_rel, ph.d_tile_base, reinterpret_cast<const EmitChunk*>(d + o_chunk), n_chunks,
+                       shift, ph.n_tiles, ph.interleave ? kXcds : 1u, ph.d_tiles, ph.d_ptrs, p->d_offset,
+                       ph.d_items);
     SR_HIP_TRY(hipGetLastError());
   }
   SR_HIP_TRY(hipEventRecord(ph.ev_setup, stream));
@@ -1267,25 +1265,33 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
   if (rc != SR_OK) return rc;
   const uint32_t n = uint32_t(ph.rel.size());
   if (!ph.ready) {
-    // A phase's first use builds its tables and binds the pointers on the
-    // device's setup stream: they are the library's own memory and read no
-    // caller data, so they may run while earlier work on `stream` (such as
-    // the previous launch group's copy) is still going.
-    hipStream_t setup = nullptr;
-    if ((rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
+    // A phase's first use builds its tables and binds the pointers.  They
+    // are the library's own memory and read no caller data: while earlier
+    // work on `stream` (such as the previous launch group's copy) is still
+    // going, they run beside it on the device's setup stream; on an idle
+    // `stream` they run on it directly, since a wait across streams costs
+    // the host more than the setup kernel takes on the GPU.
+    const hipError_t busy = hipStreamQuery(stream);
+    (void)hipGetLastError();   // "not ready" is an answer, not an error
+    if (busy != hipSuccess && busy != hipErrorNotReady)
+      return fail(SR_EHIP, "hipStreamQuery failed: %s", hipGetErrorString(busy));
+    hipStream_t setup = stream;
+    if (busy == hipErrorNotReady && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
     rc = setup_phase(p, ph, kind != kGather, ptrs, setup);
     if (rc != SR_OK) return rc;
-    SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
+    if (setup != stream) SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
   } else if (rebind) {
-    // Later rebinds run on `stream`, after the latest bind (which reads the
-    // pointer table in the staging buffer: the host rewrites it only once
-    // that bind is done) and after the phase's previous launch (which may
-    // still read the item table).
+    // Later rebinds run on `stream`, after the latest bind (whose copy out
+    // of the staging buffer must be done before the host rewrites it) and
+    // after the phase's previous launch (which may still read the item and
+    // pointer tables).
     if (!ph.ev_staging && (rc = table_cache().get_event(p->device, &ph.ev_staging)) != SR_OK) return rc;
     SR_HIP_TRY(hipEventSynchronize(ph.ev_bound));
     std::memcpy(ph.h_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t));
     SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_bound, 0));
     SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_kernel, 0));
+    SR_HIP_TRY(hipMemcpyAsync(ph.d_ptrs, ph.h_ptrs, ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice,
+                              stream));
     hipLaunchKernelGGL(sr_bind_kernel, dim3((n + kSetupBlock - 1) / kSetupBlock), dim3(kSetupBlock), 0,
                        stream, ph.d_rel, n, ph.d_ptrs, p->d_offset, ph.d_items);
     SR_HIP_TRY(hipGetLastError());
@@ -1401,7 +1407,7 @@ int scratch_base(int device, unsigned char** out) {
 
 // Where the gather phase's tables sit in the scratch, and how much it needs.
 struct ScratchLayout {
-  size_t rel, ptrs, items, base, tiles, end;
+  size_t rel, ptrs, items, base, chunks, tiles, end;
 };
 
 ScratchLayout scratch_layout(const Phase& ph) {
@@ -1411,6 +1417,7 @@ ScratchLayout scratch_layout(const Phase& ph) {
   size_t end = 0;
   L.rel = carve(end, n * sizeof(DevRel));
   L.base = carve(end, (n + 1) * sizeof(uint64_t));
+  L.chunks = carve(end, ph.emit_chunks.size() * sizeof(EmitChunk));
   L.ptrs = carve(end, nptr * sizeof(uint64_t));
   L.items = carve(end, n * sizeof(DevItem));
   L.tiles = carve(end, size_t(ph.n_tiles) * sizeof(DevTile));
@@ -1882,13 +1889,17 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
   SR_HIP_TRY(hipMemcpyAsync(d_rel, ph.rel.data(), n * sizeof(DevRel), hipMemcpyHostToDevice, stream));
   SR_HIP_TRY(hipMemcpyAsync(d_base, ph.tile_base.data(), (size_t(n) + 1) * sizeof(uint64_t),
                             hipMemcpyHostToDevice, stream));
+  EmitChunk* d_chunks = reinterpret_cast<EmitChunk*>(s + L.chunks);
+  const uint32_t n_chunks = uint32_t(ph.emit_chunks.size());
+  SR_HIP_TRY(hipMemcpyAsync(d_chunks, ph.emit_chunks.data(), n_chunks * sizeof(EmitChunk), hipMemcpyHostToDevice,
+                            stream));
   SR_HIP_TRY(hipMemcpyAsync(d_ptrs, ptrs.data(), ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice,
                             stream));
   const uint32_t shift = log2u(plan->opt.tile_bytes);
   // gather items read no buffer offsets (no side is a peer buffer)
-  hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n, 65535u)), dim3(kSetupBlock), 0, stream,
-                     d_rel, d_base, n, shift, ph.n_tiles, ph.interleave ? kXcds : 1u, d_tiles, d_ptrs,
-                     static_cast<const uint64_t*>(nullptr), d_items);
+  hipLaunchKernelGGL(sr_tile_emit_kernel, dim3(std::min<uint32_t>(n_chunks, 65535u)), dim3(kSetupBlock), 0,
+                     stream, d_rel, d_base, d_chunks, n_chunks, shift, ph.n_tiles, ph.interleave ? kXcds : 1u,
+                     d_tiles, d_ptrs, static_cast<const uint64_t*>(nullptr), d_items);
   SR_HIP_TRY(hipGetLastError());
 
   const uint32_t n_tiles = uint32_t(ph.n_tiles);

@@ -25,6 +25,7 @@ intended ``cat`` in ascending piece order.
 from __future__ import annotations
 
 import gc
+import time
 from dataclasses import replace
 from typing import Any, Callable, Dict, List, Mapping, Optional, Tuple, Union
 
@@ -182,6 +183,17 @@ def execute_param_transfer(
             # Each group is planned on the host while the GPU runs the
             # previous group's launch.
             for group in groups:
+                if route == "direct" and arena_views is None:
+                    # plan (shapes, dtypes and addresses read from the source
+                    # tensors, each checked once), fresh destinations and the
+                    # gather into them: one native call
+                    prof.start("execute gather")
+                    plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
+                                                            options=plan_options, rank=rank, stream=stream)
+                    prof.stop("execute gather")
+                    plans.append(plan)
+                    target.update(part)
+                    continue
                 prof.start("execute schedule lowering")
                 # shapes, dtypes and addresses read from the source tensors (each
                 # checked once: contiguous, on this device)
@@ -317,12 +329,14 @@ def _arena_views(ops: List[TransferOp], source: Callable[[int], StateDict], fiel
     return _lib.host().arena_tensors(ops, source, order, targets, device)
 
 
-def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int,
-                     tensors_per_name: int = 1) -> List[List[TransferOp]]:
-    """Cut the ops into at most ``pipeline`` launch groups of whole tensors
-    (all ops of a name stay together, so each group's plan covers its
-    destinations completely), each planned on the host while the GPU runs
-    the previous one.
+_clock_ns = time.perf_counter_ns   # the launch groups' planning timer
+
+
+class _LaunchGroups:
+    """The launch groups of one rank's ops, cut as the call goes: whole
+    tensors per group (all ops of a name stay together, so each group's plan
+    covers its destinations completely), each group planned on the host
+    while the GPU runs the previous one.
 
     A two-stage pipeline (host planning, then GPU copy) finishes soonest
     when the jobs heavy on the second stage go first (Johnson's rule): the
@@ -330,19 +344,91 @@ def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int,
     planned in little time, and the small tensors, cheap to copy but as
     costly to plan as large ones, come last.  The first group carries
     FIRST_GROUP_NS of GPU work; each next group holds as many tensors as the
-    host can plan in PLAN_SHARE of the previous group's GPU time (the cost
-    model above); the rest forms the last group once a next group would
-    hold fewer than MIN_GROUP_TENSORS tensors or less GPU time than its own
-    planning overhead (PLAN_NS_PER_GROUP), or at the ``pipeline``-th group.
-    Within a group the tensors keep their schedule order.
+    host can plan in PLAN_SHARE of the previous group's GPU time, at the
+    host's planning rate measured on the groups so far (PLAN_NS_PER_TENSOR
+    until a group of at least MIN_GROUP_TENSORS names was timed); the rest
+    forms the last group once a next group would hold fewer than
+    MIN_GROUP_TENSORS names or less GPU time than its own planning overhead
+    (PLAN_NS_PER_GROUP), or at the ``pipeline``-th group.  Within a group
+    the ops keep their schedule order.
 
-    ``elem_bytes`` is the bytes per element over all moved fields,
-    ``tensors_per_name`` the destination tensors per name (fields and
-    recast copies)."""
-    ops = list(ops)
-    return _lib.host().launch_groups(ops, 2.0 * elem_bytes / GATHER_BYTES_PER_NS, int(pipeline), FIRST_GROUP_NS,
-                                     PLAN_SHARE, PLAN_NS_PER_GROUP, PLAN_NS_PER_TENSOR * max(1, tensors_per_name),
-                                     MIN_GROUP_TENSORS)
+    Iterating yields the groups; the time between two requests is taken as
+    the planning time of the group handed out first.  ``elem_bytes`` is the
+    bytes per element over all moved fields, ``tensors_per_name`` the
+    destination tensors per name (fields and recast copies)."""
+
+    def __init__(self, ops: List[TransferOp], elem_bytes: int, pipeline: int, tensors_per_name: int = 1):
+        self.ops = list(ops)
+        self.pipeline = int(pipeline)
+        self.per_name = max(1, int(tensors_per_name))
+        # op indices tensor by tensor, tensors in order of first appearance
+        self.order, self.starts, numel, self.single = _lib.host().name_runs(self.ops)
+        self.n = len(numel)
+        gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
+        self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
+        self.cum = np.cumsum(gpu_ns[self.rank])
+        self.plan_ns = float(PLAN_NS_PER_TENSOR)                 # per destination tensor
+
+    def _gpu(self, a: int, b: int) -> float:
+        return float(self.cum[b - 1] - (self.cum[a - 1] if a else 0.0))
+
+    def _take(self, a: int, b: int) -> List[TransferOp]:
+        if a == 0 and b == self.n:
+            return self.ops
+        mask = np.zeros(self.n, dtype=bool)
+        mask[self.rank[a:b]] = True
+        idx = self.order[np.repeat(mask, np.diff(self.starts))]
+        ops = self.ops
+        return [ops[i] for i in idx.tolist()]
+
+    def _next_end(self, start: int, end: int, groups: int) -> int:
+        """End of the group after [start, end), the group number `groups`."""
+        if groups >= self.pipeline:
+            return self.n
+        per_tensor = self.plan_ns * self.per_name
+        fits = (self._gpu(start, end) * PLAN_SHARE - PLAN_NS_PER_GROUP) / per_tensor
+        if fits < MIN_GROUP_TENSORS:
+            return self.n
+        nxt = min(self.n, end + int(fits))
+        # a group that is not the last pays its planning overhead back only
+        # if the GPU runs it at least that long (while the host plans on)
+        if nxt < self.n and self._gpu(end, nxt) < PLAN_NS_PER_GROUP:
+            return self.n
+        return nxt
+
+    def __iter__(self):
+        if self.pipeline <= 1 or self.n <= 1:
+            yield self.ops
+            return
+        end = min(self.n, int(np.searchsorted(self.cum, FIRST_GROUP_NS, side="left")) + 1)
+        start, groups = 0, 1
+        while True:
+            t0 = _clock_ns()
+            yield self._take(start, end)
+            spent = _clock_ns() - t0
+            if end >= self.n:
+                return
+            names = end - start
+            if names >= MIN_GROUP_TENSORS:
+                self.plan_ns = max(0.0, spent - PLAN_NS_PER_GROUP) / (names * self.per_name)
+            start, end = end, self._next_end(start, end, groups + 1)
+            groups += 1
+
+    def cut(self) -> List[List[TransferOp]]:
+        """All groups at once, at the prior planning rate (no timing)."""
+        if self.pipeline <= 1 or self.n <= 1:
+            return [self.ops]
+        bounds = [0, min(self.n, int(np.searchsorted(self.cum, FIRST_GROUP_NS, side="left")) + 1)]
+        while bounds[-1] < self.n:
+            bounds.append(self._next_end(bounds[-2], bounds[-1], len(bounds)))
+        return [self._take(a, b) for a, b in zip(bounds[:-1], bounds[1:])]
+
+
+def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int,
+                     tensors_per_name: int = 1):
+    """The launch groups of ``ops`` (an iterable of op lists, see
+    ``_LaunchGroups``)."""
+    return _LaunchGroups(ops, elem_bytes, pipeline, tensors_per_name)
 
 
 def schedule_and_execute_param_transfer(

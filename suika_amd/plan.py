@@ -146,6 +146,27 @@ class ReshardPlan:
         Each tensor is read once: it must be a contiguous CUDA tensor on
         ``device``.  ``rank`` (the executing rank) only prefixes messages.
         """
+        plan, src_ptrs, _ = cls._native(ops, source, fields, device, recast, options, rank)
+        return plan, src_ptrs
+
+    @classmethod
+    def gather_sources(cls, ops: Sequence[TransferOp], source: Callable[[int], Mapping],
+                       fields: Sequence[str], device: torch.device,
+                       recast: Optional[Mapping[str, str]] = None,
+                       options: Optional[PlanOptions] = None,
+                       rank: Optional[int] = None,
+                       stream=None) -> Tuple["ReshardPlan", Dict[str, Dict[str, torch.Tensor]]]:
+        """``from_sources``, fresh destination tensors (as ``alloc_dst``) and
+        the gather into them on ``stream`` (default: the current stream), in
+        one native call: the drop-in call's direct route.  Returns the plan
+        (its kernels possibly still running: ``close`` waits for them) and
+        the destinations ``{name: {field: tensor}}``."""
+        plan, _, part = cls._native(ops, source, fields, device, recast, options, rank, gather=True,
+                                    stream=_stream_handle(stream).value or 0)
+        return plan, part
+
+    @classmethod
+    def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0):
         self = cls.__new__(cls)
         self._configure(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
@@ -153,18 +174,18 @@ class ReshardPlan:
         opt = self.options.to_c()
         self._L = _lib.lib()
         # grouping, shards, tables, source checks, sr_lower and sr_plan_create
-        # in one native call
+        # (and with `gather` the destinations and the launch) in one native call
         (handle, self._names, self.dst_metas, self._op_names, self.dst_rank, self._dtypes, src_ptrs,
          self._src_arr, self._dst_arr, self._piece_arr, self.peers, self._src_rows, self._dst_rows,
-         self._empty_rows, self.peer_bytes, info) = _lib.host().plan_sources(
-            self._ops, source, self.fields, [1 if f in self._recast_of else 0 for f in self.fields],
+         self._empty_rows, self.peer_bytes, info, part) = _lib.host().plan_sources(
+            self._ops, source, self.fields, [self._recast_of.get(f) for f in self.fields],
             infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
-            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE)
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream)
         self._handle = ctypes.c_void_p(handle)
         self.info = _lib.SrPlanInfo.from_buffer_copy(info)
         self.n_pieces = len(self._piece_arr)
         self._views = self._pieces_view = self._c_src_view = self._c_dst_view = None
-        return self, src_ptrs
+        return self, src_ptrs, part
 
     def _configure(self, ops, fields, recast, options) -> None:
         """Fields, recast map and options, validated."""

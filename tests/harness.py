@@ -174,6 +174,7 @@ def poisoned_allocations():
     from suika_amd.plan import ReshardPlan
     alloc_dst, alloc_dst_ptrs = ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs
     alloc_buffers, arena_views = ReshardPlan.alloc_buffers, migration._arena_views
+    gather_sources = ReshardPlan.__dict__["gather_sources"]
 
     poisoned = {"tensors": 0}
 
@@ -200,18 +201,31 @@ def poisoned_allocations():
     def arena(*a, **kw):
         return poison(arena_views(*a, **kw))
 
+    def gather(cls, ops, source, fields, device, recast=None, options=None, rank=None, stream=None):
+        # the one-call direct route, composed of its parts so that the
+        # destinations can be poisoned between allocation and launch
+        plan, src_ptrs = cls.from_sources(ops, source, fields, device, recast=recast, options=options, rank=rank)
+        part, ptrs = plan.alloc_dst_ptrs(device)
+        poison(part)
+        plan.gather_ptrs(src_ptrs, ptrs, stream)
+        return plan, part
+
     ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = dst, dst_ptrs
     ReshardPlan.alloc_buffers, migration._arena_views = buffers, arena
+    ReshardPlan.gather_sources = classmethod(gather)
     try:
         yield poisoned
     finally:
         ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = alloc_dst, alloc_dst_ptrs
         ReshardPlan.alloc_buffers, migration._arena_views = alloc_buffers, arena_views
+        ReshardPlan.gather_sources = gather_sources
 
 
 def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers", arena=False):
     """Product path: execute_param_transfer on the GPU with peer shards
-    resident; destinations and buffers start as POISON bytes."""
+    resident; destinations and buffers start as POISON bytes (the direct
+    route's one native call is taken apart for it: the fused call itself is
+    checked by dirty_cache_execute)."""
     from suika_amd import execute_param_transfer
     ops = w.ops()
     fake = to_device(srcs_np, w, device)
@@ -327,3 +341,31 @@ def round_robin_groups(k: int):
             out[g].append(op)
         return [g for g in out if g]
     return groups
+
+
+def dirty_allocator_cache(device="cuda", total=256 << 20):
+    """Leave torch's caching allocator holding freed blocks full of POISON
+    bytes (large ones, and small ones for tensors under 1 MiB), so that
+    destinations it hands out next hold POISON rather than zeros unless the
+    kernels write them.  A best effort: the allocator decides which blocks
+    it reuses."""
+    torch.cuda.empty_cache()
+    held = [torch.full((total,), POISON, dtype=torch.uint8, device=device)]
+    held += [torch.full((s,), POISON, dtype=torch.uint8, device=device) for s in (512 << 10,) * 16]
+    held += [torch.full((s,), POISON, dtype=torch.uint8, device=device) for s in (4096,) * 64]
+    torch.cuda.synchronize()
+    del held
+
+
+def dirty_cache_execute(w: Workload, srcs_np, device="cuda", plan_options=None):
+    """The drop-in call's default path (route "direct", fresh destinations:
+    one native call per launch group) on the GPU, after dirtying the
+    allocator cache."""
+    from suika_amd import execute_param_transfer
+    fake = to_device(srcs_np, w, device)
+    dirty_allocator_cache(device)
+    out = execute_param_transfer(w.ops(), {}, torch.device(device), [(f, "normal") for f in w.src_fields],
+                                 rank=w.dst_rank, fake_source_state_dicts=fake, recast=w.recast_map,
+                                 plan_options=plan_options)
+    torch.cuda.synchronize()
+    return {n: {f: t2np(t) for f, t in e.items()} for n, e in out.items()}

@@ -66,6 +66,31 @@ def test_gpu_pipelined_launch_groups_match_oracle(w, route, monkeypatch):
     assert list(got) == list(dict.fromkeys(op.param_name for op in w.ops()))
 
 
+@pytest.mark.parametrize("groups", [1, 4])
+@pytest.mark.parametrize("w", SMALL, ids=[w.key for w in SMALL])
+def test_gpu_one_call_direct_route_matches_oracle(w, groups, monkeypatch):
+    """The drop-in call's default path -- per launch group one native call
+    that plans, allocates the destinations and launches the gather -- run
+    as is (no poisoning between allocation and launch, so the allocator's
+    cache is left full of POISON bytes first), in one and in four launch
+    groups, bit-exact against the oracle and listing the tensors in
+    schedule order."""
+    from suika_amd import migration
+    from tests.harness import dirty_cache_execute, round_robin_groups
+    print(f"[gpu parity] one-call {w.key} groups={groups}", flush=True)
+    if groups > 1:
+        monkeypatch.setattr(migration, "_pipeline_groups", round_robin_groups(groups))
+    glob = index_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    got = dirty_cache_execute(w, srcs)
+    assert list(got) == list(dict.fromkeys(op.param_name for op in w.ops()))
+    for name in want:
+        assert set(got[name]) == set(want[name]), name
+        for f in want[name]:
+            np.testing.assert_array_equal(got[name][f], want[name][f], err_msg=f"{w.key}: {name}/{f}")
+
+
 SWEEP = cases.alignment_cases() + list(cases.scaled_configs().values())
 
 

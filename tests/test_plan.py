@@ -320,7 +320,7 @@ def test_pipeline_groups_keep_tensors_whole():
         tpn = len(w.src_fields) + len(w.recast_map)
         position = {id(op): i for i, op in enumerate(ops)}
         for pipeline in (1, 2, 3, 4, 8, 100):
-            groups = migration._pipeline_groups(ops, elem, pipeline, tpn)
+            groups = migration._pipeline_groups(ops, elem, pipeline, tpn).cut()
             assert sorted(position[id(op)] for g in groups for op in g) == list(range(len(ops)))
             assert 1 <= len(groups) <= pipeline
             seen = set()
@@ -340,7 +340,7 @@ def test_pipeline_groups_keep_tensors_whole():
     w = CONFIGS["llama7b_tp4pp2_tp2pp2"]
     ops = list(w.ops())
     ops = ops[1:] + ops[:1]                  # the first tensor's first op moves to the end
-    groups = migration._pipeline_groups(ops, 14, 8, 5)
+    groups = migration._pipeline_groups(ops, 14, 8, 5).cut()
     owner = {}
     for gi, g in enumerate(groups):
         for op in g:
@@ -360,7 +360,7 @@ def test_pipeline_groups_follow_the_cost_model():
         ops = w.ops()
         elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
         tpn = len(w.src_fields) + len(w.recast_map)
-        groups = M._pipeline_groups(ops, elem, 8, tpn)
+        groups = M._pipeline_groups(ops, elem, 8, tpn).cut()
         costs = _group_costs(w, groups, elem, tpn)
         sizes = []
         for g in groups:
@@ -380,12 +380,43 @@ def test_pipeline_groups_follow_the_cost_model():
             assert costs[j][1] >= M.PLAN_NS_PER_GROUP, (key, j)
     # the benchmark shares pipeline in 3 or 4 groups; a single tensor or
     # pipeline=1 runs as one
-    shapes = {key: len(M._pipeline_groups(CONFIGS[key].ops(), 14, 8, 5)) for key in CONFIG_ORDER}
+    shapes = {key: len(M._pipeline_groups(CONFIGS[key].ops(), 14, 8, 5).cut()) for key in CONFIG_ORDER}
     assert all(2 <= k <= 8 for k in shapes.values()), shapes
     w = CONFIGS["gpt125m_tp2_tp4"]
     one = [op for op in w.ops() if op.param_name == w.ops()[0].param_name]
-    assert M._pipeline_groups(one, 12, 8, 3) == [one]
-    assert M._pipeline_groups([], 12, 8, 3) == [[]]
+    assert M._pipeline_groups(one, 12, 8, 3).cut() == [one] == list(M._pipeline_groups(one, 12, 8, 3))
+    assert M._pipeline_groups([], 12, 8, 3).cut() == [[]]
+
+
+def test_launch_groups_adapt_to_the_measured_planning_rate(monkeypatch):
+    """Iterated, the launch groups are sized by the planning rate measured on
+    the groups so far: on a host four times slower than the prior, later
+    groups get smaller, and every group after a timed one is planned within
+    PLAN_SHARE of its predecessor's GPU time at that rate."""
+    from suika_amd import migration as M
+    clock = [0]
+    monkeypatch.setattr(M, "_clock_ns", lambda: clock[0])
+    w = CONFIGS["gpt6.7b_tp1pp4_tp8"]
+    ops = w.ops()
+    elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+    tpn = len(w.src_fields) + len(w.recast_map)
+    runs = {}
+    for rate in (M.PLAN_NS_PER_TENSOR, 4 * M.PLAN_NS_PER_TENSOR):
+        groups = []
+        for g in M._pipeline_groups(ops, elem, 8, tpn):
+            groups.append(g)
+            names = len({op.param_name for op in g})
+            clock[0] += M.PLAN_NS_PER_GROUP + rate * tpn * names     # the simulated planning time
+        assert sorted(map(id, (op for g in groups for op in g))) == sorted(map(id, ops))
+        costs = _group_costs(w, groups, elem, tpn)
+        sizes = [len({op.param_name for op in g}) for g in groups]
+        for j in range(2, len(groups) - 1):
+            plan = M.PLAN_NS_PER_GROUP + rate * tpn * sizes[j]
+            assert plan <= costs[j - 1][1] * M.PLAN_SHARE + 1e-6, (rate, j)
+        runs[rate] = sizes
+    fast, slow = runs[M.PLAN_NS_PER_TENSOR], runs[4 * M.PLAN_NS_PER_TENSOR]
+    assert fast[:2] == slow[:2]                  # sized before any group was timed
+    assert slow[2] < fast[2], (fast, slow)
 
 
 def test_ops_of_rank_and_tensor_runs():

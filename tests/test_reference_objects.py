@@ -104,10 +104,10 @@ def test_reference_ops_plan_like_own_ops(case, monkeypatch):
         plan_ref.close()
         plan_own.close()
     # launch grouping (the host extension's run and size helpers) reads them too
-    groups = _pipeline_groups(ref_ops, 14, 8, 5)
+    groups = _pipeline_groups(ref_ops, 14, 8, 5).cut()
     assert sorted(map(id, (op for g in groups for op in g))) == sorted(map(id, ref_ops))
     assert [[op.param_name for op in g] for g in groups] == \
-        [[op.param_name for op in g] for g in _pipeline_groups(own, 14, 8, 5)]
+        [[op.param_name for op in g] for g in _pipeline_groups(own, 14, 8, 5).cut()]
     numels = _lib.host().piece_numels(ref_ops).tolist()
     assert numels == _lib.host().piece_numels(own).tolist()
 
