@@ -65,6 +65,9 @@ def parse_args(argv=None):
     ap.add_argument("--row-sweep", type=int, default=0, metavar="BYTES",
                     help="strided dim -1 pieces (cat / split) of several row widths against a flat "
                          "copy, BYTES read and written per case, then exit")
+    ap.add_argument("--api-phases", action="store_true",
+                    help="host-time breakdown of the drop-in execute_param_transfer call for --config "
+                         "(--steps calls, each followed by a gather of the whole share for comparison)")
     ap.add_argument("--handoff", action="store_true",
                     help="only run the live migration of the workload between old and new processes on "
                          "this GPU (migration_save / migration_load) and print its timings, then exit")
@@ -314,6 +317,117 @@ def api_latency(w, sources, dev, repeats: int = 3, check=None) -> dict:
             "runs": repeats,
             "includes": "region lowering, sr_plan_create, destination allocation (warm caching "
                         "allocator), device-side tile/offset/item tables, gather launch, synchronize"}
+
+
+class _PhaseTimer:
+    """A ``prof`` object as execute_param_transfer takes it (start / stop by
+    region name, like the reference's profiler): host seconds per region."""
+
+    def __init__(self):
+        self.total, self._open = {}, {}
+
+    def start(self, name, **_):
+        self._open[name] = time.perf_counter()
+
+    def stop(self, name, **_):
+        self.total[name] = self.total.get(name, 0.0) + time.perf_counter() - self._open.pop(name)
+
+
+def api_phases(w, sources, dev, calls: int) -> dict:
+    """Host-time breakdown of the drop-in call (route "direct", fresh
+    destinations) on this GPU's share, sources resident.  Each of ``calls``
+    timed calls (after 3 untimed) is followed by one gather of the whole
+    share as a single plan (HIP events), so call and copy time come from the
+    same moments of the box.  Regions: the executor's own prof regions
+    (prologue: the rank's ops and the launch groups; gather: per group, the
+    native call that plans, allocates the destinations and launches; post
+    process: the result dict; wait: the kernels still running).  The parts
+    of a group's native call are timed on the same groups by calling them
+    one by one (plan; destination tensors; launch)."""
+    import statistics
+
+    import torch
+    from suika_amd import execute_param_transfer, schedule_param_transfer
+    from suika_amd.migration import _pipeline_groups
+    from suika_amd.plan import PlanOptions, ReshardPlan
+
+    ops = schedule_param_transfer(*w.layouts())
+    mine = [op for op in ops if op.dst_rank == w.dst_rank]
+    fields = [(f, "normal") for f in w.src_fields]
+    normal = list(w.src_fields)
+    stream = torch.cuda.current_stream()
+    whole, wsp = ReshardPlan.from_sources(mine, lambda r: sources[r], normal, dev, recast=w.recast_map,
+                                          options=PlanOptions(gather_only=True))
+    wdst, wdp = whole.alloc_dst_ptrs(dev)
+
+    def one_call(prof=None):
+        fake = {r: {n: dict(e) for n, e in sd.items()} for r, sd in sources.items()}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = execute_param_transfer(ops, {}, dev, fields, rank=w.dst_rank, fake_source_state_dicts=fake,
+                                     recast=w.recast_map, prof=prof)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        del out, fake
+        return dt
+
+    def one_gather():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        whole.gather_ptrs(wsp, wdp, stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3
+
+    for _ in range(3):
+        one_call()
+        one_gather()
+    call_s, gather_s, regions = [], [], {}
+    for _ in range(calls):
+        timer = _PhaseTimer()
+        call_s.append(one_call(timer))
+        gather_s.append(one_gather())
+        for k, v in timer.total.items():
+            regions.setdefault(k, []).append(v)
+    # the parts of the native per-group call, one by one on the same groups
+    elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+    groups = _pipeline_groups(mine, elem, 8, len(normal) + len(w.recast_map)).cut()
+    opts = PlanOptions(gather_only=True)
+    parts = {"plan": [], "destinations": [], "launch": []}
+    for _ in range(calls):
+        t = {k: 0.0 for k in parts}
+        plans = []
+        for g in groups:
+            t0 = time.perf_counter()
+            plan, sp = ReshardPlan.from_sources(g, lambda r: sources[r], normal, dev, recast=w.recast_map,
+                                                options=opts)
+            t1 = time.perf_counter()
+            dst, dp = plan.alloc_dst_ptrs(dev)
+            t2 = time.perf_counter()
+            plan.gather_ptrs(sp, dp, stream)
+            t3 = time.perf_counter()
+            t["plan"] += t1 - t0
+            t["destinations"] += t2 - t1
+            t["launch"] += t3 - t2
+            plans.append((plan, dst))
+        torch.cuda.synchronize()
+        for plan, _ in plans:
+            plan.close()
+        del plans
+        for k in parts:
+            parts[k].append(t[k])
+    whole.close()
+    del wdst
+
+    def ms(v):
+        return round(statistics.median(v) * 1e3, 3)
+
+    call, gather = ms(call_s), ms(gather_s)
+    return {"config": w.key, "calls": calls, "launch_groups": len(groups),
+            "names": len({op.param_name for op in mine}), "ops": len(mine),
+            "call_ms": call, "gather_ms": gather, "over_gather": round(call / gather - 1.0, 4),
+            "regions_ms": {k: ms(v) for k, v in regions.items()},
+            "group_parts_ms": {k: ms(v) for k, v in parts.items()}}
 
 
 def host_sources_leg(plan, sources, sp, dp, stream, repeats: int = 3) -> dict:
@@ -630,6 +744,12 @@ def main(argv=None) -> int:
     w = CONFIGS[key]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.api_phases:
+        ranks = sorted({op.src_rank for op in w.ops()})
+        print(f"[bench] api phases {key}: generating sources", file=sys.stderr, flush=True)
+        rec = api_phases(w, make_source_state(w, ranks, dev), dev, args.steps)
+        print(json.dumps({"api_phases": rec}), flush=True)
+        return 0
     print(f"[bench] workload {key}: planning", file=sys.stderr, flush=True)
     ops = w.ops()
     dt = w.dtypes

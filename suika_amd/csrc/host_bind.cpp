@@ -639,31 +639,33 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
 // Elements of every op's piece (op.dst_meta): a row interval times the
 // other dims, else the global size over the tp degree (TensorMeta.numel of
 // a chunk piece).  Used to balance launch groups.
-py::array_t<int64_t> piece_numels(py::list ops) {
+int64_t piece_numel(PyObject* op) {
   const Names& N = names_();
+  py::object m = attr(op, N.dst_meta);
+  py::object shape = attr(m.ptr(), N.shape), tp = tp_meta_of(m.ptr()), rows = rows_of(m.ptr());
+  if (!PyTuple_Check(shape.ptr())) throw py::type_error("TensorMeta.shape must be a tuple");
+  const Py_ssize_t nd = PyTuple_GET_SIZE(shape.ptr());
+  int64_t v = 1;
+  if (rows.ptr() != Py_None) {
+    if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2) throw py::value_error("malformed rows");
+    v = as_int(PyTuple_GET_ITEM(rows.ptr(), 1)) - as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
+    for (Py_ssize_t d = 1; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
+  } else {
+    for (Py_ssize_t d = 0; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
+    if (tp.ptr() != Py_None) {
+      if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("malformed tp_meta");
+      const int64_t deg = as_int(PyTuple_GET_ITEM(tp.ptr(), 2));
+      if (deg > 0) v /= deg;
+    }
+  }
+  return v;
+}
+
+py::array_t<int64_t> piece_numels(py::list ops) {
   const int64_t n = int64_t(ops.size());
   py::array_t<int64_t> out({n});
   int64_t* o = out.mutable_data();
-  for (int64_t k = 0; k < n; ++k) {
-    py::object m = attr(PyList_GET_ITEM(ops.ptr(), k), N.dst_meta);
-    py::object shape = attr(m.ptr(), N.shape), tp = tp_meta_of(m.ptr()), rows = rows_of(m.ptr());
-    if (!PyTuple_Check(shape.ptr())) throw py::type_error("TensorMeta.shape must be a tuple");
-    const Py_ssize_t nd = PyTuple_GET_SIZE(shape.ptr());
-    int64_t v = 1;
-    if (rows.ptr() != Py_None) {
-      if (!PyTuple_Check(rows.ptr()) || PyTuple_GET_SIZE(rows.ptr()) != 2) throw py::value_error("malformed rows");
-      v = as_int(PyTuple_GET_ITEM(rows.ptr(), 1)) - as_int(PyTuple_GET_ITEM(rows.ptr(), 0));
-      for (Py_ssize_t d = 1; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
-    } else {
-      for (Py_ssize_t d = 0; d < nd; ++d) v *= as_int(PyTuple_GET_ITEM(shape.ptr(), d));
-      if (tp.ptr() != Py_None) {
-        if (!PyTuple_Check(tp.ptr()) || PyTuple_GET_SIZE(tp.ptr()) != 3) throw py::value_error("malformed tp_meta");
-        const int64_t deg = as_int(PyTuple_GET_ITEM(tp.ptr(), 2));
-        if (deg > 0) v /= deg;
-      }
-    }
-    o[k] = v;
-  }
+  for (int64_t k = 0; k < n; ++k) o[k] = piece_numel(PyList_GET_ITEM(ops.ptr(), k));
   return out;
 }
 
@@ -716,45 +718,77 @@ py::tuple tensor_runs(py::list ops) {
 // indices tensor by tensor, where each tensor's indices start (one entry
 // per tensor plus the end), elements of each tensor's pieces, whether every
 // tensor's ops are already consecutive -- the order is then the identity).
+py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n);
+
 py::tuple name_runs(py::list ops) {
-  const Names& N = names_();
   py::array_t<int64_t> numel = piece_numels(ops);
   const int64_t* e = numel.data();
   const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
+  return runs_of(ops, e, n);
+}
+
+// The ops of `rank` out of a whole schedule (any sequence), and their
+// name_runs, in one pass over the schedule: (ops, order, starts, elements
+// per tensor, single).
+py::tuple rank_runs(py::object schedule, int64_t rank) {
+  const Names& N = names_();
+  py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(schedule.ptr(), "ops must be a sequence"));
+  if (!seq) throw py::error_already_set();
+  const Py_ssize_t total = PySequence_Fast_GET_SIZE(seq.ptr());
+  PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
+  py::list ops;
+  std::vector<int64_t> numel;
+  for (Py_ssize_t k = 0; k < total; ++k) {
+    if (as_int(attr(items[k], N.dst_rank).ptr()) != rank) continue;
+    if (PyList_Append(ops.ptr(), items[k]) != 0) throw py::error_already_set();
+    numel.push_back(piece_numel(items[k]));
+  }
+  py::tuple runs = runs_of(ops, numel.data(), Py_ssize_t(numel.size()));
+  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3]);
+}
+
+py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {
+  const Names& N = names_();
+  // tensor id of every op: consecutive ops of one name (the usual case)
+  // share the name object, so only a change of name consults the dict
   py::dict ids;
-  std::vector<std::vector<int64_t>> members;
-  std::vector<int64_t> sums;
+  std::vector<int64_t> nid(static_cast<size_t>(n)), sums;
   bool single = true;
-  size_t prev = SIZE_MAX;
+  PyObject* prev_name = nullptr;
+  int64_t prev = -1;
   for (Py_ssize_t k = 0; k < n; ++k) {
     py::object name = attr(PyList_GET_ITEM(ops.ptr(), k), N.param_name);
-    PyObject* id = PyDict_GetItemWithError(ids.ptr(), name.ptr());
-    size_t nid;
-    if (id) {
-      nid = size_t(as_int(id));
-      if (nid != prev) single = false;
+    int64_t id;
+    if (name.ptr() == prev_name) {
+      id = prev;
     } else {
-      if (PyErr_Occurred()) throw py::error_already_set();
-      nid = members.size();
-      py::int_ v(nid);
-      if (PyDict_SetItem(ids.ptr(), name.ptr(), v.ptr()) != 0) throw py::error_already_set();
-      members.emplace_back();
-      sums.push_back(0);
+      PyObject* found = PyDict_GetItemWithError(ids.ptr(), name.ptr());
+      if (found) {
+        id = as_int(found);
+        if (id != prev) single = false;
+      } else {
+        if (PyErr_Occurred()) throw py::error_already_set();
+        id = int64_t(sums.size());
+        py::object v = py::reinterpret_steal<py::object>(PyLong_FromLongLong(id));
+        if (!v || PyDict_SetItem(ids.ptr(), name.ptr(), v.ptr()) != 0) throw py::error_already_set();
+        sums.push_back(0);
+      }
+      prev_name = name.ptr();   // alive: `ids` holds a reference
     }
-    members[nid].push_back(k);
-    sums[nid] += e[k];
-    prev = nid;
+    nid[size_t(k)] = id;
+    sums[size_t(id)] += e[k];
+    prev = id;
   }
-  const int64_t m = int64_t(members.size());
+  // op indices tensor by tensor (a counting sort, stable)
+  const int64_t m = int64_t(sums.size());
   py::array_t<int64_t> order({int64_t(n)}), starts({m + 1}), total({m});
   int64_t* o = order.mutable_data();
   int64_t* st = starts.mutable_data();
-  int64_t at = 0;
-  for (int64_t i = 0; i < m; ++i) {
-    st[i] = at;
-    for (int64_t k : members[size_t(i)]) o[at++] = k;
-  }
-  st[m] = at;
+  std::fill(st, st + m + 1, 0);
+  for (Py_ssize_t k = 0; k < n; ++k) ++st[nid[size_t(k)] + 1];
+  for (int64_t i = 0; i < m; ++i) st[i + 1] += st[i];
+  std::vector<int64_t> fill(st, st + m);
+  for (Py_ssize_t k = 0; k < n; ++k) o[fill[size_t(nid[size_t(k)])]++] = k;
   std::copy(sums.begin(), sums.end(), total.mutable_data());
   return py::make_tuple(order, starts, total, single);
 }
@@ -1169,6 +1203,7 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("ops_of_rank", &ops_of_rank, py::arg("ops"), py::arg("rank"));
   m.def("tensor_runs", &tensor_runs, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
+  m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"));
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),

@@ -139,7 +139,11 @@ def execute_param_transfer(
     if rank is None:
         rank = _current_rank(world)
 
-    ops = _lib.host().ops_of_rank(list(transfer_ops), int(rank))
+    prof.start("execute prologue")
+    # this rank's ops, grouped by tensor with each tensor's elements, in one
+    # pass over the schedule
+    runs = _lib.host().rank_runs(transfer_ops, int(rank))
+    ops = runs[0]
     normal = [f for f, t in expected_sub_fields if not _is_meta_field(t)]
     scalars = [f for f, t in expected_sub_fields if _is_meta_field(t)]
     recast = dict(recast or {})
@@ -160,7 +164,7 @@ def execute_param_transfer(
         first = source(ops[0].src_rank).get(ops[0].param_name, {})
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
-    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies)
+    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:])
     if route == "direct":   # the plans only ever gather
         plan_options = replace(plan_options or PlanOptions(), gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
@@ -178,6 +182,7 @@ def execute_param_transfer(
             stream.wait_stream(cur)
     gc_was_enabled = gc.isenabled()
     gc.disable()
+    prof.stop("execute prologue")
     try:
         with torch.cuda.device(device):
             # Each group is planned on the host while the GPU runs the
@@ -228,6 +233,7 @@ def execute_param_transfer(
         # The rest of the host work runs while the last launches finish.
         # 1-element sub-fields ride along whole; the first op's source wins,
         # matching tensors[0].clone() of migration.py:538.
+        prof.start("execute post process")
         for f in scalars:
             for op in ops:
                 entry = target.get(op.param_name)
@@ -241,11 +247,14 @@ def execute_param_transfer(
         # recast targets first, then the sub-fields in their order
         field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
         ordered: StateDict = _lib.host().ordered_result(ops, target, field_order)
+        prof.stop("execute post process")
     finally:
         # destroying a plan waits for its launches: buffers and sources may
         # be released afterwards whatever stream the kernels ran on
+        prof.start("execute wait")
         for plan in plans:
             plan.close()
+        prof.stop("execute wait")
         if gc_was_enabled:
             gc.enable()
     del buffers
@@ -357,12 +366,14 @@ class _LaunchGroups:
     bytes per element over all moved fields, ``tensors_per_name`` the
     destination tensors per name (fields and recast copies)."""
 
-    def __init__(self, ops: List[TransferOp], elem_bytes: int, pipeline: int, tensors_per_name: int = 1):
+    def __init__(self, ops: List[TransferOp], elem_bytes: int, pipeline: int, tensors_per_name: int = 1,
+                 runs=None):
         self.ops = list(ops)
         self.pipeline = int(pipeline)
         self.per_name = max(1, int(tensors_per_name))
-        # op indices tensor by tensor, tensors in order of first appearance
-        self.order, self.starts, numel, self.single = _lib.host().name_runs(self.ops)
+        # op indices tensor by tensor, tensors in order of first appearance,
+        # and each tensor's elements (``runs``: already computed for ``ops``)
+        self.order, self.starts, numel, self.single = runs if runs is not None else _lib.host().name_runs(self.ops)
         self.n = len(numel)
         gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
         self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
@@ -425,10 +436,10 @@ class _LaunchGroups:
 
 
 def _pipeline_groups(ops: List[TransferOp], elem_bytes: int, pipeline: int,
-                     tensors_per_name: int = 1):
+                     tensors_per_name: int = 1, runs=None):
     """The launch groups of ``ops`` (an iterable of op lists, see
     ``_LaunchGroups``)."""
-    return _LaunchGroups(ops, elem_bytes, pipeline, tensors_per_name)
+    return _LaunchGroups(ops, elem_bytes, pipeline, tensors_per_name, runs)
 
 
 def schedule_and_execute_param_transfer(

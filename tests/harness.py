@@ -333,7 +333,7 @@ def round_robin_groups(k: int):
     groups (whole tensors, not contiguous in schedule order), as a stand-in
     for ``migration._pipeline_groups`` that forces several launch groups on
     small cases."""
-    def groups(ops, elem_bytes, pipeline, tensors_per_name=1):
+    def groups(ops, elem_bytes, pipeline, tensors_per_name=1, runs=None):
         index: Dict[str, int] = {}
         out: List[list] = [[] for _ in range(k)]
         for op in ops:
