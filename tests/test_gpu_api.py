@@ -87,6 +87,29 @@ def test_execute_rejects_cpu_and_bad_shapes():
                                fake_source_state_dicts=gpu)
 
 
+def test_execute_rejects_one_tensor_with_two_source_dtypes():
+    """The two sources of one tensor hold uint8 and int8: the library sees
+    one byte type, so the drop-in call's planner itself checks that the
+    torch dtype of a (tensor, field) agrees across sources, and names it."""
+    dst = TensorMeta(name="a", dtype=torch.uint8, shape=(64, 32), tp_meta=(0, 0, 1))
+    ops = [TransferOp("a", r, 0, TensorMeta(name="a", dtype=torch.uint8, shape=(64, 32), tp_meta=(0, r, 2)),
+                      TensorMeta(name="a", dtype=torch.uint8, shape=(64, 32), tp_meta=(0, r, 2)), dst)
+           for r in (0, 1)]
+    dev = torch.device("cuda")
+    fake = {0: {"a": {"param": torch.zeros((32, 32), dtype=torch.uint8, device=dev)}},
+            1: {"a": {"param": torch.zeros((32, 32), dtype=torch.int8, device=dev)}}}
+    print("[gpu api] two source dtypes", flush=True)
+    for route in ("direct", "buffers"):
+        with pytest.raises(AssertionError, match="a/param: dtype differs between sources"):
+            execute_param_transfer(ops, {}, dev, [("param", "normal")], rank=0, fake_source_state_dicts=fake,
+                                   route=route)
+    fake[1]["a"]["param"] = torch.ones((32, 32), dtype=torch.uint8, device=dev)
+    out = execute_param_transfer(ops, {}, dev, [("param", "normal")], rank=0, fake_source_state_dicts=fake)
+    torch.cuda.synchronize()
+    want = torch.cat([torch.zeros((32, 32), dtype=torch.uint8), torch.ones((32, 32), dtype=torch.uint8)])
+    assert torch.equal(out["a"]["param"].cpu(), want)
+
+
 def test_boundary_rejects_misaligned_and_null_pointers():
     src = TensorMeta(name="a", dtype=torch.float32, shape=(64, 32), tp_meta=(0, 0, 2))
     dst = TensorMeta(name="a", dtype=torch.float32, shape=(64, 32), tp_meta=(0, 0, 1))

@@ -441,6 +441,40 @@ def test_ops_of_rank_and_tensor_runs():
     assert host.tensor_runs([])[0].size == 0
 
 
+def test_rank_runs_and_ordered_result():
+    """The one-pass prologue (a rank's ops, their tensor groups in order of
+    first appearance and each tensor's elements) against a Python
+    restatement, with tensors whose ops are not consecutive and a tuple
+    schedule; and the result dict's order (schedule order of names, the
+    given field order, absent fields skipped)."""
+    from suika_amd import _lib
+    host = _lib.host()
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        world = schedule_param_transfer(*w.layouts())
+        for sched in (world, tuple(world[::-1]), world[5:] + world[:5]):
+            for r in sorted({op.dst_rank for op in sched}):
+                ops, order, starts, numel, single = host.rank_runs(sched, r)
+                want_ops = [op for op in sched if op.dst_rank == r]
+                assert ops == want_ops, (key, r)
+                names = list(dict.fromkeys(op.param_name for op in want_ops))
+                members = {n: [i for i, op in enumerate(want_ops) if op.param_name == n] for n in names}
+                assert order.tolist() == [i for n in names for i in members[n]]
+                assert starts.tolist() == [0] + list(np.cumsum([len(members[n]) for n in names]))
+                assert numel.tolist() == [sum(want_ops[i].dst_meta.numel() for i in members[n]) for n in names]
+                assert single == all(m == list(range(m[0], m[0] + len(m))) for m in members.values())
+    assert host.rank_runs([], 0)[0] == []
+    ops = CONFIGS["gpt125m_tp2_tp4"].ops()
+    target = {}
+    for op in reversed(ops):
+        target[op.param_name] = {"exp_avg": 1, "param": 2, "master": 3}
+    out = host.ordered_result(ops, target, ["master", "param", "step", "exp_avg"])
+    assert list(out) == list(dict.fromkeys(op.param_name for op in ops))
+    assert all(list(e) == ["master", "param", "exp_avg"] for e in out.values())
+    with pytest.raises(KeyError):
+        host.ordered_result(ops, {}, ["param"])
+
+
 def test_from_sources_rejects_bad_sources_by_name():
     """ReshardPlan.from_sources (the drop-in operator's planner) reads the
     source tensors themselves; what it cannot use is rejected with the
