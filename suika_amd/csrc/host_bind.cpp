@@ -265,20 +265,22 @@ py::array_t<uint64_t> bind_dst(py::dict part, const RowTable& rows, py::list nam
       if (!THPDtype_Check(dt.ptr())) throw py::type_error("dtypes must hold torch.dtype objects");
       st = reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type;
     }
-    const std::string what = "(" + py::repr(name).cast<std::string>() + ", " +
-                             py::repr(field).cast<std::string>() + ")";
+    // the message is built only when a check fails
+    auto what = [&]() {
+      return "(" + py::repr(name).cast<std::string>() + ", " + py::repr(field).cast<std::string>() + ")";
+    };
     py::object entry = lookup(part.ptr(), name.ptr());
     py::object obj = entry ? lookup(entry.ptr(), field.ptr()) : py::object();
-    if (!obj) assertion(what + ": no destination tensor");
-    if (!THPVariable_Check(obj.ptr())) assertion(what + ": not a tensor");
+    if (!obj) assertion(what() + ": no destination tensor");
+    if (!THPVariable_Check(obj.ptr())) assertion(what() + ": not a tensor");
     const at::Tensor& t = THPVariable_Unpack(obj.ptr());
     if (t.device() != device)
-      assertion(what + ": tensor is on " + t.device().str() + ", the kernels run on " + device.str());
-    if (!t.is_contiguous()) assertion(what + ": tensor is not contiguous");
-    if (t.scalar_type() != st) assertion(what + ": dtype differs from the planned one");
+      assertion(what() + ": tensor is on " + t.device().str() + ", the kernels run on " + device.str());
+    if (!t.is_contiguous()) assertion(what() + ": tensor is not contiguous");
+    if (t.scalar_type() != st) assertion(what() + ": dtype differs from the planned one");
     bool same = t.dim() == nd;
     for (int64_t d = 0; same && d < nd; ++d) same = t.size(d) == r[5 + d];
-    if (!same) assertion(what + ": shape differs from the planned one");
+    if (!same) assertion(what() + ": shape differs from the planned one");
     pp[i] = reinterpret_cast<uint64_t>(t.data_ptr());
   }
   return ptrs;
@@ -984,8 +986,9 @@ py::list device_views(uint64_t base, py::list views, int64_t device_index) {
 // name)`), the op / meta tables (encode_ops), the source tensors
 // (collect_sources), then sr_lower and sr_plan_create of libsuika_reshard.so
 // on its tables, with nothing copied through Python in between.  With
-// `gather`, also the fresh destination tensors (alloc_dst) and sr_gather
-// into them on `stream` (the drop-in call's direct route).  Raises
+// `gather`, also the destination tensors -- fresh ones (alloc_dst), or those
+// of `dst_part` checked against their slots (bind_dst) -- and sr_gather into
+// them on `stream` (the drop-in call's direct route).  Raises
 // suika_amd._lib.PlanError (or ReshardError for device and memory failures)
 // with the library's message, tensor ids replaced by names.
 
@@ -1059,7 +1062,7 @@ static_assert(sizeof(sr_op) == 9 * sizeof(int64_t), "an sr_op row is 9 int64 wor
 py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::list recast_names,
                        py::function infer_shard, int64_t device_index, const std::string& who,
                        uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
-                       py::dtype piece_dt, bool gather, uint64_t stream) {
+                       py::dtype piece_dt, bool gather, uint64_t stream, py::object dst_part) {
   const Names& N = names_();
   const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
   const int64_t nf = int64_t(fields.size());
@@ -1167,11 +1170,21 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
   py::array_t<int64_t> dst_rows = key_table(low->dst_key, low->n_dst), empty_rows = key_table(low->empty, low->n_empty);
   py::object part = py::none();
   if (gather) {
-    // fresh destinations, then the gather on `stream`
-    py::tuple fresh = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
-                                at::Device(at::kCUDA, c10::DeviceIndex(device_index)));
-    part = fresh[0];
-    py::array_t<uint64_t> dst_ptrs = fresh[1].cast<py::array_t<uint64_t>>();
+    // fresh destinations (or the caller's, each checked against its slot),
+    // then the gather on `stream`
+    const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
+    py::array_t<uint64_t> dst_ptrs;
+    if (dst_part.is_none()) {
+      py::tuple fresh = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
+                                  device);
+      part = fresh[0];
+      dst_ptrs = fresh[1].cast<py::array_t<uint64_t>>();
+    } else {
+      if (!PyDict_Check(dst_part.ptr())) throw py::type_error("destinations must be a dict");
+      dst_ptrs = bind_dst(dst_part.cast<py::dict>(), dst_rows, op_names, fields, recast_names,
+                          col[1].cast<py::list>(), device);
+      part = dst_part;
+    }
     rc = sr_gather(plan, reinterpret_cast<const void* const*>(src_ptrs.data()),
                    reinterpret_cast<void* const*>(dst_ptrs.data()), reinterpret_cast<hipStream_t>(stream));
     if (rc != SR_OK) raise_status(rc, "sr_gather", sr_last_error());
@@ -1212,5 +1225,5 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
         py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),
         py::arg("tile_bytes"), py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"),
-        py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0);
+        py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0, py::arg("dst_part") = py::none());
 }

@@ -188,13 +188,18 @@ def execute_param_transfer(
             # Each group is planned on the host while the GPU runs the
             # previous group's launch.
             for group in groups:
-                if route == "direct" and arena_views is None:
+                if route == "direct":
                     # plan (shapes, dtypes and addresses read from the source
-                    # tensors, each checked once), fresh destinations and the
-                    # gather into them: one native call
+                    # tensors, each checked once), the destinations (fresh, or
+                    # the arena's views) and the gather into them: one native
+                    # call
+                    part = None
+                    if arena_views is not None:
+                        part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
                     prof.start("execute gather")
                     plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
-                                                            options=plan_options, rank=rank, stream=stream)
+                                                            options=plan_options, rank=rank, stream=stream,
+                                                            dst=part)
                     prof.stop("execute gather")
                     plans.append(plan)
                     target.update(part)

@@ -155,18 +155,20 @@ class ReshardPlan:
                        recast: Optional[Mapping[str, str]] = None,
                        options: Optional[PlanOptions] = None,
                        rank: Optional[int] = None,
-                       stream=None) -> Tuple["ReshardPlan", Dict[str, Dict[str, torch.Tensor]]]:
-        """``from_sources``, fresh destination tensors (as ``alloc_dst``) and
-        the gather into them on ``stream`` (default: the current stream), in
-        one native call: the drop-in call's direct route.  Returns the plan
-        (its kernels possibly still running: ``close`` waits for them) and
-        the destinations ``{name: {field: tensor}}``."""
+                       stream=None, dst=None) -> Tuple["ReshardPlan", Dict[str, Dict[str, torch.Tensor]]]:
+        """``from_sources``, the destination tensors and the gather into them
+        on ``stream`` (default: the current stream), in one native call: the
+        drop-in call's direct route.  The destinations are fresh tensors (as
+        ``alloc_dst``), or ``dst`` ``{name: {field: tensor}}``, each checked
+        against its slot (as ``bind_dst_ptrs``).  Returns the plan (its
+        kernels possibly still running: ``close`` waits for them) and the
+        destinations."""
         plan, _, part = cls._native(ops, source, fields, device, recast, options, rank, gather=True,
-                                    stream=_stream_handle(stream).value or 0)
+                                    stream=_stream_handle(stream).value or 0, dst=dst)
         return plan, part
 
     @classmethod
-    def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0):
+    def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0, dst=None):
         self = cls.__new__(cls)
         self._configure(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
@@ -180,7 +182,7 @@ class ReshardPlan:
          self._empty_rows, self.peer_bytes, info, part) = _lib.host().plan_sources(
             self._ops, source, self.fields, [self._recast_of.get(f) for f in self.fields],
             infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
-            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream)
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst)
         self._handle = ctypes.c_void_p(handle)
         self.info = _lib.SrPlanInfo.from_buffer_copy(info)
         self.n_pieces = len(self._piece_arr)

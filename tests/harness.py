@@ -201,12 +201,16 @@ def poisoned_allocations():
     def arena(*a, **kw):
         return poison(arena_views(*a, **kw))
 
-    def gather(cls, ops, source, fields, device, recast=None, options=None, rank=None, stream=None):
-        # the one-call direct route, composed of its parts so that the
-        # destinations can be poisoned between allocation and launch
+    def gather(cls, ops, source, fields, device, recast=None, options=None, rank=None, stream=None, dst=None):
+        # the one-call direct route, composed of its parts so that fresh
+        # destinations can be poisoned between allocation and launch (arena
+        # views come poisoned from _arena_views)
         plan, src_ptrs = cls.from_sources(ops, source, fields, device, recast=recast, options=options, rank=rank)
-        part, ptrs = plan.alloc_dst_ptrs(device)
-        poison(part)
+        if dst is None:
+            part, ptrs = plan.alloc_dst_ptrs(device)
+            poison(part)
+        else:
+            part, ptrs = dst, plan.bind_dst_ptrs(dst, device)
         plan.gather_ptrs(src_ptrs, ptrs, stream)
         return plan, part
 
