@@ -24,6 +24,7 @@ intended ``cat`` in ascending piece order.
 """
 from __future__ import annotations
 
+import contextlib
 import gc
 import time
 from dataclasses import replace
@@ -42,6 +43,9 @@ from . import _lib
 from .plan import PlanOptions, ReshardPlan
 
 StateDict = Dict[str, Dict[str, Tensor]]
+
+
+_GATHER_ONLY = PlanOptions(gather_only=True)
 
 
 class _NoProf:
@@ -166,7 +170,7 @@ def execute_param_transfer(
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
     groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:])
     if route == "direct":   # the plans only ever gather
-        plan_options = replace(plan_options or PlanOptions(), gather_only=True)
+        plan_options = _GATHER_ONLY if plan_options is None else replace(plan_options, gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
@@ -184,7 +188,8 @@ def execute_param_transfer(
     gc.disable()
     prof.stop("execute prologue")
     try:
-        with torch.cuda.device(device):
+        with (contextlib.nullcontext() if device.index == torch.cuda.current_device()
+              else torch.cuda.device(device)):
             # Each group is planned on the host while the GPU runs the
             # previous group's launch.
             for group in groups:
@@ -252,6 +257,11 @@ def execute_param_transfer(
         # recast targets first, then the sub-fields in their order
         field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
         ordered: StateDict = _lib.host().ordered_result(ops, target, field_order)
+        if gc_was_enabled:
+            # the youngest generation, thousands of objects made by this call
+            # (tensors, dicts), is collected now, while the last launches
+            # run, instead of on the caller's first allocation afterwards
+            gc.collect(0)
         prof.stop("execute post process")
     finally:
         # destroying a plan waits for its launches: buffers and sources may

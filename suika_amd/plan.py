@@ -58,7 +58,7 @@ def sr_dtype(dtype: torch.dtype) -> int:
     return _DTYPES[dtype]
 
 
-@dataclass
+@dataclass(frozen=True)
 class PlanOptions:
     tile_bytes: int = 0          # 0 = library default
     max_blocks: int = 0          # 0 = one workgroup per tile
