@@ -329,6 +329,10 @@ def _piece_aliases_source(op: TransferOp) -> bool:
 PLAN_NS_PER_GROUP = 60_000
 PLAN_NS_PER_TENSOR = 1_000
 GATHER_BYTES_PER_NS = 6_100
+# Floor of a measured per-tensor planning time: a group planned faster than
+# PLAN_NS_PER_GROUP still costs its tensors something (allocating one alone
+# takes longer than this).
+MIN_PLAN_NS_PER_TENSOR = 100
 # GPU work of the first launch group: the host then plans the second while
 # it runs.
 FIRST_GROUP_NS = 100_000
@@ -436,7 +440,8 @@ class _LaunchGroups:
                 return
             names = end - start
             if names >= MIN_GROUP_TENSORS:
-                self.plan_ns = max(0.0, spent - PLAN_NS_PER_GROUP) / (names * self.per_name)
+                self.plan_ns = max(float(MIN_PLAN_NS_PER_TENSOR),
+                                   (spent - PLAN_NS_PER_GROUP) / (names * self.per_name))
             start, end = end, self._next_end(start, end, groups + 1)
             groups += 1
 

@@ -419,6 +419,33 @@ def test_launch_groups_adapt_to_the_measured_planning_rate(monkeypatch):
     assert slow[2] < fast[2], (fast, slow)
 
 
+@pytest.mark.parametrize("share", [0.0, 1e-5, 1.0])
+def test_launch_groups_survive_a_group_planned_within_the_overhead(monkeypatch, share):
+    """A timed group of MIN_GROUP_TENSORS or more names planned in no more
+    than PLAN_NS_PER_GROUP (a fast host, or a consumer that plans nothing)
+    still yields every op exactly once: the measured per-tensor rate is
+    floored at MIN_PLAN_NS_PER_TENSOR instead of reaching zero, and the next
+    group then takes all that is left."""
+    from suika_amd import migration as M
+    spent_ns = int(share * M.PLAN_NS_PER_GROUP)   # none, 0.6 ns, exactly the overhead
+    clock = [0]
+    monkeypatch.setattr(M, "_clock_ns", lambda: clock[0])
+    w = CONFIGS["gpt125m_tp2_tp4"]
+    ops = w.ops()
+    elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+    tpn = len(w.src_fields) + len(w.recast_map)
+    groups = []
+    for g in M._pipeline_groups(ops, elem, 8, tpn):
+        groups.append(g)
+        # the first group is slow; the later ones take spent_ns
+        clock[0] += 10 * M.PLAN_NS_PER_GROUP if len(groups) == 1 else spent_ns
+    assert sorted(map(id, (op for g in groups for op in g))) == sorted(map(id, ops))
+    sizes = [len({op.param_name for op in g}) for g in groups]
+    timed = [j for j in range(1, len(sizes) - 1) if sizes[j] >= M.MIN_GROUP_TENSORS]
+    assert timed, sizes                           # a group was timed at spent_ns
+    assert len(groups) == timed[0] + 2, sizes     # and the one after it takes the rest
+
+
 def test_ops_of_rank_and_tensor_runs():
     """The drop-in call's native prologue: a rank's ops in schedule order, and
     runs of a tensor's consecutive ops with the elements of their pieces."""
