@@ -24,22 +24,34 @@
 //   piece_numels:    elements per op's piece (launch-group balancing);
 //   ops_of_rank:     the ops one destination rank executes;
 //   tensor_runs:     runs of a tensor's consecutive ops and their elements;
-//   device_views:    tensors over a mapped hand-off allocation (no copy).
+//   device_views:    tensors over a mapped hand-off allocation (no copy);
+//   plan_sources:    one launch group: the above in one call, with the
+//                    destinations' allocations made on a helper thread while
+//                    this thread plans.
 //
 // No device work happens here; the tensors come from torch's caching
 // allocator on the device's current stream, as torch.empty would.
 
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
+#include <c10/core/StreamGuard.h>
+#include <c10/core/impl/VirtualGuardImpl.h>
 #include <torch/csrc/Dtype.h>
 #include <torch/csrc/DynamicTypes.h>
 #include <pybind11/numpy.h>
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
 #include <cstdint>
 #include <cstring>
+#include <deque>
 #include <memory>
+#include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -176,18 +188,26 @@ class FreshTensors {
     if (alloc_ == nullptr) throw std::runtime_error("no allocator for " + device.str());
   }
 
-  at::Tensor make(at::IntArrayRef sizes, at::ScalarType st) const {
+  static size_t bytes_of(at::IntArrayRef sizes, at::ScalarType st) {
     int64_t numel = 1;
     for (int64_t s : sizes) {
       if (s < 0 || __builtin_mul_overflow(numel, s, &numel)) throw py::value_error("bad destination shape");
     }
-    const size_t nbytes = size_t(numel) * c10::elementSize(st);
-    c10::Storage storage(c10::Storage::use_byte_size_t(), nbytes, alloc_->allocate(nbytes), alloc_,
-                         /*resizable=*/true);
+    return size_t(numel) * c10::elementSize(st);
+  }
+
+  // A tensor on `block` (nbytes from this allocator, see BlockJob), else on
+  // a new allocation.
+  at::Tensor make(at::IntArrayRef sizes, at::ScalarType st, c10::DataPtr* block = nullptr) const {
+    const size_t nbytes = bytes_of(sizes, st);
+    c10::Storage storage(c10::Storage::use_byte_size_t(), nbytes,
+                         block ? std::move(*block) : alloc_->allocate(nbytes), alloc_, /*resizable=*/true);
     auto impl = c10::make_intrusive<c10::TensorImpl>(std::move(storage), keys_, c10::scalarTypeToTypeMeta(st));
     impl->set_sizes_contiguous(sizes);
     return at::Tensor(std::move(impl));
   }
+
+  c10::Allocator* allocator() const { return alloc_; }
 
  private:
   c10::DeviceGuard guard_;   // the allocator serves the current device
@@ -196,15 +216,160 @@ class FreshTensors {
   c10::Allocator* alloc_;
 };
 
+// ------------------------------------------------------------ destination blocks made ahead
+//
+// On a share of many small tensors the caching-allocator call behind each
+// fresh destination tensor is a large part of the host's time per tensor.
+// Once a launch group's sources are read (their dtypes fix the bytes), its
+// destination blocks are handed to a helper thread, which allocates them on
+// the call's device and current stream -- the allocations at::empty would
+// make -- while the calling thread lowers and plans the group.  The tensors
+// are then built on those blocks: each still has an allocation of its own.
+// A block the helper did not make (an allocation failed, the job was
+// stopped) or whose size is not the planned tensor's is not used; the
+// tensor is allocated on the calling thread instead, which also reports
+// any allocation failure.  Unused blocks are freed before the group's
+// launch, on the calling thread.
+
+// One launch group's blocks: slot i has nbytes[i] bytes (0: no block).
+class BlockJob {
+ public:
+  BlockJob(c10::Allocator* alloc, c10::Stream stream, std::vector<size_t> nbytes)
+      : alloc_(alloc), stream_(stream), nbytes_(std::move(nbytes)), blocks_(nbytes_.size()) {}
+
+  // On the helper thread.  Slot i belongs to the helper until ready_ > i.
+  void run() noexcept {
+    try {
+      c10::StreamGuard guard(stream_);   // the device and stream the calling thread allocates on
+      for (size_t i = 0; i < nbytes_.size() && !stop_.load(std::memory_order_relaxed); ++i) {
+        if (nbytes_[i]) blocks_[i] = alloc_->allocate(nbytes_[i]);
+        ready_.store(i + 1, std::memory_order_release);
+      }
+    } catch (...) {
+      // out of device memory, say: the remaining slots get no block
+    }
+    done_.store(true, std::memory_order_release);
+  }
+
+  // Slot i's block when the helper made one of `bytes` bytes, moved into
+  // `out`; waits for the helper (without the GIL, which it may need).
+  bool take(size_t i, size_t bytes, c10::DataPtr* out) {
+    if (i >= nbytes_.size() || bytes == 0 || nbytes_[i] != bytes) return false;
+    if (ready_.load(std::memory_order_acquire) <= i) {
+      py::gil_scoped_release nogil;
+      while (ready_.load(std::memory_order_acquire) <= i && !done_.load(std::memory_order_acquire))
+        std::this_thread::yield();
+    }
+    if (ready_.load(std::memory_order_acquire) <= i || !blocks_[i]) return false;
+    *out = std::move(blocks_[i]);
+    return true;
+  }
+
+  // Stops the helper on this job, waits until it is done with it and frees
+  // the blocks nobody took.  Called with or without the GIL; never throws.
+  void finish() noexcept {
+    stop_.store(true, std::memory_order_relaxed);
+    if (!done_.load(std::memory_order_acquire)) {
+      auto wait = [this] {
+        while (!done_.load(std::memory_order_acquire)) std::this_thread::yield();
+      };
+      if (PyGILState_Check()) {
+        py::gil_scoped_release nogil;
+        wait();
+      } else {
+        wait();
+      }
+    }
+    std::vector<c10::DataPtr>().swap(blocks_);
+  }
+
+ private:
+  c10::Allocator* const alloc_;
+  const c10::Stream stream_;
+  const std::vector<size_t> nbytes_;
+  std::vector<c10::DataPtr> blocks_;
+  std::atomic<size_t> ready_{0};
+  std::atomic<bool> done_{false}, stop_{false};
+};
+
+// The helper thread: runs jobs in submission order.  Its state is created
+// by the first submission (under the GIL, so once per process) and again in
+// a forked child, which has no helper thread; it is never destroyed, so the
+// detached thread never outlives it.
+class BlockHelper {
+ public:
+  // false when no helper thread could be started (the caller then allocates
+  // everything itself)
+  static bool submit(std::shared_ptr<BlockJob> job) {
+    BlockHelper* h = instance();
+    if (!h) return false;
+    {
+      std::lock_guard<std::mutex> lk(h->mutex_);
+      h->queue_.push_back(std::move(job));
+    }
+    h->cv_.notify_one();
+    return true;
+  }
+
+ private:
+  static BlockHelper* instance() {
+    static BlockHelper* helper = nullptr;
+    static pid_t owner = 0;
+    if (helper && owner == getpid()) return helper;
+    BlockHelper* h = new BlockHelper();
+    try {
+      std::thread([h] { h->loop(); }).detach();
+    } catch (const std::exception&) {
+      delete h;
+      return nullptr;
+    }
+    helper = h;
+    owner = getpid();
+    return helper;
+  }
+
+  void loop() {
+    for (;;) {
+      std::shared_ptr<BlockJob> job;
+      {
+        std::unique_lock<std::mutex> lk(mutex_);
+        cv_.wait(lk, [this] { return !queue_.empty(); });
+        job = std::move(queue_.front());
+        queue_.pop_front();
+      }
+      job->run();
+    }
+  }
+
+  std::mutex mutex_;
+  std::condition_variable cv_;
+  std::deque<std::shared_ptr<BlockJob>> queue_;
+};
+
+// Destination tensors built on a block made ahead, and those a job covered
+// that were allocated on the calling thread instead (process totals).
+std::atomic<uint64_t> g_blocks_taken{0}, g_blocks_missed{0};
+
+// Slot of (tensor nid of a group, field f, recast copy or not) in the
+// group's BlockJob, nf fields.
+inline size_t block_slot(size_t nid, int64_t f, bool recast, int64_t nf) {
+  return (nid * 2 + (recast ? 1 : 0)) * size_t(nf) + size_t(f);
+}
+
 // Fresh destination tensors for the slot rows (and the zero-element ones).
+// With `job`, a tensor takes the block made ahead for it (slot block_slot of
+// op k's tensor op_nid[k]) when there is one of its size.
 py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list names, py::list fields,
-                    py::list recast_names, py::list dtypes, at::Device device) {
+                    py::list recast_names, py::list dtypes, at::Device device, const FreshTensors* made = nullptr,
+                    BlockJob* job = nullptr, const std::vector<size_t>* op_nid = nullptr) {
   const int64_t nf = int64_t(fields.size());
   py::dict out;
   const int64_t n = rows.ndim() == 2 ? rows.shape(0) : 0;
   py::array_t<uint64_t> ptrs({n});
   uint64_t* pp = ptrs.mutable_data();
-  const FreshTensors fresh(device);
+  std::unique_ptr<FreshTensors> own;
+  if (!made) made = (own = std::make_unique<FreshTensors>(device)).get();
+  const FreshTensors& fresh = *made;
   for (int pass = 0; pass < 2; ++pass) {
     const auto& tbl = pass == 0 ? rows : empty_rows;
     const int64_t m = tbl.ndim() == 2 ? tbl.shape(0) : 0;
@@ -225,7 +390,12 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
         st = reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type;
         field = fields[f];
       }
-      at::Tensor t = fresh.make(at::IntArrayRef(r + 5, size_t(nd)), st);
+      const at::IntArrayRef sizes(r + 5, size_t(nd));
+      c10::DataPtr block;
+      const bool ahead = job && job->take(block_slot((*op_nid)[size_t(k)], f, is_recast != 0, nf),
+                                          FreshTensors::bytes_of(sizes, st), &block);
+      if (job) (ahead ? g_blocks_taken : g_blocks_missed).fetch_add(1, std::memory_order_relaxed);
+      at::Tensor t = fresh.make(sizes, st, ahead ? &block : nullptr);
       py::handle name = names[k];
       PyObject* entry = PyDict_GetItemWithError(out.ptr(), name.ptr());
       if (!entry) {
@@ -719,7 +889,8 @@ py::tuple tensor_runs(py::list ops) {
 // The ops grouped by tensor, tensors in order of first appearance: (op
 // indices tensor by tensor, where each tensor's indices start (one entry
 // per tensor plus the end), elements of each tensor's pieces, whether every
-// tensor's ops are already consecutive -- the order is then the identity).
+// tensor's ops are already consecutive -- the order is then the identity --,
+// and {name: tensor index}).
 py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n);
 
 py::tuple name_runs(py::list ops) {
@@ -731,7 +902,7 @@ py::tuple name_runs(py::list ops) {
 
 // The ops of `rank` out of a whole schedule (any sequence), and their
 // name_runs, in one pass over the schedule: (ops, order, starts, elements
-// per tensor, single).
+// per tensor, single, {name: tensor index}).
 py::tuple rank_runs(py::object schedule, int64_t rank) {
   const Names& N = names_();
   py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(schedule.ptr(), "ops must be a sequence"));
@@ -746,7 +917,7 @@ py::tuple rank_runs(py::object schedule, int64_t rank) {
     numel.push_back(piece_numel(items[k]));
   }
   py::tuple runs = runs_of(ops, numel.data(), Py_ssize_t(numel.size()));
-  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3]);
+  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3], runs[4]);
 }
 
 py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {
@@ -792,7 +963,39 @@ py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {
   std::vector<int64_t> fill(st, st + m);
   for (Py_ssize_t k = 0; k < n; ++k) o[fill[size_t(nid[size_t(k)])]++] = k;
   std::copy(sums.begin(), sums.end(), total.mutable_data());
-  return py::make_tuple(order, starts, total, single);
+  return py::make_tuple(order, starts, total, single, ids);
+}
+
+// The ops of the tensors `picked` (indices into runs_of's tensors, any
+// order, each once): tensor by tensor in index order -- order of first
+// appearance --, each tensor's ops in schedule order.  A launch group.
+py::list take_ops(py::list ops, const RowTable& order, const RowTable& starts, const RowTable& picked) {
+  const int64_t n_ops = int64_t(PyList_GET_SIZE(ops.ptr()));
+  if (order.ndim() != 1 || order.shape(0) != n_ops || starts.ndim() != 1 || starts.shape(0) < 1 ||
+      picked.ndim() != 1)
+    throw py::value_error("take_ops: order, starts and picked must be 1-D, order one entry per op");
+  const int64_t m = starts.shape(0) - 1;
+  const int64_t *st = starts.data(), *o = order.data();
+  std::vector<int64_t> sel(picked.data(), picked.data() + picked.shape(0));
+  std::sort(sel.begin(), sel.end());
+  Py_ssize_t total = 0;
+  for (size_t j = 0; j < sel.size(); ++j) {
+    const int64_t i = sel[j];
+    if (i < 0 || i >= m || (j && sel[j - 1] == i) || st[i] < 0 || st[i] > st[i + 1] || st[i + 1] > n_ops)
+      throw py::value_error("take_ops: bad tensor index or runs");
+    total += Py_ssize_t(st[i + 1] - st[i]);
+  }
+  py::list out(total);
+  Py_ssize_t j = 0;
+  for (int64_t i : sel)
+    for (int64_t q = st[i]; q < st[i + 1]; ++q) {
+      const int64_t k = o[q];
+      if (k < 0 || k >= n_ops) throw py::value_error("take_ops: op index out of range");
+      PyObject* op = PyList_GET_ITEM(ops.ptr(), k);
+      Py_INCREF(op);
+      PyList_SET_ITEM(out.ptr(), j++, op);
+    }
+  return out;
 }
 
 // The drop-in call's result: {name: {field: tensor}} with the names in
@@ -1062,7 +1265,8 @@ static_assert(sizeof(sr_op) == 9 * sizeof(int64_t), "an sr_op row is 9 int64 wor
 py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::list recast_names,
                        py::function infer_shard, int64_t device_index, const std::string& who,
                        uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
-                       py::dtype piece_dt, bool gather, uint64_t stream, py::object dst_part) {
+                       py::dtype piece_dt, bool gather, uint64_t stream, py::object dst_part,
+                       py::object ahead) {
   const Names& N = names_();
   const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
   const int64_t nf = int64_t(fields.size());
@@ -1112,16 +1316,14 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
     }
     shards[names[i]] = shard;
   }
-  py::tuple enc = encode_ops(ops, shards, name_ids);
-  py::array_t<int64_t> metas = enc[0].cast<py::array_t<int64_t>>(), op_rows = enc[1].cast<py::array_t<int64_t>>();
   py::tuple col = collect_sources(ops, source, fields, device_index, who);
   py::array_t<int64_t> specs = col[0].cast<py::array_t<int64_t>>();
   py::array_t<uint64_t> ptrs = col[2].cast<py::array_t<uint64_t>>();
   // one torch dtype per (tensor, field) across its sources: the library
   // compares element types, which several torch dtypes share
+  std::vector<PyObject*> first(by_name.size() * size_t(nf), nullptr);
   {
     py::list dtypes = col[1].cast<py::list>();
-    std::vector<PyObject*> first(by_name.size() * size_t(nf), nullptr);
     for (Py_ssize_t k = 0; k < n; ++k)
       for (int64_t f = 0; f < nf; ++f) {
         PyObject* dt = PyList_GET_ITEM(dtypes.ptr(), k * nf + f);
@@ -1132,6 +1334,51 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
                     ": dtype differs between sources");
       }
   }
+  // Fresh destinations: their blocks are made on the helper thread from
+  // here on, while this thread lowers and plans.  `ahead` = (name -> index,
+  // elements per index) gives each tensor's elements (its pieces' total).
+  const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
+  std::unique_ptr<FreshTensors> fresh;
+  std::shared_ptr<BlockJob> job;
+  struct Finish {
+    std::shared_ptr<BlockJob>& job;
+    ~Finish() {
+      if (job) job->finish();
+    }
+  } finish_job{job};
+  if (gather && dst_part.is_none()) {
+    fresh = std::make_unique<FreshTensors>(device);
+    if (!ahead.is_none()) {
+      py::tuple a = ahead.cast<py::tuple>();
+      if (a.size() != 2 || !PyDict_Check(a[0].ptr())) throw py::value_error("ahead must be (dict, elements)");
+      PyObject* index = a[0].ptr();
+      const RowTable numel = a[1].cast<RowTable>();
+      const int64_t n_numel = numel.ndim() == 1 ? numel.shape(0) : 0;
+      std::vector<size_t> nbytes(by_name.size() * 2 * size_t(nf), 0);
+      for (size_t i = 0; i < by_name.size(); ++i) {
+        PyObject* at = PyDict_GetItemWithError(index, names[i].ptr());
+        if (!at) {
+          if (PyErr_Occurred()) throw py::error_already_set();
+          continue;
+        }
+        const int64_t id = as_int(at);
+        if (id < 0 || id >= n_numel || numel.data()[id] <= 0) continue;
+        const size_t elems = size_t(numel.data()[id]);
+        for (int64_t f = 0; f < nf; ++f) {
+          PyObject* dt = first[i * size_t(nf) + size_t(f)];
+          if (dt && THPDtype_Check(dt))
+            nbytes[block_slot(i, f, false, nf)] =
+                elems * c10::elementSize(reinterpret_cast<THPDtype*>(dt)->scalar_type);
+          if (recast[size_t(f)]) nbytes[block_slot(i, f, true, nf)] = elems * c10::elementSize(at::kBFloat16);
+        }
+      }
+      const c10::Stream current = c10::impl::VirtualGuardImpl(device.type()).getStream(device);
+      job = std::make_shared<BlockJob>(fresh->allocator(), current, std::move(nbytes));
+      if (!BlockHelper::submit(job)) job.reset();
+    }
+  }
+  py::tuple enc = encode_ops(ops, shards, name_ids);
+  py::array_t<int64_t> metas = enc[0].cast<py::array_t<int64_t>>(), op_rows = enc[1].cast<py::array_t<int64_t>>();
   const int64_t no_recast = 0;
 
   sr_lowering* low = nullptr;
@@ -1172,13 +1419,13 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
   if (gather) {
     // fresh destinations (or the caller's, each checked against its slot),
     // then the gather on `stream`
-    const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
     py::array_t<uint64_t> dst_ptrs;
     if (dst_part.is_none()) {
-      py::tuple fresh = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
-                                  device);
-      part = fresh[0];
-      dst_ptrs = fresh[1].cast<py::array_t<uint64_t>>();
+      py::tuple made = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
+                                 device, fresh.get(), job.get(), &op_nid);
+      if (job) job->finish();   // blocks no tensor took are freed before the launch
+      part = made[0];
+      dst_ptrs = made[1].cast<py::array_t<uint64_t>>();
     } else {
       if (!PyDict_Check(dst_part.ptr())) throw py::type_error("destinations must be a dict");
       dst_ptrs = bind_dst(dst_part.cast<py::dict>(), dst_rows, op_names, fields, recast_names,
@@ -1203,20 +1450,32 @@ PYBIND11_MODULE(_suika_host, m) {
   m.doc() = "Per-tensor host work of execute_param_transfer (source checks, destination allocation)";
   m.def("collect_sources", &collect_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
         py::arg("device_index"), py::arg("who"));
-  m.def("alloc_dst", &alloc_dst, py::arg("rows"), py::arg("empty_rows"), py::arg("names"), py::arg("fields"),
-        py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
+  m.def(
+      "alloc_dst",
+      [](const RowTable& rows, const RowTable& empty_rows, py::list names, py::list fields, py::list recast_names,
+         py::list dtypes, at::Device device) {
+        return alloc_dst(rows, empty_rows, names, fields, recast_names, dtypes, device);
+      },
+      py::arg("rows"), py::arg("empty_rows"), py::arg("names"), py::arg("fields"), py::arg("recast_names"),
+      py::arg("dtypes"), py::arg("device"));
   m.def("bind_dst", &bind_dst, py::arg("part"), py::arg("rows"), py::arg("names"), py::arg("fields"),
         py::arg("recast_names"), py::arg("dtypes"), py::arg("device"));
   m.def("arena_views", &arena_views, py::arg("buf"), py::arg("names"), py::arg("fields"), py::arg("rows"),
         py::arg("dtypes"));
   m.def("arena_tensors", &arena_tensors, py::arg("ops"), py::arg("source"), py::arg("order"), py::arg("targets"),
         py::arg("device"));
+  m.def(
+      "blocks_ahead",
+      [] { return py::make_tuple(g_blocks_taken.load(), g_blocks_missed.load()); },
+      "(destination tensors built on blocks the helper thread made, those allocated on the calling "
+      "thread instead) since the process started");
   m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
   m.def("piece_numels", &piece_numels, py::arg("ops"));
   m.def("ops_of_rank", &ops_of_rank, py::arg("ops"), py::arg("rank"));
   m.def("tensor_runs", &tensor_runs, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
   m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"));
+  m.def("take_ops", &take_ops, py::arg("ops"), py::arg("order"), py::arg("starts"), py::arg("picked"));
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
@@ -1225,5 +1484,6 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
         py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),
         py::arg("tile_bytes"), py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"),
-        py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0, py::arg("dst_part") = py::none());
+        py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0, py::arg("dst_part") = py::none(),
+        py::arg("ahead") = py::none());
 }

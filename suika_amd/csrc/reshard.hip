@@ -540,6 +540,10 @@ constexpr int kSetupBlock = 256;
 // Tiles one workgroup of the emit kernel writes at most (16 per lane): a
 // large item's tiles are spread over several workgroups.
 constexpr uint32_t kEmitTiles = 4096;
+// Phases of at most this many tiles set up on the caller's stream even
+// while earlier work still runs there: their setup takes a few microseconds
+// of GPU time, less than a wait across streams costs the host.
+constexpr uint64_t kInlineSetupTiles = 65536;
 
 struct EmitChunk {
   uint32_t item;
@@ -1268,15 +1272,18 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
     // A phase's first use builds its tables and binds the pointers.  They
     // are the library's own memory and read no caller data: while earlier
     // work on `stream` (such as the previous launch group's copy) is still
-    // going, they run beside it on the device's setup stream; on an idle
-    // `stream` they run on it directly, since a wait across streams costs
-    // the host more than the setup kernel takes on the GPU.
-    const hipError_t busy = hipStreamQuery(stream);
-    (void)hipGetLastError();   // "not ready" is an answer, not an error
-    if (busy != hipSuccess && busy != hipErrorNotReady)
-      return fail(SR_EHIP, "hipStreamQuery failed: %s", hipGetErrorString(busy));
+    // going, a large phase's setup runs beside it on the device's setup
+    // stream; on an idle `stream`, or for a small phase, it runs on
+    // `stream` directly, since a wait across streams costs the host more
+    // than the setup kernel takes on the GPU.
     hipStream_t setup = stream;
-    if (busy == hipErrorNotReady && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
+    if (ph.n_tiles > kInlineSetupTiles) {
+      const hipError_t busy = hipStreamQuery(stream);
+      (void)hipGetLastError();   // "not ready" is an answer, not an error
+      if (busy != hipSuccess && busy != hipErrorNotReady)
+        return fail(SR_EHIP, "hipStreamQuery failed: %s", hipGetErrorString(busy));
+      if (busy == hipErrorNotReady && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
+    }
     rc = setup_phase(p, ph, kind != kGather, ptrs, setup);
     if (rc != SR_OK) return rc;
     if (setup != stream) SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));

@@ -168,10 +168,13 @@ def execute_param_transfer(
         first = source(ops[0].src_rank).get(ops[0].param_name, {})
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
-    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:])
+    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:5])
     if route == "direct":   # the plans only ever gather
         plan_options = _GATHER_ONLY if plan_options is None else replace(plan_options, gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
+    # fresh destinations: each group's allocations are made on a helper
+    # thread while the group is planned (each tensor's elements: its pieces')
+    ahead = (runs[5], runs[3]) if arena_views is None else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
@@ -204,7 +207,7 @@ def execute_param_transfer(
                     prof.start("execute gather")
                     plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
                                                             options=plan_options, rank=rank, stream=stream,
-                                                            dst=part)
+                                                            dst=part, ahead=ahead)
                     prof.stop("execute gather")
                     plans.append(plan)
                     target.update(part)
@@ -257,10 +260,13 @@ def execute_param_transfer(
         # recast targets first, then the sub-fields in their order
         field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
         ordered: StateDict = _lib.host().ordered_result(ops, target, field_order)
-        if gc_was_enabled:
+        if gc_was_enabled and not (stream or torch.cuda.current_stream(device)).query():
             # the youngest generation, thousands of objects made by this call
-            # (tensors, dicts), is collected now, while the last launches
-            # run, instead of on the caller's first allocation afterwards
+            # (tensors, dicts), is collected while the last launches still
+            # run, where it costs nothing, instead of on the caller's first
+            # allocation afterwards; once the kernels are done it would only
+            # delay the return, and the interpreter collects it later as
+            # after any call that returns many objects
             gc.collect(0)
         prof.stop("execute post process")
     finally:
@@ -392,7 +398,8 @@ class _LaunchGroups:
         self.per_name = max(1, int(tensors_per_name))
         # op indices tensor by tensor, tensors in order of first appearance,
         # and each tensor's elements (``runs``: already computed for ``ops``)
-        self.order, self.starts, numel, self.single = runs if runs is not None else _lib.host().name_runs(self.ops)
+        self.order, self.starts, numel, self.single = (runs if runs is not None
+                                                       else _lib.host().name_runs(self.ops))[:4]
         self.n = len(numel)
         gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
         self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
@@ -405,11 +412,7 @@ class _LaunchGroups:
     def _take(self, a: int, b: int) -> List[TransferOp]:
         if a == 0 and b == self.n:
             return self.ops
-        mask = np.zeros(self.n, dtype=bool)
-        mask[self.rank[a:b]] = True
-        idx = self.order[np.repeat(mask, np.diff(self.starts))]
-        ops = self.ops
-        return [ops[i] for i in idx.tolist()]
+        return _lib.host().take_ops(self.ops, self.order, self.starts, self.rank[a:b])
 
     def _next_end(self, start: int, end: int, groups: int) -> int:
         """End of the group after [start, end), the group number `groups`."""

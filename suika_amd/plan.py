@@ -23,6 +23,7 @@ current HIP stream.
 from __future__ import annotations
 
 import ctypes
+import functools
 import re
 from dataclasses import dataclass
 from typing import Callable, Dict, List, Mapping, Optional, Sequence, Tuple
@@ -69,14 +70,18 @@ class PlanOptions:
     row_groups: bool = True      # side-by-side strided pieces dealt out by row block (default)
     gather_only: bool = False    # build only the gather phase (no pack / unpack)
 
+    @functools.cached_property
+    def flags(self) -> int:
+        """The SR_OPT_* flags of these options (computed once)."""
+        return (0 if self.nontemporal else _lib.SR_OPT_TEMPORAL) | \
+            (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0) | \
+            (0 if self.address_order else _lib.SR_OPT_PIECE_ORDER) | \
+            (0 if self.xcd_order else _lib.SR_OPT_NO_XCD_INTERLEAVE) | \
+            (0 if self.row_groups else _lib.SR_OPT_NO_ROW_GROUPS) | \
+            (_lib.SR_OPT_GATHER_ONLY if self.gather_only else 0)
+
     def to_c(self) -> _lib.SrPlanOptions:
-        flags = (0 if self.nontemporal else _lib.SR_OPT_TEMPORAL) | \
-                (_lib.SR_OPT_SKIP_COVERAGE if self.skip_coverage else 0) | \
-                (0 if self.address_order else _lib.SR_OPT_PIECE_ORDER) | \
-                (0 if self.xcd_order else _lib.SR_OPT_NO_XCD_INTERLEAVE) | \
-                (0 if self.row_groups else _lib.SR_OPT_NO_ROW_GROUPS) | \
-                (_lib.SR_OPT_GATHER_ONLY if self.gather_only else 0)
-        return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, flags, 0)
+        return _lib.SrPlanOptions(self.tile_bytes, self.max_blocks, self.flags, 0)
 
 
 @dataclass(frozen=True)
@@ -155,25 +160,28 @@ class ReshardPlan:
                        recast: Optional[Mapping[str, str]] = None,
                        options: Optional[PlanOptions] = None,
                        rank: Optional[int] = None,
-                       stream=None, dst=None) -> Tuple["ReshardPlan", Dict[str, Dict[str, torch.Tensor]]]:
+                       stream=None, dst=None, ahead=None) -> Tuple["ReshardPlan", Dict[str, Dict[str, torch.Tensor]]]:
         """``from_sources``, the destination tensors and the gather into them
         on ``stream`` (default: the current stream), in one native call: the
         drop-in call's direct route.  The destinations are fresh tensors (as
         ``alloc_dst``), or ``dst`` ``{name: {field: tensor}}``, each checked
-        against its slot (as ``bind_dst_ptrs``).  Returns the plan (its
-        kernels possibly still running: ``close`` waits for them) and the
-        destinations."""
+        against its slot (as ``bind_dst_ptrs``).  With ``ahead`` = ({name:
+        index}, elements per index) -- each tensor's elements --, the fresh
+        tensors' allocations are made on a helper thread while the plan is
+        built.  Returns the plan (its kernels possibly still running:
+        ``close`` waits for them) and the destinations."""
         plan, _, part = cls._native(ops, source, fields, device, recast, options, rank, gather=True,
-                                    stream=_stream_handle(stream).value or 0, dst=dst)
+                                    stream=_stream_handle(stream).value or 0, dst=dst, ahead=ahead)
         return plan, part
 
     @classmethod
-    def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0, dst=None):
+    def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0, dst=None,
+                ahead=None):
         self = cls.__new__(cls)
         self._configure(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
         who = f"[{rank}]" if rank is not None else ""
-        opt = self.options.to_c()
+        opt = self.options
         self._L = _lib.lib()
         # grouping, shards, tables, source checks, sr_lower and sr_plan_create
         # (and with `gather` the destinations and the launch) in one native call
@@ -182,7 +190,7 @@ class ReshardPlan:
          self._empty_rows, self.peer_bytes, info, part) = _lib.host().plan_sources(
             self._ops, source, self.fields, [self._recast_of.get(f) for f in self.fields],
             infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
-            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst)
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst, ahead)
         self._handle = ctypes.c_void_p(handle)
         self.info = _lib.SrPlanInfo.from_buffer_copy(info)
         self.n_pieces = len(self._piece_arr)

@@ -201,10 +201,12 @@ def poisoned_allocations():
     def arena(*a, **kw):
         return poison(arena_views(*a, **kw))
 
-    def gather(cls, ops, source, fields, device, recast=None, options=None, rank=None, stream=None, dst=None):
+    def gather(cls, ops, source, fields, device, recast=None, options=None, rank=None, stream=None, dst=None,
+               ahead=None):
         # the one-call direct route, composed of its parts so that fresh
         # destinations can be poisoned between allocation and launch (arena
-        # views come poisoned from _arena_views)
+        # views come poisoned from _arena_views); `ahead` only moves where
+        # the fresh tensors are allocated
         plan, src_ptrs = cls.from_sources(ops, source, fields, device, recast=recast, options=options, rank=rank)
         if dst is None:
             part, ptrs = plan.alloc_dst_ptrs(device)

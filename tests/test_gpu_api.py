@@ -326,6 +326,12 @@ def test_forcefully_free_releases_what_the_reference_frees(key):
     assert not any(k[2] == "step_cpu" for k in freed)
 
 
+def _blocks_of(tensors) -> int:
+    """Bytes torch's caching allocator counts for one allocation per tensor
+    (its request rounded up to 512 bytes; none for an empty tensor)."""
+    return sum(-(-t.untyped_storage().nbytes() // 512) * 512 for t in tensors)
+
+
 def test_fresh_destinations_are_ordinary_independent_tensors():
     """Destinations come from torch's caching allocator like torch.empty:
     the same device, counted by torch's memory statistics, one storage each
@@ -342,10 +348,13 @@ def test_fresh_destinations_are_ordinary_independent_tensors():
     out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
                                  rank=w.dst_rank, fake_source_state_dicts=fake)
     torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated()
     ref = torch.empty(1, device="cuda")
     tensors = [t for e in out.values() for t in e.values()]
     total = sum(t.untyped_storage().nbytes() for t in tensors)
-    assert torch.cuda.memory_allocated() - before >= total > 0
+    # one caching-allocator block per tensor (rounded to 512 bytes) and
+    # nothing else left allocated: no block made ahead and left unused
+    assert after - before == _blocks_of(tensors) and total > 0
     assert all(t.device == ref.device and t.is_contiguous() for t in tensors)
     assert len({t.untyped_storage().data_ptr() for t in tensors}) == len(tensors)
     assert all(t.untyped_storage().nbytes() == t.numel() * t.element_size() for t in tensors)
@@ -355,3 +364,52 @@ def test_fresh_destinations_are_ordinary_independent_tensors():
         for f, a in e.items():
             if out[name][f] is not victim:
                 np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
+@pytest.mark.parametrize("groups", [None, 4])
+def test_destination_blocks_made_ahead(groups, monkeypatch):
+    """The direct route's fresh destinations are allocated on a helper thread
+    while each launch group is planned.  Every tensor whose pieces cover it
+    (all but padded vocab shards and empty tensors) is built on such a block,
+    sized by that tensor's own source dtype -- here one tensor's param is
+    float64 among float32 ones --; the rest are allocated on the calling
+    thread.  The result matches the oracle, each tensor holds one allocation
+    of its own and no block is left over."""
+    from suika_amd import _lib
+    from suika_amd import migration as M
+    from tests.harness import round_robin_groups
+    if groups:
+        monkeypatch.setattr(M, "_pipeline_groups", round_robin_groups(groups))
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] blocks ahead {w.key} groups={groups}", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    fake = to_device(srcs, w, "cuda")
+    ops = w.ops()
+    odd = next(op.param_name for op in ops if op.param_name.endswith("c_fc.linear.weight"))
+    for sd in fake.values():
+        if odd in sd:
+            sd[odd]["param"] = sd[odd]["param"].double()
+    pieces = {}
+    for op in ops:
+        pieces[op.param_name] = pieces.get(op.param_name, 0) + op.dst_meta.numel()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    taken0, missed0 = _lib.host().blocks_ahead()
+    out = execute_param_transfer(ops, {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                 rank=w.dst_rank, fake_source_state_dicts=fake)
+    torch.cuda.synchronize()
+    taken, missed = (a - b for a, b in zip(_lib.host().blocks_ahead(), (taken0, missed0)))
+    tensors = [t for e in out.values() for t in e.values()]
+    assert torch.cuda.memory_allocated() - before == _blocks_of(tensors)
+    assert len({t.untyped_storage().data_ptr() for t in tensors if t.numel()}) == sum(1 for t in tensors if t.numel())
+    own = sum(len(e) for n, e in out.items() if pieces[n] != next(iter(e.values())).numel() or pieces[n] == 0)
+    assert (taken, missed) == (len(tensors) - own, own), (taken, missed, own)
+    assert out[odd]["param"].dtype == torch.float64
+    for name, e in want.items():
+        for f, a in e.items():
+            got = out[name][f]
+            if name == odd and f == "param":
+                got = got.to(torch.float32)      # exact: float64 copies of float32 values
+            np.testing.assert_array_equal(t2np(got), a, err_msg=f"{name}/{f}")

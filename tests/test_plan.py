@@ -481,7 +481,7 @@ def test_rank_runs_and_ordered_result():
         world = schedule_param_transfer(*w.layouts())
         for sched in (world, tuple(world[::-1]), world[5:] + world[:5]):
             for r in sorted({op.dst_rank for op in sched}):
-                ops, order, starts, numel, single = host.rank_runs(sched, r)
+                ops, order, starts, numel, single, index = host.rank_runs(sched, r)
                 want_ops = [op for op in sched if op.dst_rank == r]
                 assert ops == want_ops, (key, r)
                 names = list(dict.fromkeys(op.param_name for op in want_ops))
@@ -490,7 +490,23 @@ def test_rank_runs_and_ordered_result():
                 assert starts.tolist() == [0] + list(np.cumsum([len(members[n]) for n in names]))
                 assert numel.tolist() == [sum(want_ops[i].dst_meta.numel() for i in members[n]) for n in names]
                 assert single == all(m == list(range(m[0], m[0] + len(m))) for m in members.values())
+                assert index == {n: i for i, n in enumerate(names)}
     assert host.rank_runs([], 0)[0] == []
+    # a launch group's ops: the picked tensors in index order, each one's ops
+    # in schedule order (tensors whose ops are not consecutive included)
+    sched = CONFIGS["llama7b_tp4pp2_tp2pp2"].ops()
+    sched = sched[7:] + sched[:7]
+    ops, order, starts, numel, single, index = host.rank_runs(sched, sched[0].dst_rank)
+    names = list(index)
+    rng = np.random.default_rng(5)
+    for size in (1, 5, len(names)):
+        picked = rng.permutation(len(names))[:size]
+        want = [op for i in sorted(picked) for op in ops if op.param_name == names[i]]
+        assert host.take_ops(ops, order, starts, picked) == want
+    assert host.take_ops(ops, order, starts, np.array([], dtype=np.int64)) == []
+    for bad in ([len(names)], [-1], [2, 2]):
+        with pytest.raises(ValueError, match="take_ops"):
+            host.take_ops(ops, order, starts, np.array(bad, dtype=np.int64))
     ops = CONFIGS["gpt125m_tp2_tp4"].ops()
     target = {}
     for op in reversed(ops):
