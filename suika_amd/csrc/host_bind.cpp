@@ -1336,7 +1336,8 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
   }
   // Fresh destinations: their blocks are made on the helper thread from
   // here on, while this thread lowers and plans.  `ahead` = (name -> index,
-  // elements per index) gives each tensor's elements (its pieces' total).
+  // elements per index) gives each tensor's elements (its pieces' total,
+  // which is the tensor's size unless the shard has rows no piece covers).
   const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
   std::unique_ptr<FreshTensors> fresh;
   std::shared_ptr<BlockJob> job;
@@ -1356,6 +1357,17 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
       const int64_t n_numel = numel.ndim() == 1 ? numel.shape(0) : 0;
       std::vector<size_t> nbytes(by_name.size() * 2 * size_t(nf), 0);
       for (size_t i = 0; i < by_name.size(); ++i) {
+        // a padded vocabulary shard holds rows no piece covers: its size is
+        // not its pieces' total, and it is allocated on this thread
+        PyObject* shard = PyDict_GetItemWithError(shards.ptr(), names[i].ptr());
+        if (!shard) {
+          if (PyErr_Occurred()) throw py::error_already_set();
+          continue;
+        }
+        py::object kind = kind_of(shard);
+        const int padded = PyObject_RichCompareBool(kind.ptr(), N.vocab_pad, Py_EQ);
+        if (padded < 0) throw py::error_already_set();
+        if (padded) continue;
         PyObject* at = PyDict_GetItemWithError(index, names[i].ptr());
         if (!at) {
           if (PyErr_Occurred()) throw py::error_already_set();

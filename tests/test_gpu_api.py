@@ -367,49 +367,58 @@ def test_fresh_destinations_are_ordinary_independent_tensors():
 
 
 @pytest.mark.parametrize("groups", [None, 4])
-def test_destination_blocks_made_ahead(groups, monkeypatch):
+@pytest.mark.parametrize("key", ["gpt125m_tp2_tp4", "qwen7b_tp2_tp4"])
+def test_destination_blocks_made_ahead(key, groups, monkeypatch):
     """The direct route's fresh destinations are allocated on a helper thread
     while each launch group is planned.  Every tensor whose pieces cover it
-    (all but padded vocab shards and empty tensors) is built on such a block,
-    sized by that tensor's own source dtype -- here one tensor's param is
-    float64 among float32 ones --; the rest are allocated on the calling
-    thread.  The result matches the oracle, each tensor holds one allocation
-    of its own and no block is left over."""
+    (all but vocabulary shards, which may be padded, and empty tensors) is
+    built on such a block, sized by that tensor's own source dtype -- here
+    one tensor's exp_avg is float64 among float32 ones -- and bf16 recast
+    copies included; the rest are allocated on the calling thread.  The
+    result matches the oracle, each tensor holds one allocation of its own
+    and no block is left over."""
     from suika_amd import _lib
     from suika_amd import migration as M
     from tests.harness import round_robin_groups
     if groups:
         monkeypatch.setattr(M, "_pipeline_groups", round_robin_groups(groups))
-    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    w = cases.scaled_configs()[key]
     print(f"[gpu api] blocks ahead {w.key} groups={groups}", flush=True)
     glob = global_state(w, _names(w))
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     want = oracle_dest(w, srcs)
     fake = to_device(srcs, w, "cuda")
     ops = w.ops()
-    odd = next(op.param_name for op in ops if op.param_name.endswith("c_fc.linear.weight"))
+    odd = next(op.param_name for op in ops
+               if op.dst_shard_meta.kind == "chunk" and len(op.dst_shard_meta.shape) == 2)
     for sd in fake.values():
         if odd in sd:
-            sd[odd]["param"] = sd[odd]["param"].double()
-    pieces = {}
+            assert sd[odd]["exp_avg"].dtype == torch.float32
+            sd[odd]["exp_avg"] = sd[odd]["exp_avg"].double()
+    pieces, vocab = {}, set()
     for op in ops:
         pieces[op.param_name] = pieces.get(op.param_name, 0) + op.dst_meta.numel()
+        if op.dst_shard_meta.kind == "vocab_pad":
+            vocab.add(op.param_name)
+    assert bool(vocab) == (key == "qwen7b_tp2_tp4") and bool(w.recast_map) == bool(vocab)
     torch.cuda.synchronize()
     before = torch.cuda.memory_allocated()
     taken0, missed0 = _lib.host().blocks_ahead()
     out = execute_param_transfer(ops, {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
-                                 rank=w.dst_rank, fake_source_state_dicts=fake)
+                                 rank=w.dst_rank, fake_source_state_dicts=fake, recast=w.recast_map)
     torch.cuda.synchronize()
+    after = torch.cuda.memory_allocated()
     taken, missed = (a - b for a, b in zip(_lib.host().blocks_ahead(), (taken0, missed0)))
     tensors = [t for e in out.values() for t in e.values()]
-    assert torch.cuda.memory_allocated() - before == _blocks_of(tensors)
+    assert after - before == _blocks_of(tensors)
     assert len({t.untyped_storage().data_ptr() for t in tensors if t.numel()}) == sum(1 for t in tensors if t.numel())
-    own = sum(len(e) for n, e in out.items() if pieces[n] != next(iter(e.values())).numel() or pieces[n] == 0)
+    own = sum(len(e) for n, e in out.items()
+              if n in vocab or pieces[n] == 0 or pieces[n] != next(iter(e.values())).numel())
     assert (taken, missed) == (len(tensors) - own, own), (taken, missed, own)
-    assert out[odd]["param"].dtype == torch.float64
+    assert out[odd]["exp_avg"].dtype == torch.float64
     for name, e in want.items():
         for f, a in e.items():
             got = out[name][f]
-            if name == odd and f == "param":
+            if name == odd and f == "exp_avg":
                 got = got.to(torch.float32)      # exact: float64 copies of float32 values
             np.testing.assert_array_equal(t2np(got), a, err_msg=f"{name}/{f}")
