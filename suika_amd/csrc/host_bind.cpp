@@ -22,8 +22,9 @@
 //   make_ops:        sr_schedule's op table as TransferOp objects;
 //   encode_ops:      one rank's TransferOps as sr_lower's op and meta tables;
 //   piece_numels:    elements per op's piece (launch-group balancing);
-//   ops_of_rank:     the ops one destination rank executes;
-//   tensor_runs:     runs of a tensor's consecutive ops and their elements;
+//   rank_runs:       the ops one destination rank executes, grouped by tensor
+//                    with their elements (the drop-in call's prologue);
+//   take_ops:        one launch group's ops;
 //   device_views:    tensors over a mapped hand-off allocation (no copy);
 //   plan_sources:    one launch group: the above in one call, with the
 //                    destinations' allocations made on a helper thread while
@@ -841,51 +842,6 @@ py::array_t<int64_t> piece_numels(py::list ops) {
   return out;
 }
 
-// The ops of `rank` (op.dst_rank == rank), in order.
-py::list ops_of_rank(py::list ops, int64_t rank) {
-  const Names& N = names_();
-  py::list out;
-  const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
-  for (Py_ssize_t k = 0; k < n; ++k) {
-    PyObject* op = PyList_GET_ITEM(ops.ptr(), k);
-    if (as_int(attr(op, N.dst_rank).ptr()) == rank && PyList_Append(out.ptr(), op) != 0)
-      throw py::error_already_set();
-  }
-  return out;
-}
-
-// Runs of consecutive ops of one tensor: (first op of each run, elements of
-// the run's pieces, whether every tensor forms a single run).
-py::tuple tensor_runs(py::list ops) {
-  const Names& N = names_();
-  py::array_t<int64_t> numel = piece_numels(ops);
-  const int64_t* e = numel.data();
-  const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
-  std::vector<int64_t> starts, sums;
-  py::set seen;
-  bool single = true;
-  py::object prev;
-  for (Py_ssize_t k = 0; k < n; ++k) {
-    py::object name = attr(PyList_GET_ITEM(ops.ptr(), k), N.param_name);
-    const bool same = prev && (prev.ptr() == name.ptr() || PyObject_RichCompareBool(prev.ptr(), name.ptr(), Py_EQ) == 1);
-    if (PyErr_Occurred()) throw py::error_already_set();
-    if (!same) {
-      const int had = PySet_Contains(seen.ptr(), name.ptr());
-      if (had < 0) throw py::error_already_set();
-      if (had) single = false;
-      else if (PySet_Add(seen.ptr(), name.ptr()) != 0) throw py::error_already_set();
-      starts.push_back(k);
-      sums.push_back(0);
-      prev = name;
-    }
-    sums.back() += e[k];
-  }
-  py::array_t<int64_t> a({int64_t(starts.size())}), b({int64_t(sums.size())});
-  std::copy(starts.begin(), starts.end(), a.mutable_data());
-  std::copy(sums.begin(), sums.end(), b.mutable_data());
-  return py::make_tuple(a, b, single);
-}
-
 // The ops grouped by tensor, tensors in order of first appearance: (op
 // indices tensor by tensor, where each tensor's indices start (one entry
 // per tensor plus the end), elements of each tensor's pieces, whether every
@@ -1483,8 +1439,6 @@ PYBIND11_MODULE(_suika_host, m) {
       "thread instead) since the process started");
   m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
   m.def("piece_numels", &piece_numels, py::arg("ops"));
-  m.def("ops_of_rank", &ops_of_rank, py::arg("ops"), py::arg("rank"));
-  m.def("tensor_runs", &tensor_runs, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
   m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"));
   m.def("take_ops", &take_ops, py::arg("ops"), py::arg("order"), py::arg("starts"), py::arg("picked"));

@@ -446,28 +446,6 @@ def test_launch_groups_survive_a_group_planned_within_the_overhead(monkeypatch, 
     assert len(groups) == timed[0] + 2, sizes     # and the one after it takes the rest
 
 
-def test_ops_of_rank_and_tensor_runs():
-    """The drop-in call's native prologue: a rank's ops in schedule order, and
-    runs of a tensor's consecutive ops with the elements of their pieces."""
-    from suika_amd import _lib
-    host = _lib.host()
-    for key in CONFIG_ORDER:
-        w = CONFIGS[key]
-        world = schedule_param_transfer(*w.layouts())
-        for r in sorted({op.dst_rank for op in world}):
-            assert host.ops_of_rank(world, r) == [op for op in world if op.dst_rank == r], (key, r)
-        ops = host.ops_of_rank(world, w.dst_rank)
-        starts, numel, single = host.tensor_runs(ops)
-        names = [op.param_name for op in ops]
-        want = [i for i in range(len(ops)) if i == 0 or names[i] != names[i - 1]]
-        assert starts.tolist() == want and single == (len(want) == len(set(names)))
-        ends = want[1:] + [len(ops)]
-        assert numel.tolist() == [sum(op.dst_meta.numel() for op in ops[a:b]) for a, b in zip(want, ends)]
-    ops = host.ops_of_rank(schedule_param_transfer(*CONFIGS["gpt125m_tp2_tp4"].layouts()), 0)
-    assert host.tensor_runs(ops + ops[:1])[2] is False          # a tensor whose ops come back later
-    assert host.tensor_runs([])[0].size == 0
-
-
 def test_rank_runs_and_ordered_result():
     """The one-pass prologue (a rank's ops, their tensor groups in order of
     first appearance and each tensor's elements) against a Python
