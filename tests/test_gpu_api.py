@@ -422,3 +422,35 @@ def test_destination_blocks_made_ahead(key, groups, monkeypatch):
             if name == odd and f == "exp_avg":
                 got = got.to(torch.float32)      # exact: float64 copies of float32 values
             np.testing.assert_array_equal(t2np(got), a, err_msg=f"{name}/{f}")
+
+
+def test_destination_blocks_with_memory_history_recording():
+    """With torch's allocator history recording Python stacks, every
+    allocation -- the helper thread's too -- takes the GIL to record its
+    context.  The calling thread waits for the helper only with the GIL
+    released, so the call completes, matches the oracle, and the snapshot
+    holds the destinations' allocations."""
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] blocks ahead under memory history {w.key}", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    fake = to_device(srcs, w, "cuda")
+    from suika_amd import _lib
+    torch.cuda.synchronize()
+    taken0 = _lib.host().blocks_ahead()[0]
+    torch.cuda.memory._record_memory_history(max_entries=100000, stacks="python")
+    try:
+        out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                     rank=w.dst_rank, fake_source_state_dicts=fake)
+        torch.cuda.synchronize()
+        snap = torch.cuda.memory._snapshot()
+    finally:
+        torch.cuda.memory._record_memory_history(enabled=None)
+    assert _lib.host().blocks_ahead()[0] > taken0, "the helper thread made no block"
+    ptrs = {t.untyped_storage().data_ptr() for e in out.values() for t in e.values() if t.numel()}
+    traced = {ev["addr"] for trace in snap["device_traces"] for ev in trace if ev["action"] == "alloc"}
+    assert ptrs <= traced, f"{len(ptrs - traced)} destinations not in the allocator's history"
+    for name, e in want.items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
