@@ -248,6 +248,21 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
                       hipStream_t stream);
 
 /*
+ * Pay this process's first-use costs of the library on the current device
+ * now: load its GPU code (one empty launch), create the device's setup
+ * stream and events, and make one host-to-device copy from pinned memory on
+ * `stream` and on the setup stream (a process's first copies on a stream
+ * set up the runtime's copy path).  Returns when that work is done; the
+ * memory used goes to the library's table cache.  Optional: every entry
+ * point does the same on first use.  No counterpart in the reference: it
+ * serves callers that start fresh processes for a live migration (the old
+ * and new worlds' ranks), which can pay these costs -- tens of milliseconds
+ * with many processes on one GPU -- while they wait for each other instead
+ * of inside the transfer.
+ */
+int sr_prepare(hipStream_t stream);
+
+/*
  * Release a plan and its device tables.  Waits for the plan's own launches
  * still in flight (it may follow an asynchronous call directly); does not
  * synchronize anything else.  NULL is ignored.  The table memory and events

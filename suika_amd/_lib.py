@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "sr_unpack",
     "sr_gather",
     "sr_gather_noalloc",
+    "sr_prepare",
     "sr_plan_destroy",
     "sr_schedule",
     "sr_lower",
@@ -311,6 +312,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_gather.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_gather_noalloc.restype = ctypes.c_int
     lib.sr_gather_noalloc.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
+    lib.sr_prepare.restype = ctypes.c_int
+    lib.sr_prepare.argtypes = [vp]
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
     i64 = ctypes.c_int64

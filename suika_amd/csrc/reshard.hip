@@ -545,6 +545,9 @@ constexpr uint32_t kEmitTiles = 4096;
 // of GPU time, less than a wait across streams costs the host.
 constexpr uint64_t kInlineSetupTiles = 65536;
 
+// An empty kernel: launching it loads the library's GPU code (sr_prepare).
+__global__ void sr_prepare_kernel() {}
+
 struct EmitChunk {
   uint32_t item;
   uint32_t chunk;   // the item's tiles [chunk * kEmitTiles, (chunk + 1) * kEmitTiles)
@@ -1853,6 +1856,52 @@ int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
   if (rc != SR_OK) return rc;
   return run_phase(plan, plan->gather, kGather,
                    pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size()), stream);
+}
+
+int sr_prepare(hipStream_t stream) {
+  int dev = -1;
+  SR_HIP_TRY(hipGetDevice(&dev));
+  TableCache& cache = table_cache();
+  hipStream_t setup = nullptr;
+  int rc = cache.setup_stream(dev, &setup);
+  if (rc != SR_OK) return rc;
+  // one upload of half a block on each stream (a first copy of that size
+  // sets up the runtime's copy path for the stream) and one launch (loads
+  // the library's GPU code); the blocks then go back to the cache
+  constexpr size_t kBytes = size_t(1) << 20;
+  void* d = nullptr;
+  unsigned char* h = nullptr;
+  size_t dcap = 0, hcap = 0;
+  if ((rc = cache.get(false, dev, kBytes, &d, &dcap)) != SR_OK) return rc;
+  if ((rc = cache.get(true, dev, kBytes, reinterpret_cast<void**>(&h), &hcap)) != SR_OK) {
+    cache.put(false, dev, d, dcap);
+    return rc;
+  }
+  std::memset(h, 0, hcap);
+  const size_t half = std::min(dcap, hcap) / 2;
+  const hipStream_t streams[2] = {stream, setup};
+  hipError_t err = hipSuccess;
+  for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+    err = hipMemcpyAsync(static_cast<unsigned char*>(d) + i * half, h + i * half, half, hipMemcpyHostToDevice,
+                         streams[i]);
+    if (err == hipSuccess) {
+      hipLaunchKernelGGL(sr_prepare_kernel, dim3(1), dim3(64), 0, streams[i]);
+      err = hipGetLastError();
+    }
+  }
+  for (hipStream_t st : streams) {
+    const hipError_t e = hipStreamSynchronize(st);
+    if (err == hipSuccess) err = e;
+  }
+  cache.put(false, dev, d, dcap);
+  cache.put(true, dev, h, hcap);
+  if (err != hipSuccess) return fail(SR_EHIP, "sr_prepare: %s", hipGetErrorString(err));
+  // events for the first plans' phases
+  hipEvent_t ev[8] = {};
+  for (hipEvent_t& e : ev)
+    if ((rc = cache.get_event(dev, &e)) != SR_OK) break;
+  for (hipEvent_t e : ev) cache.put_event(dev, e);
+  return rc;
 }
 
 int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,

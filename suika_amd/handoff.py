@@ -39,6 +39,7 @@ does, reading from the mapped memory.
 from __future__ import annotations
 
 import ctypes
+import threading
 import time
 from collections import OrderedDict
 from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple
@@ -248,6 +249,9 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
     from .migration import forcefully_free_tensor, merge_model_and_optimizer_state_dict
 
     rank = dist.get_rank(world)
+    # the library's first-use costs are paid while the new world starts
+    warm = _WarmUp(device, optimizer=False)
+    warm.start()
     if rank == 0:
         old_world_size = dist.get_world_size(world)
         IPC_queues[0].put(old_world_size)
@@ -257,6 +261,7 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
         is_scale_up = new_world_size = None
     is_scale_up, new_world_size = _broadcast_objects(is_scale_up, new_world_size, group=world)
     log_func(f"migration_save: is_scale_up = {is_scale_up} (new world size {new_world_size})")
+    warm.join()
 
     param_layout = ParamLayout()
     param_layout.gather(model, world)
@@ -276,7 +281,11 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
     del source_state_dict
     # and return the memory to the device for the new plan's processes, as
     # the reference's cuda_gc does after sending (utils.py:248-253, 385)
+    t2 = time.perf_counter()
     torch.cuda.empty_cache()
+    t3 = time.perf_counter()
+    log_func(f"migration_save: state released ({(t2 - t1) * 1e3:.2f} ms), device memory returned "
+             f"({(t3 - t2) * 1e3:.2f} ms)")
     try:
         records = [None] * dist.get_world_size(world)
         dist.all_gather_object(records, handoff.record(), group=world)
@@ -294,6 +303,53 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
     finally:
         handoff.release()
     log_func("migration_save: end")
+
+
+class _WarmUp(threading.Thread):
+    """First-use costs of a fresh process of a live migration, paid on a
+    thread while it waits for the other world (the old ranks for the new
+    world's handshake, the new ranks for the old world's message):
+
+    * the reshard library's: ``sr_prepare`` loads its GPU code and sets up
+      its streams and the runtime's copy path, and one tiny gather warms
+      the drop-in call's host side.  With twelve processes on one MI355X
+      these took 30-57 ms per first launch, 40-54 ms per first table upload
+      and 26 ms for the setup stream, inside the pack and the reshard;
+    * with an optimizer to build, torch.optim's: a process's first optimizer
+      imports torch's compiler front end (torch._dynamo, about 0.4 s).
+
+    ``library_done`` is set once the library is no longer in use here; the
+    caller waits for it before its own library calls and joins the thread
+    before building its optimizer.  Failures are ignored: the real calls
+    report their own."""
+
+    def __init__(self, device: torch.device, optimizer: bool):
+        super().__init__(name="suika-warm-up", daemon=True)
+        self.device = device
+        self.optimizer = optimizer
+        self.library_done = threading.Event()
+
+    def run(self) -> None:
+        try:
+            from .meta import TensorMeta, TransferOp
+            from .migration import execute_param_transfer
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device).cuda_stream
+                _lib.lib().sr_prepare(ctypes.c_void_p(stream))
+                meta = TensorMeta(name="warm-up", dtype=torch.float32, shape=(64,))
+                src = {0: {"warm-up": {"param": torch.zeros(64, device=self.device)}}}
+                execute_param_transfer([TransferOp("warm-up", 0, 0, meta, meta)], {}, self.device,
+                                       [("param", "normal")], rank=0, fake_source_state_dicts=src)
+                torch.cuda.synchronize(self.device)
+        except Exception:
+            pass
+        finally:
+            self.library_done.set()
+        if self.optimizer:
+            try:
+                torch.optim.SGD([torch.nn.Parameter(torch.zeros(1))], lr=0.0)
+            except Exception:
+                pass
 
 
 def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.device, world,
@@ -316,9 +372,13 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
 
     target_param_layout = ParamLayout()
     target_param_layout.gather(model, world)
-    # old rank i's message, or the launcher's placeholder when there is none
+    # old rank i's message, or the launcher's placeholder when there is none;
+    # the process's first-use costs are paid meanwhile
+    warm = _WarmUp(device, optimizer_provider is not None)
+    warm.start()
     msg = IPC_queues[0].get(block=True)
     log_func("migration_load: hand-off message received")
+    warm.library_done.wait()
     source_param_layout, other_context_dict, records = _broadcast_objects(
         msg.get("source_param_layout"), msg.get("other_context_dict"), msg.get("handoff"), group=world)
     del msg
@@ -327,6 +387,7 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
         log_func("migration_load: no checkpoint received; skip loading")
         if hasattr(model, "instantiate") and getattr(model, "on_meta", False):
             model.instantiate()
+        warm.join()
         return (optimizer_provider(), None) if optimizer_provider else None
 
     t0 = time.perf_counter()
@@ -356,6 +417,7 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
     model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
     model.load_state_dict(model_state_dict, assign=True)
     log_func("migration_load: model state adopted")
+    warm.join()
     if optimizer_provider:
         optimizer = optimizer_provider()
     if optimizer:

@@ -454,3 +454,27 @@ def test_destination_blocks_with_memory_history_recording():
     for name, e in want.items():
         for f, a in e.items():
             np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
+def test_prepare_then_reshard():
+    """sr_prepare (a process's first-use costs paid ahead: GPU code, setup
+    stream, copy path) succeeds on the current stream and on another one,
+    any number of times, and the reshards after it are unchanged."""
+    import ctypes
+
+    from suika_amd import _lib
+    L = _lib.lib()
+    print("[gpu api] sr_prepare", flush=True)
+    side = torch.cuda.Stream()
+    for stream in (torch.cuda.current_stream(), side, torch.cuda.current_stream()):
+        assert L.sr_prepare(ctypes.c_void_p(stream.cuda_stream)) == _lib.SR_OK, _lib.last_error(L)
+    w = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    out = execute_param_transfer(w.ops(), {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                 rank=w.dst_rank, fake_source_state_dicts=to_device(srcs, w, "cuda"))
+    torch.cuda.synchronize()
+    for name, e in want.items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
