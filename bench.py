@@ -682,12 +682,16 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
     new_recs = [results[("loaded", r)] for r in range(new_ws)]
     start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done: packing begins
     pack_ms = max((at(l, "packed") - at(l, "is_scale_up")) * 1e3 for l in old_logs)
+    # the old state's release: its tensors freed and the allocator's cache
+    # returned to the device (one hipFree per segment), before the message
+    release_ms = max((at(l, "state released") - at(l, "packed")) * 1e3 for l in old_logs)
     end = max(rec["t_return"] for rec in new_recs)
     reshard = [(at(rec["log"], "resharded") - at(rec["log"], "mapped the state")) * 1e3 for rec in new_recs]
     return {
         "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
         "state_bytes_received": sum(rec["bytes"] for rec in new_recs),
         "pack_ms_max": round(pack_ms, 2),
+        "release_ms_max": round(release_ms, 2),
         "reshard_ms_max": round(max(reshard), 2),
         "handoff_ms": round((end - start) * 1e3, 1),
         "handoff_ms_note": ("wall time from the old world's handshake to the last new rank's return from "
