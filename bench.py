@@ -682,11 +682,11 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
     new_recs = [results[("loaded", r)] for r in range(new_ws)]
     start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done: packing begins
     pack_ms = max((at(l, "packed") - at(l, "is_scale_up")) * 1e3 for l in old_logs)
-    # the old state's release: its tensors freed and the allocator's cache
-    # returned to the device (one hipFree per segment), before the message
+    # the old state's release after the message is sent: its tensors freed and
+    # the allocator's cache returned to the device (one hipFree per segment)
     release_ms = max((at(l, "state released") - at(l, "packed")) * 1e3 for l in old_logs)
     end = max(rec["t_return"] for rec in new_recs)
-    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "mapped the state")) * 1e3 for rec in new_recs]
+    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "old world has released")) * 1e3 for rec in new_recs]
     return {
         "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
         "state_bytes_received": sum(rec["bytes"] for rec in new_recs),

@@ -65,6 +65,9 @@ dummy_migration_IPC_state_dict = {
 }
 
 DONE = "suika_amd: handoff complete"
+# Old rank 0 to new rank 0, after the message: every old rank has released
+# its state and returned the memory to the device.
+RELEASED = "suika_amd: old state released"
 
 
 def pack_layout(nbytes: Sequence[int], chunk_bytes: int = CHUNK_BYTES) -> Tuple[List[Tuple[int, int]], List[int]]:
@@ -272,20 +275,6 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
     t1 = time.perf_counter()
     log_func(f"migration_save: packed {handoff.bytes / 1e9:.3f} GB into {len(handoff.chunks)} hand-off "
              f"allocation(s) in {(t1 - t0) * 1e3:.2f} ms")
-    # the state now lives in the hand-off allocations; release it as the
-    # reference releases every tensor it has sent (utils.py:372-376)
-    for entry in source_state_dict.values():
-        for t in entry.values():
-            if isinstance(t, Tensor) and t.is_cuda:
-                forcefully_free_tensor(t)
-    del source_state_dict
-    # and return the memory to the device for the new plan's processes, as
-    # the reference's cuda_gc does after sending (utils.py:248-253, 385)
-    t2 = time.perf_counter()
-    torch.cuda.empty_cache()
-    t3 = time.perf_counter()
-    log_func(f"migration_save: state released ({(t2 - t1) * 1e3:.2f} ms), device memory returned "
-             f"({(t3 - t2) * 1e3:.2f} ms)")
     try:
         records = [None] * dist.get_world_size(world)
         dist.all_gather_object(records, handoff.record(), group=world)
@@ -294,8 +283,27 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
             IPC_queues[0].put({"source_param_layout": param_layout, "source_state_dict": {},
                                "other_context_dict": other_context_dict, "handoff": records})
             log_func("migration_save: hand-off sent to the new rank")
+        # The state now lives in the hand-off allocations: release it, as the
+        # reference releases every tensor it has sent (utils.py:372-376), and
+        # return the memory to the device for the new world, as its cuda_gc
+        # does after sending (utils.py:248-253, 385).  The new world maps the
+        # hand-off and plans meanwhile; it allocates its destinations only
+        # after old rank 0's RELEASED, sent once every old rank is done.
+        t2 = time.perf_counter()
+        for entry in source_state_dict.values():
+            for t in entry.values():
+                if isinstance(t, Tensor) and t.is_cuda:
+                    forcefully_free_tensor(t)
+        del source_state_dict
+        t3 = time.perf_counter()
+        torch.cuda.empty_cache()
+        t4 = time.perf_counter()
+        log_func(f"migration_save: state released ({(t3 - t2) * 1e3:.2f} ms), device memory returned "
+                 f"({(t4 - t3) * 1e3:.2f} ms)")
+        dist.barrier(world)
         # the new world maps these allocations until it has resharded
         if rank == 0:
+            IPC_queues[0].put(RELEASED)
             ack = IPC_queues[1].get(block=True)
             assert ack == DONE, f"migration_save: unexpected acknowledgement {ack!r}"
         dist.barrier(world)
@@ -394,8 +402,16 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
     ops = schedule_param_transfer(source_param_layout, target_param_layout)
     needed = sorted({op.src_rank for op in ops if op.dst_rank == rank})
     mapped = MappedSources(records, needed, device)
+    t_map = time.perf_counter()
     log_func(f"migration_load: mapped the state of old rank(s) {needed}")
     try:
+        # the destinations are allocated only once the old world has
+        # returned its state's memory to the device
+        if rank == 0:
+            note = IPC_queues[0].get(block=True)
+            assert note == RELEASED, f"migration_load: unexpected message {note!r}"
+        dist.barrier(world)
+        log_func("migration_load: the old world has released its state")
         t1 = time.perf_counter()
         target_state_dict = execute_param_transfer(
             transfer_ops=ops, source_state_dict={}, device=device,
@@ -405,7 +421,7 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
         t2 = time.perf_counter()
     finally:
         mapped.close()
-    log_func(f"migration_load: mapped {len(needed)} old rank(s) in {(t1 - t0) * 1e3:.2f} ms, resharded in "
+    log_func(f"migration_load: mapped {len(needed)} old rank(s) in {(t_map - t0) * 1e3:.2f} ms, resharded in "
              f"{(t2 - t1) * 1e3:.2f} ms")
     dist.barrier(world)
     if rank == 0:
