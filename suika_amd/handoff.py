@@ -15,18 +15,21 @@ Here, with every old and new rank on the same GPU:
   the queues, :1395-1405 / :1587-1598);
 * each old rank packs its merged state (``merge_model_and_optimizer_state_dict``)
   into a few device allocations of its own with one gather launch, exports
-  them (``sr_handoff_alloc``, at most 1 GiB each, always below 2 GiB), frees
-  its state tensors as the reference frees each sent tensor, and the old world
-  all-gathers the export records (handles, offsets, shapes: CPU objects);
+  them (``sr_handoff_alloc``, at most 1 GiB each, always below 2 GiB), and the
+  old world all-gathers the export records (handles, offsets, shapes: CPU
+  objects);
 * old rank ``i`` sends the source layout, the context and every old rank's
   record to new rank ``i`` over its forward queue; new ranks without an old
   counterpart read the launcher's placeholder (``dummy_migration_IPC_state_dict``),
   and the new world takes rank 0's message;
+* each old rank then frees its state tensors, as the reference frees each sent
+  tensor, and returns the memory to the device; once all have, old rank 0
+  sends ``RELEASED`` after its message;
 * each new rank maps the allocations of the old ranks its pieces come from
-  (``sr_handoff_open``), views the state there as tensors without copying, and
-  runs ``execute_param_transfer`` (one gather per launch group) straight from
-  them into one destination arena that the model adopts with
-  ``load_state_dict(assign=True)``;
+  (``sr_handoff_open``) and views the state there as tensors without copying;
+  after ``RELEASED`` it runs ``execute_param_transfer`` (one gather per launch
+  group) straight from them into one destination arena that the model adopts
+  with ``load_state_dict(assign=True)``;
 * after the new world's barrier, new rank 0 acknowledges on rank 0's backward
   queue; the old world then frees its allocations and returns.
 
