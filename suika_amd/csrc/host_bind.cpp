@@ -5,8 +5,8 @@
 // tensor (to check it and read its shape, dtype and address) and allocates
 // every destination tensor.  In Python that costs a few microseconds per
 // tensor, which on transfers of many small tensors exceeds the GPU time of
-// the copy itself.  These two functions do the same walks over the state
-// dicts and the slot tables in C++:
+// the copy itself.  These functions do the same walks over the state dicts,
+// the ops and the slot tables in C++:
 //
 //   collect_sources: (ops, rank -> state dict, fields) -> source specs
 //                    (sr_src_spec rows), dtypes and device addresses, with
@@ -28,10 +28,12 @@
 //   device_views:    tensors over a mapped hand-off allocation (no copy);
 //   plan_sources:    one launch group: the above in one call, with the
 //                    destinations' allocations made on a helper thread while
-//                    this thread plans.
+//                    this thread plans, and the launch;
+//   blocks_ahead:    counts of destinations built on the helper's blocks.
 //
-// No device work happens here; the tensors come from torch's caching
-// allocator on the device's current stream, as torch.empty would.
+// Apart from plan_sources' launch, no device work happens here; the tensors
+// come from torch's caching allocator on the device's current stream, as
+// torch.empty would.
 
 #include <torch/extension.h>
 #include <c10/core/DeviceGuard.h>
