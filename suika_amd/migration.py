@@ -398,8 +398,7 @@ class _LaunchGroups:
         self.per_name = max(1, int(tensors_per_name))
         # op indices tensor by tensor, tensors in order of first appearance,
         # and each tensor's elements (``runs``: already computed for ``ops``)
-        self.order, self.starts, numel, self.single = (runs if runs is not None
-                                                       else _lib.host().name_runs(self.ops))[:4]
+        self.order, self.starts, numel = (runs if runs is not None else _lib.host().name_runs(self.ops))[:3]
         self.n = len(numel)
         gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
         self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
