@@ -106,3 +106,26 @@ def test_fuzz_gpu(seed):
     for name, ent in want.items():
         for f, a in ent.items():
             np.testing.assert_array_equal(got[name][f], a, err_msg=f"{w.key}: {name}/{f}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", GPU_SEEDS[::3])
+def test_fuzz_gpu_fused_direct(seed, monkeypatch):
+    """The drop-in call's default path -- one native call per launch group,
+    fresh destinations built on the helper thread's blocks -- on random
+    layouts, after dirtying the allocator cache; every other case in three
+    round-robin launch groups."""
+    from suika_amd import migration as M
+    from tests.harness import dirty_cache_execute, round_robin_groups
+    if seed % 2:
+        monkeypatch.setattr(M, "_pipeline_groups", round_robin_groups(3))
+    w = random_case(seed)
+    print(f"[gpu fuzz fused] {w}", flush=True)
+    glob = index_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    got = dirty_cache_execute(w, srcs)
+    assert set(got) == set(want)
+    for name, ent in want.items():
+        for f, a in ent.items():
+            np.testing.assert_array_equal(got[name][f], a, err_msg=f"{w.key}: {name}/{f}")
