@@ -71,6 +71,10 @@ def parse_args(argv=None):
     ap.add_argument("--handoff", action="store_true",
                     help="only run the live migration of the workload between old and new processes on "
                          "this GPU (migration_save / migration_load) and print its timings, then exit")
+    ap.add_argument("--checkpoint", metavar="DIR", default=None,
+                    help="only run the checkpoint-based migration of the workload (the reference's "
+                         "comparator to live migration): the old world's processes checkpoint_save into "
+                         "DIR, then new processes checkpoint_load it on this GPU; print the timings, then exit")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -539,25 +543,12 @@ def _handoff_old(rank, key, port, queues, events):
     try:
         os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
         from suika_amd import migration_save
-        from suika_amd.inventory import build_module
-        from suika_amd.workloads import CONFIGS, shard_global
+        from suika_amd.workloads import CONFIGS
         w = CONFIGS[key]
         dist.init_process_group("gloo", rank=rank, world_size=w.src.world)
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
-        dt = w.dtypes
-        pfield = "param" if "param" in w.src_fields else "master"
-        model = build_module(w.model, w.src, rank, dt[pfield], device=dev)
-        opt = _state_optimizer(model.parameters())
-        metas = w.layouts()[0].layout[rank]
-        for name, p in model.named_parameters():
-            glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
-            with torch.no_grad():
-                p.copy_(shard_global(glob[pfield], metas[name]))
-            opt.state[p] = {f: shard_global(glob[f], metas[name]) for f in w.src_fields if f != pfield}
-            del glob
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
+        model, opt = _seed_old_rank(w, rank, dev)
         log = []
         events.put(("ready", rank, None))
         migration_save(queues[rank], model, opt, other_context={"iter": 1}, log_func=_timed_log(log))
@@ -579,37 +570,21 @@ def _handoff_new(rank, key, port, queues, events):
         os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
         from suika_amd import migration_load
         from suika_amd.inventory import build_module
-        from suika_amd.workloads import CONFIGS, shard_global
+        from suika_amd.workloads import CONFIGS
         w = CONFIGS[key]
         dist.init_process_group("gloo", rank=rank, world_size=w.dst.world)
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
-        dt = w.dtypes
         pfield = "param" if "param" in w.src_fields else "master"
-        model = build_module(w.model, w.dst, rank, dt[pfield], device="meta")
+        model = build_module(w.model, w.dst, rank, w.dtypes[pfield], device="meta")
         log = []
         t0 = time.time()
         opt, ctx = migration_load(queues[rank], model, lambda: _state_optimizer(model.parameters()),
                                   log_func=_timed_log(log))
         t1 = time.time()
-        # every received tensor against the same seeded state, cut for this rank
-        metas = w.layouts()[1].layout[rank]
-        state = opt.state_dict()["state"]
-        n, bad = 0, []
-        for idx, (name, p) in enumerate(model.named_parameters()):
-            glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
-            got = {pfield: p, **{f: state[idx][f] for f in w.src_fields if f != pfield}}
-            for f, t in got.items():
-                want = shard_global(glob[f], metas[name])
-                n += 1
-                if t.dtype != want.dtype or t.shape != want.shape or \
-                        not torch.equal(t.reshape(-1).view(torch.uint8), want.reshape(-1).view(torch.uint8)):
-                    bad.append(f"{name}/{f}")
-            del glob
-        nbytes = sum(p.numel() * p.element_size() for p in model.parameters()) + \
-            sum(t.numel() * t.element_size() for e in state.values() for t in e.values() if torch.is_tensor(t))
-        events.put(("loaded", rank, {"log": log, "t_call": t0, "t_return": t1, "tensors": n, "bad": bad[:5],
-                                     "mismatched": len(bad), "bytes": nbytes}))
+        rec = _check_new_rank(w, rank, model, opt, dev)
+        rec.update(log=log, t_call=t0, t_return=t1)
+        events.put(("loaded", rank, rec))
     except BaseException:
         events.put(("error", rank, traceback.format_exc()))
     finally:
@@ -707,6 +682,201 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
     }
 
 
+def _seed_old_rank(w, rank: int, dev):
+    """An old rank's model (parameters on ``dev``) and state optimizer holding
+    its shard of the seeded global state."""
+    import torch
+    from suika_amd.inventory import build_module
+    from suika_amd.workloads import shard_global
+    dt = w.dtypes
+    pfield = "param" if "param" in w.src_fields else "master"
+    model = build_module(w.model, w.src, rank, dt[pfield], device=dev)
+    opt = _state_optimizer(model.parameters())
+    metas = w.layouts()[0].layout[rank]
+    for name, p in model.named_parameters():
+        glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
+        with torch.no_grad():
+            p.copy_(shard_global(glob[pfield], metas[name]))
+        opt.state[p] = {f: shard_global(glob[f], metas[name]) for f in w.src_fields if f != pfield}
+        del glob
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return model, opt
+
+
+def _check_new_rank(w, rank: int, model, opt, dev) -> dict:
+    """Every tensor a new rank received against the seeded state cut for it."""
+    import torch
+    from suika_amd.workloads import shard_global
+    pfield = "param" if "param" in w.src_fields else "master"
+    metas = w.layouts()[1].layout[rank]
+    state = opt.state_dict()["state"]
+    n, bad = 0, []
+    for idx, (name, p) in enumerate(model.named_parameters()):
+        glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
+        got = {pfield: p, **{f: state[idx][f] for f in w.src_fields if f != pfield}}
+        for f, t in got.items():
+            want = shard_global(glob[f], metas[name])
+            n += 1
+            if t.dtype != want.dtype or t.shape != want.shape or \
+                    not torch.equal(t.reshape(-1).view(torch.uint8), want.reshape(-1).view(torch.uint8)):
+                bad.append(f"{name}/{f}")
+        del glob
+    nbytes = sum(p.numel() * p.element_size() for p in model.parameters()) + \
+        sum(t.numel() * t.element_size() for e in state.values() for t in e.values() if torch.is_tensor(t))
+    return {"tensors": n, "bad": bad[:5], "mismatched": len(bad), "bytes": nbytes}
+
+
+def _ckpt_old(rank, key, port, ckpt_dir, events):
+    import traceback
+
+    import torch
+    import torch.distributed as dist
+    try:
+        os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
+        from suika_amd import checkpoint_save
+        from suika_amd.workloads import CONFIGS
+        w = CONFIGS[key]
+        dist.init_process_group("gloo", rank=rank, world_size=w.src.world)
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        model, opt = _seed_old_rank(w, rank, dev)
+        dist.barrier()
+        t0 = time.time()
+        checkpoint_save(model, opt, {"iter": 1}, ckpt_dir)
+        dist.barrier()
+        events.put(("saved", rank, {"t_call": t0, "t_return": time.time()}))
+    except BaseException:
+        events.put(("error", rank, traceback.format_exc()))
+    finally:
+        import torch.distributed as dist
+        if dist.is_initialized():
+            dist.destroy_process_group()
+
+
+def _ckpt_new(rank, key, port, ckpt_dir, start, events):
+    import traceback
+
+    import torch
+    import torch.distributed as dist
+    try:
+        os.environ.update(MASTER_ADDR="127.0.0.1", MASTER_PORT=str(port))
+        from suika_amd import checkpoint_load
+        from suika_amd.inventory import build_module
+        from suika_amd.workloads import CONFIGS
+        w = CONFIGS[key]
+        dist.init_process_group("gloo", rank=rank, world_size=w.dst.world)
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        pfield = "param" if "param" in w.src_fields else "master"
+        model = build_module(w.model, w.dst, rank, w.dtypes[pfield], device="meta")
+        events.put(("ready", rank, None))
+        start.wait()
+        t0 = time.time()
+        opt, ctx = checkpoint_load(model, lambda: _state_optimizer(model.parameters()), ckpt_dir, device=dev)
+        t1 = time.time()
+        rec = _check_new_rank(w, rank, model, opt, dev)
+        rec.update(t_call=t0, t_return=t1)
+        events.put(("loaded", rank, rec))
+    except BaseException:
+        events.put(("error", rank, traceback.format_exc()))
+    finally:
+        import torch.distributed as dist
+        if dist.is_initialized():
+            dist.destroy_process_group()
+
+
+def checkpoint_leg(key: str, ckpt_dir: str, timeout_s: float = 900.0) -> dict:
+    """Checkpoint-based migration of workload ``key`` on this GPU, the
+    reference's comparator to live migration (Suika/migration.py:1156-1305):
+    the old plan's ranks (seeded state) checkpoint_save into ``ckpt_dir``,
+    then the new plan's ranks, started and waiting, checkpoint_load it; every
+    received tensor is checked bit for bit."""
+    import multiprocessing as mp
+    import queue as _queue
+    import shutil
+    import socket
+
+    from suika_amd.workloads import CONFIGS
+    w = CONFIGS[key]
+    old_ws, new_ws = w.src.world, w.dst.world
+    assert max(old_ws, new_ws) <= 16, "at most 16 processes on the GPU"
+    os.makedirs(ckpt_dir, exist_ok=True)
+    # the files hold the whole model state once
+    per_elem = sum(w.dtypes[f].itemsize for f in w.src_fields)
+    need = sum(m.numel() for metas in w.layouts()[0].layout.values() for m in metas.values()) * per_elem
+    free = shutil.disk_usage(ckpt_dir).free
+    assert need <= free, f"checkpoint leg: {need / 1e9:.1f} GB needed in {ckpt_dir}, {free / 1e9:.1f} GB free"
+    ctx = mp.get_context("spawn")
+    events = ctx.Queue()
+    start = ctx.Event()
+    results = {}
+    deadline = time.time() + timeout_s
+
+    def wait_for(kind, count):
+        while sum(1 for ev, _ in results if ev == kind) < count:
+            try:
+                ev, rank, payload = events.get(timeout=max(1.0, deadline - time.time()))
+            except _queue.Empty:
+                raise RuntimeError(f"checkpoint leg: timed out waiting for {kind}; have {sorted(results)}")
+            if ev == "error":
+                raise RuntimeError(f"checkpoint leg: rank {rank} failed:\n{payload}")
+            results[(ev, rank)] = payload
+            print(f"[bench] checkpoint: {ev} {rank}", file=sys.stderr, flush=True)
+
+    def port():
+        with socket.socket() as s_:
+            s_.bind(("127.0.0.1", 0))
+            return s_.getsockname()[1]
+
+    procs = []
+    try:
+        p_old, p_new = port(), port()
+        for r in range(old_ws):
+            procs.append(ctx.Process(target=_ckpt_old, args=(r, key, p_old, ckpt_dir, events)))
+            procs[-1].start()
+        wait_for("saved", old_ws)
+        for p in procs:
+            p.join(timeout=max(1.0, deadline - time.time()))
+        # the new world starts once the old one has exited, as after a restart
+        new_procs = [ctx.Process(target=_ckpt_new, args=(r, key, p_new, ckpt_dir, start, events))
+                     for r in range(new_ws)]
+        for p in new_procs:
+            p.start()
+        procs += new_procs
+        wait_for("ready", new_ws)
+        start.set()
+        wait_for("loaded", new_ws)
+        for p in new_procs:
+            p.join(timeout=max(1.0, deadline - time.time()))
+    finally:
+        for p in procs:
+            if p.is_alive():
+                p.kill()
+                p.join(10)
+        for f in os.listdir(ckpt_dir):
+            if f.startswith("state_dict_") or f in ("param_layout.pt", "other_context.pt"):
+                os.remove(os.path.join(ckpt_dir, f))
+
+    saved = [results[("saved", r)] for r in range(old_ws)]
+    loaded = [results[("loaded", r)] for r in range(new_ws)]
+    save_ms = (max(r["t_return"] for r in saved) - min(r["t_call"] for r in saved)) * 1e3
+    load_ms = (max(r["t_return"] for r in loaded) - min(r["t_call"] for r in loaded)) * 1e3
+    return {
+        "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
+        "state_bytes_received": sum(r["bytes"] for r in loaded),
+        "save_ms": round(save_ms, 1), "load_ms": round(load_ms, 1),
+        "checkpoint_ms": round(save_ms + load_ms, 1),
+        "checkpoint_ms_note": ("checkpoint_save of every old rank (first call to the last return, with a "
+                               "barrier after) plus checkpoint_load of every new rank (processes started and "
+                               "waiting; first call to the last return); process start and exit excluded"),
+        "parity": {"tensors": sum(r["tensors"] for r in loaded),
+                   "mismatched": sum(r["mismatched"] for r in loaded),
+                   "first_mismatches": [b for r in loaded for b in r["bad"]][:5],
+                   "against": "the same seeded global tensors cut for each new rank"},
+    }
+
+
 def cpu_model() -> str:
     try:
         import subprocess
@@ -744,6 +914,10 @@ def main(argv=None) -> int:
     if args.handoff:
         rec = handoff_leg(key)
         print(json.dumps({"handoff": rec}), flush=True)
+        return 0 if rec["parity"]["mismatched"] == 0 else 1
+    if args.checkpoint:
+        rec = checkpoint_leg(key, args.checkpoint)
+        print(json.dumps({"checkpoint": rec}), flush=True)
         return 0 if rec["parity"]["mismatched"] == 0 else 1
     w = CONFIGS[key]
     dev = torch.device("cuda", 0)

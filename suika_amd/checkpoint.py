@@ -241,6 +241,11 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
     else:
         raise TypeError(f"optimizer should be Optimizer or Callable, but got {type(optimizer)}")
     rank, _ = _rank_and_world(world)
+    # a fresh process's first-use costs (the library's, torch.optim's) are
+    # paid on a thread while this one reads the checkpoint
+    from .handoff import _WarmUp
+    warm = _WarmUp(device, optimizer_provider is not None)
+    warm.start()
 
     try:
         source_layout = layout_from_reference(load_reference_object(os.path.join(checkpoint_dir, LAYOUT_FILE)))
@@ -248,6 +253,7 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
             load_reference_object(os.path.join(checkpoint_dir, CONTEXT_FILE)))
     except FileNotFoundError as e:
         log_func(f"checkpoint_load: [warning] checkpoint file not found, skip loading\n{e}")
+        warm.join()
         return (optimizer_provider(), None) if optimizer_provider else None
 
     target_layout = _gather_layout(model, world)
@@ -268,6 +274,7 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
                      for name in needed[src] if name in sd}
         del sd
     self_source = fake.get(rank, {})
+    warm.library_done.wait()
     target = execute_param_transfer(
         transfer_ops=ops, source_state_dict=dict(self_source), device=device,
         expected_sub_fields=other_context_dict["expected_sub_fields"], world=world,
@@ -280,6 +287,7 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
     model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
     on_meta = any(p.is_meta for p in model.parameters())
     model.load_state_dict(model_state_dict, assign=on_meta)
+    warm.join()
     if optimizer_provider:
         optimizer = optimizer_provider()
     if optimizer is not None and optimizer_state_dict["param_groups"] is not None:
