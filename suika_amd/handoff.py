@@ -317,9 +317,10 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
 
 
 class _WarmUp(threading.Thread):
-    """First-use costs of a fresh process of a live migration, paid on a
-    thread while it waits for the other world (the old ranks for the new
-    world's handshake, the new ranks for the old world's message):
+    """First-use costs of a fresh process of a migration, paid on a thread
+    while it waits: in a live migration the old ranks for the new world's
+    handshake and the new ranks for the old world's message; in
+    ``checkpoint_load`` while the files are read:
 
     * the reshard library's: ``sr_prepare`` loads its GPU code and sets up
       its streams and the runtime's copy path, and one tiny gather warms
