@@ -252,8 +252,9 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
  * now: load its GPU code (one empty launch), create the device's setup
  * stream and events, and make one host-to-device copy from pinned memory on
  * `stream` and on the setup stream (a process's first copies on a stream
- * set up the runtime's copy path).  Returns when that work is done; the
- * memory used goes to the library's table cache.  Optional: every entry
+ * set up the runtime's copy path).  Returns when that work, and whatever was
+ * queued on `stream` before it, is done; the memory used goes to the
+ * library's table cache.  Optional: every entry
  * point does the same on first use.  No counterpart in the reference: it
  * serves callers that start fresh processes for a live migration (the old
  * and new worlds' ranks), which can pay these costs -- tens of milliseconds
