@@ -44,6 +44,32 @@ def test_execute_semantics_step_and_clear():
         assert out[name]["step"].device.type == "cuda" and out[name]["step"].numel() == 1
 
 
+@pytest.mark.parametrize("route", ["direct", "buffers"])
+def test_execute_with_no_ops_for_this_rank(route):
+    """A rank the schedule sends nothing to (an empty schedule, or one for
+    other ranks only) gets an empty state and its own dict cleared, on both
+    routes, and the next call is unaffected."""
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] no ops for this rank, {route}", flush=True)
+    dev = torch.device("cuda")
+    own = {"x": {"param": torch.zeros(4, device=dev)}}
+    assert execute_param_transfer([], own, dev, [("param", "normal")], rank=0, route=route) == {}
+    assert own == {}
+    others = [op for op in w.ops()]      # every op targets w.dst_rank
+    stranger = w.dst_rank + 1000
+    assert execute_param_transfer(others, {}, dev, [(f, "normal") for f in w.src_fields], rank=stranger,
+                                  route=route) == {}
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    out = execute_param_transfer(w.ops(), {}, dev, [(f, "normal") for f in w.src_fields], rank=w.dst_rank,
+                                 fake_source_state_dicts=to_device(srcs, w, "cuda"), route=route)
+    torch.cuda.synchronize()
+    for name, e in want.items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
 def test_execute_rejects_remote_without_exchange():
     w = cases.scaled_configs()["llama7b_tp4pp2_tp2pp2"]
     ops = w.ops()
