@@ -113,6 +113,43 @@ def test_execute_rejects_cpu_and_bad_shapes():
                                fake_source_state_dicts=gpu)
 
 
+@pytest.mark.parametrize("groups", [1, 4])
+def test_failed_call_frees_its_destinations(groups, monkeypatch):
+    """A launch group that fails after its destination blocks went to the
+    helper thread (the lowering rejects a source of the wrong shape) leaves
+    no device memory behind: torch's allocated bytes return to where they
+    were, and the next call on the same sources is exact."""
+    from suika_amd import migration as M
+    from tests.harness import round_robin_groups
+    monkeypatch.setattr(M, "_pipeline_groups", round_robin_groups(groups))
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    print(f"[gpu api] failed call frees its destinations, {groups} group(s)", flush=True)
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    gpu = to_device(srcs, w, "cuda")
+    fields = [(f, "normal") for f in w.src_fields]
+    ops = w.ops()
+    last = ops[-1]                                # in the last group of the round robin
+    good = gpu[last.src_rank][last.param_name]["exp_avg"]
+    gpu[last.src_rank][last.param_name]["exp_avg"] = good.reshape(-1)[:-1].clone()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    with pytest.raises(AssertionError, match=f"param {last.param_name} - src_tensor shape"):
+        execute_param_transfer(ops, {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                               fake_source_state_dicts={r: {n: dict(e) for n, e in sd.items()}
+                                                        for r, sd in gpu.items()})
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == before
+    gpu[last.src_rank][last.param_name]["exp_avg"] = good
+    out = execute_param_transfer(ops, {}, torch.device("cuda"), fields, rank=w.dst_rank,
+                                 fake_source_state_dicts=gpu)
+    torch.cuda.synchronize()
+    for name, e in want.items():
+        for f, a in e.items():
+            np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
 def test_execute_rejects_one_tensor_with_two_source_dtypes():
     """The two sources of one tensor hold uint8 and int8: the library sees
     one byte type, so the drop-in call's planner itself checks that the
