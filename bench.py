@@ -73,8 +73,9 @@ def parse_args(argv=None):
                          "this GPU (migration_save / migration_load) and print its timings, then exit")
     ap.add_argument("--checkpoint", metavar="DIR", default=None,
                     help="only run the checkpoint-based migration of the workload (the reference's "
-                         "comparator to live migration): the old world's processes checkpoint_save into "
-                         "DIR, then new processes checkpoint_load it on this GPU; print the timings, then exit")
+                         "comparator to live migration): the old world's processes checkpoint_save into a "
+                         "new directory inside DIR (removed afterwards), then new processes checkpoint_load "
+                         "it on this GPU; print the timings, then exit")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -807,6 +808,10 @@ def checkpoint_leg(key: str, ckpt_dir: str, timeout_s: float = 900.0) -> dict:
     need = sum(m.numel() for metas in w.layouts()[0].layout.values() for m in metas.values()) * per_elem
     free = shutil.disk_usage(ckpt_dir).free
     assert need <= free, f"checkpoint leg: {need / 1e9:.1f} GB needed in {ckpt_dir}, {free / 1e9:.1f} GB free"
+    # a directory of its own inside ckpt_dir, removed afterwards: nothing
+    # already in ckpt_dir is written over or deleted
+    import tempfile
+    ckpt_dir = tempfile.mkdtemp(prefix="suika_checkpoint_leg_", dir=ckpt_dir)
     ctx = mp.get_context("spawn")
     events = ctx.Queue()
     start = ctx.Event()
@@ -854,9 +859,7 @@ def checkpoint_leg(key: str, ckpt_dir: str, timeout_s: float = 900.0) -> dict:
             if p.is_alive():
                 p.kill()
                 p.join(10)
-        for f in os.listdir(ckpt_dir):
-            if f.startswith("state_dict_") or f in ("param_layout.pt", "other_context.pt"):
-                os.remove(os.path.join(ckpt_dir, f))
+        shutil.rmtree(ckpt_dir, ignore_errors=True)
 
     saved = [results[("saved", r)] for r in range(old_ws)]
     loaded = [results[("loaded", r)] for r in range(new_ws)]
