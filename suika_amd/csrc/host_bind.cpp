@@ -111,6 +111,32 @@ py::object lookup(PyObject* d, PyObject* key) {
   return py::reinterpret_steal<py::object>(v);
 }
 
+// Interned attribute names (created once, never released).
+struct Names {
+  PyObject *dtype, *shape, *kind_args, *tp_meta, *kind, *rows, *name, *dict;
+  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta;
+  PyObject *chunk, *vocab_pad, *qkv_heads;
+  Names() {
+    auto in = [](const char* s) { return PyUnicode_InternFromString(s); };
+    dtype = in("dtype"); shape = in("shape"); kind_args = in("kind_args"); tp_meta = in("tp_meta");
+    kind = in("kind"); rows = in("rows"); name = in("name"); dict = in("__dict__");
+    param_name = in("param_name"); src_rank = in("src_rank"); dst_rank = in("dst_rank");
+    src_meta = in("src_meta"); dst_meta = in("dst_meta"); dst_shard_meta = in("dst_shard_meta");
+    chunk = in("chunk"); vocab_pad = in("vocab_pad"); qkv_heads = in("qkv_heads");
+  }
+};
+
+const Names& names_() {
+  static Names* n = new Names();
+  return *n;
+}
+
+py::object attr(PyObject* o, PyObject* key) {
+  PyObject* v = PyObject_GetAttr(o, key);
+  if (!v) throw py::error_already_set();
+  return py::reinterpret_steal<py::object>(v);
+}
+
 constexpr int64_t kSpecWords = 10;   // sr_src_spec: dtype, ndim, shape[8]
 constexpr int64_t kKeyWords = 13;    // sr_slot_key: op, field, recast, dtype, ndim, shape[8]
 
@@ -120,6 +146,7 @@ constexpr int64_t kKeyWords = 13;    // sr_slot_key: op, field, recast, dtype, n
 // loop (migration.py:426-494).
 py::tuple collect_sources(py::list ops, py::function source, py::list fields, int64_t device_index,
                           const std::string& who) {
+  const Names& N = names_();
   py::dict sources;
   const int64_t n = int64_t(ops.size()), nf = int64_t(fields.size());
   py::array_t<int64_t> specs({n * nf * kSpecWords});
@@ -130,23 +157,24 @@ py::tuple collect_sources(py::list ops, py::function source, py::list fields, in
   std::fill(sp, sp + n * nf * kSpecWords, 0);
   const std::string want_device = "cuda:" + std::to_string(device_index);
   for (int64_t k = 0; k < n; ++k) {
-    py::handle op = ops[k];
-    py::object rank = op.attr("src_rank");
-    py::object name = op.attr("param_name");
+    PyObject* op = PyList_GET_ITEM(ops.ptr(), k);
+    py::object rank = attr(op, N.src_rank);
+    py::object name = attr(op, N.param_name);
     py::object sd = lookup(sources.ptr(), rank.ptr());
     if (!sd) {
       sd = source(rank);
       sources[rank] = sd;
     }
     py::object entry = lookup(sd.ptr(), name.ptr());
-    const std::string nm = py::str(name).cast<std::string>();
-    if (!entry) assertion(who + ": param missing in source " + nm);
+    // messages are built only on the failing path
+    auto nm = [&]() { return py::str(name).cast<std::string>(); };
+    if (!entry) assertion(who + ": param missing in source " + nm());
     for (int64_t f = 0; f < nf; ++f) {
       py::handle field = fields[f];
       py::object obj = lookup(entry.ptr(), field.ptr());
-      if (!obj) assertion("expected_sub_fields mismatch: " + nm + " has no " + py::str(field).cast<std::string>());
+      if (!obj) assertion("expected_sub_fields mismatch: " + nm() + " has no " + py::str(field).cast<std::string>());
       if (!THPVariable_Check(obj.ptr()))
-        assertion("source " + nm + "/" + py::str(field).cast<std::string>() + " of rank " +
+        assertion("source " + nm() + "/" + py::str(field).cast<std::string>() + " of rank " +
                   py::str(rank).cast<std::string>() + ": not a tensor");
       const at::Tensor& t = THPVariable_Unpack(obj.ptr());
       const int64_t code = sr_code(t.scalar_type());
@@ -154,11 +182,11 @@ py::tuple collect_sources(py::list ops, py::function source, py::list fields, in
       if (!t.is_cuda() || t.get_device() != device_index || !t.is_contiguous() || code < 0 || nd > 8) {
         // the rare path: build the message
         const std::string fs = py::str(field).cast<std::string>();
-        const std::string what = "source " + nm + "/" + fs + " of rank " + py::str(rank).cast<std::string>();
+        const std::string what = "source " + nm() + "/" + fs + " of rank " + py::str(rank).cast<std::string>();
         if (!t.is_cuda() || t.get_device() != device_index)
           assertion(what + " is on " + t.device().str() + ", not on " + want_device);
         if (!t.is_contiguous()) assertion(what + " is not contiguous");
-        assertion("source " + nm + "/" + fs + ": " + py::str(dtype_object(t.scalar_type())).cast<std::string>() +
+        assertion("source " + nm() + "/" + fs + ": " + py::str(dtype_object(t.scalar_type())).cast<std::string>() +
                   ", " + std::to_string(nd) + "-D is not supported by the reshard engine");
       }
       int64_t* row = sp + (k * nf + f) * kSpecWords;
@@ -517,32 +545,6 @@ int64_t as_int(PyObject* o) {
   return int64_t(v);
 }
 
-// Interned attribute names (created once, never released).
-struct Names {
-  PyObject *dtype, *shape, *kind_args, *tp_meta, *kind, *rows, *name, *dict;
-  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta;
-  PyObject *chunk, *vocab_pad, *qkv_heads;
-  Names() {
-    auto in = [](const char* s) { return PyUnicode_InternFromString(s); };
-    dtype = in("dtype"); shape = in("shape"); kind_args = in("kind_args"); tp_meta = in("tp_meta");
-    kind = in("kind"); rows = in("rows"); name = in("name"); dict = in("__dict__");
-    param_name = in("param_name"); src_rank = in("src_rank"); dst_rank = in("dst_rank");
-    src_meta = in("src_meta"); dst_meta = in("dst_meta"); dst_shard_meta = in("dst_shard_meta");
-    chunk = in("chunk"); vocab_pad = in("vocab_pad"); qkv_heads = in("qkv_heads");
-  }
-};
-
-const Names& names_() {
-  static Names* n = new Names();
-  return *n;
-}
-
-py::object attr(PyObject* o, PyObject* key) {
-  PyObject* v = PyObject_GetAttr(o, key);
-  if (!v) throw py::error_already_set();
-  return py::reinterpret_steal<py::object>(v);
-}
-
 // An attribute the reference's own objects do not carry: TensorMeta has only
 // name, dtype, shape and tp_meta (Suika/migration.py:29-58; tp_meta is left
 // unset when built from dtype and shape alone) and TransferOp only
@@ -762,14 +764,14 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
     py::object m = attr(op, N.dst_meta);
     int64_t idx = 0, deg = 0, r0 = -1, r1 = -1;
     if (m.ptr() != shard) {
-      const std::string nm = py::str(name).cast<std::string>();
+      auto nm = [&]() { return py::str(name).cast<std::string>(); };   // for messages only
       py::object mk = kind_of(m.ptr()), sk = kind_of(shard);
       py::object ms = attr(m.ptr(), N.shape), ss = attr(shard, N.shape);
       const int same_kind = PyObject_RichCompareBool(mk.ptr(), sk.ptr(), Py_EQ);
       const int same_shape = PyObject_RichCompareBool(ms.ptr(), ss.ptr(), Py_EQ);
       if (same_kind < 0 || same_shape < 0) throw py::error_already_set();
       if (!same_kind || !same_shape)
-        assertion(nm + ": piece " + py::str(m).cast<std::string>() + " is not part of shard " +
+        assertion(nm() + ": piece " + py::str(m).cast<std::string>() + " is not part of shard " +
                   py::str(py::handle(shard)).cast<std::string>());
       py::object tp = tp_meta_of(m.ptr()), stp = tp_meta_of(shard);
       if (tp.ptr() == Py_None) {   // an unsplit piece: the whole tensor
@@ -781,7 +783,7 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
                                                         PyTuple_GET_ITEM(stp.ptr(), 0), Py_EQ);
           if (same_dim < 0) throw py::error_already_set();
           if (!same_dim)
-            assertion(nm + ": piece " + py::str(m).cast<std::string>() + " is split along another dim than shard " +
+            assertion(nm() + ": piece " + py::str(m).cast<std::string>() + " is split along another dim than shard " +
                       py::str(py::handle(shard)).cast<std::string>());
         }
         idx = as_int(PyTuple_GET_ITEM(tp.ptr(), 1));
@@ -1029,7 +1031,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
   py::dict sources;
   for (size_t i = 0; i < n_names; ++i) {
     PyObject* first = groups[i][0];
-    const std::string nm = py::str(names[i]).cast<std::string>();
+    auto nm = [&]() { return py::str(names[i]).cast<std::string>(); };   // for messages only
     sr_meta m;
     int64_t* row = reinterpret_cast<int64_t*>(&m);
     sr_internal::View v;
@@ -1039,7 +1041,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
       v = sr_internal::view_of(m);
     } else {
       meta_row(attr(first, N.dst_meta).ptr(), 0, 0, row);
-      if (m.row0 >= 0) assertion(nm + ": vocab pieces need dst_shard_meta");
+      if (m.row0 >= 0) assertion(nm() + ": vocab pieces need dst_shard_meta");
       v = sr_internal::view_of(m);
       if (m.tp_deg > 0 && groups[i].size() > 1) {
         std::vector<int64_t> idx;
@@ -1056,7 +1058,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
         if (!ok) {
           std::string list = "[";
           for (int64_t j = 0; j < cnt; ++j) list += (j ? ", " : "") + std::to_string(idx[j]);
-          assertion(nm + ": pieces " + list + "] at degree " + std::to_string(T) + " do not form one shard");
+          assertion(nm() + ": pieces " + list + "] at degree " + std::to_string(T) + " do not form one shard");
         }
         v.tp_index = idx[0] / cnt;
         v.tp_deg = T / cnt;
@@ -1064,11 +1066,11 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
       }
     }
     if (!sr_internal::actual_shape(v, &dims[i * SR_MAX_DIMS]))
-      assertion(nm + ": destination shard shape overflows");
+      assertion(nm() + ": destination shard shape overflows");
     ndim[i] = m.ndim;
     for (int64_t d = 0; d < m.ndim; ++d) {
       const int64_t e = dims[i * SR_MAX_DIMS + d];
-      if (e < 0 || __builtin_mul_overflow(numel[i], e, &numel[i])) assertion(nm + ": bad destination shape");
+      if (e < 0 || __builtin_mul_overflow(numel[i], e, &numel[i])) assertion(nm() + ": bad destination shape");
     }
     // dtypes: bf16 for recast targets, else the source tensor's
     py::object rank = attr(first, N.src_rank);
@@ -1078,7 +1080,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
       sources[rank] = sd;
     }
     py::object entry = lookup(sd.ptr(), names[i].ptr());
-    if (!entry) assertion("param missing in source " + nm);
+    if (!entry) assertion("param missing in source " + nm());
     for (size_t k = 0; k < n_fields; ++k) {
       if (is_target[k]) {
         st[k * n_names + i] = at::kBFloat16;
@@ -1086,7 +1088,7 @@ py::dict arena_tensors(py::list ops, py::function source, py::list order, py::li
       }
       py::object t = lookup(entry.ptr(), order[k].ptr());
       if (!t || !THPVariable_Check(t.ptr()))
-        assertion("expected_sub_fields mismatch: " + nm + " has no tensor " + py::str(order[k]).cast<std::string>());
+        assertion("expected_sub_fields mismatch: " + nm() + " has no tensor " + py::str(order[k]).cast<std::string>());
       st[k * n_names + i] = THPVariable_Unpack(t.ptr()).scalar_type();
     }
   }
