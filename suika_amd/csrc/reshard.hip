@@ -830,29 +830,36 @@ int check_region(const sr_tensor& t, uint64_t r0, uint64_t c0, uint64_t rows, ui
 struct Box {
   uint64_t r0, r1, c0, c1;
   int32_t piece;
+  int32_t slot;   // destination slot written
 };
 
 // Every destination slot must be written exactly once: boxes pairwise
-// disjoint and their areas summing to the slot's area.
-int check_coverage(const std::vector<std::vector<Box>>& boxes, const std::vector<sr_tensor>& dst) {
-  for (size_t s = 0; s < boxes.size(); ++s) {
-    std::vector<Box> b = boxes[s];
-    std::sort(b.begin(), b.end(), [](const Box& x, const Box& y) {
-      return x.r0 != y.r0 ? x.r0 < y.r0 : x.c0 < y.c0;
-    });
+// disjoint and their areas summing to the slot's area.  `boxes` holds the
+// regions of all slots (any order; sorted here by slot, row, column).
+int check_coverage(std::vector<Box>& boxes, const std::vector<sr_tensor>& dst) {
+  std::sort(boxes.begin(), boxes.end(), [](const Box& x, const Box& y) {
+    if (x.slot != y.slot) return x.slot < y.slot;
+    return x.r0 != y.r0 ? x.r0 < y.r0 : x.c0 < y.c0;
+  });
+  size_t at = 0;
+  for (size_t s = 0; s < dst.size(); ++s) {
+    size_t end = at;
+    while (end < boxes.size() && boxes[end].slot == int32_t(s)) ++end;
     unsigned __int128 area = 0;
-    for (size_t i = 0; i < b.size(); ++i) {
-      area += (unsigned __int128)(b[i].r1 - b[i].r0) * (b[i].c1 - b[i].c0);
-      for (size_t j = i + 1; j < b.size() && b[j].r0 < b[i].r1; ++j) {
-        if (b[j].c0 < b[i].c1 && b[i].c0 < b[j].c1)
-          return fail(SR_EOVERLAP, "dst[%zu]: pieces %d and %d write overlapping regions", s,
-                      b[i].piece, b[j].piece);
+    for (size_t i = at; i < end; ++i) {
+      const Box& bi = boxes[i];
+      area += (unsigned __int128)(bi.r1 - bi.r0) * (bi.c1 - bi.c0);
+      for (size_t j = i + 1; j < end && boxes[j].r0 < bi.r1; ++j) {
+        if (boxes[j].c0 < bi.c1 && bi.c0 < boxes[j].c1)
+          return fail(SR_EOVERLAP, "dst[%zu]: pieces %d and %d write overlapping regions", s, bi.piece,
+                      boxes[j].piece);
       }
     }
     const unsigned __int128 full = (unsigned __int128)dst[s].rows * dst[s].cols;
     if (area != full)
       return fail(SR_EOVERLAP, "dst[%zu]: pieces cover %llu of %llu elements", s,
                   (unsigned long long)area, (unsigned long long)full);
+    at = end;
   }
   return SR_OK;
 }
@@ -1520,7 +1527,8 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
   p->piece_offset.assign(n_pieces, UINT64_MAX);
   p->peer_bytes.assign(n_peers, 0);
 
-  std::vector<std::vector<Box>> cover(n_dst);
+  std::vector<Box> cover;   // every destination region, for the coverage check
+  cover.reserve(size_t(n_pieces) * 2);
   const uint64_t max_row = (uint64_t(1) << 31) - opt.tile_bytes;
   const bool buffers = (opt.flags & SR_OPT_GATHER_ONLY) == 0;   // build the pack and unpack phases
   if (buffers) {
@@ -1570,7 +1578,7 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       p->unpack.bytes_written += pc.rows * pc.cols * es;
       p->gather.items.push_back(it);
       p->gather.bytes_written += pc.rows * pc.cols * es;
-      cover[pc.dst].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+      cover.push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k, pc.dst});
       continue;
     }
 
@@ -1598,12 +1606,12 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       if (dst == dst2) return bad(fail(SR_EINVAL, "piece %d: dst and dst2 are the same slot", k));
       if ((rc = check_region(p->dst[dst2], pc.dst_row, pc.dst_col, pc.rows, pc.cols, "dst2", k)) != SR_OK)
         return bad(rc);
-      cover[dst2].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+      cover.push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k, dst2});
     }
     if (dst >= 0) {
       if ((rc = check_region(p->dst[dst], pc.dst_row, pc.dst_col, pc.rows, pc.cols, "dst", k)) != SR_OK)
         return bad(rc);
-      cover[dst].push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k});
+      cover.push_back({pc.dst_row, pc.dst_row + pc.rows, pc.dst_col, pc.dst_col + pc.cols, k, dst});
     }
 
     // Buffer placement: pieces of a peer in piece order, 256-byte aligned.

@@ -124,6 +124,30 @@ def test_overlap_and_holes_rejected():
     _lib.lib().sr_plan_destroy(h)
 
 
+def test_coverage_checked_per_destination():
+    """Coverage is kept per destination slot, whatever order the pieces come in:
+    the same region of two slots is no overlap, and a fault in one slot names it."""
+    src, dst = [(4, 8, F32)], [(4, 8, F32)] * 3
+    halves = lambda d: [piece(dst=d, rows=2), piece(dst=d, rows=2, sr=2, dr=2)]
+    # slots interleaved (2, 0, 1, 2, 0, 1), every slot covered once: valid
+    pcs = [p for pair in zip(halves(2), halves(0), halves(1)) for p in pair]
+    rc, h = _plan(src, dst, 1, pcs)
+    assert rc == 0, _lib.last_error()
+    _lib.lib().sr_plan_destroy(h)
+    # slot 1 gets a third piece over its first half: the overlap names slot 1
+    rc, _ = _plan(src, dst, 1, pcs + [piece(dst=1, rows=1, cols=1)])
+    assert rc == _lib.SR_EOVERLAP
+    assert _lib.last_error().startswith("dst[1]: pieces") and "overlapping" in _lib.last_error()
+    # slot 0 has no pieces at all: reported as covering none of its elements
+    rc, _ = _plan(src, dst, 1, halves(1) + halves(2))
+    assert rc == _lib.SR_EOVERLAP
+    assert "dst[0]: pieces cover 0 of 32 elements" in _lib.last_error()
+    # the last slot short by a half
+    rc, _ = _plan(src, dst, 1, halves(0) + halves(1) + halves(2)[:1])
+    assert rc == _lib.SR_EOVERLAP
+    assert "dst[2]: pieces cover 16 of 32 elements" in _lib.last_error()
+
+
 def test_recast_and_zero_rules():
     # f32 source -> f32 dst 0 and bf16 dst 1; zero fill the remaining rows of both
     pcs = [piece(kind=_lib.SR_PIECE_RECAST, dst=0, dst2=1, rows=3),
