@@ -71,6 +71,9 @@ def parse_args(argv=None):
     ap.add_argument("--handoff", action="store_true",
                     help="only run the live migration of the workload between old and new processes on "
                          "this GPU (migration_save / migration_load) and print its timings, then exit")
+    ap.add_argument("--handoff-wait-release", action="store_true",
+                    help="with --handoff: the new world allocates its destinations only after the old "
+                         "world has released its state, even when the device has room for both")
     ap.add_argument("--checkpoint", metavar="DIR", default=None,
                     help="only run the checkpoint-based migration of the workload (the reference's "
                          "comparator to live migration): the old world's processes checkpoint_save into a "
@@ -562,7 +565,7 @@ def _handoff_old(rank, key, port, queues, events):
             dist.destroy_process_group()
 
 
-def _handoff_new(rank, key, port, queues, events):
+def _handoff_new(rank, key, port, queues, events, wait_for_release=None):
     import traceback
 
     import torch
@@ -581,7 +584,7 @@ def _handoff_new(rank, key, port, queues, events):
         log = []
         t0 = time.time()
         opt, ctx = migration_load(queues[rank], model, lambda: _state_optimizer(model.parameters()),
-                                  log_func=_timed_log(log))
+                                  log_func=_timed_log(log), wait_for_release=wait_for_release)
         t1 = time.time()
         rec = _check_new_rank(w, rank, model, opt, dev)
         rec.update(log=log, t_call=t0, t_return=t1)
@@ -594,7 +597,7 @@ def _handoff_new(rank, key, port, queues, events):
             dist.destroy_process_group()
 
 
-def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
+def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> dict:
     """Live migration of workload ``key`` between processes on this GPU: the
     old plan's ranks (seeded state) call migration_save, the new plan's ranks
     migration_load; every received tensor is checked bit for bit."""
@@ -639,7 +642,7 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
             procs[-1].start()
         wait_for("ready", old_ws)
         for r in range(new_ws):
-            procs.append(ctx.Process(target=_handoff_new, args=(r, key, p_new, queues, events)))
+            procs.append(ctx.Process(target=_handoff_new, args=(r, key, p_new, queues, events, wait_for_release)))
             procs[-1].start()
         wait_for("loaded", new_ws)
         wait_for("saved", old_ws)
@@ -658,17 +661,22 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
     new_recs = [results[("loaded", r)] for r in range(new_ws)]
     start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done: packing begins
     pack_ms = max((at(l, "packed") - at(l, "is_scale_up")) * 1e3 for l in old_logs)
-    # the old state's release after the message is sent: its tensors freed and
-    # the allocator's cache returned to the device (one hipFree per segment)
-    release_ms = max((at(l, "state released") - at(l, "packed")) * 1e3 for l in old_logs)
+    # the old state's release once the new world has mapped the hand-off and
+    # allocated (or asked for the memory): its tensors freed and the
+    # allocator's cache returned to the device (one hipFree per segment)
+    noted = [next(t for t, m in l if "has allocated its destinations" in m or "waits for this state's" in m)
+             for l in old_logs]
+    release_ms = max((at(l, "state released") - t) * 1e3 for l, t in zip(old_logs, noted))
     end = max(rec["t_return"] for rec in new_recs)
-    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "old world has released")) * 1e3 for rec in new_recs]
+    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "destinations of")) * 1e3 for rec in new_recs]
+    waited = any("after the old world released" in m for rec in new_recs for _, m in rec["log"])
     return {
         "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
         "state_bytes_received": sum(rec["bytes"] for rec in new_recs),
         "pack_ms_max": round(pack_ms, 2),
         "release_ms_max": round(release_ms, 2),
         "reshard_ms_max": round(max(reshard), 2),
+        "destinations_waited_for_release": waited,
         "handoff_ms": round((end - start) * 1e3, 1),
         "handoff_ms_note": ("wall time from the old world's handshake to the last new rank's return from "
                             "migration_load: pack, queue messages, IPC mapping, reshard, load_state_dict; "
@@ -680,6 +688,10 @@ def handoff_leg(key: str, timeout_s: float = 600.0) -> dict:
         "per_new_rank_log_ms": [
             {m.split(":", 1)[1].strip()[:40]: round((t - rec["t_call"]) * 1e3, 1) for t, m in rec["log"]}
             for rec in new_recs],
+        "per_old_rank_log_ms": [
+            {m.split(":", 1)[1].strip()[:40]: round((t - start) * 1e3, 1) for t, m in l} for l in old_logs],
+        "timing_lines": {"old": [[m for _, m in l if " ms" in m] for l in old_logs],
+                         "new": [[m for _, m in rec["log"] if " ms" in m] for rec in new_recs]},
     }
 
 
@@ -915,7 +927,7 @@ def main(argv=None) -> int:
 
     key = args.config or BENCH_CONFIG
     if args.handoff:
-        rec = handoff_leg(key)
+        rec = handoff_leg(key, wait_for_release=True if args.handoff_wait_release else None)
         print(json.dumps({"handoff": rec}), flush=True)
         return 0 if rec["parity"]["mismatched"] == 0 else 1
     if args.checkpoint:

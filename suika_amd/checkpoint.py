@@ -352,7 +352,8 @@ def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = N
 def migration_load(IPC_queues, model: Module,
                    optimizer: Union[Optimizer, Callable[[], Optimizer], None] = None,
                    device: Optional[torch.device] = None, world: Optional[dist.ProcessGroup] = None,
-                   log_func: Optional[Callable] = None, checkpoint_resume: Optional[str] = None):
+                   log_func: Optional[Callable] = None, checkpoint_resume: Optional[str] = None, *,
+                   wait_for_release: Optional[bool] = None):
     """Suika's load-side migration API (Suika/migration.py:1546-1727).
 
     With ``checkpoint_resume`` the checkpoint is resharded into ``model`` on
@@ -361,7 +362,12 @@ def migration_load(IPC_queues, model: Module,
     straight from their memory (``suika_amd.handoff.live_load``).  Returns
     ``other_context``, or ``(optimizer, other_context)`` for an optimizer
     provider; a fresh launch (the launcher's placeholder on the queue)
-    returns ``None`` / ``(optimizer_provider(), None)``."""
+    returns ``None`` / ``(optimizer_provider(), None)``.
+
+    ``wait_for_release`` (not in the reference) chooses when a live
+    migration allocates its destinations: ``None`` beside the old state when
+    the device has room, else after the old world released it; ``True``
+    always after."""
     if log_func is None:
         log_func = lambda msg: None  # noqa: E731
     device = _device(device)
@@ -377,4 +383,4 @@ def migration_load(IPC_queues, model: Module,
     else:
         raise TypeError(f"optimizer should be Optimizer or Callable, but got {type(optimizer)}")
     from .handoff import live_load
-    return live_load(IPC_queues, model, optimizer_provider, optimizer, device, world, log_func)
+    return live_load(IPC_queues, model, optimizer_provider, optimizer, device, world, log_func, wait_for_release)

@@ -22,16 +22,24 @@ Here, with every old and new rank on the same GPU:
   record to new rank ``i`` over its forward queue; new ranks without an old
   counterpart read the launcher's placeholder (``dummy_migration_IPC_state_dict``),
   and the new world takes rank 0's message;
-* each old rank then frees its state tensors, as the reference frees each sent
-  tensor, and returns the memory to the device; once all have, old rank 0
-  sends ``RELEASED`` after its message;
 * each new rank maps the allocations of the old ranks its pieces come from
   (``sr_handoff_open``) and views the state there as tensors without copying;
-  after ``RELEASED`` it runs ``execute_param_transfer`` (one gather per launch
-  group) straight from them into one destination arena that the model adopts
-  with ``load_state_dict(assign=True)``;
-* after the new world's barrier, new rank 0 acknowledges on rank 0's backward
-  queue; the old world then frees its allocations and returns.
+* the new world sums its destination bytes.  When the device has room for
+  them beside the old state and the hand-off (its 288 GiB of HBM hold all
+  three for a 7B model's fp32 Adam state), every new rank takes that memory
+  and new rank 0 sends ``ALLOCATED``; otherwise it sends ``WANT_RELEASED``
+  and waits for ``RELEASED``;
+* only then does each old rank free its state tensors, as the reference frees
+  each sent tensor, and return the memory to the device (memory another
+  process has just freed is slow to allocate); once all have, old rank 0
+  sends ``RELEASED``;
+* each new rank runs ``execute_param_transfer`` (one gather per launch group)
+  straight from the mapped memory into one destination arena that the model
+  adopts with ``load_state_dict(assign=True)``, beside the old state's
+  release when the memory allowed it, and builds its optimizer;
+* new rank 0, holding ``RELEASED``, acknowledges on rank 0's backward queue
+  and the new world returns; the old world then frees the hand-off
+  allocations and returns.
 
 The packed allocations are the per-peer buffers of a pack -> unpack reshard:
 the old side reads and writes P bytes, the new side reads P and writes D, and
@@ -68,9 +76,21 @@ dummy_migration_IPC_state_dict = {
 }
 
 DONE = "suika_amd: handoff complete"
-# Old rank 0 to new rank 0, after the message: every old rank has released
+# New rank 0 to old rank 0 once every new rank has mapped the hand-off: either
+# every new rank holds the memory for its destinations (ALLOCATED), or the
+# device lacks room for them beside the old state (WANT_RELEASED).  The old
+# ranks release their state only then, so memory they free is not what the
+# new ranks allocate at once.
+ALLOCATED = "suika_amd: destinations allocated"
+WANT_RELEASED = "suika_amd: waiting for the old state's release"
+# Old rank 0 to new rank 0, after either note: every old rank has released
 # its state and returned the memory to the device.
 RELEASED = "suika_amd: old state released"
+# Device memory kept free per new rank beyond its destinations when they are
+# allocated beside the old state (plan tables, allocator rounding).
+HEADROOM_BYTES = 1 << 30
+# Taken beyond a new rank's destination bytes when it reserves them.
+ARENA_SLACK_BYTES = 64 << 20
 
 
 def pack_layout(nbytes: Sequence[int], chunk_bytes: int = CHUNK_BYTES) -> Tuple[List[Tuple[int, int]], List[int]]:
@@ -289,9 +309,14 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
         # The state now lives in the hand-off allocations: release it, as the
         # reference releases every tensor it has sent (utils.py:372-376), and
         # return the memory to the device for the new world, as its cuda_gc
-        # does after sending (utils.py:248-253, 385).  The new world maps the
-        # hand-off and plans meanwhile; it allocates its destinations only
-        # after old rank 0's RELEASED, sent once every old rank is done.
+        # does after sending (utils.py:248-253, 385) -- once the new world
+        # has mapped the hand-off and either allocated its destinations
+        # beside this state or asked for the memory.
+        note = IPC_queues[1].get(block=True) if rank == 0 else None
+        note = _broadcast_objects(note, group=world)
+        assert note in (ALLOCATED, WANT_RELEASED), f"migration_save: unexpected message {note!r}"
+        log_func("migration_save: the new world " + ("has allocated its destinations" if note == ALLOCATED
+                                                     else "waits for this state's memory"))
         t2 = time.perf_counter()
         for entry in source_state_dict.values():
             for t in entry.values():
@@ -364,13 +389,39 @@ class _WarmUp(threading.Thread):
                 pass
 
 
+def _destination_bytes(ops, rank: int, records: Sequence[Dict[str, Any]]) -> int:
+    """Device bytes of ``rank``'s destination tensors: per name, the elements
+    of its shard on this rank times the item sizes of the fields the old
+    ranks' hand-off records hold on the device, each tensor rounded up to
+    256 bytes."""
+    by_rank = {rec["rank"]: rec for rec in records}
+    per_name: Dict[str, int] = {}
+    for op in ops:
+        if op.dst_rank != rank or op.param_name in per_name:
+            continue
+        numel = 1
+        for d in op.dst_shard_meta.actual_shape():
+            numel *= int(d)
+        fields = by_rank[op.src_rank]["tensors"].get(op.param_name, {})
+        per_name[op.param_name] = sum((numel * _dtype_of(f[3]).itemsize + ALIGN - 1) // ALIGN * ALIGN
+                                      for f in fields.values())
+    return sum(per_name.values())
+
+
 def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.device, world,
-              log_func: Callable[[str], None]):
-    """The new side of a live migration (Suika/migration.py:1586-1727)."""
+              log_func: Callable[[str], None], wait_for_release: Optional[bool] = None):
+    """The new side of a live migration (Suika/migration.py:1586-1727).
+
+    The destinations are allocated beside the old state when the device has
+    room for every new rank's (``wait_for_release=None``), else after the old
+    world has released its state; ``True`` always waits."""
     from .meta import ParamLayout, schedule_param_transfer
     from .migration import execute_param_transfer, split_model_and_optimizer_state_dict
 
     rank = dist.get_rank(world)
+    # the process's first-use costs are paid while it waits for the old world
+    warm = _WarmUp(device, optimizer_provider is not None)
+    warm.start()
     if rank == 0:
         old_world_size = IPC_queues[0].get(block=True)
         new_world_size = dist.get_world_size(world)
@@ -384,13 +435,9 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
 
     target_param_layout = ParamLayout()
     target_param_layout.gather(model, world)
-    # old rank i's message, or the launcher's placeholder when there is none;
-    # the process's first-use costs are paid meanwhile
-    warm = _WarmUp(device, optimizer_provider is not None)
-    warm.start()
+    # old rank i's message, or the launcher's placeholder when there is none
     msg = IPC_queues[0].get(block=True)
     log_func("migration_load: hand-off message received")
-    warm.library_done.wait()
     source_param_layout, other_context_dict, records = _broadcast_objects(
         msg.get("source_param_layout"), msg.get("other_context_dict"), msg.get("handoff"), group=world)
     del msg
@@ -405,17 +452,42 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
     t0 = time.perf_counter()
     ops = schedule_param_transfer(source_param_layout, target_param_layout)
     needed = sorted({op.src_rank for op in ops if op.dst_rank == rank})
+    t_sched = time.perf_counter()
+    # Old state, hand-off and destinations side by side when the device has
+    # room for all of them: each new rank takes its destinations' memory
+    # before the old world frees anything.  Else the destinations wait for
+    # the old world to return its state's memory.
+    mine = _destination_bytes(ops, rank, records)
+    need = torch.tensor([mine], dtype=torch.int64)
+    dist.all_reduce(need, group=world)
+    wait = None
+    if rank == 0:
+        free, _ = torch.cuda.mem_get_info(device)
+        room = int(need.item()) + HEADROOM_BYTES * dist.get_world_size(world)
+        wait = bool(wait_for_release) if wait_for_release is not None else free < room
+    wait = _broadcast_objects(wait, group=world)
+    if not wait:
+        # the destination arena's memory, taken now and kept in this
+        # process's allocator cache, where the arena finds it
+        torch.empty(mine + ARENA_SLACK_BYTES, dtype=torch.uint8, device=device)
+    t_alloc = time.perf_counter()
+    # mapped before the old world frees anything: IPC opens beside other
+    # processes' frees were 20-40x slower
     mapped = MappedSources(records, needed, device)
     t_map = time.perf_counter()
     log_func(f"migration_load: mapped the state of old rank(s) {needed}")
     try:
-        # the destinations are allocated only once the old world has
-        # returned its state's memory to the device
-        if rank == 0:
-            note = IPC_queues[0].get(block=True)
-            assert note == RELEASED, f"migration_load: unexpected message {note!r}"
         dist.barrier(world)
-        log_func("migration_load: the old world has released its state")
+        if rank == 0:
+            IPC_queues[1].put(WANT_RELEASED if wait else ALLOCATED)
+        warm.library_done.wait()
+        if wait:
+            if rank == 0:
+                note = IPC_queues[0].get(block=True)
+                assert note == RELEASED, f"migration_load: unexpected message {note!r}"
+            dist.barrier(world)
+        log_func(f"migration_load: destinations of {int(need.item()) / 1e9:.3f} GB "
+                 + ("after the old world released its state" if wait else "beside the old state"))
         t1 = time.perf_counter()
         target_state_dict = execute_param_transfer(
             transfer_ops=ops, source_state_dict={}, device=device,
@@ -425,11 +497,11 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
         t2 = time.perf_counter()
     finally:
         mapped.close()
-    log_func(f"migration_load: mapped {len(needed)} old rank(s) in {(t_map - t0) * 1e3:.2f} ms, resharded in "
-             f"{(t2 - t1) * 1e3:.2f} ms")
+    log_func(f"migration_load: scheduled in {(t_sched - t0) * 1e3:.2f} ms, "
+             + ("" if wait else f"destinations' memory taken in {(t_alloc - t_sched) * 1e3:.2f} ms, ")
+             + f"mapped {len(needed)} old rank(s) in {(t_map - t_alloc) * 1e3:.2f} ms, "
+             f"resharded in {(t2 - t1) * 1e3:.2f} ms")
     dist.barrier(world)
-    if rank == 0:
-        IPC_queues[1].put(DONE)
     log_func("migration_load: every new rank has resharded")
 
     model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
@@ -444,5 +516,14 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
         # one parameter group, as the reference (migration.py:1712-1716)
         optimizer_state_dict["param_groups"][0]["params"] = optimizer.state_dict()["param_groups"][0]["params"]
         optimizer.load_state_dict(optimizer_state_dict)
+    # the old world's state released (beside which the destinations may have
+    # been allocated) before any new rank returns; then the old world may
+    # free the hand-off
+    if rank == 0:
+        if not wait:
+            note = IPC_queues[0].get(block=True)
+            assert note == RELEASED, f"migration_load: unexpected message {note!r}"
+        IPC_queues[1].put(DONE)
+    dist.barrier(world)
     log_func("migration_load: end")
     return (optimizer, other_context) if optimizer_provider else other_context

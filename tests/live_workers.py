@@ -85,7 +85,7 @@ def old_rank(rank, world, port, queues, old, new, events):
             dist.destroy_process_group()
 
 
-def new_rank(rank, world, port, queues, old, new, events):
+def new_rank(rank, world, port, queues, old, new, events, wait_for_release=None):
     from suika_amd import migration_load
     log = []
     try:
@@ -94,7 +94,7 @@ def new_rank(rank, world, port, queues, old, new, events):
         model = build_module(w.model, new, rank, torch.float32, device="meta")
         optimizer, ctx = migration_load(queues[rank], model,
                                         lambda: torch.optim.AdamW(model.parameters(), lr=1e-3),
-                                        log_func=_logger("new", rank, log))
+                                        log_func=_logger("new", rank, log), wait_for_release=wait_for_release)
         assert ctx == {"iter": 42}, ctx
         _, tpl = w.layouts()
         glob = _glob(w)

@@ -116,7 +116,8 @@ def test_migration_api_matches_the_reference_signatures():
     """migration_save / migration_load take the reference's parameters, in
     its order and with its defaults (Suika/migration.py:1357-1366,
     1546-1554); the launcher's placeholder has the reference's keys
-    (:1314-1318)."""
+    (:1314-1318).  An option of this build's own comes after them,
+    keyword-only."""
     import inspect
 
     from suika_amd import dummy_migration_IPC_state_dict
@@ -124,7 +125,9 @@ def test_migration_api_matches_the_reference_signatures():
     load = inspect.signature(migration_load).parameters
     assert list(save) == ["IPC_queues", "model", "optimizer", "other_context", "device", "world", "log_func",
                           "checkpoint_resume"]
-    assert list(load) == ["IPC_queues", "model", "optimizer", "device", "world", "log_func", "checkpoint_resume"]
+    assert list(load) == ["IPC_queues", "model", "optimizer", "device", "world", "log_func", "checkpoint_resume",
+                          "wait_for_release"]
+    assert load["wait_for_release"].kind is inspect.Parameter.KEYWORD_ONLY
     for params in (save, load):
         for name in list(params)[2:]:
             assert params[name].default is None, name

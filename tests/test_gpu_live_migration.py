@@ -14,6 +14,10 @@ Both of the reference's branches run:
 * one that grows (TP1 -> TP2);
 * one of equal size whose stages change (TP2 x PP2 -> TP4: 4 + 4 processes).
 
+The small states leave room on the device, so the new world allocates its
+destinations beside the old state; one more run of the last case makes it
+wait for the old world's release (``WANT_RELEASED`` / ``RELEASED``) first.
+
 Every process uses the GPU.  All stay within the box's per-card process limit.
 """
 import multiprocessing as mp
@@ -37,7 +41,7 @@ def _free_port() -> int:
         return s.getsockname()[1]
 
 
-def _run(old: Parallel, new: Parallel):
+def _run(old: Parallel, new: Parallel, wait_for_release=None):
     from tests import live_workers as W
     ctx = mp.get_context("spawn")
     n = max(old.world, new.world)
@@ -69,7 +73,8 @@ def _run(old: Parallel, new: Parallel):
             procs.append(p)
         wait_for("ready", old.world)
         for r in range(new.world):
-            p = ctx.Process(target=W.new_rank, args=(r, new.world, p_new, queues, old, new, events))
+            p = ctx.Process(target=W.new_rank, args=(r, new.world, p_new, queues, old, new, events,
+                                                     wait_for_release))
             p.start()
             procs.append(p)
         wait_for("loaded", new.world)
@@ -100,3 +105,17 @@ def test_live_migration_on_one_gpu(old, new):
     for r in range(old.world):
         log = res[("saved", r)]
         assert any("packed" in m for m in log) and log[-1] == "migration_save: end", log
+    for r in range(new.world):
+        assert any("beside the old state" in m for m in res[("loaded", r)]["log"]), res[("loaded", r)]["log"]
+
+
+def test_live_migration_waiting_for_release():
+    old, new = Parallel(tp=2, pp=2), Parallel(tp=4)
+    print(f"[gpu live migration] {old} -> {new}, destinations after the old world's release", flush=True)
+    res = _run(old, new, wait_for_release=True)
+    for r in range(new.world):
+        rec = res[("loaded", r)]
+        assert rec["tensors"] > 0 and rec["bad"] == [], f"new rank {r}: {rec['bad'][:5]}"
+        assert any("after the old world released its state" in m for m in rec["log"]), rec["log"]
+    for r in range(old.world):
+        assert res[("saved", r)][-1] == "migration_save: end"
