@@ -47,3 +47,30 @@ def test_pack_layout_refuses_tensors_beyond_the_limit():
         pack_layout([0])
     where, sizes = pack_layout([_lib.HANDOFF_MAX_BYTES, 1])
     assert sizes == [_lib.HANDOFF_MAX_BYTES, 1] and where == [(0, 0), (1, 0)]
+
+
+def test_destination_bytes_sum_the_new_ranks_shards():
+    """The bytes a new rank reserves beside the old state: every name of its
+    layout once, its shard's elements times each field's item size from the
+    old ranks' records, each tensor rounded up to 256 bytes."""
+    from suika_amd import schedule_param_transfer
+    from suika_amd.handoff import _destination_bytes
+    from suika_amd.workloads import CONFIGS
+    w = CONFIGS["gpt125m_tp2_tp4"]
+    spl, tpl = w.layouts()
+    ops = schedule_param_transfer(spl, tpl)
+    fields = {"param": "torch.bfloat16", "exp_avg": "torch.float32", "exp_avg_sq": "torch.float32"}
+    records = [{"rank": r, "tensors": {n: {f: (0, 0, tuple(m.actual_shape()), dt) for f, dt in fields.items()}
+                                       for n, m in metas.items()}}
+               for r, metas in spl.layout.items()]
+    per_elem = {"torch.bfloat16": 2, "torch.float32": 4}
+    for rank, metas in tpl.layout.items():
+        want = 0
+        for n, m in metas.items():
+            numel = 1
+            for d in m.actual_shape():
+                numel *= int(d)
+            want += sum((numel * per_elem[dt] + ALIGN - 1) // ALIGN * ALIGN for dt in fields.values())
+        assert _destination_bytes(ops, rank, records) == want, rank
+    # a rank with no ops of its own needs nothing
+    assert _destination_bytes([op for op in ops if op.dst_rank != 0], 0, records) == 0
