@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SR_ABI_VERSION 4
+#define SR_ABI_VERSION 5
 
 typedef enum sr_status {
   SR_OK = 0,
@@ -246,6 +246,85 @@ int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
  */
 int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
                       hipStream_t stream);
+
+/* ------------------------------------------------ host-resident state
+ * The reference's fake-source (checkpoint) mode slices sources that live in
+ * host memory and moves each piece with .to(device), and returns the new
+ * state on the device it is asked for, "cpu" included
+ * (Suika/migration.py:477-482, 1235-1244).  Here the pieces' bytes, and only
+ * they, cross to the GPU in the peer-buffer layout; the GPU unpacks them
+ * (sr_unpack); sr_download brings results back to host memory.  Both go
+ * through a ring of SR_STAGE_WINDOWS pinned windows of SR_STAGE_WINDOW_BYTES
+ * per device, allocated on first use and held until the process exits, and
+ * copy between the caller's host memory and the windows on a pool of host
+ * threads (sr_set_host_threads).  A device's ring serves one call at a time:
+ * concurrent calls on one device wait for each other. */
+#define SR_STAGE_WINDOW_BYTES (16u << 20)
+#define SR_STAGE_WINDOWS 4
+
+/*
+ * Stage: sr_pack for sources in host memory.  Writes into the device peer
+ * buffers exactly the bytes sr_pack would write from the same source
+ * contents, so that sr_unpack then completes the reshard.  Each source slot
+ * a non-ZERO piece reads is classified by its address: in host memory
+ * (pageable or pinned), host threads copy the piece's rows into the pinned
+ * windows and each window goes to the device with host-to-device copies on
+ * `stream`; in device memory, the piece is copied on the device on `stream`
+ * (2-D copies).  Only piece bytes are read: a dim 0 piece is a row range of
+ * its source, a dim -1 piece one run per row.  The bytes between payloads
+ * (256-byte alignment) are left undefined; nothing reads them.
+ * Returns once every host source byte has been read (host sources may then
+ * change or be freed); the copies finish in stream order.  Replaces
+ * get_send_tensor(src).to(device) of the fake-source mode
+ * (Suika/migration.py:290-312, 477-482).
+ */
+int sr_stage_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs,
+                  hipStream_t stream);
+
+/*
+ * The host half of sr_stage_pack, for callers that move the buffers
+ * themselves (to a file, a socket, their own copy engine): every non-ZERO
+ * piece's source region, read from host memory at src_ptrs, is copied by
+ * host threads into host buffers peer_bufs in the peer-buffer layout
+ * (sr_plan_peer_bytes, sr_plan_piece_offset); a NULL buffer skips its peer
+ * and the slots only its pieces read.  No HIP call: no device, stream or
+ * pinned memory is involved, and the call returns when the buffers are
+ * written.  Same bytes as sr_pack from the same source contents.
+ */
+int sr_pack_host(const sr_plan* plan, const void* const* src_ptrs, void* const* peer_bufs);
+
+/*
+ * Copy `n` device regions into host memory: region i is bytes[i] bytes at
+ * device address dev_ptrs[i], written to host address host_ptrs[i]
+ * (pageable or pinned; regions may not overlap).  The device-to-host copies
+ * run on `stream` after the work queued there (for example the sr_unpack
+ * that wrote the regions), through the pinned windows, adjacent device
+ * regions in one copy; host threads move each window to its destinations.
+ * Returns when every host byte is written.  Serves execute_param_transfer's
+ * device="cpu" (Suika/migration.py:1235-1244), whose result the reference
+ * returns in host memory.
+ */
+int sr_download(const void* const* dev_ptrs, void* const* host_ptrs, const uint64_t* bytes, int32_t n,
+                hipStream_t stream);
+
+/*
+ * Host threads that sr_stage_pack and sr_download copy with, the calling
+ * thread included: n in [1, 256], or 0 for the default, the CPUs in the
+ * process's affinity mask up to 16.
+ */
+int sr_set_host_threads(int32_t n);
+
+/* Totals since the library was loaded (every device, every thread). */
+typedef struct sr_stage_counters {
+  uint64_t host_bytes_up;     /* bytes sr_stage_pack copied host -> device (windows: piece
+                                 bytes plus the alignment gaps between adjacent pieces) */
+  uint64_t host_piece_bytes;  /* piece bytes among them */
+  uint64_t device_piece_bytes;/* piece bytes sr_stage_pack copied on the device */
+  uint64_t bytes_down;        /* bytes sr_download copied device -> host */
+  uint64_t windows;           /* pinned windows filled or drained */
+} sr_stage_counters;
+
+int sr_stage_counters_get(sr_stage_counters* out);
 
 /*
  * Pay this process's first-use costs of the library on the current device

@@ -64,6 +64,11 @@ EXPORTED_SYMBOLS = (
     "sr_gather",
     "sr_gather_noalloc",
     "sr_prepare",
+    "sr_stage_pack",
+    "sr_pack_host",
+    "sr_download",
+    "sr_set_host_threads",
+    "sr_stage_counters_get",
     "sr_plan_destroy",
     "sr_schedule",
     "sr_lower",
@@ -82,10 +87,26 @@ class SrIpcHandle(ctypes.Structure):
     """The 64 opaque bytes of an exported hand-off allocation (sr_ipc_handle)."""
     _fields_ = [("bytes", ctypes.c_ubyte * 64)]
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Device bytes per GPU that sr_gather_noalloc keeps its tables in (SR_SCRATCH_BYTES).
 SCRATCH_BYTES = 64 << 20
+
+# Pinned staging windows of sr_stage_pack / sr_download (SR_STAGE_WINDOW_BYTES,
+# SR_STAGE_WINDOWS).
+STAGE_WINDOW_BYTES = 16 << 20
+STAGE_WINDOWS = 4
+
+
+class SrStageCounters(ctypes.Structure):
+    """Process totals of the host staging calls (sr_stage_counters)."""
+    _fields_ = [
+        ("host_bytes_up", ctypes.c_uint64),
+        ("host_piece_bytes", ctypes.c_uint64),
+        ("device_piece_bytes", ctypes.c_uint64),
+        ("bytes_down", ctypes.c_uint64),
+        ("windows", ctypes.c_uint64),
+    ]
 
 
 class SrTensor(ctypes.Structure):
@@ -278,6 +299,12 @@ class PlanError(AssertionError):
     ``assert`` checks (Suika/migration.py:293-294, 311, 356, 436, 441)."""
 
 
+class HostSourceError(PlanError):
+    """A source tensor in host memory where the device route takes only
+    tensors on the device; ``execute_param_transfer`` then stages the
+    transfer from host memory (``sr_stage_pack``)."""
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -314,6 +341,16 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.sr_gather_noalloc.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
     lib.sr_prepare.restype = ctypes.c_int
     lib.sr_prepare.argtypes = [vp]
+    lib.sr_stage_pack.restype = ctypes.c_int
+    lib.sr_stage_pack.argtypes = [vp, vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
+    lib.sr_pack_host.restype = ctypes.c_int
+    lib.sr_pack_host.argtypes = [vp, vp, vp]   # pointer arrays: ctypes arrays or addresses
+    lib.sr_download.restype = ctypes.c_int
+    lib.sr_download.argtypes = [vp, vp, vp, ctypes.c_int32, vp]
+    lib.sr_set_host_threads.restype = ctypes.c_int
+    lib.sr_set_host_threads.argtypes = [ctypes.c_int32]
+    lib.sr_stage_counters_get.restype = ctypes.c_int
+    lib.sr_stage_counters_get.argtypes = [ctypes.POINTER(SrStageCounters)]
     lib.sr_plan_destroy.restype = None
     lib.sr_plan_destroy.argtypes = [vp]
     i64 = ctypes.c_int64
@@ -374,6 +411,13 @@ def host():
         spec.loader.exec_module(mod)
         _host = mod
     return _host
+
+
+def stage_counters() -> SrStageCounters:
+    """The library's staging totals (sr_stage_counters_get)."""
+    out = SrStageCounters()
+    check(lib().sr_stage_counters_get(ctypes.byref(out)), "sr_stage_counters_get")
+    return out
 
 
 def last_error(handle: Optional[ctypes.CDLL] = None) -> str:

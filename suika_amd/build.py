@@ -6,7 +6,9 @@ any other FFI -- can load.  hipcc cross-compiles for gfx950 without a GPU
 present.  Sources: ``reshard.hip`` (plan builder and kernels),
 ``schedule.cpp`` and ``lower.cpp`` (the host-only planner: transfer schedule
 and its lowering to region moves), ``handoff.cpp`` (exported device
-allocations for the same-GPU state hand-off between processes).
+allocations for the same-GPU state hand-off between processes), ``stage.cpp``
+(sources in host memory packed into device buffers, results copied back to
+host memory, through pinned windows and a host thread pool).
 
 ``build_host`` compiles ``host_bind.cpp`` into ``suika_amd/lib/_suika_host.so``,
 the CPython extension (on torch's C++ API) that does the drop-in operator's
@@ -24,7 +26,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 SOURCES = [PKG_DIR / "csrc" / "reshard.hip", PKG_DIR / "csrc" / "schedule.cpp",
-           PKG_DIR / "csrc" / "lower.cpp", PKG_DIR / "csrc" / "handoff.cpp"]
+           PKG_DIR / "csrc" / "lower.cpp", PKG_DIR / "csrc" / "handoff.cpp", PKG_DIR / "csrc" / "stage.cpp"]
 INCLUDE = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "lib"
 LIB = LIB_DIR / "libsuika_reshard.so"

@@ -12,8 +12,10 @@ Same names, arguments, files and control flow as the reference's
 
 The reference reshards on the CPU (``execute_param_transfer`` with
 ``device="cpu"``, migration.py:1235-1244); here the source files are
-memory-mapped, only the tensors this rank's pieces read are copied to HBM,
-and the HIP engine reshards them (``route="direct"``: one gather launch).
+memory-mapped and handed to ``execute_param_transfer`` in host memory, which
+sends only the bytes of this rank's pieces to HBM (packed by host threads
+into the peer-buffer layout) and unpacks them on the GPU straight into the
+new state on ``device``.
 
 The files are the reference's: ``param_layout.pt`` is a pickled
 ``Suika.migration.ParamLayout`` of ``Suika.migration.TensorMeta`` objects and
@@ -266,12 +268,12 @@ def checkpoint_load(model: Module, optimizer: Union[Callable[[], Optimizer], Opt
     _barrier(world)
     fake = {}
     for src in sorted(needed):
-        # memory-mapped, so the shards this rank does not read are never
-        # paged in; the reference loads whole files to the CPU (migration.py:1223-1233)
+        # memory-mapped and handed over in host memory: the transfer reads
+        # only its pieces' bytes (pages) from the file and sends only those to
+        # the GPU; the reference loads whole files to the CPU (migration.py:1223-1233)
         sd = torch.load(os.path.join(checkpoint_dir, f"state_dict_{src}.pt"), weights_only=True,
                         map_location="cpu", mmap=True)
-        fake[src] = {name: {f: t.to(device) for f, t in sd[name].items()}
-                     for name in needed[src] if name in sd}
+        fake[src] = {name: sd[name] for name in needed[src] if name in sd}
         del sd
     self_source = fake.get(rank, {})
     warm.library_done.wait()

@@ -140,12 +140,23 @@ py::object attr(PyObject* o, PyObject* key) {
 constexpr int64_t kSpecWords = 10;   // sr_src_spec: dtype, ndim, shape[8]
 constexpr int64_t kKeyWords = 13;    // sr_slot_key: op, field, recast, dtype, ndim, shape[8]
 
+// A source in host memory met where only device sources are taken:
+// suika_amd._lib.HostSourceError (an AssertionError), which the drop-in
+// call answers by staging the transfer from host memory.
+[[noreturn]] void host_source(const std::string& msg) {
+  static PyObject* cls = py::object(py::module_::import("suika_amd._lib").attr("HostSourceError")).release().ptr();
+  PyErr_SetString(cls, msg.c_str());
+  throw py::error_already_set();
+}
+
 // The source tensor of every (op, field), checked once.  `source(rank)`
 // returns a rank's state dict; it is called once per rank, when the first op
 // of that rank is reached, so errors come in op order as in the reference's
-// loop (migration.py:426-494).
+// loop (migration.py:426-494).  A tensor is on device `device_index`, or,
+// with `host_ok`, in host memory (the addresses are then host addresses,
+// for sr_stage_pack only).
 py::tuple collect_sources(py::list ops, py::function source, py::list fields, int64_t device_index,
-                          const std::string& who) {
+                          const std::string& who, bool host_ok) {
   const Names& N = names_();
   py::dict sources;
   const int64_t n = int64_t(ops.size()), nf = int64_t(fields.size());
@@ -179,12 +190,13 @@ py::tuple collect_sources(py::list ops, py::function source, py::list fields, in
       const at::Tensor& t = THPVariable_Unpack(obj.ptr());
       const int64_t code = sr_code(t.scalar_type());
       const int64_t nd = t.dim();
-      if (!t.is_cuda() || t.get_device() != device_index || !t.is_contiguous() || code < 0 || nd > 8) {
+      const bool here = (t.is_cuda() && t.get_device() == device_index) || (host_ok && t.is_cpu());
+      if (!here || !t.is_contiguous() || code < 0 || nd > 8) {
         // the rare path: build the message
         const std::string fs = py::str(field).cast<std::string>();
         const std::string what = "source " + nm() + "/" + fs + " of rank " + py::str(rank).cast<std::string>();
-        if (!t.is_cuda() || t.get_device() != device_index)
-          assertion(what + " is on " + t.device().str() + ", not on " + want_device);
+        if (!here && t.is_cpu()) host_source(what + " is in host memory, not on " + want_device);
+        if (!here) assertion(what + " is on " + t.device().str() + ", not on " + want_device);
         if (!t.is_contiguous()) assertion(what + " is not contiguous");
         assertion("source " + nm() + "/" + fs + ": " + py::str(dtype_object(t.scalar_type())).cast<std::string>() +
                   ", " + std::to_string(nd) + "-D is not supported by the reshard engine");
@@ -1226,7 +1238,9 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
                        py::function infer_shard, int64_t device_index, const std::string& who,
                        uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
                        py::dtype piece_dt, bool gather, uint64_t stream, py::object dst_part,
-                       py::object ahead) {
+                       py::object ahead, bool host_ok) {
+  // host addresses are for sr_stage_pack alone: a kernel must never see one
+  if (gather && host_ok) throw py::value_error("host-resident sources cannot be gathered on the device");
   const Names& N = names_();
   const Py_ssize_t n = PyList_GET_SIZE(ops.ptr());
   const int64_t nf = int64_t(fields.size());
@@ -1276,7 +1290,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
     }
     shards[names[i]] = shard;
   }
-  py::tuple col = collect_sources(ops, source, fields, device_index, who);
+  py::tuple col = collect_sources(ops, source, fields, device_index, who, host_ok);
   py::array_t<int64_t> specs = col[0].cast<py::array_t<int64_t>>();
   py::array_t<uint64_t> ptrs = col[2].cast<py::array_t<uint64_t>>();
   // one torch dtype per (tensor, field) across its sources: the library
@@ -1421,7 +1435,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
 PYBIND11_MODULE(_suika_host, m) {
   m.doc() = "Per-tensor host work of execute_param_transfer (source checks, destination allocation)";
   m.def("collect_sources", &collect_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
-        py::arg("device_index"), py::arg("who"));
+        py::arg("device_index"), py::arg("who"), py::arg("host_ok") = false);
   m.def(
       "alloc_dst",
       [](const RowTable& rows, const RowTable& empty_rows, py::list names, py::list fields, py::list recast_names,
@@ -1455,5 +1469,5 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),
         py::arg("tile_bytes"), py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"),
         py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0, py::arg("dst_part") = py::none(),
-        py::arg("ahead") = py::none());
+        py::arg("ahead") = py::none(), py::arg("host_ok") = false);
 }

@@ -91,6 +91,19 @@ int fail(int code, const char* fmt, ...) {
 
 const char* last_error() { return g_last_error.c_str(); }
 
+int dtype_size(int32_t dt) {
+  switch (dt) {
+    case SR_DT_U8: return 1;
+    case SR_DT_BF16: return 2;
+    case SR_DT_F16: return 2;
+    case SR_DT_F32: return 4;
+    case SR_DT_F64: return 8;
+    case SR_DT_I32: return 4;
+    case SR_DT_I64: return 8;
+    default: return 0;
+  }
+}
+
 }  // namespace sr_internal
 
 namespace {
@@ -139,18 +152,7 @@ using sr_internal::fail;
       return fail(SR_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));    \
   } while (0)
 
-int dtype_size(int32_t dt) {
-  switch (dt) {
-    case SR_DT_U8: return 1;
-    case SR_DT_BF16: return 2;
-    case SR_DT_F16: return 2;
-    case SR_DT_F32: return 4;
-    case SR_DT_F64: return 8;
-    case SR_DT_I32: return 4;
-    case SR_DT_I64: return 8;
-    default: return 0;
-  }
-}
+using sr_internal::dtype_size;
 
 // ------------------------------------------------ invariant integer division
 // Granlund & Montgomery, "Division by invariant integers using
@@ -796,6 +798,13 @@ struct sr_plan {
   uint64_t* d_payload = nullptr;
   hipEvent_t ev_offsets = nullptr;
 };
+
+namespace sr_internal {
+PlanView plan_view(const sr_plan* p) {
+  return PlanView{p->src.data(), p->src.size(), p->pieces.data(), p->pieces.size(), p->piece_offset.data(),
+                  p->peer_bytes.data(), p->n_peers, p->peer_begin.data(), p->peer_list.data()};
+}
+}  // namespace sr_internal
 
 namespace {
 

@@ -12,7 +12,13 @@ into a ``ReshardPlan`` and runs it on the GPU, either as one gather pass
 (sources -> destination) or as pack -> per-peer buffers -> unpack.  On one
 GPU all peers' shards are resident in this GPU's HBM
 (``fake_source_state_dicts`` holds them, as in the reference's checkpoint
-path, migration.py:1223-1244).  A cross-GPU exchange between pack and unpack is not
+path, migration.py:1223-1244).  Sources may also live in host memory, as the
+reference's checkpoint path loads them (migration.py:477-482, 583), and the
+result may be asked for on ``device="cpu"`` (:1235-1244): then only the
+pieces' bytes go to the GPU, packed by host threads through pinned windows
+(``sr_stage_pack``), the GPU unpacks them, and a host result comes back
+through the same windows (``sr_download``).  There is no CPU reshard: without
+a GPU the call raises.  A cross-GPU exchange between pack and unpack is not
 part of this build: ops from a remote rank without a local copy of its shards
 raise ``NotImplementedError``.
 
@@ -40,7 +46,7 @@ from torch.optim import Optimizer
 from .meta import (CHUNK, QKV_HEADS, ParamLayout, TensorMeta, TransferOp,
                    get_named_parameters_and_persistent_buffers, schedule_param_transfer)
 from . import _lib
-from .plan import PlanOptions, ReshardPlan
+from .plan import PlanOptions, ReshardPlan, download
 
 StateDict = Dict[str, Dict[str, Tensor]]
 
@@ -127,6 +133,14 @@ def execute_param_transfer(
     stream (which may be producing the sources).  The returned dict lists
     the tensors in schedule order whatever the launch order.  The call
     returns when the kernels are done.
+
+    ``device`` is where the new state is returned: a GPU, or ``"cpu"`` (the
+    reference's checkpoint_load, migration.py:1235-1244), whose result is
+    resharded on the current GPU and copied back to host memory.  Sources
+    in host memory (the fake-source mode, migration.py:477-482) are staged:
+    only the bytes of the pieces this rank reads cross to the GPU, packed by
+    host threads into the peer-buffer layout, and the GPU unpacks them; such
+    a transfer runs as one launch group (the host copies set its pace).
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     _lib.lib()   # raises when the HIP library is missing: there is no other path
@@ -136,10 +150,16 @@ def execute_param_transfer(
         prof = _NoProf()
     if not isinstance(device, torch.device):
         device = torch.device(device)
-    assert device.type == "cuda", \
-        f"execute_param_transfer runs on the GPU reshard engine; got device {device}"
-    if device.index is None:
+    assert device.type in ("cuda", "cpu"), \
+        f"execute_param_transfer returns state on a GPU or in host memory; got device {device}"
+    if device.type == "cuda" and device.index is None:
         device = torch.device("cuda", torch.cuda.current_device())
+    # the GPU the reshard runs on: the device asked for, or for host results
+    # the current one (the kernels do the work either way; no CPU path)
+    if device.type == "cpu" and not torch.cuda.is_available():
+        raise RuntimeError("execute_param_transfer reshards on the GPU engine, also for device='cpu'; "
+                           "no GPU is available")
+    gpu = device if device.type == "cuda" else torch.device("cuda", torch.cuda.current_device())
     if rank is None:
         rank = _current_rank(world)
 
@@ -169,6 +189,9 @@ def execute_param_transfer(
         elem_bytes = sum(first[f].element_size() for f in normal if f in first)
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
     groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:5])
+    # the staged route (sources in host memory, or results for the host)
+    # packs on the host and unpacks on the GPU: its plans keep both phases
+    stage_options = replace(plan_options, gather_only=False) if plan_options is not None else None
     if route == "direct":   # the plans only ever gather
         plan_options = _GATHER_ONLY if plan_options is None else replace(plan_options, gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
@@ -178,68 +201,121 @@ def execute_param_transfer(
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
+
+    def staged(todo: List[TransferOp]) -> None:
+        """The transfer of ``todo`` from sources wherever they are: the
+        pieces' bytes packed on the host (or on the GPU for sources there)
+        into peer buffers in HBM, the unpack on the GPU, and for host results
+        the copy back.  One launch group: the copies to and from the host
+        set the pace, the GPU's unpack takes a small share of it."""
+        prof.start("execute stage")
+        plan, src_ptrs = ReshardPlan.from_sources(todo, source, normal, gpu, recast=recast, options=stage_options,
+                                                  rank=rank, host_ok=True)
+        plans.append(plan)
+        bufs = plan.alloc_buffers(gpu)
+        buffers.append(bufs)
+        buf_ptrs = [b.data_ptr() for b in bufs]
+        plan.stage_pack_ptrs(src_ptrs, buf_ptrs, stream)
+        names = dict.fromkeys(op.param_name for op in todo)
+        if device.type == "cuda":
+            if arena_views is None:
+                part, dst_ptrs = plan.alloc_dst_ptrs(device)
+            else:
+                part = {name: arena_views[name] for name in names}
+                dst_ptrs = plan.bind_dst_ptrs(part, device)
+            plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
+        else:
+            # the GPU's result in one temporary allocation, then host memory
+            hbm = plan.alloc_dst(gpu, arena=True)
+            plan.unpack_ptrs(buf_ptrs, plan.bind_dst_ptrs(hbm, gpu), stream)
+            if arena_views is not None:
+                part = {name: arena_views[name] for name in names}
+            else:
+                part = {name: {f: torch.empty(t.shape, dtype=t.dtype) for f, t in ent.items()}
+                        for name, ent in hbm.items()}
+            download([(t, part[name][f]) for name, ent in hbm.items() for f, t in ent.items()], stream)
+            del hbm
+        target.update(part)
+        prof.stop("execute stage")
+
+    def _device_group(group: List[TransferOp]) -> None:
+        """One launch group from sources on the device: planned, allocated
+        and gathered in one native call (direct route), or packed into peer
+        buffers and unpacked (buffers route).  A source in host memory
+        raises ``_lib.HostSourceError`` before any allocation or launch."""
+        if route == "direct":
+            # plan (shapes, dtypes and addresses read from the source
+            # tensors, each checked once), the destinations (fresh, or
+            # the arena's views) and the gather into them: one native
+            # call
+            part = None
+            if arena_views is not None:
+                part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
+            prof.start("execute gather")
+            try:
+                plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
+                                                        options=plan_options, rank=rank, stream=stream,
+                                                        dst=part, ahead=ahead)
+            finally:
+                prof.stop("execute gather")
+            plans.append(plan)
+            target.update(part)
+            return
+        prof.start("execute schedule lowering")
+        # shapes, dtypes and addresses read from the source tensors (each
+        # checked once: contiguous, on this device)
+        try:
+            plan, src_ptrs = ReshardPlan.from_sources(group, source, normal, device, recast=recast,
+                                                      options=plan_options, rank=rank)
+        finally:
+            prof.stop("execute schedule lowering")
+        plans.append(plan)
+        if arena_views is None:
+            # fresh tensors of the planned shapes: their addresses need no check
+            part, dst_ptrs = plan.alloc_dst_ptrs(device)
+        else:
+            part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
+            dst_ptrs = plan.bind_dst_ptrs(part, device)
+        bufs = plan.alloc_buffers(device)
+        buffers.append(bufs)
+        buf_ptrs = [b.data_ptr() for b in bufs]
+        prof.start("execute pack")
+        plan.pack_ptrs(src_ptrs, buf_ptrs, stream)
+        prof.stop("execute pack")
+        prof.start("execute unpack")
+        plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
+        prof.stop("execute unpack")
+        target.update(part)
+
     # A full pass of Python's cyclic collector over a large heap (tens of ms)
     # would stall the host between launch groups and idle the GPU; it is
     # paused for the call (reference counting still frees memory).
     if stream is not None:
         # the sources (and memory the allocator hands out) may still be in
         # use by work queued on the current stream
-        cur = torch.cuda.current_stream(device)
+        cur = torch.cuda.current_stream(gpu)
         if stream != cur:
             stream.wait_stream(cur)
     gc_was_enabled = gc.isenabled()
     gc.disable()
     prof.stop("execute prologue")
     try:
-        with (contextlib.nullcontext() if device.index == torch.cuda.current_device()
-              else torch.cuda.device(device)):
+        with (contextlib.nullcontext() if gpu.index == torch.cuda.current_device()
+              else torch.cuda.device(gpu)):
             # Each group is planned on the host while the GPU runs the
-            # previous group's launch.
-            for group in groups:
-                if route == "direct":
-                    # plan (shapes, dtypes and addresses read from the source
-                    # tensors, each checked once), the destinations (fresh, or
-                    # the arena's views) and the gather into them: one native
-                    # call
-                    part = None
-                    if arena_views is not None:
-                        part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
-                    prof.start("execute gather")
-                    plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
-                                                            options=plan_options, rank=rank, stream=stream,
-                                                            dst=part, ahead=ahead)
-                    prof.stop("execute gather")
-                    plans.append(plan)
-                    target.update(part)
-                    continue
-                prof.start("execute schedule lowering")
-                # shapes, dtypes and addresses read from the source tensors (each
-                # checked once: contiguous, on this device)
-                plan, src_ptrs = ReshardPlan.from_sources(group, source, normal, device, recast=recast,
-                                                          options=plan_options, rank=rank)
-                prof.stop("execute schedule lowering")
-                plans.append(plan)
-                if arena_views is None:
-                    # fresh tensors of the planned shapes: their addresses need no check
-                    part, dst_ptrs = plan.alloc_dst_ptrs(device)
-                else:
-                    part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
-                    dst_ptrs = plan.bind_dst_ptrs(part, device)
-                if route == "direct":
-                    prof.start("execute gather")
-                    plan.gather_ptrs(src_ptrs, dst_ptrs, stream)
-                    prof.stop("execute gather")
-                else:
-                    bufs = plan.alloc_buffers(device)
-                    buffers.append(bufs)
-                    buf_ptrs = [b.data_ptr() for b in bufs]
-                    prof.start("execute pack")
-                    plan.pack_ptrs(src_ptrs, buf_ptrs, stream)
-                    prof.stop("execute pack")
-                    prof.start("execute unpack")
-                    plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
-                    prof.stop("execute unpack")
-                target.update(part)
+            # previous group's launch.  A source in host memory sends the
+            # rest of the transfer through the staged route.
+            done_names: Dict[str, None] = {}
+            for group in (() if device.type == "cpu" else groups):
+                try:
+                    _device_group(group)
+                except _lib.HostSourceError:
+                    staged([op for op in ops if op.param_name not in done_names] if done_names else ops)
+                    break
+                done_names.update(dict.fromkeys(op.param_name for op in group))
+            else:
+                if device.type == "cpu":
+                    staged(ops)
         log_func(f"=== reshard plan: {sum(p.n_pieces for p in plans)} pieces in {len(plans)} "
                  f"launch group(s), {sum(p.info.buffer_bytes for p in plans) / 1e6:.1f} MB of buffers ===")
 
@@ -260,7 +336,7 @@ def execute_param_transfer(
         # recast targets first, then the sub-fields in their order
         field_order = list(recast) + [f for f, _ in expected_sub_fields if f not in recast]
         ordered: StateDict = _lib.host().ordered_result(ops, target, field_order)
-        if gc_was_enabled and not (stream or torch.cuda.current_stream(device)).query():
+        if gc_was_enabled and not (stream or torch.cuda.current_stream(gpu)).query():
             # the youngest generation, thousands of objects made by this call
             # (tensors, dicts), is collected while the last launches still
             # run, where it costs nothing, instead of on the caller's first

@@ -113,6 +113,31 @@ def _stream_handle(stream) -> ctypes.c_void_p:
     return ctypes.c_void_p(int(stream))
 
 
+def download(pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]], stream=None) -> None:
+    """Copy each device tensor of ``pairs`` (device, host) into its host
+    tensor (``sr_download``: through the library's pinned windows, on
+    ``stream`` after the work queued there); returns when the host tensors
+    hold the bytes."""
+    dev, host, nbytes = [], [], []
+    cur = torch.cuda.current_device()
+    for d, h in pairs:
+        n = d.numel() * d.element_size()
+        assert d.is_cuda and d.get_device() == cur and d.is_contiguous(), "download: source must be on the device"
+        assert h.is_cpu and h.is_contiguous() and h.numel() * h.element_size() == n, \
+            "download: destination must be a contiguous host tensor of the same size"
+        if n:
+            dev.append(d.data_ptr())
+            host.append(h.data_ptr())
+            nbytes.append(n)
+    if not nbytes:
+        return
+    L = _lib.lib()
+    k = len(nbytes)
+    rc = L.sr_download((ctypes.c_void_p * k)(*dev), (ctypes.c_void_p * k)(*host), (ctypes.c_uint64 * k)(*nbytes),
+                       k, _stream_handle(stream))
+    _lib.check(rc, "sr_download", L)
+
+
 class ReshardPlan:
     """Pack/unpack plan of one destination rank's share of a reshard."""
 
@@ -142,16 +167,21 @@ class ReshardPlan:
                      fields: Sequence[str], device: torch.device,
                      recast: Optional[Mapping[str, str]] = None,
                      options: Optional[PlanOptions] = None,
-                     rank: Optional[int] = None) -> Tuple["ReshardPlan", List[int]]:
+                     rank: Optional[int] = None,
+                     host_ok: bool = False) -> Tuple["ReshardPlan", List[int]]:
         """The plan of ``ops`` with shapes and dtypes read from the source
-        tensors themselves, and the device address of every source slot (a
-        uint64 array).
+        tensors themselves, and the address of every source slot (a uint64
+        array).
 
         ``source(r)`` is rank ``r``'s state dict ``{name: {field: Tensor}}``.
         Each tensor is read once: it must be a contiguous CUDA tensor on
-        ``device``.  ``rank`` (the executing rank) only prefixes messages.
+        ``device`` -- or, with ``host_ok``, a contiguous tensor in host
+        memory, whose address is then a host address that only
+        ``stage_pack_ptrs`` may be given (a source in host memory without
+        ``host_ok`` raises ``_lib.HostSourceError``).  ``rank`` (the
+        executing rank) only prefixes messages.
         """
-        plan, src_ptrs, _ = cls._native(ops, source, fields, device, recast, options, rank)
+        plan, src_ptrs, _ = cls._native(ops, source, fields, device, recast, options, rank, host_ok=host_ok)
         return plan, src_ptrs
 
     @classmethod
@@ -176,7 +206,7 @@ class ReshardPlan:
 
     @classmethod
     def _native(cls, ops, source, fields, device, recast, options, rank, gather=False, stream=0, dst=None,
-                ahead=None):
+                ahead=None, host_ok=False):
         self = cls.__new__(cls)
         self._configure(ops, fields, recast, options)
         dev_index = device.index if device.index is not None else torch.cuda.current_device()
@@ -190,7 +220,7 @@ class ReshardPlan:
          self._empty_rows, self.peer_bytes, info, part) = _lib.host().plan_sources(
             self._ops, source, self.fields, [self._recast_of.get(f) for f in self.fields],
             infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
-            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst, ahead)
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst, ahead, host_ok)
         self._handle = ctypes.c_void_p(handle)
         self.info = _lib.SrPlanInfo.from_buffer_copy(info)
         self.n_pieces = len(self._piece_arr)
@@ -523,6 +553,14 @@ class ReshardPlan:
                                _stream_handle(stream))
         _lib.check(rc, "sr_gather", self._L)
 
+    def stage_pack_ptrs(self, src_ptrs, buf_ptrs: List[int], stream=None) -> None:
+        """``sr_stage_pack``: the pack, for sources in host memory (or on the
+        device), into device peer buffers, through the library's pinned
+        windows; returns once the host sources have been read."""
+        rc = self._L.sr_stage_pack(self._handle, self._carray(src_ptrs), self._carray(buf_ptrs),
+                                   _stream_handle(stream))
+        _lib.check(rc, "sr_stage_pack", self._L)
+
     def gather_noalloc_ptrs(self, src_ptrs: List[int], dst_ptrs: List[int], stream=None) -> None:
         """``sr_gather_noalloc``: the same gather with its device tables in
         the library's static per-GPU scratch (no device allocation); calls
@@ -546,6 +584,28 @@ class ReshardPlan:
     def unpack(self, buffers, dst, stream=None) -> None:
         """Peer buffers -> destination shards (async on ``stream``)."""
         self.unpack_ptrs(self.buf_pointers(buffers), self.dst_pointers(dst), stream)
+
+    def pack_host_ptrs(self, src_ptrs, buf_ptrs) -> None:
+        """``sr_pack_host``: the pack from host-memory sources into host
+        buffers (a null buffer address skips its peer), on host threads."""
+        rc = self._L.sr_pack_host(self._handle, self._carray(src_ptrs), self._carray(buf_ptrs))
+        _lib.check(rc, "sr_pack_host", self._L)
+
+    def stage_pack(self, sources, buffers, stream=None) -> None:
+        """Source shards in host memory (or on the device) -> peer buffers on
+        the device (``sr_stage_pack``); the buffers then hold what ``pack``
+        writes from the same contents."""
+        ptrs = []
+        for key in self.src_keys:
+            rank, name, field = key
+            t = sources[rank][name][field]
+            spec = self.src_specs[key]
+            assert isinstance(t, torch.Tensor) and t.is_contiguous(), f"{key}: not a contiguous tensor"
+            assert tuple(t.shape) == tuple(spec.shape) and t.dtype == spec.dtype, \
+                f"{key}: {tuple(t.shape)} {t.dtype} != {spec.shape} {spec.dtype}"
+            assert t.is_cpu or t.get_device() == torch.cuda.current_device(), f"{key}: on {t.device}"
+            ptrs.append(t.data_ptr())
+        self.stage_pack_ptrs(ptrs, self.buf_pointers(buffers), stream)
 
     def close(self) -> None:
         if getattr(self, "_handle", None) is not None and self._handle.value:

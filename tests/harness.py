@@ -251,18 +251,19 @@ def simulate_plan(plan, srcs_np, esize_of) -> Dict[Tuple[str, str], np.ndarray]:
     """Execute a ReshardPlan's pieces with numpy (bytes), pack then unpack.
 
     Checks the host lowering and the library's buffer layout without a GPU."""
+    return simulate_unpack(plan, simulate_pack(plan, srcs_np, esize_of), esize_of)
+
+
+def simulate_pack(plan, srcs_np, esize_of) -> List[np.ndarray]:
+    """The peer buffers of a ReshardPlan, packed with numpy from the source
+    bit patterns ``srcs_np[rank][name][field]``; gaps between payloads are 0."""
     from suika_amd import _lib
     src_mats = []
     for (r, name, f) in plan.src_keys:
         a = np.ascontiguousarray(srcs_np[r][name][f])
         src_mats.append(a)
     bufs = [np.zeros(max(1, n), dtype=np.uint8) for n in plan.peer_bytes]
-    dst = {}
-    for key in plan.dst_keys:
-        spec = plan.dst_specs[key]
-        dst[key] = np.full(int(np.prod(spec.shape)) * spec.dtype.itemsize, 0xAB, dtype=np.uint8)
     c_src = plan.c_src
-    c_dst = plan.c_dst
     for k, pc in enumerate(plan.pieces):
         if pc.kind == _lib.SR_PIECE_ZERO:
             continue
@@ -273,6 +274,31 @@ def simulate_plan(plan, srcs_np, esize_of) -> Dict[Tuple[str, str], np.ndarray]:
         off = plan.piece_offset(k)
         n = payload.size
         bufs[pc.peer][off:off + n] = payload.reshape(-1)
+    return bufs
+
+
+def payload_spans(plan, esize_of) -> List[Tuple[int, int, int]]:
+    """(peer, offset, bytes) of every non-ZERO piece's payload."""
+    from suika_amd import _lib
+    out = []
+    c_src = plan.c_src
+    for k, pc in enumerate(plan.pieces):
+        if pc.kind == _lib.SR_PIECE_ZERO:
+            continue
+        out.append((pc.peer, plan.piece_offset(k), pc.rows * pc.cols * esize_of(c_src[pc.src].dtype)))
+    return out
+
+
+def simulate_unpack(plan, bufs, esize_of) -> Dict[Tuple[str, str], np.ndarray]:
+    """The destinations a ReshardPlan's unpack writes from peer buffers
+    ``bufs`` (numpy bytes), computed with numpy."""
+    from suika_amd import _lib
+    dst = {}
+    for key in plan.dst_keys:
+        spec = plan.dst_specs[key]
+        dst[key] = np.full(int(np.prod(spec.shape)) * spec.dtype.itemsize, 0xAB, dtype=np.uint8)
+    c_src = plan.c_src
+    c_dst = plan.c_dst
     for k, pc in enumerate(plan.pieces):
         if pc.kind == _lib.SR_PIECE_ZERO:
             dt_ = c_dst[pc.dst]

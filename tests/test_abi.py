@@ -21,7 +21,7 @@ def header_functions():
 
 def test_library_loads_and_version():
     L = _lib.lib()
-    assert L.sr_abi_version() == _lib.ABI_VERSION == 4
+    assert L.sr_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_every_declared_symbol_is_exported():

@@ -57,10 +57,10 @@ def rank_state(par: Parallel, rank: int, glob, device="cpu"):
     return mod, opt
 
 
-def _save_worker(rank, world, port, ckpt):
+def _save_worker(rank, world, port, ckpt, save_par=SAVE_PAR):
     dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank, world_size=world)
     try:
-        mod, opt = rank_state(Parallel(*SAVE_PAR), rank, global_tensors())
+        mod, opt = rank_state(Parallel(*save_par), rank, global_tensors())
         checkpoint_save(mod, opt, {"iteration": 7, "tag": "ckpt"}, ckpt)
         dist.barrier()
     finally:
@@ -73,9 +73,9 @@ def _free_port():
         return s.getsockname()[1]
 
 
-def write_checkpoint(ckpt):
-    par = Parallel(*SAVE_PAR)
-    mp.spawn(_save_worker, args=(par.world, _free_port(), str(ckpt)), nprocs=par.world, join=True)
+def write_checkpoint(ckpt, save_par=SAVE_PAR):
+    par = Parallel(*save_par)
+    mp.spawn(_save_worker, args=(par.world, _free_port(), str(ckpt), save_par), nprocs=par.world, join=True)
 
 
 def test_layout_plain_roundtrip():
@@ -135,9 +135,9 @@ def test_migration_api_matches_the_reference_signatures():
                                               "other_context_dict": {}}
 
 
-def _check_loaded(model, opt, par, rank, glob):
+def _check_loaded(model, opt, par, rank, glob, save_par=SAVE_PAR):
     metas = build_layout(MODEL, par, torch.float32).layout[rank]
-    src_layout = build_layout(MODEL, Parallel(*SAVE_PAR), torch.float32)
+    src_layout = build_layout(MODEL, Parallel(*save_par), torch.float32)
     ops = [op for op in schedule_param_transfer(src_layout, build_layout(MODEL, par, torch.float32))
            if op.dst_rank == rank]
     first_src = {}
@@ -182,6 +182,31 @@ def test_migration_load_checkpoint_resume_tp4_stage(tmp_path):
     ctx = migration_load(None, model, opt, checkpoint_resume=str(tmp_path))
     assert ctx == {"iteration": 7, "tag": "ckpt"}
     _check_loaded(model, opt, par, 0, global_tensors())
+
+
+@pytest.mark.gpu
+def test_checkpoint_tp1_to_tp4_stages_only_piece_bytes(tmp_path):
+    """A TP1 checkpoint loaded by rank 0 of TP4: the state files stay in host
+    memory (memory-mapped) and only this rank's pieces -- a quarter of every
+    split tensor -- go to HBM, which is exactly the new shard's bytes."""
+    from suika_amd import _lib
+    print("[gpu checkpoint] tp1 -> tp4 staged bytes", flush=True)
+    write_checkpoint(tmp_path, save_par=(1, 1))
+    par = Parallel(4)
+    model = build_module(MODEL, par, 0, torch.float32, "cuda")
+    before = _lib.stage_counters()
+    opt, ctx = checkpoint_load(model, lambda: torch.optim.AdamW(model.parameters(), lr=1e-3), str(tmp_path))
+    after = _lib.stage_counters()
+    assert ctx == {"iteration": 7, "tag": "ckpt"}
+    _check_loaded(model, opt, par, 0, global_tensors(), save_par=(1, 1))
+    shard_bytes = 3 * sum(p.numel() * p.element_size() for p in model.parameters())   # param, exp_avg, exp_avg_sq
+    whole_bytes = 3 * sum(int(np.prod(m.shape)) * 4
+                          for m in build_layout(MODEL, Parallel(1), torch.float32).layout[0].values())
+    assert after.host_piece_bytes - before.host_piece_bytes == shard_bytes
+    assert after.device_piece_bytes == before.device_piece_bytes, "no source was on the device"
+    staged = after.host_bytes_up - before.host_bytes_up
+    assert shard_bytes <= staged <= shard_bytes + 256 * 3 * len(list(model.parameters()))
+    assert staged < whole_bytes / 3, (staged, whole_bytes)
 
 
 @pytest.mark.gpu

@@ -509,7 +509,7 @@ def test_from_sources_rejects_bad_sources_by_name():
     def plan(sd):
         return ReshardPlan.from_sources(ops, lambda r: sd, ["param"], dev, rank=0)
 
-    with pytest.raises(AssertionError, match=r"source w/param of rank 3 is on cpu, not on cuda:0"):
+    with pytest.raises(AssertionError, match=r"source w/param of rank 3 is in host memory, not on cuda:0"):
         plan({"w": {"param": torch.zeros(4, 4)}})
     with pytest.raises(AssertionError, match=r"\[0\]: param missing in source w"):
         plan({})
