@@ -79,6 +79,10 @@ def parse_args(argv=None):
                          "comparator to live migration): the old world's processes checkpoint_save into a "
                          "new directory inside DIR (removed afterwards), then new processes checkpoint_load "
                          "it on this GPU; print the timings, then exit")
+    ap.add_argument("--host-state", action="store_true",
+                    help="only time the checkpoint-resume reshard of --config from source shards in host "
+                         "memory (result on device='cpu' and on the GPU) beside the torch-CPU reference, "
+                         "--steps timed calls each, then exit")
     ap.add_argument("--traffic-file", default=str(ROOT / "profiles" / "traffic.json"),
                     help="measured HBM bytes per launch (from rocprofv3 --pmc), if present")
     ap.add_argument("--json-out", default=None)
@@ -101,7 +105,8 @@ def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0, srcs=None
     host copies of what the GPU resharded); without them (the sample) they
     are generated with the workload's seed on the CPU.  Returns (seconds per
     run, algorithmic bytes of the share, runs, decoder layers of the share,
-    the untimed run's output if ``keep_output``)."""
+    the untimed run's output if ``keep_output``, the bytes the CPU path moves:
+    P read + D written)."""
     import torch
     from oracle import reshard_oracle as O
     from oracle.torch_ref import execute_torch_cpu
@@ -144,10 +149,11 @@ def cpu_baseline(w, threads: int, min_seconds: float, layers: int = 0, srcs=None
              for op in ops_p for f in ws.src_fields}
     plan = ReshardPlan(ops_p, specs, list(ws.src_fields), recast=ws.recast_map)
     b_alg = plan.pack_bytes + plan.unpack_bytes
+    b_min = int(plan.info.pack_bytes_read + plan.info.unpack_bytes_written)
     plan.close()
     dst_pp = ws.dst.coord(ws.dst_rank)[0]
     n_dst_layers = layer_partition(ws.model.n_layer, ws.dst.pp)[dst_pp]
-    return total / runs, b_alg, runs, n_dst_layers, kept
+    return total / runs, b_alg, runs, n_dst_layers, kept, b_min
 
 
 def mismatches(keys, got, want, device=None) -> list:
@@ -480,6 +486,114 @@ def host_sources_leg(plan, sources, sp, dp, stream, repeats: int = 3) -> dict:
             "gather_ms": round(g_ms, 3), "total_ms": round(h_ms + g_ms, 2),
             "pcie_inclusive_GBps": round(b_gather / ((h_ms + g_ms) * 1e-3) / 1e9, 1),
             "note": "gather bytes (P + D) over host-to-device copies + gather; not the headline value"}
+
+
+class _PhaseTimes:
+    """A profiler for execute_param_transfer's ``prof``: host wall time per
+    bracket (ms, summed over the call)."""
+
+    def __init__(self):
+        self.ms = {}
+        self._t0 = {}
+
+    def start(self, name):
+        self._t0[name] = time.perf_counter()
+
+    def stop(self, name):
+        self.ms[name] = self.ms.get(name, 0.0) + (time.perf_counter() - self._t0.pop(name)) * 1e3
+
+
+def host_state_leg(w, dev, repeats: int, cpu_seconds: float) -> dict:
+    """The reference's checkpoint-resume reshard (migration.py:1235-1244) on
+    the share of ``w``: the source shards in pageable host memory (as
+    torch.load returns them), resharded by execute_param_transfer with the
+    result on ``device="cpu"`` (the reference's call) and on the GPU (the
+    on-load of migration.py:583).  Beside them: the torch-CPU reshard of the
+    same host tensors (the reference's own path) and the whole source tensors
+    copied to HBM before a gather (what checkpoint_load did before staging
+    only piece bytes).  Wall time of the call, host to host (or host to HBM);
+    the first call of each kind is untimed."""
+    import torch
+    from suika_amd import _lib, execute_param_transfer
+    from suika_amd.workloads import make_source_state
+    ops = w.ops()
+    ranks = sorted({op.src_rank for op in ops})
+    print(f"[bench] host state {w.key}: generating sources", file=sys.stderr, flush=True)
+    src_dev = make_source_state(w, ranks, dev)
+    host = {r: {n: {f: t.cpu() for f, t in e.items()} for n, e in sd.items()} for r, sd in src_dev.items()}
+    del src_dev
+    torch.cuda.empty_cache()
+    esf = [(f, "normal") for f in w.src_fields]
+    threads = len(os.sched_getaffinity(0))
+    print(f"[bench] host state: torch-CPU reshard, {threads} threads", file=sys.stderr, flush=True)
+    t_cpu, _, runs_cpu, _, want, b_min = cpu_baseline(w, threads, cpu_seconds, srcs=host, keep_output=True)
+    keys = [(n, f) for n, e in want.items() for f in e]
+    out = {"workload": w.description or w.key, "key": w.key, "runs": repeats, "B_min_bytes": b_min,
+           "cpu_reference": {"ms": round(t_cpu * 1e3, 2), "threads": threads, "runs": runs_cpu,
+                             "GBps": round(b_min / t_cpu / 1e9, 2), "cpu_model": cpu_model(),
+                             "what": "torch-CPU chunk/contiguous/cat reshard (oracle/torch_ref.py) of the "
+                                     "same host tensors"},
+           "parity": {"tensors": len(keys), "mismatched": 0}}
+
+    def call(device):
+        prof = _PhaseTimes()
+        c0 = _lib.stage_counters()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = execute_param_transfer(ops, {}, device, esf, rank=w.dst_rank, prof=prof,
+                                     fake_source_state_dicts=host, recast=w.recast_map)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3
+        c1 = _lib.stage_counters()
+        return res, ms, prof.ms, (c1.host_piece_bytes - c0.host_piece_bytes, c1.host_bytes_up - c0.host_bytes_up,
+                                  c1.bytes_down - c0.bytes_down)
+
+    for device in ("cpu", "cuda"):
+        walls, phases = [], {}
+        for i in range(repeats + 1):
+            res, ms, ph, moved = call(device)
+            if i == 0:
+                bad = mismatches(keys, res, want, device=dev if device == "cuda" else None)
+                out["parity"]["mismatched"] += len(bad)
+                if bad:
+                    out["parity"].setdefault("first_mismatches", {})[device] = bad[:5]
+                    print(f"[bench] PARITY: device={device} differs in {len(bad)} tensors", file=sys.stderr,
+                          flush=True)
+            else:
+                walls.append(ms)
+                for k, v in ph.items():
+                    phases[k] = phases.get(k, 0.0) + v / repeats
+            del res
+        ms = sum(walls) / len(walls)
+        out[f"device_{device}"] = {
+            "ms": round(ms, 2), "ms_runs": [round(x, 2) for x in walls],
+            "speedup_vs_cpu_reference": round(t_cpu * 1e3 / ms, 2),
+            "piece_bytes_up": moved[0], "window_bytes_up": moved[1], "bytes_down": moved[2],
+            "host_link_GBps": round((moved[1] + moved[2]) / (ms * 1e-3) / 1e9, 1),
+            "phases_ms": {k.replace("execute ", ""): round(v, 2) for k, v in sorted(phases.items())}}
+        print(f"[bench] host state device={device}: {ms:.1f} ms (CPU reference {t_cpu * 1e3:.1f} ms)",
+              file=sys.stderr, flush=True)
+
+    # what checkpoint_load did before: whole source tensors to HBM, then the gather
+    needed = {}
+    for op in ops:
+        needed.setdefault(op.src_rank, set()).add(op.param_name)
+    walls = []
+    for i in range(repeats + 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fake = {r: {n: {f: t.to(dev) for f, t in host[r][n].items()} for n in names} for r, names in needed.items()}
+        res = execute_param_transfer(ops, {}, dev, esf, rank=w.dst_rank, fake_source_state_dicts=fake,
+                                     recast=w.recast_map)
+        torch.cuda.synchronize()
+        if i:
+            walls.append((time.perf_counter() - t0) * 1e3)
+        whole = sum(t.numel() * t.element_size() for sd in fake.values() for e in sd.values() for t in e.values())
+        del res, fake
+    out["whole_tensors_then_gather"] = {"ms": round(sum(walls) / len(walls), 2), "bytes_up": whole,
+                                        "what": "every source tensor a piece reads copied to HBM with "
+                                                ".to(device) (pageable), then the drop-in gather"}
+    return out
 
 
 # ---------------------------------------------------------------- live hand-off leg
@@ -937,6 +1051,10 @@ def main(argv=None) -> int:
     w = CONFIGS[key]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.host_state:
+        rec = host_state_leg(w, dev, args.steps, args.cpu_seconds)
+        print(json.dumps({"host_state": rec}), flush=True)
+        return 0 if rec["parity"]["mismatched"] == 0 else 1
     if args.api_phases:
         ranks = sorted({op.src_rank for op in w.ops()})
         print(f"[bench] api phases {key}: generating sources", file=sys.stderr, flush=True)
@@ -1125,8 +1243,8 @@ def main(argv=None) -> int:
         threads = len(os.sched_getaffinity(0))
         print(f"[bench] CPU baseline: torch-CPU reshard, {threads} threads", file=sys.stderr,
               flush=True)
-        t_n, b_n, runs_n, nl, cpu_out = cpu_baseline(w, threads, args.cpu_seconds, args.cpu_layers,
-                                                     srcs=srcs_cpu, keep_output=srcs_cpu is not None)
+        t_n, b_n, runs_n, nl, cpu_out, bmin_n = cpu_baseline(w, threads, args.cpu_seconds, args.cpu_layers,
+                                                             srcs=srcs_cpu, keep_output=srcs_cpu is not None)
         if cpu_out is not None:
             print("[bench] comparing every destination tensor with the torch-CPU reshard",
                   file=sys.stderr, flush=True)
@@ -1134,11 +1252,12 @@ def main(argv=None) -> int:
             parity["cpu_reference"] = ("torch-CPU reshard (oracle/torch_ref.py: the reference's fake-source "
                                        "chunk/contiguous/cat loop) of the same seeded source shards")
             del cpu_out
-        t_1, b_1, runs_1, nl1, _ = cpu_baseline(w, 1, args.cpu_seconds, args.cpu_layers, srcs=srcs_cpu)
+        t_1, b_1, runs_1, nl1, _, bmin_1 = cpu_baseline(w, 1, args.cpu_seconds, args.cpu_layers, srcs=srcs_cpu)
         del srcs_cpu
-        rate_n = b_n / t_n / 1e9
-        rate_1 = b_1 / t_1 / 1e9
-        full_ms = b_alg / (rate_n * 1e9) * 1e3
+        # the bytes the CPU path moves (P read + D written: no buffers) per second
+        rate_n = bmin_n / t_n / 1e9
+        rate_1 = bmin_1 / t_1 / 1e9
+        full_ms = b_min / (rate_n * 1e9) * 1e3
         what = "the full destination share" if not args.cpu_layers else \
             f"a sample with {nl} destination-stage layers"
         result["cpu_baseline"] = {
@@ -1148,10 +1267,12 @@ def main(argv=None) -> int:
             "kind": "port",
             "sample": (f"torch-CPU chunk/contiguous/cat reshard (oracle/torch_ref.py) of {what}, "
                        f"seeded source shards (host copies of the GPU's inputs), "
-                       f"{b_n / 1e9:.2f} GB algorithmic, {runs_n} timed runs of {t_n:.3f} s"),
+                       f"{bmin_n / 1e9:.2f} GB moved (P + D), {runs_n} timed runs of {t_n:.3f} s"),
+            "value_bytes": "B_min = P + D, the bytes the CPU path reads and writes",
+            "B_alg_GBps": round(b_n / t_n / 1e9, 2),
             "ms": round(full_ms, 1),
             "one_thread_GBps": round(rate_1, 2),
-            "one_thread_ms": round(b_alg / (rate_1 * 1e9) * 1e3, 1),
+            "one_thread_ms": round(b_min / (rate_1 * 1e9) * 1e3, 1),
             "one_thread_sample": f"{runs_1} timed runs of {t_1:.3f} s",
             "cpu_model": cpu_model(),
             "speedup_gpu_vs_cpu": round(full_ms / total_ms, 1),

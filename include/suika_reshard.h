@@ -254,11 +254,13 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
  * (Suika/migration.py:477-482, 1235-1244).  Here the pieces' bytes, and only
  * they, cross to the GPU in the peer-buffer layout; the GPU unpacks them
  * (sr_unpack); sr_download brings results back to host memory.  Both go
- * through a ring of SR_STAGE_WINDOWS pinned windows of SR_STAGE_WINDOW_BYTES
- * per device, allocated on first use and held until the process exits, and
- * copy between the caller's host memory and the windows on a pool of host
- * threads (sr_set_host_threads).  A device's ring serves one call at a time:
- * concurrent calls on one device wait for each other. */
+ * through rings of SR_STAGE_WINDOWS pinned windows of SR_STAGE_WINDOW_BYTES,
+ * one per device and copy direction, allocated on first use and held until
+ * the process exits, and copy between the caller's host memory and the
+ * windows on a pool of host threads (sr_set_host_threads).  A ring serves one
+ * call at a time: concurrent uploads (or downloads) on one device wait for
+ * each other, while an upload and a download can run at once on two streams,
+ * one per link direction. */
 #define SR_STAGE_WINDOW_BYTES (16u << 20)
 #define SR_STAGE_WINDOWS 4
 
@@ -300,6 +302,9 @@ int sr_pack_host(const sr_plan* plan, const void* const* src_ptrs, void* const* 
  * run on `stream` after the work queued there (for example the sr_unpack
  * that wrote the regions), through the pinned windows, adjacent device
  * regions in one copy; host threads move each window to its destinations.
+ * Host regions are advised for transparent huge pages (madvise
+ * MADV_HUGEPAGE on their whole 2 MiB pages) before they are written: fresh
+ * memory is then mapped 2 MiB per fault instead of 4 KiB.
  * Returns when every host byte is written.  Serves execute_param_transfer's
  * device="cpu" (Suika/migration.py:1235-1244), whose result the reference
  * returns in host memory.

@@ -30,6 +30,7 @@
 
 #include <hip/hip_runtime.h>
 #include <sched.h>
+#include <sys/mman.h>
 #include <unistd.h>
 
 #include <algorithm>
@@ -168,8 +169,11 @@ class Pool {
 };
 
 // ------------------------------------------------------------ window ring
+enum Direction { kUp = 0, kDown = 1 };
+
 struct Ring {
   int device = -1;
+  int direction = kUp;
   unsigned char* base = nullptr;            // kWindows * kWindow pinned bytes
   hipEvent_t ev[kWindows] = {};
   bool pending[kWindows] = {};              // ev[i] recorded after a copy of window i
@@ -195,19 +199,23 @@ struct Ring {
   }
 };
 
-// One ring per device, created on first use with that device current and
-// kept until the process exits (no HIP call from a static destructor).
-int ring_of(int device, Ring** out) {
+// One ring per device and direction (host to device for sr_stage_pack,
+// device to host for sr_download, so that an upload and a download can run
+// at once, one per copy direction of the link), created on first use with
+// that device current and kept until the process exits (no HIP call from a
+// static destructor).
+int ring_of(int device, Direction dir, Ring** out) {
   static std::mutex mu;
   static std::vector<Ring*>* rings = new std::vector<Ring*>();
   std::lock_guard<std::mutex> lock(mu);
   for (Ring* r : *rings)
-    if (r->device == device) {
+    if (r->device == device && r->direction == dir) {
       *out = r;
       return SR_OK;
     }
   Ring* r = new Ring();
   r->device = device;
+  r->direction = dir;
   void* p = nullptr;
   hipError_t e = hipHostMalloc(&p, size_t(kWindows) * kWindow, hipHostMallocDefault);
   if (e != hipSuccess) {
@@ -446,7 +454,7 @@ int sr_stage_pack(sr_plan* plan, const void* const* src_ptrs, void* const* peer_
   bool any_host = false;
   for (size_t s = 0; s < v.n_src && !any_host; ++s) any_host = dev_slot[s] == 0;
   if (!any_host) return SR_OK;
-  if ((rc = ring_of(dev, &ring)) != SR_OK) return rc;
+  if ((rc = ring_of(dev, kUp, &ring)) != SR_OK) return rc;
   std::lock_guard<std::mutex> lock(ring->mu);
   std::vector<Segment> segs;
   size_t fill = 0;
@@ -525,10 +533,19 @@ int sr_download(const void* const* dev_ptrs, void* const* host_ptrs, const uint6
     total += bytes[i];
   }
   if (total == 0) return SR_OK;
+  // Fresh host memory is mapped at its first write, a 4 KiB page per fault
+  // unless the range asks for transparent huge pages: large destinations do
+  // (a hint; the kernel may decline it, and the call does not depend on it).
+  for (int32_t i = 0; i < n; ++i) {
+    constexpr uintptr_t kHuge = uintptr_t(2) << 20;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(host_ptrs[i]);
+    const uintptr_t lo = (a + kHuge - 1) & ~(kHuge - 1), hi = (a + bytes[i]) & ~(kHuge - 1);
+    if (bytes[i] && hi > lo) (void)madvise(reinterpret_cast<void*>(lo), hi - lo, MADV_HUGEPAGE);
+  }
   int dev = -1;
   ST_HIP_TRY(hipGetDevice(&dev));
   Ring* ring = nullptr;
-  int rc = ring_of(dev, &ring);
+  int rc = ring_of(dev, kDown, &ring);
   if (rc != SR_OK) return rc;
   std::lock_guard<std::mutex> lock(ring->mu);
   if ((rc = ring->wait_all()) != SR_OK) return rc;

@@ -206,37 +206,77 @@ def execute_param_transfer(
         """The transfer of ``todo`` from sources wherever they are: the
         pieces' bytes packed on the host (or on the GPU for sources there)
         into peer buffers in HBM, the unpack on the GPU, and for host results
-        the copy back.  One launch group: the copies to and from the host
-        set the pace, the GPU's unpack takes a small share of it."""
-        prof.start("execute stage")
-        plan, src_ptrs = ReshardPlan.from_sources(todo, source, normal, gpu, recast=recast, options=stage_options,
-                                                  rank=rank, host_ok=True)
-        plans.append(plan)
-        bufs = plan.alloc_buffers(gpu)
-        buffers.append(bufs)
-        buf_ptrs = [b.data_ptr() for b in bufs]
-        plan.stage_pack_ptrs(src_ptrs, buf_ptrs, stream)
-        names = dict.fromkeys(op.param_name for op in todo)
-        if device.type == "cuda":
-            if arena_views is None:
-                part, dst_ptrs = plan.alloc_dst_ptrs(device)
-            else:
-                part = {name: arena_views[name] for name in names}
-                dst_ptrs = plan.bind_dst_ptrs(part, device)
-            plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
+        the copy back.  It runs in groups of whole tensors of about
+        ``_stage_group_bytes`` piece bytes each: a group's buffers are
+        released once it is unpacked, and a host result's download (its own
+        stream, the device-to-host direction of the link) overlaps the next
+        group's upload."""
+        if todo is ops:
+            order, starts, numel = runs[1], runs[2], runs[3]
         else:
-            # the GPU's result in one temporary allocation, then host memory
-            hbm = plan.alloc_dst(gpu, arena=True)
-            plan.unpack_ptrs(buf_ptrs, plan.bind_dst_ptrs(hbm, gpu), stream)
-            if arena_views is not None:
-                part = {name: arena_views[name] for name in names}
-            else:
-                part = {name: {f: torch.empty(t.shape, dtype=t.dtype) for f, t in ent.items()}
-                        for name, ent in hbm.items()}
-            download([(t, part[name][f]) for name, ent in hbm.items() for f, t in ent.items()], stream)
-            del hbm
-        target.update(part)
-        prof.stop("execute stage")
+            order, starts, numel = _lib.host().name_runs(todo)[:3]
+        picks = _stage_groups(np.asarray(numel, dtype=np.int64) * max(1, elem_bytes))
+        # buffers allocated on the current stream may be released per group
+        # only when the kernels run on that stream
+        cur = torch.cuda.current_stream(gpu)
+        keep_buffers = stream is not None and stream != cur
+        down = pending = None
+        if device.type == "cpu":
+            down = _Download.stream(gpu)
+            pending = []
+        try:
+            for pick in picks:
+                group = todo if len(picks) == 1 else _lib.host().take_ops(todo, order, starts, pick)
+                prof.start("execute stage plan")
+                try:
+                    plan, src_ptrs = ReshardPlan.from_sources(group, source, normal, gpu, recast=recast,
+                                                              options=stage_options, rank=rank, host_ok=True)
+                finally:
+                    prof.stop("execute stage plan")
+                plans.append(plan)
+                bufs = plan.alloc_buffers(gpu)
+                buf_ptrs = [b.data_ptr() for b in bufs]
+                prof.start("execute stage pack")
+                plan.stage_pack_ptrs(src_ptrs, buf_ptrs, stream)
+                prof.stop("execute stage pack")
+                names = dict.fromkeys(op.param_name for op in group)
+                if device.type == "cuda":
+                    if arena_views is None:
+                        part, dst_ptrs = plan.alloc_dst_ptrs(device)
+                    else:
+                        part = {name: arena_views[name] for name in names}
+                        dst_ptrs = plan.bind_dst_ptrs(part, device)
+                    plan.unpack_ptrs(buf_ptrs, dst_ptrs, stream)
+                else:
+                    # the GPU's result in one temporary allocation, then host
+                    # memory, on the download stream after the unpack
+                    hbm = plan.alloc_dst(gpu, arena=True)
+                    plan.unpack_ptrs(buf_ptrs, plan.bind_dst_ptrs(hbm, gpu), stream)
+                    unpacked = torch.cuda.Event()
+                    unpacked.record(stream or cur)
+                    prof.start("execute stage host tensors")
+                    if arena_views is not None:
+                        part = {name: arena_views[name] for name in names}
+                    else:
+                        part = {name: {f: torch.empty(t.shape, dtype=t.dtype) for f, t in ent.items()}
+                                for name, ent in hbm.items()}
+                    prof.stop("execute stage host tensors")
+                    pairs = [(t, part[name][f]) for name, ent in hbm.items() for f, t in ent.items()]
+                    del hbm
+                    pending.append(_Download.submit(gpu, down, unpacked, pairs))
+                    del pairs
+                if keep_buffers:
+                    buffers.append(bufs)
+                del bufs
+                target.update(part)
+        finally:
+            if pending is not None:
+                # every download ends before the call returns (or raises)
+                prof.start("execute stage download wait")
+                errors = [e for e in (job.result() for job in pending) if e is not None]
+                prof.stop("execute stage download wait")
+                if errors:
+                    raise errors[0]
 
     def _device_group(group: List[TransferOp]) -> None:
         """One launch group from sources on the device: planned, allocated
@@ -371,6 +411,77 @@ def execute_param_transfer(
                     forcefully_free_tensor(t)
     source_state_dict.clear()
     return ordered
+
+
+# Piece bytes per launch group of the staged route: about 1/STAGE_GROUPS of
+# the transfer, between the two bounds (a group costs about a millisecond of
+# planning; the first upload and the last download do not overlap).
+STAGE_GROUPS = 16
+STAGE_GROUP_MIN = 32 << 20
+STAGE_GROUP_MAX = 1 << 30
+
+
+def _stage_groups(tensor_bytes: np.ndarray) -> List[np.ndarray]:
+    """Tensor indices (order of first appearance) cut into consecutive
+    groups of about max(STAGE_GROUP_MIN, min(STAGE_GROUP_MAX, total /
+    STAGE_GROUPS)) bytes; a tensor larger than that is a group of its own."""
+    n = len(tensor_bytes)
+    if n == 0:
+        return [np.arange(0)]
+    total = int(tensor_bytes.sum())
+    target = max(STAGE_GROUP_MIN, min(STAGE_GROUP_MAX, total // STAGE_GROUPS))
+    out, start, acc = [], 0, 0
+    for i in range(n):
+        acc += int(tensor_bytes[i])
+        if acc >= target:
+            out.append(np.arange(start, i + 1))
+            start, acc = i + 1, 0
+    if start < n:
+        out.append(np.arange(start, n))
+    return out
+
+
+class _Download:
+    """Downloads of host results, one at a time on a worker thread (so that
+    a group's download overlaps the next group's upload on the calling
+    thread) and on one stream per device (default priority): the download
+    stream waits for the group's unpack, then sr_download copies every
+    (device, host) pair.  ``submit`` returns a future whose result is None
+    or the exception raised.  A forked child makes its own worker."""
+
+    _pool = None
+    _pid = None
+    _streams: Dict[int, torch.cuda.Stream] = {}
+
+    @classmethod
+    def _ensure(cls) -> None:
+        import os
+        if cls._pool is None or cls._pid != os.getpid():
+            from concurrent.futures import ThreadPoolExecutor
+            cls._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="suika-download")
+            cls._pid = os.getpid()
+            cls._streams = {}
+
+    @classmethod
+    def stream(cls, gpu: torch.device) -> torch.cuda.Stream:
+        cls._ensure()
+        if gpu.index not in cls._streams:
+            cls._streams[gpu.index] = torch.cuda.Stream(gpu)
+        return cls._streams[gpu.index]
+
+    @classmethod
+    def submit(cls, gpu, stream, after, pairs):
+        cls._ensure()
+
+        def job():
+            try:
+                with torch.cuda.device(gpu):
+                    stream.wait_event(after)
+                    download(pairs, stream)
+                return None
+            except BaseException as e:   # handed to the caller, which raises it
+                return e
+        return cls._pool.submit(job)
 
 
 def _tp_deg(meta) -> int:

@@ -23,10 +23,11 @@ def test_cpu_baseline_sample():
     sys.path.insert(0, str(ROOT))
     import bench
     from suika_amd.workloads import CONFIGS
-    t, nbytes, runs, layers, out = bench.cpu_baseline(CONFIGS["gpt125m_tp2_tp4"], 2, 0.0, layers=1,
-                                                      keep_output=True)
+    t, nbytes, runs, layers, out, b_min = bench.cpu_baseline(CONFIGS["gpt125m_tp2_tp4"], 2, 0.0, layers=1,
+                                                             keep_output=True)
     assert t > 0 and runs >= 1 and layers == 1
     assert 0 < nbytes < 4 * 0.835e9       # below the full share's B_alg
+    assert 0 < b_min < nbytes             # P + D of the sample, below its 3P + D
     # the sample's output is the oracle's reshard of the same seeded shards
     from dataclasses import replace
 

@@ -174,3 +174,21 @@ def test_download_argument_checks():
     zero = (ctypes.c_uint64 * 1)(0)
     nul = (ctypes.c_void_p * 1)(None)
     assert L.sr_download(nul, nul, zero, 1, None) == _lib.SR_OK   # nothing to copy: no device needed
+
+
+def test_stage_groups_cut_whole_tensors_by_bytes():
+    from suika_amd.migration import STAGE_GROUP_MAX, STAGE_GROUP_MIN, _stage_groups
+    assert [g.tolist() for g in _stage_groups(np.zeros(0, dtype=np.int64))] == [[]]
+    small = np.full(10, 1 << 20, dtype=np.int64)          # 10 MiB in all: one group
+    assert [g.tolist() for g in _stage_groups(small)] == [list(range(10))]
+    big = np.full(64, 256 << 20, dtype=np.int64)           # 16 GiB: groups of 1 GiB (4 tensors)
+    groups = _stage_groups(big)
+    assert all(len(g) == 4 for g in groups) and len(groups) == 16
+    mixed = np.array([3 << 30, 1, 1, 40 << 20, 1 << 20, 1 << 20], dtype=np.int64)
+    groups = _stage_groups(mixed)
+    assert np.concatenate(groups).tolist() == list(range(6))   # every tensor once, in order
+    assert groups[0].tolist() == [0]                            # a tensor above the bound stands alone
+    total = int(mixed.sum())
+    target = max(STAGE_GROUP_MIN, min(STAGE_GROUP_MAX, total // 16))
+    for g in groups[:-1]:
+        assert mixed[g].sum() >= target
