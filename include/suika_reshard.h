@@ -223,23 +223,30 @@ int sr_gather(sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
 
 /*
  * Gather without allocating.  No counterpart in the reference: this is for
- * callers that cannot allocate device memory -- code under HIP graph capture,
- * tight serving loops, harnesses that forbid hipMalloc.  Same plan, pointers
- * and result as sr_gather, but the phase's device tables (descriptors,
- * pointer table, items, tile prefix sums and tile list) are placed in a
- * static array of SR_SCRATCH_BYTES per GPU, part of the library's code object
- * and held by every GPU the library runs on until the process exits.  The
- * call makes no hipMalloc, hipHostMalloc or hipFree, creates no event or
- * stream, and leaves the plan's own device state untouched.
- *   - The tables need 96 + 64 + 8 bytes per piece, 8 per tensor slot and 24
- *     per tile (tile = plan tile_bytes of source data; the Llama2-7B share
- *     needs 35 MB at 16 KiB).  A plan that needs more than SR_SCRATCH_BYTES
- *     is rejected with SR_ENOMEM before any device work: create it with a
- *     larger tile_bytes, or split the transfer into several plans.
+ * callers that cannot allocate device memory -- tight serving loops and
+ * harnesses that forbid hipMalloc.  Same plan, pointers and result as
+ * sr_gather, but the phase's device tables (descriptors, pointer table,
+ * items, tile prefix sums and tile list) are placed in a static array of
+ * SR_SCRATCH_BYTES per GPU, part of the library's code object: every process
+ * that loads the library's GPU code on a device (any entry point that
+ * launches a kernel there) holds that array on the device until it exits.
+ * The call makes no hipMalloc, hipHostMalloc or hipFree, creates no event or
+ * stream, and leaves the plan's own device state untouched.  The first call
+ * in a process that has launched nothing of the library yet loads its GPU
+ * code object, which is when the array is placed.
+ *   - The tables need 96 + 64 + 8 + 8 bytes per piece (descriptor, item, tile
+ *     prefix, emit chunk), 8 per tensor slot and 24 per tile (tile = plan
+ *     tile_bytes of source data; the Llama2-7B share needs 35 MB at 16 KiB).
+ *     A plan that needs more than SR_SCRATCH_BYTES is rejected with SR_ENOMEM
+ *     before any device work: create it with a larger tile_bytes, or split
+ *     the transfer into several plans.
  *   - The descriptors and pointers are uploaded from pageable host memory at
- *     every call, which HIP performs synchronously: the call returns once the
- *     work queued on `stream` before it has finished and the tables are on
- *     the device; the tile, bind and copy kernels then run asynchronously.
+ *     every call, which HIP performs synchronously: the call blocks the host
+ *     until the work queued on `stream` before it has finished and the tables
+ *     are on the device; the tile, bind and copy kernels then run
+ *     asynchronously.  For the same reason the call cannot be recorded into a
+ *     HIP graph: on a stream that is capturing it returns SR_EINVAL and does
+ *     nothing.
  *   - Every call on one GPU uses that GPU's single scratch array, which keeps
  *     the last call's tables: calls on one stream are ordered, but calls that
  *     overlap on one GPU (different streams or threads) race.

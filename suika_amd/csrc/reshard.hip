@@ -1924,6 +1924,17 @@ int sr_prepare(hipStream_t stream) {
 int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
                       hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
+  // The tables go up from pageable host memory that is released when the
+  // call returns: a graph captured from this call would replay copies out of
+  // freed memory, so a capturing stream is refused before any device work.
+  {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SR_HIP_TRY(hipStreamIsCapturing(stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(SR_EINVAL,
+                  "sr_gather_noalloc: the stream is capturing a graph; this call uploads its tables from "
+                  "pageable host memory at every call and cannot be captured");
+  }
   const Phase& ph = plan->gather;
   // The size check comes first: it needs neither the pointers nor a device.
   const ScratchLayout L = scratch_layout(ph);

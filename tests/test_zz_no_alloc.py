@@ -106,3 +106,59 @@ def test_noalloc_full_size_share_matches_gather():
     bad = [(name, f) for name, ent in ref.items() for f, t in ent.items()
            if not torch.equal(got[name][f].view(torch.uint8), t.view(torch.uint8))]
     assert not bad, f"{len(bad)} tensors differ, first {bad[:5]}"
+
+
+def _small_plan():
+    w = cases.scaled_configs()["gpt125m_tp2_tp4"]
+    dev = torch.device("cuda", torch.cuda.current_device())
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), global_state(w, _names(w)))
+    fake = to_device(srcs, w, dev)
+    ops = [op for op in w.ops() if op.dst_rank == w.dst_rank]
+    plan, src_ptrs = ReshardPlan.from_sources(ops, lambda r: fake[r], list(w.src_fields), dev,
+                                              recast=w.recast_map, rank=w.dst_rank)
+    dst, dst_ptrs = _poisoned_dst(plan, dev)
+    return plan, fake, src_ptrs, dst, dst_ptrs
+
+
+def test_noalloc_second_call_allocates_nothing():
+    """After a first call (which, in a fresh process, also loads the
+    library's GPU code and so places the scratch), a call changes neither
+    the device's free memory nor torch's reserved memory."""
+    print("[noalloc] allocation check", flush=True)
+    plan, fake, src_ptrs, dst, dst_ptrs = _small_plan()
+    try:
+        plan.gather_noalloc_ptrs(src_ptrs, dst_ptrs)
+        torch.cuda.synchronize()
+        free0, _ = torch.cuda.mem_get_info()
+        reserved0 = torch.cuda.memory_reserved()
+        plan.gather_noalloc_ptrs(src_ptrs, dst_ptrs)
+        torch.cuda.synchronize()
+        free1, _ = torch.cuda.mem_get_info()
+        assert free1 == free0, f"device free memory changed by {free0 - free1} bytes"
+        assert torch.cuda.memory_reserved() == reserved0
+    finally:
+        plan.close()
+
+
+def test_noalloc_refuses_graph_capture():
+    """A stream that is capturing a graph is refused before any device work
+    (the tables are uploaded from pageable memory at every call); the
+    capture itself stays valid and holds only the work around the call."""
+    print("[noalloc] capture refused", flush=True)
+    plan, fake, src_ptrs, dst, dst_ptrs = _small_plan()
+    try:
+        plan.gather_noalloc_ptrs(src_ptrs, dst_ptrs)
+        torch.cuda.synchronize()
+        x = torch.zeros(16, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(AssertionError, match="capturing a graph"):
+            with torch.cuda.graph(g):
+                x.add_(1)
+                plan.gather_noalloc_ptrs(src_ptrs, dst_ptrs)
+        torch.cuda.synchronize()
+        for k in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            assert float(x[0]) == k + 1
+    finally:
+        plan.close()
