@@ -74,6 +74,16 @@ def parse_args(argv=None):
     ap.add_argument("--handoff-wait-release", action="store_true",
                     help="with --handoff: the new world allocates its destinations only after the old "
                          "world has released its state, even when the device has room for both")
+    ap.add_argument("--handoff-return-early", action="store_true",
+                    help="with --handoff: the new world returns once its state is adopted, without "
+                         "waiting for the old world's release (migration_load(return_before_release=True))")
+    ap.add_argument("--handoff-mode", choices=("whole", "waves"), default=None,
+                    help="with --handoff: force the hand-off's order (default: whole when it fits)")
+    ap.add_argument("--handoff-wave-bytes", type=int, default=None,
+                    help="with --handoff-mode waves: bytes per wave (default: a third of the free memory)")
+    ap.add_argument("--handoff-squeeze", type=float, default=None, metavar="F",
+                    help="with --handoff: hold device memory once every process is up until only F x the "
+                         "old state is free (F < 1: a whole hand-off does not fit)")
     ap.add_argument("--checkpoint", metavar="DIR", default=None,
                     help="only run the checkpoint-based migration of the workload (the reference's "
                          "comparator to live migration): the old world's processes checkpoint_save into a "
@@ -653,7 +663,32 @@ def _timed_log(sink):
     return log
 
 
-def _handoff_old(rank, key, port, queues, events):
+def _expected_shard(G, meta):
+    """The shard ``meta`` describes, cut from its global tensor ``G`` by
+    closed form, written here so the hand-off leg's seeding and check share
+    no code with the product's geometry: ``torch.chunk`` along the split dim
+    (the reference's column and row splits, tensor_parallel.py:200-204,
+    378-381); for a fused QKV weight, the same chunk of each projection's
+    rows; for a vocabulary-parallel table, the rank's chunk of the table
+    padded with zero rows to a multiple of pad_multiple x TP."""
+    import torch
+    if meta.tp_meta is None:
+        return G
+    dim, idx, deg = (int(v) for v in meta.tp_meta)
+    if meta.kind == "vocab_pad":
+        step = int(meta.kind_args[0]) * deg
+        rows = -(-G.shape[0] // step) * step
+        padded = torch.zeros((rows,) + tuple(G.shape[1:]), dtype=G.dtype, device=G.device)
+        padded[:G.shape[0]] = G
+        return torch.chunk(padded, deg, dim=0)[idx].contiguous()
+    if meta.kind == "qkv_heads":
+        nq, nkv, hd = (int(v) for v in meta.kind_args)
+        q, k, v = torch.split(G, [nq * hd, nkv * hd, nkv * hd], dim=0)
+        return torch.cat([torch.chunk(x, deg, dim=0)[idx] for x in (q, k, v)], dim=0)
+    return torch.chunk(G, deg, dim=dim)[idx].contiguous()
+
+
+def _handoff_old(rank, key, port, queues, events, opts):
     import traceback
 
     import torch
@@ -669,7 +704,10 @@ def _handoff_old(rank, key, port, queues, events):
         model, opt = _seed_old_rank(w, rank, dev)
         log = []
         events.put(("ready", rank, None))
-        migration_save(queues[rank], model, opt, other_context={"iter": 1}, log_func=_timed_log(log))
+        if opts.get("gate") is not None:
+            assert opts["gate"].wait(600), "the bench never opened the gate"
+        migration_save(queues[rank], model, opt, other_context={"iter": 1}, log_func=_timed_log(log),
+                       handoff_mode=opts.get("mode"), wave_bytes=opts.get("wave_bytes"))
         events.put(("saved", rank, log))
     except BaseException:
         events.put(("error", rank, traceback.format_exc()))
@@ -679,7 +717,7 @@ def _handoff_old(rank, key, port, queues, events):
             dist.destroy_process_group()
 
 
-def _handoff_new(rank, key, port, queues, events, wait_for_release=None):
+def _handoff_new(rank, key, port, queues, events, opts):
     import traceback
 
     import torch
@@ -695,10 +733,19 @@ def _handoff_new(rank, key, port, queues, events, wait_for_release=None):
         torch.cuda.set_device(dev)
         pfield = "param" if "param" in w.src_fields else "master"
         model = build_module(w.model, w.dst, rank, w.dtypes[pfield], device="meta")
+        if opts.get("gate") is not None:
+            # first-use costs and allocations in place before the bench takes
+            # the device memory it holds
+            from suika_amd.handoff import _WarmUp
+            _WarmUp(dev, optimizer=True).run()
+            torch.cuda.synchronize()
+            events.put(("ready-new", rank, None))
+            assert opts["gate"].wait(600), "the bench never opened the gate"
         log = []
         t0 = time.time()
         opt, ctx = migration_load(queues[rank], model, lambda: _state_optimizer(model.parameters()),
-                                  log_func=_timed_log(log), wait_for_release=wait_for_release)
+                                  log_func=_timed_log(log), wait_for_release=opts.get("wait_for_release"),
+                                  return_before_release=opts.get("return_before_release", False))
         t1 = time.time()
         rec = _check_new_rank(w, rank, model, opt, dev)
         rec.update(log=log, t_call=t0, t_return=t1)
@@ -711,15 +758,21 @@ def _handoff_new(rank, key, port, queues, events, wait_for_release=None):
             dist.destroy_process_group()
 
 
-def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> dict:
+def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None, mode=None, wave_bytes=None,
+                squeeze=None, return_before_release=False) -> dict:
     """Live migration of workload ``key`` between processes on this GPU: the
     old plan's ranks (seeded state) call migration_save, the new plan's ranks
-    migration_load; every received tensor is checked bit for bit."""
+    migration_load; every received tensor is checked bit for bit.
+
+    ``squeeze``: once every process is up, this process holds device memory
+    until only that fraction of the old state is free, so the old world
+    picks its order (waves when the whole does not fit) under a real
+    shortage."""
     import multiprocessing as mp
     import queue as _queue
     import socket
 
-    from suika_amd.handoff import dummy_migration_IPC_state_dict
+    from suika_amd.handoff import RESERVE_BYTES, dummy_migration_IPC_state_dict
     from suika_amd.workloads import CONFIGS
     w = CONFIGS[key]
     old_ws, new_ws = w.src.world, w.dst.world
@@ -731,6 +784,10 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> di
     events = ctx.Queue()
     results = {}
     deadline = time.time() + timeout_s
+    opts = {"wait_for_release": wait_for_release, "mode": mode, "wave_bytes": wave_bytes,
+            "return_before_release": return_before_release}
+    if squeeze is not None:
+        opts["gate"] = ctx.Event()
 
     def wait_for(kind, count):
         while sum(1 for ev, _ in results if ev == kind) < count:
@@ -749,15 +806,30 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> di
             return s_.getsockname()[1]
 
     procs = []
+    held = {}
     try:
         p_old, p_new = port(), port()
         for r in range(old_ws):
-            procs.append(ctx.Process(target=_handoff_old, args=(r, key, p_old, queues, events)))
+            procs.append(ctx.Process(target=_handoff_old, args=(r, key, p_old, queues, events, opts)))
             procs[-1].start()
         wait_for("ready", old_ws)
         for r in range(new_ws):
-            procs.append(ctx.Process(target=_handoff_new, args=(r, key, p_new, queues, events, wait_for_release)))
+            procs.append(ctx.Process(target=_handoff_new, args=(r, key, p_new, queues, events, opts)))
             procs[-1].start()
+        if squeeze is not None:
+            import torch
+            wait_for("ready-new", new_ws)
+            torch.cuda.set_device(0)
+            torch.cuda.synchronize()
+            free, _ = torch.cuda.mem_get_info()
+            hold = free - int(squeeze * _old_state_bytes(w))
+            assert hold > 0, "the device already has less free memory than asked for"
+            held["t"] = torch.empty(hold, dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            held["free"] = torch.cuda.mem_get_info()[0]
+            print(f"[bench] hand-off: holding {hold / 1e9:.1f} GB, {held['free'] / 1e9:.2f} GB free",
+                  file=sys.stderr, flush=True)
+            opts["gate"].set()
         wait_for("loaded", new_ws)
         wait_for("saved", old_ws)
         for p in procs:
@@ -767,38 +839,69 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> di
             if p.is_alive():
                 p.kill()
                 p.join(10)
+        if held.pop("t", None) is not None:
+            import torch
+            torch.cuda.empty_cache()
 
     def at(log, text):
         return next(t for t, m in log if text in m)
 
+    def low_water(log):
+        m = next(m for _, m in log if "low-water free device memory" in m)
+        return float(m.rsplit("memory", 1)[1].split()[0]) * 1e9
+
     old_logs = [results[("saved", r)] for r in range(old_ws)]
     new_recs = [results[("loaded", r)] for r in range(new_ws)]
-    start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done: packing begins
-    pack_ms = max((at(l, "packed") - at(l, "is_scale_up")) * 1e3 for l in old_logs)
-    # the old state's release once the new world has mapped the hand-off and
-    # allocated (or asked for the memory): its tensors freed and the
-    # allocator's cache returned to the device (one hipFree per segment)
-    noted = [next(t for t, m in l if "has allocated its destinations" in m or "waits for this state's" in m)
-             for l in old_logs]
-    release_ms = max((at(l, "state released") - t) * 1e3 for l, t in zip(old_logs, noted))
+    start = min(at(l, "is_scale_up") for l in old_logs)         # handshake done
+    order_line = next(m for _, m in old_logs[0] if "hand-off whole" in m or "hand-off in waves" in m)
+    whole = "hand-off whole" in order_line
     end = max(rec["t_return"] for rec in new_recs)
-    reshard = [(at(rec["log"], "resharded") - at(rec["log"], "destinations of")) * 1e3 for rec in new_recs]
-    waited = any("after the old world released" in m for rec in new_recs for _, m in rec["log"])
-    return {
+    adopted = max(at(rec["log"], "model state adopted") for rec in new_recs)
+    device_free = max(at(l, "migration_save: end") for l in old_logs)
+    out = {
         "workload": w.description or key, "old_ranks": old_ws, "new_ranks": new_ws,
         "state_bytes_received": sum(rec["bytes"] for rec in new_recs),
-        "pack_ms_max": round(pack_ms, 2),
-        "release_ms_max": round(release_ms, 2),
-        "reshard_ms_max": round(max(reshard), 2),
-        "destinations_waited_for_release": waited,
+        "order": order_line.split(": ", 1)[1],
         "handoff_ms": round((end - start) * 1e3, 1),
         "handoff_ms_note": ("wall time from the old world's handshake to the last new rank's return from "
                             "migration_load: pack, queue messages, IPC mapping, reshard, load_state_dict; "
                             "new processes are fresh (first HIP use included)"),
+        "state_adopted_ms": round((adopted - start) * 1e3, 1),
+        "device_free_ms": round((device_free - start) * 1e3, 1),
+        "end_points_note": ("state adopted: the last new rank's load_state_dict done; device free: the last "
+                            "old rank has released its state and the hand-off allocations (its return from "
+                            "migration_save); both from the handshake"),
+        "return_before_release": bool(return_before_release),
+    }
+    if whole:
+        # the old state's release once the new world has mapped the hand-off
+        # and allocated (or asked for the memory): its tensors freed and the
+        # allocator's cache returned to the device (one hipFree per segment)
+        noted = [next(t for t, m in l if "has allocated its destinations" in m or "waits for this state's" in m)
+                 for l in old_logs]
+        out.update(
+            pack_ms_max=round(max((at(l, "packed") - at(l, "hand-off whole")) * 1e3 for l in old_logs), 2),
+            release_ms_max=round(max((at(l, "state released") - t) * 1e3 for l, t in zip(old_logs, noted)), 2),
+            reshard_ms_max=round(max((at(rec["log"], "resharded in") - at(rec["log"], "destinations of")) * 1e3
+                                     for rec in new_recs), 2),
+            destinations_waited_for_release=any("after the old world released" in m
+                                                for rec in new_recs for _, m in rec["log"]))
+    if squeeze is not None:
+        lows = [low_water(l) for l in old_logs] + [low_water(rec["log"]) for rec in new_recs]
+        out["memory"] = {
+            "old_state_bytes": _old_state_bytes(w),
+            "free_at_start_bytes": held["free"],
+            "peak_beyond_start_bytes": int(held["free"] - min(lows)),
+            "reserve_bytes": RESERVE_BYTES * (old_ws + new_ws),
+            "note": ("this process held device memory until squeeze x the old state was free; peak = free "
+                     "memory at the start less the lowest free memory any rank sampled (after each pack "
+                     "and each reshard)")}
+    out.update({
         "parity": {"tensors": sum(rec["tensors"] for rec in new_recs),
                    "mismatched": sum(rec["mismatched"] for rec in new_recs),
                    "first_mismatches": [b for rec in new_recs for b in rec["bad"]][:5],
-                   "against": "the same seeded global tensors cut for each new rank (suika_amd.workloads.shard_global)"},
+                   "against": ("the same seeded global tensors cut for each new rank by the closed form in "
+                               "bench.py (torch.chunk, per-projection QKV chunks, zero-padded vocabulary)")},
         "per_new_rank_log_ms": [
             {m.split(":", 1)[1].strip()[:40]: round((t - rec["t_call"]) * 1e3, 1) for t, m in rec["log"]}
             for rec in new_recs],
@@ -806,7 +909,21 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None) -> di
             {m.split(":", 1)[1].strip()[:40]: round((t - start) * 1e3, 1) for t, m in l} for l in old_logs],
         "timing_lines": {"old": [[m for _, m in l if " ms" in m] for l in old_logs],
                          "new": [[m for _, m in rec["log"] if " ms" in m] for rec in new_recs]},
-    }
+    })
+    return out
+
+
+def _old_state_bytes(w) -> int:
+    """Device bytes of every old rank's fields."""
+    spl, _ = w.layouts()
+    n = 0
+    for metas in spl.layout.values():
+        for m in metas.values():
+            numel = 1
+            for d in m.actual_shape():
+                numel *= int(d)
+            n += numel * sum(w.dtypes[f].itemsize for f in w.src_fields)
+    return n
 
 
 def _seed_old_rank(w, rank: int, dev):
@@ -814,17 +931,15 @@ def _seed_old_rank(w, rank: int, dev):
     its shard of the seeded global state."""
     import torch
     from suika_amd.inventory import build_module
-    from suika_amd.workloads import shard_global
-    dt = w.dtypes
     pfield = "param" if "param" in w.src_fields else "master"
-    model = build_module(w.model, w.src, rank, dt[pfield], device=dev)
+    model = build_module(w.model, w.src, rank, w.dtypes[pfield], device=dev)
     opt = _state_optimizer(model.parameters())
     metas = w.layouts()[0].layout[rank]
     for name, p in model.named_parameters():
         glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
         with torch.no_grad():
-            p.copy_(shard_global(glob[pfield], metas[name]))
-        opt.state[p] = {f: shard_global(glob[f], metas[name]) for f in w.src_fields if f != pfield}
+            p.copy_(_expected_shard(glob[pfield], metas[name]))
+        opt.state[p] = {f: _expected_shard(glob[f], metas[name]).clone() for f in w.src_fields if f != pfield}
         del glob
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -832,9 +947,9 @@ def _seed_old_rank(w, rank: int, dev):
 
 
 def _check_new_rank(w, rank: int, model, opt, dev) -> dict:
-    """Every tensor a new rank received against the seeded state cut for it."""
+    """Every tensor a new rank received against the seeded state cut for it
+    by the closed form above."""
     import torch
-    from suika_amd.workloads import shard_global
     pfield = "param" if "param" in w.src_fields else "master"
     metas = w.layouts()[1].layout[rank]
     state = opt.state_dict()["state"]
@@ -843,7 +958,7 @@ def _check_new_rank(w, rank: int, model, opt, dev) -> dict:
         glob = _seeded_global(w, name, tuple(int(x) for x in metas[name].shape), dev)
         got = {pfield: p, **{f: state[idx][f] for f in w.src_fields if f != pfield}}
         for f, t in got.items():
-            want = shard_global(glob[f], metas[name])
+            want = _expected_shard(glob[f], metas[name])
             n += 1
             if t.dtype != want.dtype or t.shape != want.shape or \
                     not torch.equal(t.reshape(-1).view(torch.uint8), want.reshape(-1).view(torch.uint8)):
@@ -1041,7 +1156,9 @@ def main(argv=None) -> int:
 
     key = args.config or BENCH_CONFIG
     if args.handoff:
-        rec = handoff_leg(key, wait_for_release=True if args.handoff_wait_release else None)
+        rec = handoff_leg(key, wait_for_release=True if args.handoff_wait_release else None,
+                          mode=args.handoff_mode, wave_bytes=args.handoff_wave_bytes,
+                          squeeze=args.handoff_squeeze, return_before_release=args.handoff_return_early)
         print(json.dumps({"handoff": rec}), flush=True)
         return 0 if rec["parity"]["mismatched"] == 0 else 1
     if args.checkpoint:

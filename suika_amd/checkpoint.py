@@ -330,7 +330,8 @@ def _device(device) -> torch.device:
 def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = None,
                    other_context: Any = None, device: Optional[torch.device] = None,
                    world: Optional[dist.ProcessGroup] = None, log_func: Optional[Callable] = None,
-                   checkpoint_resume: Optional[str] = None):
+                   checkpoint_resume: Optional[str] = None, *, handoff_mode: Optional[str] = None,
+                   wave_bytes: Optional[int] = None):
     """Suika's save-side migration API (Suika/migration.py:1357-1486).
 
     With ``checkpoint_resume`` it writes the checkpoint (:1382-1392).
@@ -338,7 +339,12 @@ def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = N
     same GPU over ``IPC_queues`` (forward, backward), as
     ``suika_amd.handoff.live_save`` describes: the world-size handshake, the
     state packed into exported device allocations, and their release once
-    the new world has resharded from them."""
+    the new world has resharded from them.
+
+    ``handoff_mode`` and ``wave_bytes`` (not in the reference) force the
+    hand-off's order: ``"whole"``, or ``"waves"`` of at most ``wave_bytes``
+    (default: a third of the free memory); ``None`` moves the state whole
+    when the device has room for it beside the old state, else in waves."""
     if log_func is None:
         log_func = lambda msg: None  # noqa: E731
     device = _device(device)
@@ -348,14 +354,15 @@ def migration_save(IPC_queues, model: Module, optimizer: Optional[Optimizer] = N
         return checkpoint_save(model=model, optimizer=optimizer, other_context=other_context,
                                checkpoint_dir=checkpoint_resume, world=world, log_func=log_func)
     from .handoff import live_save
-    return live_save(IPC_queues, model, optimizer, other_context, device, world, log_func)
+    return live_save(IPC_queues, model, optimizer, other_context, device, world, log_func,
+                     mode=handoff_mode, wave_bytes=wave_bytes)
 
 
 def migration_load(IPC_queues, model: Module,
                    optimizer: Union[Optimizer, Callable[[], Optimizer], None] = None,
                    device: Optional[torch.device] = None, world: Optional[dist.ProcessGroup] = None,
                    log_func: Optional[Callable] = None, checkpoint_resume: Optional[str] = None, *,
-                   wait_for_release: Optional[bool] = None):
+                   wait_for_release: Optional[bool] = None, return_before_release: bool = False):
     """Suika's load-side migration API (Suika/migration.py:1546-1727).
 
     With ``checkpoint_resume`` the checkpoint is resharded into ``model`` on
@@ -366,10 +373,13 @@ def migration_load(IPC_queues, model: Module,
     provider; a fresh launch (the launcher's placeholder on the queue)
     returns ``None`` / ``(optimizer_provider(), None)``.
 
-    ``wait_for_release`` (not in the reference) chooses when a live
-    migration allocates its destinations: ``None`` beside the old state when
+    ``wait_for_release`` (not in the reference) chooses when a whole live
+    hand-off allocates its destinations: ``None`` beside the old state when
     the device has room, else after the old world released it; ``True``
-    always after."""
+    always after.  ``return_before_release`` (not in the reference) returns
+    once this world's state is adopted and its optimizer built, without
+    waiting for the old world to release its state (the reference's order);
+    by default no new rank returns before that release."""
     if log_func is None:
         log_func = lambda msg: None  # noqa: E731
     device = _device(device)
@@ -385,4 +395,5 @@ def migration_load(IPC_queues, model: Module,
     else:
         raise TypeError(f"optimizer should be Optimizer or Callable, but got {type(optimizer)}")
     from .handoff import live_load
-    return live_load(IPC_queues, model, optimizer_provider, optimizer, device, world, log_func, wait_for_release)
+    return live_load(IPC_queues, model, optimizer_provider, optimizer, device, world, log_func, wait_for_release,
+                     return_before_release)

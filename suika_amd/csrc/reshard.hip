@@ -1924,17 +1924,6 @@ int sr_prepare(hipStream_t stream) {
 int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* const* dst_ptrs,
                       hipStream_t stream) {
   if (!plan) return fail(SR_EINVAL, "plan is null");
-  // The tables go up from pageable host memory that is released when the
-  // call returns: a graph captured from this call would replay copies out of
-  // freed memory, so a capturing stream is refused before any device work.
-  {
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    SR_HIP_TRY(hipStreamIsCapturing(stream, &cap));
-    if (cap != hipStreamCaptureStatusNone)
-      return fail(SR_EINVAL,
-                  "sr_gather_noalloc: the stream is capturing a graph; this call uploads its tables from "
-                  "pageable host memory at every call and cannot be captured");
-  }
   const Phase& ph = plan->gather;
   // The size check comes first: it needs neither the pointers nor a device.
   const ScratchLayout L = scratch_layout(ph);
@@ -1951,6 +1940,18 @@ int sr_gather_noalloc(const sr_plan* plan, const void* const* src_ptrs, void* co
   if (ph.rel.empty()) return SR_OK;
   const std::vector<uint64_t> ptrs = pointer_table(src_ptrs, plan->src.size(), dst_ptrs, plan->dst.size());
   if ((rc = check_disjoint(ph, ptrs)) != SR_OK) return rc;
+  // The tables go up from pageable host memory that is released when the
+  // call returns: a graph captured from this call would replay copies out of
+  // freed memory, so a capturing stream is refused before any device work
+  // (the argument checks above need no device).
+  {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SR_HIP_TRY(hipStreamIsCapturing(stream, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(SR_EINVAL,
+                  "sr_gather_noalloc: the stream is capturing a graph; this call uploads its tables from "
+                  "pageable host memory at every call and cannot be captured");
+  }
 
   int dev = -1;
   SR_HIP_TRY(hipGetDevice(&dev));

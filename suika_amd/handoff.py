@@ -6,13 +6,17 @@ the processes of its new plan.  The two sets of processes run side by side;
 each guard process owns a pair of queues shared by its old and new rank
 (``IPC_queues``: forward, backward).  The reference moves every tensor through
 the queue as a CUDA-IPC handle, one acknowledgement each, clones it on the
-receiving side, and reshards over NCCL in the old world (scale-down) or the
-new one (scale-up) (Suika/utils.py:325-406).
+receiving side, frees it on the sending side once acknowledged (collecting
+the cache every 1 GiB sent), and reshards over NCCL in the old world
+(scale-down) or the new one (scale-up) (Suika/utils.py:325-406).
 
-Here, with every old and new rank on the same GPU:
+Here, with every old and new rank on the same GPU, the handshake on world
+sizes is the reference's (rank 0 of each side, over the queues, :1395-1405 /
+:1587-1598).  Then the old world sums the bytes it holds on the device and
+old rank 0 picks one of two orders from the device's free memory:
 
-* the handshake on world sizes is the reference's (rank 0 of each side, over
-  the queues, :1395-1405 / :1587-1598);
+**Whole** (the hand-off fits beside the old state):
+
 * each old rank packs its merged state (``merge_model_and_optimizer_state_dict``)
   into a few device allocations of its own with one gather launch, exports
   them (``sr_handoff_alloc``, at most 1 GiB each, always below 2 GiB), and the
@@ -32,14 +36,35 @@ Here, with every old and new rank on the same GPU:
 * only then does each old rank free its state tensors, as the reference frees
   each sent tensor, and return the memory to the device (memory another
   process has just freed is slow to allocate); once all have, old rank 0
-  sends ``RELEASED``;
+  sends ``RELEASED`` when the new world waits for it;
 * each new rank runs ``execute_param_transfer`` (one gather per launch group)
   straight from the mapped memory into one destination arena that the model
   adopts with ``load_state_dict(assign=True)``, beside the old state's
-  release when the memory allowed it, and builds its optimizer;
-* new rank 0, holding ``RELEASED``, acknowledges on rank 0's backward queue
-  and the new world returns; the old world then frees the hand-off
-  allocations and returns.
+  release when the memory allowed it; new rank 0 then sends ``DONE`` and the
+  old world frees the hand-off allocations;
+* the new world builds its optimizer and returns: by default once ``RELEASED``
+  has come (the device is then the new world's alone), or at once with
+  ``return_before_release`` (the reference's order: its new processes return
+  after their own receive and reshard).
+
+**Waves** (it does not: the device holds less than twice the state).  Names
+are cut into waves of at most a third of the free memory, in the same order
+on every old rank; a name's tensors on every old rank move in one wave, so a
+wave is a self-contained reshard.  For each wave the old ranks pack its
+tensors into hand-off allocations, free them and return their memory (the
+reference's per-tensor free and periodic ``cuda_gc``), and old rank 0 sends
+the wave's records; the new ranks map them, reshard that wave into an arena
+of its own and report it consumed, and the old ranks free its hand-off.  The
+old world packs wave ``k + 1`` while the new world reshards wave ``k``, so the
+device holds the state plus at most two waves.
+
+Every step at which one rank may fail ends in an exchange of errors within
+its world, so a failure raises on every rank of that world instead of
+leaving the others in their next collective; the world that failed sends
+``(ERROR, text)`` on the queue the other world reads next, and every queue
+read has a time limit (``QUEUE_TIMEOUT_S``).  A world that sent records
+releases their memory only after the other world has closed its mappings
+(it reported the wave consumed, said ``DONE`` or failed).
 
 The packed allocations are the per-peer buffers of a pack -> unpack reshard:
 the old side reads and writes P bytes, the new side reads P and writes D, and
@@ -50,6 +75,7 @@ does, reading from the mapped memory.
 from __future__ import annotations
 
 import ctypes
+import queue
 import threading
 import time
 from collections import OrderedDict
@@ -75,22 +101,43 @@ dummy_migration_IPC_state_dict = {
     "other_context_dict": {},
 }
 
+# New rank 0 to old rank 0 once the new world has resharded: the hand-off
+# allocations are no longer mapped.
 DONE = "suika_amd: handoff complete"
-# New rank 0 to old rank 0 once every new rank has mapped the hand-off: either
-# every new rank holds the memory for its destinations (ALLOCATED), or the
-# device lacks room for them beside the old state (WANT_RELEASED).  The old
-# ranks release their state only then, so memory they free is not what the
-# new ranks allocate at once.
+# New rank 0 to old rank 0 once every new rank has mapped the hand-off (sent
+# as {"note": ..., "await_release": bool}): either every new rank holds the
+# memory for its destinations (ALLOCATED), or the device lacks room for them
+# beside the old state (WANT_RELEASED).  The old ranks release their state
+# only then, so memory they free is not what the new ranks allocate at once.
 ALLOCATED = "suika_amd: destinations allocated"
 WANT_RELEASED = "suika_amd: waiting for the old state's release"
-# Old rank 0 to new rank 0, after either note: every old rank has released
-# its state and returned the memory to the device.
+# Old rank 0 to new rank 0, when the note asked for it: every old rank has
+# released its state and returned the memory to the device.
 RELEASED = "suika_amd: old state released"
+# (ERROR, text) on either queue: the sending world failed; the reader raises.
+ERROR = "suika_amd: handoff failed"
+# Time limit of every queue read of the protocol, in seconds.
+QUEUE_TIMEOUT_S = 600.0
 # Device memory kept free per new rank beyond its destinations when they are
-# allocated beside the old state (plan tables, allocator rounding).
+# allocated beside the old state: plan tables, allocator rounding, and the
+# library's 64 MiB static scratch array, which its code object places on the
+# device in every process that loads it (old and new ranks alike).
 HEADROOM_BYTES = 1 << 30
 # Taken beyond a new rank's destination bytes when it reserves them.
 ARENA_SLACK_BYTES = 64 << 20
+# Per process of either world, left out of the memory the waves may use:
+# the same per-process costs at the granularity one wave adds them.
+RESERVE_BYTES = 96 << 20
+
+
+class HandoffError(RuntimeError):
+    """A live migration failed; every process of the failing world raises
+    it, and so does every process of the other world that was waiting on it.
+    ``notify``: the other world has not been told yet."""
+
+    def __init__(self, msg: str, notify: bool = True):
+        super().__init__(msg)
+        self.notify = notify
 
 
 def pack_layout(nbytes: Sequence[int], chunk_bytes: int = CHUNK_BYTES) -> Tuple[List[Tuple[int, int]], List[int]]:
@@ -260,6 +307,79 @@ class MappedSources:
                 _lib.check(L.sr_handoff_close(ctypes.c_void_p(self._opened.pop())), "sr_handoff_close", L)
 
 
+def device_bytes(entry: Dict[str, Any], device: torch.device) -> int:
+    """Bytes a name's fields take in the hand-off: its non-empty tensors on
+    ``device``, each rounded up to 256 bytes."""
+    return sum((t.numel() * t.element_size() + ALIGN - 1) // ALIGN * ALIGN for t in entry.values()
+               if isinstance(t, Tensor) and t.is_cuda and t.device == device and t.numel() > 0)
+
+
+def plan_waves(per_rank: Sequence[Sequence[Tuple[str, int]]], wave_bytes: int) -> List[List[str]]:
+    """Names cut into waves for a hand-off in waves.
+
+    ``per_rank[r]`` lists old rank ``r``'s names in its own order with the
+    bytes each takes there.  Names are taken round-robin over the ranks'
+    lists (the first name of every rank, then the second, ...; each name
+    once), so pipeline stages holding different layers share every wave;
+    a wave closes before the name that would take its bytes, summed over all
+    ranks, past ``wave_bytes``.  A name larger than that is a wave alone.
+    Every rank computes the same waves from the same lists."""
+    total: Dict[str, int] = {}
+    for names in per_rank:
+        for name, n in names:
+            total[name] = total.get(name, 0) + int(n)
+    order: List[str] = []
+    seen = set()
+    for i in range(max((len(names) for names in per_rank), default=0)):
+        for names in per_rank:
+            if i < len(names) and names[i][0] not in seen:
+                seen.add(names[i][0])
+                order.append(names[i][0])
+    waves: List[List[str]] = []
+    acc = 0
+    for name in order:
+        if not waves or (acc + total[name] > wave_bytes and waves[-1]):
+            waves.append([])
+            acc = 0
+        waves[-1].append(name)
+        acc += total[name]
+    return waves
+
+
+def choose_order(state_bytes: int, largest_name_bytes: int, free_bytes: int, processes: int,
+                 mode: Optional[str] = None, wave_bytes: Optional[int] = None) -> Tuple[str, int]:
+    """``("whole", 0)`` or ``("waves", W)`` for a hand-off of ``state_bytes``
+    (the old world's device bytes) with ``free_bytes`` free on the device and
+    ``processes`` processes of both worlds on it.
+
+    The room is the free memory less ``RESERVE_BYTES`` per process.  Whole
+    needs the hand-off beside the old state (``state_bytes`` of room); the
+    new world's destinations, about as large, then fit beside the hand-off
+    once the old state is released.  Waves need two waves of room: the one
+    the new world reshards and the next being packed (each wave's sources are
+    freed once packed, and its destinations take what they held).  ``W`` is
+    ``wave_bytes`` or a third of the room, and at least the largest name's
+    bytes.  ``mode`` forces an order; ``None`` takes whole when it fits.
+    Raises ``HandoffError`` when the chosen order does not fit."""
+    if mode not in (None, "whole", "waves"):
+        raise ValueError(f"hand-off mode {mode!r}: expected None, 'whole' or 'waves'")
+    room = free_bytes - RESERVE_BYTES * processes
+    if mode == "whole" or (mode is None and state_bytes <= room):
+        if state_bytes > room:
+            raise HandoffError(f"a whole hand-off of {state_bytes / 1e9:.3f} GB does not fit beside the old "
+                               f"state: {free_bytes / 1e9:.3f} GB free on the device, "
+                               f"{RESERVE_BYTES * processes / 1e9:.3f} GB kept for {processes} processes")
+        return "whole", 0
+    w = int(wave_bytes) if wave_bytes else room // 3
+    w = max(w, int(largest_name_bytes), 1)
+    if 2 * w > room:
+        raise HandoffError(f"the device lacks memory for a hand-off in waves: {free_bytes / 1e9:.3f} GB free, "
+                           f"{RESERVE_BYTES * processes / 1e9:.3f} GB kept for {processes} processes, and two "
+                           f"waves of {w / 1e9:.3f} GB (the largest name takes "
+                           f"{largest_name_bytes / 1e9:.3f} GB) need {2 * w / 1e9:.3f} GB")
+    return "waves", w
+
+
 def _broadcast_objects(*objs, group=None):
     """Rank 0's objects on every rank of ``group`` (Suika/utils.py:98-104)."""
     lst = list(objs)
@@ -268,76 +388,300 @@ def _broadcast_objects(*objs, group=None):
     return lst[0] if len(lst) == 1 else lst
 
 
+def _error_note(text: str) -> Tuple[str, str]:
+    return (ERROR, text)
+
+
+def _is_error(msg: Any) -> bool:
+    return isinstance(msg, tuple) and len(msg) == 2 and msg[0] == ERROR
+
+
+def _recv(q, what: str) -> Any:
+    """The next message on ``q``; an error note when none comes in time."""
+    try:
+        return q.get(block=True, timeout=QUEUE_TIMEOUT_S)
+    except queue.Empty:
+        return _error_note(f"no {what} from the other world within {QUEUE_TIMEOUT_S:.0f} s")
+
+
+def _recv_on_rank0(q, what: str, world) -> Any:
+    """Rank 0 reads ``q``; every rank gets the message.  An error note from
+    the other world (or none in time) raises on every rank."""
+    msg = _recv(q, what) if dist.get_rank(world) == 0 else None
+    msg = _broadcast_objects(msg, group=world)
+    if _is_error(msg):
+        raise HandoffError(f"waiting for {what}: {msg[1]}", notify=False)
+    return msg
+
+
+def _attempt(fn: Callable[[], Any]) -> Tuple[Any, Optional[str]]:
+    """``fn()``, or its failure as text."""
+    try:
+        return fn(), None
+    except Exception as e:  # reported to every rank by _agree
+        return None, f"{type(e).__name__}: {e}"
+
+
+def _agree(world, err: Optional[str], what: str, notify: bool = True) -> None:
+    """Every rank's error (or None) to every rank; raise on all when any
+    failed (``notify``: the other world is still to be told)."""
+    errs: List[Optional[str]] = [None] * dist.get_world_size(world)
+    dist.all_gather_object(errs, err, group=world)
+    bad = [f"rank {r}: {e}" for r, e in enumerate(errs) if e is not None]
+    if bad:
+        raise HandoffError(f"{what} failed on " + "; ".join(bad), notify=notify)
+
+
+class _LowWater:
+    """The least free device memory seen at this rank's samples (taken where
+    the hand-off holds the most)."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.free: Optional[int] = None
+
+    def sample(self) -> None:
+        free, _ = torch.cuda.mem_get_info(self.device)
+        self.free = free if self.free is None else min(self.free, free)
+
+    def line(self, side: str) -> str:
+        return f"{side}: low-water free device memory {(self.free or 0) / 1e9:.3f} GB"
+
+
+def _release_state(state: Dict[str, Dict[str, Any]], names) -> None:
+    """Free the device tensors of ``names`` in ``state`` (as the reference
+    frees every tensor it has sent, utils.py:372-376), drop them from
+    ``state``, and return the freed memory to the device (its ``cuda_gc``,
+    utils.py:248-253, 379-386)."""
+    from .migration import forcefully_free_tensor
+    for name in names:
+        for t in state.pop(name, {}).values():
+            if isinstance(t, Tensor) and t.is_cuda:
+                forcefully_free_tensor(t)
+    torch.cuda.empty_cache()
+
+
+
+class _OldWorld:
+    """The old side's half of the protocol after the handshake."""
+
+    def __init__(self, queues, world, device: torch.device, new_world_size: int,
+                 log_func: Callable[[str], None]):
+        self.q = queues
+        self.world = world
+        self.rank = dist.get_rank(world)
+        self.device = device
+        self.new_world_size = new_world_size
+        self.log = log_func
+        self.low = _LowWater(device)
+        self.sent_first = False
+
+    def notify(self, text: str) -> None:
+        """Tell the new world that this one failed, where it reads next: each
+        new rank its own forward queue before the first message, new rank 0
+        the forward queue after it."""
+        if not self.sent_first:
+            if self.rank < self.new_world_size:
+                self.q[0].put(_error_note(text))
+        elif self.rank == 0:
+            self.q[0].put(_error_note(text))
+
+    def send_first(self, param_layout, other_context_dict, order) -> None:
+        """Old rank i's message to new rank i: the layout, the context and the
+        order (``"whole"`` or the number of waves); the records follow on
+        rank 0's forward queue."""
+        if self.rank < self.new_world_size:
+            self.q[0].put({"source_param_layout": param_layout, "source_state_dict": {},
+                           "other_context_dict": other_context_dict, "order": order})
+        self.sent_first = True
+
+    def _records(self, handoff: "Handoff") -> List[Dict[str, Any]]:
+        records: List[Any] = [None] * dist.get_world_size(self.world)
+        dist.all_gather_object(records, handoff.record(), group=self.world)
+        return records
+
+    def whole(self, state, param_layout, other_context_dict) -> None:
+        self.send_first(param_layout, other_context_dict, "whole")
+        t0 = time.perf_counter()
+        handoff, err = _attempt(lambda: Handoff(state, self.device, self.rank))
+        t1 = time.perf_counter()
+        self.low.sample()
+        try:
+            _agree(self.world, err, "packing the hand-off")
+            self.log(f"migration_save: packed {handoff.bytes / 1e9:.3f} GB into {len(handoff.chunks)} hand-off "
+                     f"allocation(s) in {(t1 - t0) * 1e3:.2f} ms")
+            records = self._records(handoff)
+            if self.rank == 0:
+                self.q[0].put(("records", records))
+            self.log(f"migration_save: {len(records)} hand-off record(s) sent")
+            # The state now lives in the hand-off allocations: it is released
+            # once the new world has mapped them and either allocated its
+            # destinations beside this state or asked for the memory.
+            note = _recv_on_rank0(self.q[1], "the new world's allocation note", self.world)
+            assert isinstance(note, dict) and note.get("note") in (ALLOCATED, WANT_RELEASED), \
+                f"migration_save: unexpected message {note!r}"
+            self.log("migration_save: the new world " + ("has allocated its destinations"
+                                                         if note["note"] == ALLOCATED
+                                                         else "waits for this state's memory"))
+            t2 = time.perf_counter()
+            _, rel_err = _attempt(lambda: _release_state(state, list(state)))
+            t3 = time.perf_counter()
+            self.log(f"migration_save: state released and device memory returned ({(t3 - t2) * 1e3:.2f} ms)")
+            dist.barrier(self.world)
+            if note["await_release"] and self.rank == 0:
+                self.q[0].put(RELEASED)
+            done = _recv_on_rank0(self.q[1], "the new world's DONE", self.world)
+            assert done == DONE, f"migration_save: unexpected acknowledgement {done!r}"
+            self.log("migration_save: the new world is done with the hand-off")
+            # the new world has its state; a failure to release ours is this
+            # world's alone
+            _agree(self.world, rel_err, "releasing the old state", notify=False)
+        finally:
+            if handoff is not None:
+                handoff.release()
+
+    def waves(self, state, param_layout, other_context_dict, waves: List[List[str]]) -> None:
+        self.send_first(param_layout, other_context_dict, len(waves))
+        held: List[Tuple[int, Handoff]] = []     # sent, not yet reported consumed
+        pending_err: Optional[str] = None
+        t_start = time.perf_counter()
+        packed = 0
+
+        def consumed(k: int) -> None:
+            msg = _recv_on_rank0(self.q[1], f"the new world's report on wave {k}", self.world)
+            assert msg == ("consumed", k), f"migration_save: unexpected message {msg!r}"
+
+        try:
+            for k, names in enumerate(waves):
+                part = {n: state[n] for n in names if n in state}
+                handoff, err = _attempt(lambda: Handoff(part, self.device, self.rank))
+                self.low.sample()
+                if handoff is not None:
+                    packed += handoff.bytes
+                try:
+                    _agree(self.world, err or pending_err, f"packing wave {k}")
+                except HandoffError:
+                    if handoff is not None:
+                        handoff.release()     # never sent
+                    raise
+                records = self._records(handoff)
+                held.append((k, handoff))
+                if self.rank == 0:
+                    self.q[0].put(("wave", k, list(names), records))
+                # the wave's sources are in the hand-off: their memory goes back
+                # to the device for the next wave and the new world's arenas
+                del part
+                _, pending_err = _attempt(lambda: _release_state(state, names))
+                if len(held) > 1:
+                    consumed(held[0][0])
+                    held.pop(0)[1].release()
+            while held:
+                consumed(held[0][0])
+                held.pop(0)[1].release()
+            _agree(self.world, pending_err, "releasing the old state", notify=False)
+        except HandoffError as e:
+            if e.notify:
+                self.notify(str(e))
+                e.notify = False
+                # the new world stops at this note; the waves it was sent stay
+                # mapped until it reports them consumed (or fails)
+                try:
+                    for k, _ in held:
+                        consumed(k)
+                except HandoffError:
+                    pass
+            raise
+        finally:
+            for _, h in held:
+                h.release()
+        self.log(f"migration_save: {packed / 1e9:.3f} GB handed off in {len(waves)} wave(s) in "
+                 f"{(time.perf_counter() - t_start) * 1e3:.2f} ms")
+
+
 def live_save(IPC_queues, model, optimizer, other_context, device: torch.device, world,
-              log_func: Callable[[str], None]) -> None:
-    """The old side of a live migration (Suika/migration.py:1394-1486)."""
+              log_func: Callable[[str], None], mode: Optional[str] = None,
+              wave_bytes: Optional[int] = None) -> None:
+    """The old side of a live migration (Suika/migration.py:1394-1486).
+
+    ``mode`` forces the hand-off's order (``"whole"``, or ``"waves"`` with
+    ``wave_bytes`` per wave); ``None`` takes whole when it fits beside the
+    old state.  Raises ``HandoffError`` on every old rank when the hand-off
+    fails on any rank of either world."""
     from .meta import ParamLayout
-    from .migration import forcefully_free_tensor, merge_model_and_optimizer_state_dict
+    from .migration import merge_model_and_optimizer_state_dict
 
     rank = dist.get_rank(world)
     # the library's first-use costs are paid while the new world starts
     warm = _WarmUp(device, optimizer=False)
     warm.start()
     if rank == 0:
-        old_world_size = dist.get_world_size(world)
-        IPC_queues[0].put(old_world_size)
-        new_world_size = IPC_queues[1].get(block=True)
-        is_scale_up = new_world_size >= old_world_size
+        IPC_queues[0].put(dist.get_world_size(world))
+        reply = _recv(IPC_queues[1], "world size")
     else:
-        is_scale_up = new_world_size = None
-    is_scale_up, new_world_size = _broadcast_objects(is_scale_up, new_world_size, group=world)
-    log_func(f"migration_save: is_scale_up = {is_scale_up} (new world size {new_world_size})")
+        reply = None
+    reply = _broadcast_objects(reply, group=world)
     warm.join()
+    if _is_error(reply):
+        raise HandoffError(f"migration_save: handshake: {reply[1]}", notify=False)
+    new_world_size = int(reply)
+    is_scale_up = new_world_size >= dist.get_world_size(world)
+    log_func(f"migration_save: is_scale_up = {is_scale_up} (new world size {new_world_size})")
 
     param_layout = ParamLayout()
     param_layout.gather(model, world)
-    source_state_dict, other_context_dict = merge_model_and_optimizer_state_dict(model, optimizer, other_context)
-
-    t0 = time.perf_counter()
-    handoff = Handoff(source_state_dict, device, rank)
-    t1 = time.perf_counter()
-    log_func(f"migration_save: packed {handoff.bytes / 1e9:.3f} GB into {len(handoff.chunks)} hand-off "
-             f"allocation(s) in {(t1 - t0) * 1e3:.2f} ms")
+    side = _OldWorld(IPC_queues, world, device, new_world_size, log_func)
     try:
-        records = [None] * dist.get_world_size(world)
-        dist.all_gather_object(records, handoff.record(), group=world)
-        log_func(f"migration_save: {len(records)} hand-off record(s) gathered")
-        if rank < new_world_size:
-            IPC_queues[0].put({"source_param_layout": param_layout, "source_state_dict": {},
-                               "other_context_dict": other_context_dict, "handoff": records})
-            log_func("migration_save: hand-off sent to the new rank")
-        # The state now lives in the hand-off allocations: release it, as the
-        # reference releases every tensor it has sent (utils.py:372-376), and
-        # return the memory to the device for the new world, as its cuda_gc
-        # does after sending (utils.py:248-253, 385) -- once the new world
-        # has mapped the hand-off and either allocated its destinations
-        # beside this state or asked for the memory.
-        note = IPC_queues[1].get(block=True) if rank == 0 else None
-        note = _broadcast_objects(note, group=world)
-        assert note in (ALLOCATED, WANT_RELEASED), f"migration_save: unexpected message {note!r}"
-        log_func("migration_save: the new world " + ("has allocated its destinations" if note == ALLOCATED
-                                                     else "waits for this state's memory"))
-        t2 = time.perf_counter()
-        for entry in source_state_dict.values():
-            for t in entry.values():
-                if isinstance(t, Tensor) and t.is_cuda:
-                    forcefully_free_tensor(t)
-        del source_state_dict
-        t3 = time.perf_counter()
-        torch.cuda.empty_cache()
-        t4 = time.perf_counter()
-        log_func(f"migration_save: state released ({(t3 - t2) * 1e3:.2f} ms), device memory returned "
-                 f"({(t4 - t3) * 1e3:.2f} ms)")
-        dist.barrier(world)
-        # the new world maps these allocations until it has resharded
+        # every rank's device bytes per name, checked before anything is
+        # allocated: a tensor a hand-off allocation cannot hold fails here
+        def survey():
+            state, ctx = merge_model_and_optimizer_state_dict(model, optimizer, other_context)
+            for name, entry in state.items():
+                for f, t in entry.items():
+                    if isinstance(t, Tensor) and t.is_cuda and t.device == device and t.numel() > 0:
+                        n = t.numel() * t.element_size()
+                        if n > _lib.HANDOFF_MAX_BYTES:
+                            raise ValueError(f"{name}/{f} takes {n} bytes, more than one hand-off "
+                                             f"allocation holds ({_lib.HANDOFF_MAX_BYTES} bytes)")
+                        if not t.is_contiguous():
+                            raise ValueError(f"{name}/{f} is not contiguous")
+            return state, ctx, [(name, device_bytes(entry, device)) for name, entry in state.items()]
+
+        got, err = _attempt(survey)
+        info: List[Any] = [None] * dist.get_world_size(world)
+        dist.all_gather_object(info, (err, got[2] if got else None), group=world)
+        bad = [f"rank {r}: {e}" for r, (e, _) in enumerate(info) if e is not None]
+        if bad:
+            raise HandoffError("migration_save: " + "; ".join(bad))
+        source_state_dict, other_context_dict, _ = got
+        per_rank = [names for _, names in info]
+        totals: Dict[str, int] = {}
+        for names in per_rank:
+            for name, n in names:
+                totals[name] = totals.get(name, 0) + n
+        state_bytes = sum(totals.values())
+        choice = None
         if rank == 0:
-            IPC_queues[0].put(RELEASED)
-            ack = IPC_queues[1].get(block=True)
-            assert ack == DONE, f"migration_save: unexpected acknowledgement {ack!r}"
-        dist.barrier(world)
-        log_func("migration_save: the new world is done with the hand-off")
-    finally:
-        handoff.release()
+            free, _ = torch.cuda.mem_get_info(device)
+            order, err = _attempt(lambda: choose_order(
+                state_bytes, max(totals.values(), default=0), free,
+                dist.get_world_size(world) + new_world_size, mode, wave_bytes))
+            choice = (order, err, free)
+        order, err, free = _broadcast_objects(choice, group=world)
+        if err is not None:
+            raise HandoffError(f"migration_save: {err}")
+        how, w = order
+        log_func(f"migration_save: {state_bytes / 1e9:.3f} GB on the device, {free / 1e9:.3f} GB free: hand-off "
+                 + ("whole" if how == "whole" else f"in waves of at most {w / 1e9:.3f} GB"))
+        if how == "whole":
+            side.whole(source_state_dict, param_layout, other_context_dict)
+        else:
+            side.waves(source_state_dict, param_layout, other_context_dict, plan_waves(per_rank, w))
+    except HandoffError as e:
+        if e.notify:
+            side.notify(str(e))
+        log_func(f"migration_save: failed: {e}")
+        raise
+    log_func(side.low.line("migration_save"))
     log_func("migration_save: end")
 
 
@@ -408,39 +752,187 @@ def _destination_bytes(ops, rank: int, records: Sequence[Dict[str, Any]]) -> int
     return sum(per_name.values())
 
 
+class _NewWorld:
+    """The new side's half of the protocol once the first message is in."""
+
+    def __init__(self, queues, world, device: torch.device, ops, other_context_dict,
+                 warm: "_WarmUp", log_func: Callable[[str], None]):
+        self.q = queues
+        self.world = world
+        self.rank = dist.get_rank(world)
+        self.device = device
+        self.ops = ops
+        self.fields = other_context_dict["expected_sub_fields"]
+        self.warm = warm
+        self.log = log_func
+        self.low = _LowWater(device)
+
+    def _reshard(self, ops, records, needed) -> Dict[str, Dict[str, Tensor]]:
+        """``ops``' pieces for this rank, gathered from the mapped records of
+        the old ranks ``needed`` into one arena; the mappings are closed
+        before it returns or raises."""
+        from .migration import execute_param_transfer
+        mapped = MappedSources(records, needed, self.device)
+        try:
+            out = execute_param_transfer(
+                transfer_ops=ops, source_state_dict={}, device=self.device, expected_sub_fields=self.fields,
+                world=self.world, fake_source_state_dicts=mapped.states, log_func=self.log, rank=self.rank,
+                arena=True)
+            torch.cuda.synchronize(self.device)
+            self.low.sample()
+            return out
+        finally:
+            mapped.close()
+
+    def whole(self, wait_for_release: Optional[bool], return_before_release: bool):
+        """Returns the target state and whether the caller still waits for
+        ``RELEASED`` before returning."""
+        msg = _recv_on_rank0(self.q[0], "the hand-off records", self.world)
+        assert isinstance(msg, tuple) and msg[0] == "records", f"migration_load: unexpected message {msg!r}"
+        records = msg[1]
+        rank = self.rank
+        t0 = time.perf_counter()
+        needed = sorted({op.src_rank for op in self.ops if op.dst_rank == rank})
+        # Old state, hand-off and destinations side by side when the device
+        # has room for all of them: each new rank takes its destinations'
+        # memory before the old world frees anything.  Else the destinations
+        # wait for the old world to return its state's memory.
+        mine = _destination_bytes(self.ops, rank, records)
+        need = torch.tensor([mine], dtype=torch.int64)
+        dist.all_reduce(need, group=self.world)
+        wait = None
+        if rank == 0:
+            free, _ = torch.cuda.mem_get_info(self.device)
+            room = int(need.item()) + HEADROOM_BYTES * dist.get_world_size(self.world)
+            wait = bool(wait_for_release) if wait_for_release is not None else free < room
+        wait = _broadcast_objects(wait, group=self.world)
+        await_release = wait or not return_before_release
+
+        def reserve_and_map():
+            if not wait:
+                # the destination arena's memory, taken now and kept in this
+                # process's allocator cache, where the arena finds it
+                torch.empty(mine + ARENA_SLACK_BYTES, dtype=torch.uint8, device=self.device)
+            t_alloc = time.perf_counter()
+            # mapped before the old world frees anything: IPC opens beside
+            # other processes' frees were 20-40x slower
+            return t_alloc, MappedSources(records, needed, self.device)
+
+        got, err = _attempt(reserve_and_map)
+        self.low.sample()
+        mapped = got[1] if got else None
+        try:
+            _agree(self.world, err, "taking the destinations' memory and mapping the hand-off")
+            t_alloc, t_map = got[0], time.perf_counter()
+            self.log(f"migration_load: mapped the state of old rank(s) {needed}")
+            if rank == 0:
+                self.q[1].put({"note": WANT_RELEASED if wait else ALLOCATED, "await_release": await_release})
+            self.warm.library_done.wait()
+            if wait:
+                _recv_on_rank0(self.q[0], "the old world's release", self.world)
+            self.log(f"migration_load: destinations of {int(need.item()) / 1e9:.3f} GB "
+                     + ("after the old world released its state" if wait else "beside the old state"))
+            t1 = time.perf_counter()
+
+            def reshard():
+                from .migration import execute_param_transfer
+                out = execute_param_transfer(
+                    transfer_ops=self.ops, source_state_dict={}, device=self.device,
+                    expected_sub_fields=self.fields, world=self.world,
+                    fake_source_state_dicts=mapped.states, log_func=self.log, rank=rank, arena=True)
+                torch.cuda.synchronize(self.device)
+                self.low.sample()
+                return out
+            target, err = _attempt(reshard)
+            t2 = time.perf_counter()
+        finally:
+            if mapped is not None:
+                mapped.close()
+        _agree(self.world, err, "resharding from the hand-off")
+        if rank == 0:
+            self.q[1].put(DONE)
+        self.log("migration_load: "
+                 + ("" if wait else f"destinations' memory taken in {(t_alloc - t0) * 1e3:.2f} ms, ")
+                 + f"mapped {len(needed)} old rank(s) in {(t_map - t_alloc) * 1e3:.2f} ms, "
+                 f"resharded in {(t2 - t1) * 1e3:.2f} ms")
+        return target, await_release and not wait
+
+    def waves(self, n: int):
+        target: Dict[str, Dict[str, Tensor]] = {}
+        rank = self.rank
+        t_start = time.perf_counter()
+        gather_ms = 0.0
+        for k in range(n):
+            msg = _recv_on_rank0(self.q[0], f"wave {k}", self.world)
+            assert isinstance(msg, tuple) and msg[:2] == ("wave", k), f"migration_load: unexpected message {msg!r}"
+            names, records = set(msg[2]), msg[3]
+            ops = [op for op in self.ops if op.param_name in names]
+            mine = [op for op in ops if op.dst_rank == rank]
+            needed = sorted({op.src_rank for op in mine})
+            if k == 0:
+                self.warm.library_done.wait()
+            t0 = time.perf_counter()
+            out, err = _attempt(lambda: self._reshard(ops, records, needed) if mine else {})
+            gather_ms += (time.perf_counter() - t0) * 1e3
+            _agree(self.world, err, f"resharding wave {k}")
+            target.update(out)
+            if rank == 0:
+                self.q[1].put(("consumed", k))
+        self.log(f"migration_load: destinations of {n} wave(s) resharded in {gather_ms:.2f} ms of "
+                 f"{(time.perf_counter() - t_start) * 1e3:.2f} ms")
+        return target
+
+
 def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.device, world,
-              log_func: Callable[[str], None], wait_for_release: Optional[bool] = None):
+              log_func: Callable[[str], None], wait_for_release: Optional[bool] = None,
+              return_before_release: bool = False):
     """The new side of a live migration (Suika/migration.py:1586-1727).
 
-    The destinations are allocated beside the old state when the device has
-    room for every new rank's (``wait_for_release=None``), else after the old
-    world has released its state; ``True`` always waits."""
+    In a whole hand-off the destinations are allocated beside the old state
+    when the device has room for every new rank's (``wait_for_release=None``),
+    else after the old world has released its state; ``True`` always waits.
+    The new world returns once the old world has released its state, or with
+    ``return_before_release`` as soon as its own state is adopted and its
+    optimizer built.  A hand-off in waves (the old world's choice when the
+    device lacks room for the whole) reshards wave by wave as the old world
+    releases its state.  Raises ``HandoffError`` on every new rank when the
+    hand-off fails on any rank of either world."""
     from .meta import ParamLayout, schedule_param_transfer
-    from .migration import execute_param_transfer, split_model_and_optimizer_state_dict
+    from .migration import split_model_and_optimizer_state_dict
 
     rank = dist.get_rank(world)
     # the process's first-use costs are paid while it waits for the old world
     warm = _WarmUp(device, optimizer_provider is not None)
     warm.start()
     if rank == 0:
-        old_world_size = IPC_queues[0].get(block=True)
-        new_world_size = dist.get_world_size(world)
-        if old_world_size != 0:
-            IPC_queues[1].put(new_world_size)
-        is_scale_up = new_world_size >= old_world_size
+        old_world_size = _recv(IPC_queues[0], "world size")
+        if not _is_error(old_world_size) and old_world_size != 0:
+            IPC_queues[1].put(dist.get_world_size(world))
     else:
-        is_scale_up = None
-    is_scale_up = _broadcast_objects(is_scale_up, group=world)
+        old_world_size = None
+    old_world_size = _broadcast_objects(old_world_size, group=world)
+    if _is_error(old_world_size):
+        warm.join()
+        raise HandoffError(f"migration_load: handshake: {old_world_size[1]}", notify=False)
+    is_scale_up = dist.get_world_size(world) >= old_world_size
     log_func(f"migration_load: is_scale_up = {is_scale_up}")
 
     target_param_layout = ParamLayout()
     target_param_layout.gather(model, world)
     # old rank i's message, or the launcher's placeholder when there is none
-    msg = IPC_queues[0].get(block=True)
+    own = _recv(IPC_queues[0], "hand-off message")
     log_func("migration_load: hand-off message received")
-    source_param_layout, other_context_dict, records = _broadcast_objects(
-        msg.get("source_param_layout"), msg.get("other_context_dict"), msg.get("handoff"), group=world)
-    del msg
+    first = _broadcast_objects(own, group=world)
+    err = own[1] if _is_error(own) else (first[1] if _is_error(first) else None)
+    try:
+        _agree(world, err, "receiving the old world's first message", notify=False)
+    except HandoffError:
+        warm.join()
+        raise
+    del own
+    source_param_layout, other_context_dict = first.get("source_param_layout"), first.get("other_context_dict")
+    order = first.get("order")
+    del first
 
     if source_param_layout is None:
         log_func("migration_load: no checkpoint received; skip loading")
@@ -451,79 +943,44 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
 
     t0 = time.perf_counter()
     ops = schedule_param_transfer(source_param_layout, target_param_layout)
-    needed = sorted({op.src_rank for op in ops if op.dst_rank == rank})
-    t_sched = time.perf_counter()
-    # Old state, hand-off and destinations side by side when the device has
-    # room for all of them: each new rank takes its destinations' memory
-    # before the old world frees anything.  Else the destinations wait for
-    # the old world to return its state's memory.
-    mine = _destination_bytes(ops, rank, records)
-    need = torch.tensor([mine], dtype=torch.int64)
-    dist.all_reduce(need, group=world)
-    wait = None
-    if rank == 0:
-        free, _ = torch.cuda.mem_get_info(device)
-        room = int(need.item()) + HEADROOM_BYTES * dist.get_world_size(world)
-        wait = bool(wait_for_release) if wait_for_release is not None else free < room
-    wait = _broadcast_objects(wait, group=world)
-    if not wait:
-        # the destination arena's memory, taken now and kept in this
-        # process's allocator cache, where the arena finds it
-        torch.empty(mine + ARENA_SLACK_BYTES, dtype=torch.uint8, device=device)
-    t_alloc = time.perf_counter()
-    # mapped before the old world frees anything: IPC opens beside other
-    # processes' frees were 20-40x slower
-    mapped = MappedSources(records, needed, device)
-    t_map = time.perf_counter()
-    log_func(f"migration_load: mapped the state of old rank(s) {needed}")
+    log_func(f"migration_load: scheduled in {(time.perf_counter() - t0) * 1e3:.2f} ms")
+    side = _NewWorld(IPC_queues, world, device, ops, other_context_dict, warm, log_func)
     try:
+        if order == "whole":
+            target_state_dict, await_release = side.whole(wait_for_release, return_before_release)
+        else:
+            target_state_dict, await_release = side.waves(int(order)), False
         dist.barrier(world)
-        if rank == 0:
-            IPC_queues[1].put(WANT_RELEASED if wait else ALLOCATED)
-        warm.library_done.wait()
-        if wait:
-            if rank == 0:
-                note = IPC_queues[0].get(block=True)
-                assert note == RELEASED, f"migration_load: unexpected message {note!r}"
-            dist.barrier(world)
-        log_func(f"migration_load: destinations of {int(need.item()) / 1e9:.3f} GB "
-                 + ("after the old world released its state" if wait else "beside the old state"))
-        t1 = time.perf_counter()
-        target_state_dict = execute_param_transfer(
-            transfer_ops=ops, source_state_dict={}, device=device,
-            expected_sub_fields=other_context_dict["expected_sub_fields"], world=world,
-            fake_source_state_dicts=mapped.states, log_func=log_func, rank=rank, arena=True)
-        torch.cuda.synchronize(device)
-        t2 = time.perf_counter()
-    finally:
-        mapped.close()
-    log_func(f"migration_load: scheduled in {(t_sched - t0) * 1e3:.2f} ms, "
-             + ("" if wait else f"destinations' memory taken in {(t_alloc - t_sched) * 1e3:.2f} ms, ")
-             + f"mapped {len(needed)} old rank(s) in {(t_map - t_alloc) * 1e3:.2f} ms, "
-             f"resharded in {(t2 - t1) * 1e3:.2f} ms")
-    dist.barrier(world)
-    log_func("migration_load: every new rank has resharded")
+        log_func("migration_load: every new rank has resharded")
 
-    model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
-        model=model, merged_state_dict=target_state_dict, other_context_dict=other_context_dict)
-    model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
-    model.load_state_dict(model_state_dict, assign=True)
-    log_func("migration_load: model state adopted")
-    warm.join()
-    if optimizer_provider:
-        optimizer = optimizer_provider()
-    if optimizer:
-        # one parameter group, as the reference (migration.py:1712-1716)
-        optimizer_state_dict["param_groups"][0]["params"] = optimizer.state_dict()["param_groups"][0]["params"]
-        optimizer.load_state_dict(optimizer_state_dict)
-    # the old world's state released (beside which the destinations may have
-    # been allocated) before any new rank returns; then the old world may
-    # free the hand-off
-    if rank == 0:
-        if not wait:
-            note = IPC_queues[0].get(block=True)
-            assert note == RELEASED, f"migration_load: unexpected message {note!r}"
-        IPC_queues[1].put(DONE)
-    dist.barrier(world)
+        def adopt():
+            model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
+                model=model, merged_state_dict=target_state_dict, other_context_dict=other_context_dict)
+            model_state_dict = OrderedDict(sorted(model_state_dict.items(), key=lambda x: x[0]))
+            model.load_state_dict(model_state_dict, assign=True)
+            log_func("migration_load: model state adopted")
+            warm.join()
+            opt = optimizer_provider() if optimizer_provider else optimizer
+            if opt:
+                # one parameter group, as the reference (migration.py:1712-1716)
+                optimizer_state_dict["param_groups"][0]["params"] = opt.state_dict()["param_groups"][0]["params"]
+                opt.load_state_dict(optimizer_state_dict)
+            return opt, other_context
+        got, err = _attempt(adopt)
+        # the old world is done with this one: failures from here on are
+        # this world's alone
+        _agree(world, err, "adopting the new state", notify=False)
+        optimizer, other_context = got
+        if await_release:
+            # the old world's state released (beside which the destinations
+            # may have been allocated) before any new rank returns
+            _recv_on_rank0(IPC_queues[0], "the old world's release", world)
+            log_func("migration_load: the old world has released its state")
+    except HandoffError as e:
+        if e.notify and rank == 0:
+            IPC_queues[1].put(_error_note(str(e)))
+        log_func(f"migration_load: failed: {e}")
+        raise
+    log_func(side.low.line("migration_load"))
     log_func("migration_load: end")
     return (optimizer, other_context) if optimizer_provider else other_context

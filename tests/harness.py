@@ -78,16 +78,22 @@ def global_state(w: Workload, names: Iterable[str], seed: Optional[int] = None
     return out
 
 
-def index_state(w: Workload, names: Iterable[str]) -> Dict[str, Dict[str, np.ndarray]]:
+def index_state(w: Workload, names: Iterable[str], universe: Optional[Iterable[str]] = None
+                ) -> Dict[str, Dict[str, np.ndarray]]:
     """Index-coded global tensors: element bits = f(name, field, flat index),
-    unique within a tensor and different across tensors and fields."""
+    unique within a tensor and different across tensors and fields.  A
+    name's code depends on its place among ``universe`` (default: ``names``),
+    so processes that each build a subset agree when they pass the same
+    universe."""
     spl, _ = w.layouts()
     any_meta = {}
     for metas in spl.layout.values():
         any_meta.update(metas)
     dt = w.dtypes
     out = {}
-    for t_id, name in enumerate(sorted(set(names))):
+    ids = {n: i for i, n in enumerate(sorted(set(universe if universe is not None else names)))}
+    for name in sorted(set(names)):
+        t_id = ids[name]
         shape = tuple(int(s) for s in any_meta[name].shape)
         n = int(np.prod(shape))
         idx = np.arange(n, dtype=np.uint64).reshape(shape)

@@ -94,3 +94,32 @@ def test_bench_json_line(tmp_path):
     assert p["mismatched"] == 0 and p["tensors"] > 0, p
     assert set(p["routes"]) == {"gather_vs_pack_unpack", "execute_param_transfer",
                                 "execute_param_transfer_arena"}
+
+
+def test_handoff_closed_form_matches_the_oracle():
+    """bench.py's own closed form (which seeds the hand-off leg's old ranks
+    and checks its new ranks without the product's geometry) cuts the same
+    shard as the oracle's shard_of for every kind: row and column chunks,
+    head-granular fused QKV, and zero-padded vocabulary tables."""
+    import numpy as np
+    import torch
+
+    import bench
+    from oracle import reshard_oracle as O
+    from tests import cases
+    from tests.harness import to_ometa
+    ws = list(cases.golden_cases().values()) + list(cases.scaled_configs().values()) + \
+        cases.padded_vocab_cases()
+    kinds = set()
+    for w in ws:
+        spl, tpl = w.layouts()
+        for layout in (spl, tpl):
+            for metas in layout.layout.values():
+                for name, m in metas.items():
+                    shape = tuple(int(s) for s in m.shape)
+                    G = np.arange(int(np.prod(shape)), dtype=np.int64).reshape(shape)
+                    got = bench._expected_shard(torch.from_numpy(G), m).numpy()
+                    want = O.shard_of(G, to_ometa(m))
+                    assert got.shape == want.shape and (got == want).all(), (w.key, name, m.tp_meta)
+                    kinds.add(m.kind if m.tp_meta is not None else "replicated")
+    assert kinds == {"chunk", "qkv_heads", "vocab_pad", "replicated"}, kinds

@@ -123,14 +123,18 @@ def test_migration_api_matches_the_reference_signatures():
     from suika_amd import dummy_migration_IPC_state_dict
     save = inspect.signature(migration_save).parameters
     load = inspect.signature(migration_load).parameters
-    assert list(save) == ["IPC_queues", "model", "optimizer", "other_context", "device", "world", "log_func",
-                          "checkpoint_resume"]
-    assert list(load) == ["IPC_queues", "model", "optimizer", "device", "world", "log_func", "checkpoint_resume",
-                          "wait_for_release"]
-    assert load["wait_for_release"].kind is inspect.Parameter.KEYWORD_ONLY
-    for params in (save, load):
+    ref_save = ["IPC_queues", "model", "optimizer", "other_context", "device", "world", "log_func",
+                "checkpoint_resume"]
+    ref_load = ["IPC_queues", "model", "optimizer", "device", "world", "log_func", "checkpoint_resume"]
+    assert list(save) == ref_save + ["handoff_mode", "wave_bytes"]
+    assert list(load) == ref_load + ["wait_for_release", "return_before_release"]
+    for params, ref in ((save, ref_save), (load, ref_load)):
         for name in list(params)[2:]:
-            assert params[name].default is None, name
+            if name in ref:
+                assert params[name].default is None, name
+            else:
+                assert params[name].kind is inspect.Parameter.KEYWORD_ONLY, name
+    assert load["return_before_release"].default is False
     assert dummy_migration_IPC_state_dict == {"source_param_layout": None, "source_state_dict": {},
                                               "other_context_dict": {}}
 
