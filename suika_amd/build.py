@@ -22,6 +22,7 @@ import shutil
 import subprocess
 import sys
 from pathlib import Path
+from typing import Tuple
 
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
@@ -135,7 +136,70 @@ def build_host(verbose: bool = False, out: Path = HOST_LIB) -> Path:
     return out
 
 
+SANITIZE_DIR = REPO_DIR / "_build" / "sanitize"
+
+
+def _llvm() -> Path:
+    return Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "llvm"
+
+
+def sanitizer_runtime() -> Path:
+    """clang's shared AddressSanitizer runtime (it carries UBSan's handlers
+    too), which a sanitized build needs preloaded into the Python process."""
+    found = sorted(_llvm().glob("lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    if not found:
+        raise RuntimeError(f"no libclang_rt.asan-x86_64.so under {_llvm()}")
+    return found[-1]
+
+
+def build_sanitized(verbose: bool = False, out_dir: Path = SANITIZE_DIR) -> Tuple[Path, Path]:
+    """The library and the host extension with the host code under
+    AddressSanitizer and UndefinedBehaviorSanitizer, for CPU runs.
+
+    The library's host half (the plan builder, schedule.cpp, lower.cpp,
+    handoff.cpp, stage.cpp and the host side of reshard.hip) is compiled by
+    hipcc with each sanitizer flag behind ``-Xarch_host``, so the gfx950 code
+    is built as usual; host_bind.cpp is compiled by the same clang so both
+    use one sanitizer runtime (``sanitizer_runtime()``).  Both go to
+    ``out_dir`` (outside the package, never loaded unless named by
+    SUIKA_RESHARD_LIB / SUIKA_HOST_LIB)."""
+    import sysconfig
+
+    import torch
+    from torch.utils.cpp_extension import include_paths, library_paths
+    out_dir = Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    lib, host = out_dir / "libsuika_reshard.so", out_dir / "_suika_host.so"
+    san = ["-O1", "-g", "-fno-omit-frame-pointer", "-shared-libasan"]
+    flags = [f for f in HIPCC_FLAGS if f != "-O3"]
+    cmd = [hipcc_path(), *flags, *san, "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           f"-I{INCLUDE}", *map(str, SOURCES), "-o", str(lib)]
+    runs = [("sanitized library", cmd)]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    libdirs = library_paths()
+    runs.append(("sanitized host extension", [
+        str(_llvm() / "bin" / "clang++"), *san, "-fsanitize=address,undefined", "-std=c++17", "-fPIC", "-shared",
+        "-Wno-braced-scalar-init", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-DTORCH_EXTENSION_NAME=_suika_host", *[f"-I{p}" for p in include_paths()],
+        f"-I{sysconfig.get_paths()['include']}", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}", f"-I{HOST_SRC.parent}",
+        f"-I{Path(os.environ.get('ROCM_PATH', '/opt/rocm')) / 'include'}", str(HOST_SRC),
+        *[f"-L{p}" for p in libdirs], *[f"-Wl,-rpath,{p}" for p in libdirs],
+        "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-L{out_dir}", "-lsuika_reshard",
+        "-Wl,-rpath,$ORIGIN", "-o", str(host)]))
+    for what, c in runs:
+        if verbose:
+            print(" ".join(c), flush=True)
+        res = subprocess.run(c, capture_output=True, text=True)
+        if res.returncode != 0:
+            msgs = [l for l in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in l]
+            raise RuntimeError(f"{what} build failed:\n" + "\n".join(msgs)[-6000:])
+    return lib, host
+
+
 if __name__ == "__main__":
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))
+        sys.exit(0)
     print(build(verbose="-v" in sys.argv))
     print(build_host(verbose="-v" in sys.argv))
     print(build_c_check(verbose="-v" in sys.argv))

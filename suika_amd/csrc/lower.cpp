@@ -275,7 +275,8 @@ int lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops
   }
   struct PairHash {
     size_t operator()(const std::pair<int64_t, int64_t>& p) const {
-      return std::hash<int64_t>()(p.first * 1000003 ^ p.second);
+      // unsigned: corrupted ranks must not overflow a signed product
+      return std::hash<uint64_t>()(uint64_t(p.first) * 1000003u ^ uint64_t(p.second));
     }
   };
   std::unordered_map<std::pair<int64_t, int64_t>, int32_t, PairHash> src_base;   // (rank, name) -> slot
