@@ -242,6 +242,8 @@ def row_sweep(nbytes: int, steps: int) -> list:
         dst = (_lib.SrTensor * len(dst_shapes))(*[_lib.SrTensor(r, c, d, 0) for r, c, d in dst_shapes])
         if kind == _lib.SR_PIECE_COPY:
             recs = [_lib.SrPiece(kind, 0, si, di, -1, 0, r, c, 0, sc, 0, dc) for si, di, r, c, sc, dc in pieces]
+        elif kind == _lib.SR_PIECE_ZERO:   # (dst, rows, cols)
+            recs = [_lib.SrPiece(kind, 0, -1, di, -1, 0, r, c, 0, 0, 0, 0) for di, r, c in pieces]
         else:   # RECAST: (src, f32 dst or -1, bf16 dst2, rows, cols)
             recs = [_lib.SrPiece(kind, 0, si, di, d2, 0, r, c, 0, 0, 0, 0) for si, di, d2, r, c in pieces]
         pcs = (_lib.SrPiece * len(recs))(*recs)
@@ -268,6 +270,14 @@ def row_sweep(nbytes: int, steps: int) -> list:
         return e0.elapsed_time(e1) / steps
 
     out = []
+    # the write-only ceiling through the library's own store path: one
+    # ZERO piece (the zero fill of padded vocabulary rows) over ``nbytes``
+    r, c = nbytes // 4 // 4096, 4096
+    ms = run([], [(r, c)], [(0, r, c)], kind=_lib.SR_PIECE_ZERO)
+    print(f"[bench] row sweep zero fill: {ms:.3f} ms", file=sys.stderr, flush=True)
+    out.append({"pattern": "zero_fill", "row_bytes": None, "rows": r, "bytes_moved": r * c * 4,
+                "ms": round(ms, 4), "GBps": round(r * c * 4 / (ms * 1e-3) / 1e9, 1),
+                "pct_of_peak": round(100 * r * c * 4 / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 2)})
     # the fused fp32 -> bf16 recast of unpack, contiguous: f32 + bf16 copies
     # (4 bytes read, 6 written per element) and the bf16 copy alone (4 read, 2
     # written), each reading ``nbytes``
@@ -758,6 +768,23 @@ def _handoff_new(rank, key, port, queues, events, opts):
             dist.destroy_process_group()
 
 
+def _settle_device(limit_s: float = 30.0) -> float:
+    """Wait until the device's free memory stops rising (an earlier run's
+    processes may still be returning theirs: allocations from memory in
+    that state were 20-30x slower) and return the seconds waited."""
+    import torch
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    last = torch.cuda.mem_get_info()[0]
+    while time.time() - t0 < limit_s:
+        time.sleep(0.5)
+        free = torch.cuda.mem_get_info()[0]
+        if free <= last + (64 << 20):
+            break
+        last = free
+    return time.time() - t0
+
+
 def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None, mode=None, wave_bytes=None,
                 squeeze=None, return_before_release=False) -> dict:
     """Live migration of workload ``key`` between processes on this GPU: the
@@ -807,6 +834,7 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None, mode=
 
     procs = []
     held = {}
+    settled = _settle_device()
     try:
         p_old, p_new = port(), port()
         for r in range(old_ws):
@@ -872,6 +900,7 @@ def handoff_leg(key: str, timeout_s: float = 600.0, wait_for_release=None, mode=
                             "old rank has released its state and the hand-off allocations (its return from "
                             "migration_save); both from the handshake"),
         "return_before_release": bool(return_before_release),
+        "device_settle_s": round(settled, 2),
     }
     if whole:
         # the old state's release once the new world has mapped the hand-off

@@ -74,15 +74,6 @@ def vocab_pad_rows(V: int, deg: int, multiple: int) -> int:
     return int(math.ceil(V / (multiple * deg))) * multiple * deg
 
 
-def axis_of(m: OMeta) -> Optional[int]:
-    """0: dim 0 is split; 1: the last dim is split; None: replicated."""
-    if m.tp is None:
-        return None
-    nd = len(m.shape)
-    d = m.tp[0] % nd
-    return 0 if d == 0 else 1
-
-
 def actual_shape(m: OMeta) -> Tuple[int, ...]:
     """Shard shape (migration.py:92-98; vocab_pad: padded rows / deg)."""
     s = list(m.shape)
@@ -224,14 +215,6 @@ def chunk(a: np.ndarray, chunks: int, axis: int) -> List[np.ndarray]:
 
 def cat(parts: Sequence[np.ndarray], axis: int) -> np.ndarray:
     return np.concatenate(parts, axis=axis)
-
-
-def _to_matrix(a: np.ndarray, view: int) -> np.ndarray:
-    if a.ndim == 0:
-        return a.reshape(1, 1)
-    if view == 1:
-        return a.reshape(-1, a.shape[-1])
-    return a.reshape(a.shape[0], -1)
 
 
 def get_send(op: OOp, src: np.ndarray) -> np.ndarray:

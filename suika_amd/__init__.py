@@ -18,7 +18,7 @@ from .migration import (cuda_gc, execute_param_transfer, forcefully_free_tensor,
 from .plan import PlanOptions, ReshardPlan, SlotSpec
 from ._lib import PlanError, ReshardError
 from .checkpoint import checkpoint_load, checkpoint_save, migration_load, migration_save
-from .handoff import dummy_migration_IPC_state_dict
+from .handoff import HandoffError, dummy_migration_IPC_state_dict
 
 __all__ = [
     "CHUNK", "QKV_HEADS", "VOCAB_PAD", "ParamLayout", "TensorMeta", "TransferOp",
@@ -27,5 +27,5 @@ __all__ = [
     "merge_model_and_optimizer_state_dict", "schedule_and_execute_param_transfer",
     "split_model_and_optimizer_state_dict", "PlanOptions", "ReshardPlan", "SlotSpec",
     "PlanError", "ReshardError", "checkpoint_save", "checkpoint_load", "migration_save",
-    "migration_load", "forcefully_free_tensor", "cuda_gc", "dummy_migration_IPC_state_dict",
+    "migration_load", "forcefully_free_tensor", "cuda_gc", "dummy_migration_IPC_state_dict", "HandoffError",
 ]

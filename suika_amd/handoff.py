@@ -554,7 +554,9 @@ class _OldWorld:
         try:
             for k, names in enumerate(waves):
                 part = {n: state[n] for n in names if n in state}
+                t0 = time.perf_counter()
                 handoff, err = _attempt(lambda: Handoff(part, self.device, self.rank))
+                t1 = time.perf_counter()
                 self.low.sample()
                 if handoff is not None:
                     packed += handoff.bytes
@@ -571,10 +573,15 @@ class _OldWorld:
                 # the wave's sources are in the hand-off: their memory goes back
                 # to the device for the next wave and the new world's arenas
                 del part
+                t2 = time.perf_counter()
                 _, pending_err = _attempt(lambda: _release_state(state, names))
+                t3 = time.perf_counter()
                 if len(held) > 1:
                     consumed(held[0][0])
                     held.pop(0)[1].release()
+                self.log(f"migration_save: wave {k}: {handoff.bytes / 1e9:.3f} GB packed in {(t1 - t0) * 1e3:.2f} ms, "
+                         f"sent {(t2 - t1) * 1e3:.2f} ms later, sources released in {(t3 - t2) * 1e3:.2f} ms, "
+                         f"then {(time.perf_counter() - t3) * 1e3:.2f} ms for the previous wave's report")
             while held:
                 consumed(held[0][0])
                 held.pop(0)[1].release()
@@ -685,8 +692,8 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
     log_func("migration_save: end")
 
 
-class _WarmUp(threading.Thread):
-    """First-use costs of a fresh process of a migration, paid on a thread
+class _WarmUp:
+    """First-use costs of a fresh process of a migration, paid on threads
     while it waits: in a live migration the old ranks for the new world's
     handshake and the new ranks for the old world's message; in
     ``checkpoint_load`` while the files are read:
@@ -696,21 +703,40 @@ class _WarmUp(threading.Thread):
       the drop-in call's host side.  With twelve processes on one MI355X
       these took 30-57 ms per first launch, 40-54 ms per first table upload
       and 26 ms for the setup stream, inside the pack and the reshard;
-    * with an optimizer to build, torch.optim's: a process's first optimizer
-      imports torch's compiler front end (torch._dynamo, about 0.4 s).
+    * with an optimizer to build, torch.optim's, on a thread of its own (it
+      needs no device): a process's first optimizer imports torch's compiler
+      front end (torch._dynamo, about 0.4 s).
 
-    ``library_done`` is set once the library is no longer in use here; the
-    caller waits for it before its own library calls and joins the thread
-    before building its optimizer.  Failures are ignored: the real calls
-    report their own."""
+    ``start`` runs both beside the caller, ``run`` one after the other on the
+    calling thread.  ``library_done`` is set once the library is no longer
+    in use here; the caller waits for it before its own library calls and
+    joins before building its optimizer.  Failures are ignored: the real
+    calls report their own."""
 
     def __init__(self, device: torch.device, optimizer: bool):
-        super().__init__(name="suika-warm-up", daemon=True)
         self.device = device
         self.optimizer = optimizer
         self.library_done = threading.Event()
+        self._threads: List[threading.Thread] = []
+
+    def start(self) -> None:
+        self._threads = [threading.Thread(target=self._library, name="suika-warm-up", daemon=True)]
+        if self.optimizer:
+            self._threads.append(threading.Thread(target=self._optimizer, name="suika-warm-up-optim",
+                                                  daemon=True))
+        for t in self._threads:
+            t.start()
+
+    def join(self) -> None:
+        for t in self._threads:
+            t.join()
 
     def run(self) -> None:
+        self._library()
+        if self.optimizer:
+            self._optimizer()
+
+    def _library(self) -> None:
         try:
             from .meta import TensorMeta, TransferOp
             from .migration import execute_param_transfer
@@ -726,11 +752,13 @@ class _WarmUp(threading.Thread):
             pass
         finally:
             self.library_done.set()
-        if self.optimizer:
-            try:
-                torch.optim.SGD([torch.nn.Parameter(torch.zeros(1))], lr=0.0)
-            except Exception:
-                pass
+
+    @staticmethod
+    def _optimizer() -> None:
+        try:
+            torch.optim.SGD([torch.nn.Parameter(torch.zeros(1))], lr=0.0)
+        except Exception:
+            pass
 
 
 def _destination_bytes(ops, rank: int, records: Sequence[Dict[str, Any]]) -> int:
@@ -752,6 +780,36 @@ def _destination_bytes(ops, rank: int, records: Sequence[Dict[str, Any]]) -> int
     return sum(per_name.values())
 
 
+class _Closing:
+    """A whole hand-off's mappings, closed on a thread while the new rank
+    adopts its state; ``finish`` joins it, agrees on every rank's errors
+    (reshard, close, adoption) and has new rank 0 send ``DONE``."""
+
+    def __init__(self, side: "_NewWorld", mapped: "MappedSources", err: Optional[str]):
+        self.side = side
+        self.err = err
+        self.t0 = time.perf_counter()
+        self.t_closed = self.t0
+
+        def close():
+            try:
+                mapped.close()
+            except Exception as e:
+                self.err = self.err or f"closing the hand-off: {type(e).__name__}: {e}"
+            self.t_closed = time.perf_counter()
+        self.thread = threading.Thread(target=close, name="suika-handoff-close", daemon=True)
+        self.thread.start()
+
+    def finish(self, err: Optional[str]) -> None:
+        self.thread.join()
+        t = time.perf_counter()
+        _agree(self.side.world, self.err or err, "resharding from the hand-off and adopting the state")
+        if self.side.rank == 0:
+            self.side.q[1].put(DONE)
+        self.side.log(f"migration_load: mappings closed in {(self.t_closed - self.t0) * 1e3:.2f} ms, "
+                      f"every new rank done {(time.perf_counter() - t) * 1e3:.2f} ms after this one")
+
+
 class _NewWorld:
     """The new side's half of the protocol once the first message is in."""
 
@@ -766,13 +824,16 @@ class _NewWorld:
         self.warm = warm
         self.log = log_func
         self.low = _LowWater(device)
+        self.phases = (0.0, 0.0, 0.0)
 
     def _reshard(self, ops, records, needed) -> Dict[str, Dict[str, Tensor]]:
         """``ops``' pieces for this rank, gathered from the mapped records of
         the old ranks ``needed`` into one arena; the mappings are closed
         before it returns or raises."""
         from .migration import execute_param_transfer
+        t0 = time.perf_counter()
         mapped = MappedSources(records, needed, self.device)
+        t1 = time.perf_counter()
         try:
             out = execute_param_transfer(
                 transfer_ops=ops, source_state_dict={}, device=self.device, expected_sub_fields=self.fields,
@@ -780,9 +841,11 @@ class _NewWorld:
                 arena=True)
             torch.cuda.synchronize(self.device)
             self.low.sample()
-            return out
         finally:
+            t2 = time.perf_counter()
             mapped.close()
+            self.phases = (t1 - t0, t2 - t1, time.perf_counter() - t2)
+        return out
 
     def whole(self, wait_for_release: Optional[bool], return_before_release: bool):
         """Returns the target state and whether the caller still waits for
@@ -845,17 +908,17 @@ class _NewWorld:
                 return out
             target, err = _attempt(reshard)
             t2 = time.perf_counter()
-        finally:
+        except BaseException:
             if mapped is not None:
                 mapped.close()
-        _agree(self.world, err, "resharding from the hand-off")
-        if rank == 0:
-            self.q[1].put(DONE)
+            raise
         self.log("migration_load: "
                  + ("" if wait else f"destinations' memory taken in {(t_alloc - t0) * 1e3:.2f} ms, ")
                  + f"mapped {len(needed)} old rank(s) in {(t_map - t_alloc) * 1e3:.2f} ms, "
                  f"resharded in {(t2 - t1) * 1e3:.2f} ms")
-        return target, await_release and not wait
+        # The mappings are closed beside the adoption; the old world hears
+        # DONE once every new rank has closed them (``finish``).
+        return target, await_release and not wait, _Closing(self, mapped, err)
 
     def waves(self, n: int):
         target: Dict[str, Dict[str, Tensor]] = {}
@@ -873,8 +936,12 @@ class _NewWorld:
                 self.warm.library_done.wait()
             t0 = time.perf_counter()
             out, err = _attempt(lambda: self._reshard(ops, records, needed) if mine else {})
-            gather_ms += (time.perf_counter() - t0) * 1e3
+            t1 = time.perf_counter()
+            gather_ms += (t1 - t0) * 1e3
             _agree(self.world, err, f"resharding wave {k}")
+            self.log(f"migration_load: wave {k}: mapped, resharded and closed in {(t1 - t0) * 1e3:.2f} ms "
+                     f"({' / '.join(f'{x * 1e3:.2f}' for x in self.phases)}), "
+                     f"every new rank done {(time.perf_counter() - t1) * 1e3:.2f} ms later")
             target.update(out)
             if rank == 0:
                 self.q[1].put(("consumed", k))
@@ -946,12 +1013,11 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
     log_func(f"migration_load: scheduled in {(time.perf_counter() - t0) * 1e3:.2f} ms")
     side = _NewWorld(IPC_queues, world, device, ops, other_context_dict, warm, log_func)
     try:
+        closing = None
         if order == "whole":
-            target_state_dict, await_release = side.whole(wait_for_release, return_before_release)
+            target_state_dict, await_release, closing = side.whole(wait_for_release, return_before_release)
         else:
             target_state_dict, await_release = side.waves(int(order)), False
-        dist.barrier(world)
-        log_func("migration_load: every new rank has resharded")
 
         def adopt():
             model_state_dict, optimizer_state_dict, other_context = split_model_and_optimizer_state_dict(
@@ -960,16 +1026,21 @@ def live_load(IPC_queues, model, optimizer_provider, optimizer, device: torch.de
             model.load_state_dict(model_state_dict, assign=True)
             log_func("migration_load: model state adopted")
             warm.join()
+            log_func("migration_load: first-use warm-up joined")
             opt = optimizer_provider() if optimizer_provider else optimizer
             if opt:
                 # one parameter group, as the reference (migration.py:1712-1716)
                 optimizer_state_dict["param_groups"][0]["params"] = opt.state_dict()["param_groups"][0]["params"]
                 opt.load_state_dict(optimizer_state_dict)
+                log_func("migration_load: optimizer state loaded")
             return opt, other_context
-        got, err = _attempt(adopt)
-        # the old world is done with this one: failures from here on are
-        # this world's alone
-        _agree(world, err, "adopting the new state", notify=False)
+        if closing is not None:
+            got, err = _attempt(adopt) if closing.err is None else (None, None)
+            closing.finish(err)
+        else:
+            got, err = _attempt(adopt)
+            # every wave is consumed: failures from here on are this world's alone
+            _agree(world, err, "adopting the new state", notify=False)
         optimizer, other_context = got
         if await_release:
             # the old world's state released (beside which the destinations
