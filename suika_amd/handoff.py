@@ -128,6 +128,9 @@ ARENA_SLACK_BYTES = 64 << 20
 # Per process of either world, left out of the memory the waves may use:
 # the same per-process costs at the granularity one wave adds them.
 RESERVE_BYTES = 96 << 20
+# Waves reuse two hand-off slots allocated once (the ring) when they fit;
+# False gives every wave allocations of its own.
+USE_RING = True
 
 
 class HandoffError(RuntimeError):
@@ -166,6 +169,56 @@ def _dtype_of(name: str) -> torch.dtype:
     return dt
 
 
+def _moved(state: Dict[str, Dict[str, Any]], device: torch.device):
+    """(name, field, tensor) of every non-empty tensor on ``device``, in
+    order, and every other value as (name, field, value)."""
+    moved: List[Tuple[str, str, Tensor]] = []
+    other: List[Tuple[str, str, Any]] = []
+    for name, entry in state.items():
+        for f, t in entry.items():
+            if isinstance(t, Tensor) and t.is_cuda and t.device == device and t.numel() > 0:
+                moved.append((name, f, t))
+            else:
+                other.append((name, f, t))
+    return moved, other
+
+
+def layout_of(state: Dict[str, Dict[str, Any]], device: torch.device,
+              chunk_bytes: int = CHUNK_BYTES) -> List[int]:
+    """The chunk sizes ``Handoff`` packs ``state`` into."""
+    moved, _ = _moved(state, device)
+    return pack_layout([t.numel() * t.element_size() for _, _, t in moved], chunk_bytes)[1]
+
+
+class Slot:
+    """Exported device allocations of given sizes that several hand-offs
+    pack into one after the other (the waves' ring); ``free`` releases
+    them."""
+
+    def __init__(self, sizes: Sequence[int], device: torch.device):
+        L = self._L = _lib.lib()
+        self.device = device
+        self.chunks: List[Tuple[bytes, int]] = []
+        self.ptrs: List[int] = []
+        try:
+            with torch.cuda.device(device):
+                for n in sizes:
+                    ptr, handle = ctypes.c_void_p(), _lib.SrIpcHandle()
+                    _lib.check(L.sr_handoff_alloc(n, ctypes.byref(ptr), ctypes.byref(handle)), "sr_handoff_alloc", L)
+                    self.ptrs.append(ptr.value)
+                    self.chunks.append((bytes(handle.bytes), n))
+        except BaseException:
+            self.free()
+            raise
+
+    def free(self) -> None:
+        L = self._L
+        with torch.cuda.device(self.device):
+            while self.ptrs:
+                _lib.check(L.sr_handoff_free(ctypes.c_void_p(self.ptrs.pop())), "sr_handoff_free", L)
+        self.chunks = []
+
+
 class Handoff:
     """An old rank's merged state packed into exported device allocations.
 
@@ -173,31 +226,39 @@ class Handoff:
     ``device`` are packed, in order, at 256-byte aligned offsets into
     allocations of at most ``chunk_bytes`` (a larger tensor gets one of its
     own); every other value (CPU tensors such as AdamW's ``step``, empty
-    tensors) rides along in the record as a CPU tensor.  The copies are done
-    when the constructor returns.
+    tensors) rides along in the record as a CPU tensor.  With ``slot`` the
+    tensors go into that slot's allocations (each chunk at least as large as
+    this state's layout needs), which the hand-off does not own; otherwise
+    it allocates its own.  The copies are done when the constructor
+    returns.
     """
 
     def __init__(self, state: Dict[str, Dict[str, Tensor]], device: torch.device, rank: int,
-                 chunk_bytes: int = CHUNK_BYTES):
+                 chunk_bytes: int = CHUNK_BYTES, slot: Optional[Slot] = None):
         L = self._L = _lib.lib()
         self.rank = rank
         self.device = device
         self._ptrs: List[int] = []
-        moved: List[Tuple[str, str, Tensor]] = []
         self.tensors: Dict[str, Dict[str, tuple]] = {}
         self.host: Dict[str, Dict[str, Tensor]] = {}
-        for name, entry in state.items():
-            for f, t in entry.items():
-                if not (isinstance(t, Tensor) and t.is_cuda and t.device == device and t.numel() > 0):
-                    self.host.setdefault(name, {})[f] = t.detach().cpu() if isinstance(t, Tensor) else t
-                    continue
-                assert t.is_contiguous(), f"handoff: {name}/{f} is not contiguous"
-                moved.append((name, f, t))
+        moved, other = _moved(state, device)
+        for name, f, t in other:
+            self.host.setdefault(name, {})[f] = t.detach().cpu() if isinstance(t, Tensor) else t
+        for name, f, t in moved:
+            assert t.is_contiguous(), f"handoff: {name}/{f} is not contiguous"
         where, sizes = pack_layout([t.numel() * t.element_size() for _, _, t in moved], chunk_bytes)
         packed = [(name, f, t, c, off) for (name, f, t), (c, off) in zip(moved, where)]
         for name, f, t, c, off in packed:
             self.tensors.setdefault(name, {})[f] = (c, off, tuple(t.shape), str(t.dtype))
         self.chunks: List[Tuple[bytes, int]] = []
+        if slot is not None:
+            assert len(sizes) <= len(slot.chunks) and all(n <= cap for n, (_, cap) in zip(sizes, slot.chunks)), \
+                f"handoff: chunks of {sizes} bytes do not fit the slot's {[cap for _, cap in slot.chunks]}"
+            self.chunks = list(slot.chunks)
+            if packed:
+                self._pack(packed, sizes, slot.ptrs)
+            self.bytes = sum(sizes)
+            return
         try:
             with torch.cuda.device(device):
                 for n in sizes:
@@ -206,13 +267,13 @@ class Handoff:
                     self._ptrs.append(ptr.value)
                     self.chunks.append((bytes(handle.bytes), n))
                 if packed:
-                    self._pack(packed, sizes)
+                    self._pack(packed, sizes, self._ptrs)
         except BaseException:
             self.release()
             raise
         self.bytes = sum(sizes)
 
-    def _pack(self, packed, sizes) -> None:
+    def _pack(self, packed, sizes, ptrs) -> None:
         """One gather launch: every tensor, as bytes, to its chunk offset."""
         import numpy as np
         L = self._L
@@ -233,7 +294,7 @@ class Handoff:
         try:
             vp = ctypes.c_void_p
             sp = (vp * len(packed))(*[t.data_ptr() for _, _, t, _, _ in packed])
-            dp = (vp * len(sizes))(*self._ptrs)
+            dp = (vp * len(sizes))(*ptrs[:len(sizes)])
             stream = torch.cuda.current_stream(self.device)
             _lib.check(L.sr_gather(plan, sp, dp, vp(stream.cuda_stream)), "handoff pack: sr_gather", L)
             stream.synchronize()
@@ -246,20 +307,56 @@ class Handoff:
                 "tensors": self.tensors, "host": self.host}
 
     def release(self) -> None:
-        """Free the allocations (after every new rank has closed them)."""
+        """Free the allocations it owns (after every new rank has closed
+        them); a slot's are the slot's to free."""
         L = self._L
         with torch.cuda.device(self.device):
             while self._ptrs:
                 _lib.check(L.sr_handoff_free(ctypes.c_void_p(self._ptrs.pop())), "sr_handoff_free", L)
 
 
+def _open(L, handle: bytes) -> int:
+    h = _lib.SrIpcHandle()
+    ctypes.memmove(h.bytes, handle, len(handle))
+    ptr = ctypes.c_void_p()
+    _lib.check(L.sr_handoff_open(ctypes.byref(h), ctypes.byref(ptr)), "sr_handoff_open", L)
+    return ptr.value
+
+
+class Mappings:
+    """Hand-off allocations mapped into this process once each, by handle,
+    for the waves' ring (its slots come back wave after wave); ``close``
+    unmaps them all once no view of them is left."""
+
+    def __init__(self, device: torch.device):
+        self._L = _lib.lib()
+        self.device = device
+        self._bases: Dict[bytes, int] = {}
+
+    def open(self, handle: bytes) -> int:
+        base = self._bases.get(handle)
+        if base is None:
+            base = self._bases[handle] = _open(self._L, handle)
+        return base
+
+    def close(self) -> None:
+        L = self._L
+        with torch.cuda.device(self.device):
+            while self._bases:
+                _, base = self._bases.popitem()
+                _lib.check(L.sr_handoff_close(ctypes.c_void_p(base)), "sr_handoff_close", L)
+
+
 class MappedSources:
     """Old ranks' packed state mapped into this process: ``states`` is
     ``{old rank: {name: {field: tensor}}}``, tensors viewing the mapped
-    allocations (no copy); CPU values of the records ride along.  ``close``
-    unmaps them; the views must be dropped first."""
+    allocations (no copy); CPU values of the records ride along.  Only the
+    chunks a tensor lies in are mapped, through ``cache`` when given (which
+    then keeps them mapped).  ``close`` drops the views and unmaps what it
+    mapped itself."""
 
-    def __init__(self, records: Sequence[Dict[str, Any]], ranks: Sequence[int], device: torch.device):
+    def __init__(self, records: Sequence[Dict[str, Any]], ranks: Sequence[int], device: torch.device,
+                 cache: Optional["Mappings"] = None):
         L = self._L = _lib.lib()
         self.device = device
         self._opened: List[int] = []
@@ -273,15 +370,17 @@ class MappedSources:
                     assert rec["device"] == device.index, \
                         f"rank {r}'s state is on cuda:{rec['device']}, this rank runs on {device}"
                     bases = []
-                    for handle, _ in rec["chunks"]:
-                        h = _lib.SrIpcHandle()
-                        ctypes.memmove(h.bytes, handle, len(handle))
-                        ptr = ctypes.c_void_p()
-                        _lib.check(L.sr_handoff_open(ctypes.byref(h), ctypes.byref(ptr)), "sr_handoff_open", L)
-                        self._opened.append(ptr.value)
-                        bases.append(ptr.value)
-                    state: Dict[str, Dict[str, Tensor]] = {}
                     keys = [(n, f) for n, e in rec["tensors"].items() for f in e]
+                    used = {rec["tensors"][n][f][0] for n, f in keys}
+                    for c, (handle, _) in enumerate(rec["chunks"]):
+                        if c not in used:
+                            bases.append(None)
+                        elif cache is not None:
+                            bases.append(cache.open(handle))
+                        else:
+                            bases.append(_open(L, handle))
+                            self._opened.append(bases[-1])
+                    state: Dict[str, Dict[str, Tensor]] = {}
                     per_chunk: Dict[int, List[Tuple[str, str]]] = {}
                     for n, f in keys:
                         per_chunk.setdefault(rec["tensors"][n][f][0], []).append((n, f))
@@ -540,8 +639,43 @@ class _OldWorld:
             if handoff is not None:
                 handoff.release()
 
-    def waves(self, state, param_layout, other_context_dict, waves: List[List[str]]) -> None:
+    def _ring(self, state, waves: List[List[str]], budget: int) -> List[Slot]:
+        """The waves' two hand-off slots, each chunk as large as this rank's
+        largest wave needs it, allocated once -- when every old rank's slots
+        together fit in ``budget`` bytes; else none (each wave then
+        allocates its own hand-off).  Allocations of memory another process
+        has just freed are slow, and so is mapping them: the new ranks map
+        the two slots once instead of every wave's allocations."""
+        if not USE_RING:
+            return []
+        layouts = [layout_of({n: state[n] for n in names if n in state}, self.device) for names in waves]
+        width = max((len(lay) for lay in layouts), default=0)
+        sizes = [max(lay[c] for lay in layouts if c < len(lay)) for c in range(width)]
+        totals: List[Any] = [None] * dist.get_world_size(self.world)
+        dist.all_gather_object(totals, 2 * sum(sizes), group=self.world)
+        if sum(totals) > budget:
+            self.log(f"migration_save: a ring of {sum(totals) / 1e9:.3f} GB does not fit "
+                     f"{budget / 1e9:.3f} GB: one hand-off per wave")
+            return []
+        ring: List[Slot] = []
+
+        def make():
+            for _ in range(2):
+                ring.append(Slot(sizes, self.device))
+        _, err = _attempt(make)
+        try:
+            _agree(self.world, err, "allocating the waves' ring")
+        except HandoffError:
+            for slot in ring:
+                slot.free()
+            raise
+        self.log(f"migration_save: ring of 2 x {sum(sizes) / 1e9:.3f} GB on this rank, "
+                 f"{sum(totals) / 1e9:.3f} GB in all")
+        return ring
+
+    def waves(self, state, param_layout, other_context_dict, waves: List[List[str]], ring_budget: int) -> None:
         self.send_first(param_layout, other_context_dict, len(waves))
+        ring = self._ring(state, waves, ring_budget)
         held: List[Tuple[int, Handoff]] = []     # sent, not yet reported consumed
         pending_err: Optional[str] = None
         t_start = time.perf_counter()
@@ -554,8 +688,11 @@ class _OldWorld:
         try:
             for k, names in enumerate(waves):
                 part = {n: state[n] for n in names if n in state}
+                # a ring slot is free again: the wave that used it (k - 2)
+                # was reported consumed before wave k - 1's report was awaited
+                slot = ring[k % 2] if ring else None
                 t0 = time.perf_counter()
-                handoff, err = _attempt(lambda: Handoff(part, self.device, self.rank))
+                handoff, err = _attempt(lambda: Handoff(part, self.device, self.rank, slot=slot))
                 t1 = time.perf_counter()
                 self.low.sample()
                 if handoff is not None:
@@ -568,19 +705,21 @@ class _OldWorld:
                     raise
                 records = self._records(handoff)
                 held.append((k, handoff))
-                if self.rank == 0:
-                    self.q[0].put(("wave", k, list(names), records))
                 # the wave's sources are in the hand-off: their memory goes back
-                # to the device for the next wave and the new world's arenas
+                # to the device for the next wave and the new world's arenas,
+                # before the new world hears of the wave (so its arena never
+                # sits beside these sources)
                 del part
                 t2 = time.perf_counter()
                 _, pending_err = _attempt(lambda: _release_state(state, names))
                 t3 = time.perf_counter()
+                if self.rank == 0:
+                    self.q[0].put(("wave", k, list(names), records, bool(ring)))
                 if len(held) > 1:
                     consumed(held[0][0])
                     held.pop(0)[1].release()
                 self.log(f"migration_save: wave {k}: {handoff.bytes / 1e9:.3f} GB packed in {(t1 - t0) * 1e3:.2f} ms, "
-                         f"sent {(t2 - t1) * 1e3:.2f} ms later, sources released in {(t3 - t2) * 1e3:.2f} ms, "
+                         f"sources released in {(t3 - t2) * 1e3:.2f} ms and the wave sent, "
                          f"then {(time.perf_counter() - t3) * 1e3:.2f} ms for the previous wave's report")
             while held:
                 consumed(held[0][0])
@@ -601,6 +740,8 @@ class _OldWorld:
         finally:
             for _, h in held:
                 h.release()
+            for slot in ring:
+                slot.free()
         self.log(f"migration_save: {packed / 1e9:.3f} GB handed off in {len(waves)} wave(s) in "
                  f"{(time.perf_counter() - t_start) * 1e3:.2f} ms")
 
@@ -677,12 +818,17 @@ def live_save(IPC_queues, model, optimizer, other_context, device: torch.device,
         if err is not None:
             raise HandoffError(f"migration_save: {err}")
         how, w = order
+        room = free - RESERVE_BYTES * (dist.get_world_size(world) + new_world_size)
         log_func(f"migration_save: {state_bytes / 1e9:.3f} GB on the device, {free / 1e9:.3f} GB free: hand-off "
                  + ("whole" if how == "whole" else f"in waves of at most {w / 1e9:.3f} GB"))
         if how == "whole":
             side.whole(source_state_dict, param_layout, other_context_dict)
         else:
-            side.waves(source_state_dict, param_layout, other_context_dict, plan_waves(per_rank, w))
+            # Each wave's sources are freed before the new world hears of the
+            # wave, so the device holds the state plus the hand-off memory:
+            # the ring may take all the room
+            side.waves(source_state_dict, param_layout, other_context_dict, plan_waves(per_rank, w),
+                       ring_budget=max(2 * w, room))
     except HandoffError as e:
         if e.notify:
             side.notify(str(e))
@@ -826,13 +972,14 @@ class _NewWorld:
         self.low = _LowWater(device)
         self.phases = (0.0, 0.0, 0.0)
 
-    def _reshard(self, ops, records, needed) -> Dict[str, Dict[str, Tensor]]:
+    def _reshard(self, ops, records, needed, cache: Optional[Mappings] = None) -> Dict[str, Dict[str, Tensor]]:
         """``ops``' pieces for this rank, gathered from the mapped records of
         the old ranks ``needed`` into one arena; the mappings are closed
-        before it returns or raises."""
+        (or, through ``cache``, kept for the next wave) before it returns or
+        raises."""
         from .migration import execute_param_transfer
         t0 = time.perf_counter()
-        mapped = MappedSources(records, needed, self.device)
+        mapped = MappedSources(records, needed, self.device, cache=cache)
         t1 = time.perf_counter()
         try:
             out = execute_param_transfer(
@@ -925,26 +1072,37 @@ class _NewWorld:
         rank = self.rank
         t_start = time.perf_counter()
         gather_ms = 0.0
-        for k in range(n):
-            msg = _recv_on_rank0(self.q[0], f"wave {k}", self.world)
-            assert isinstance(msg, tuple) and msg[:2] == ("wave", k), f"migration_load: unexpected message {msg!r}"
-            names, records = set(msg[2]), msg[3]
-            ops = [op for op in self.ops if op.param_name in names]
-            mine = [op for op in ops if op.dst_rank == rank]
-            needed = sorted({op.src_rank for op in mine})
-            if k == 0:
-                self.warm.library_done.wait()
-            t0 = time.perf_counter()
-            out, err = _attempt(lambda: self._reshard(ops, records, needed) if mine else {})
-            t1 = time.perf_counter()
-            gather_ms += (t1 - t0) * 1e3
-            _agree(self.world, err, f"resharding wave {k}")
-            self.log(f"migration_load: wave {k}: mapped, resharded and closed in {(t1 - t0) * 1e3:.2f} ms "
-                     f"({' / '.join(f'{x * 1e3:.2f}' for x in self.phases)}), "
-                     f"every new rank done {(time.perf_counter() - t1) * 1e3:.2f} ms later")
-            target.update(out)
-            if rank == 0:
-                self.q[1].put(("consumed", k))
+        # the old ranks' ring slots, mapped once each and closed before the
+        # last wave is reported consumed (or before an error is reported)
+        cache = Mappings(self.device)
+        try:
+            for k in range(n):
+                msg = _recv_on_rank0(self.q[0], f"wave {k}", self.world)
+                assert isinstance(msg, tuple) and msg[:2] == ("wave", k), \
+                    f"migration_load: unexpected message {msg!r}"
+                names, records, ring = set(msg[2]), msg[3], msg[4]
+                ops = [op for op in self.ops if op.param_name in names]
+                mine = [op for op in ops if op.dst_rank == rank]
+                needed = sorted({op.src_rank for op in mine})
+                if k == 0:
+                    self.warm.library_done.wait()
+                t0 = time.perf_counter()
+                out, err = _attempt(lambda: self._reshard(ops, records, needed, cache if ring else None)
+                                    if mine else {})
+                t1 = time.perf_counter()
+                gather_ms += (t1 - t0) * 1e3
+                if k == n - 1:
+                    _, close_err = _attempt(cache.close)
+                    err = err or close_err
+                _agree(self.world, err, f"resharding wave {k}")
+                self.log(f"migration_load: wave {k}: mapped, resharded and closed in {(t1 - t0) * 1e3:.2f} ms "
+                         f"({' / '.join(f'{x * 1e3:.2f}' for x in self.phases)}), "
+                         f"every new rank done {(time.perf_counter() - t1) * 1e3:.2f} ms later")
+                target.update(out)
+                if rank == 0:
+                    self.q[1].put(("consumed", k))
+        finally:
+            _attempt(cache.close)   # a no-op once closed; on a failure the caller reports it
         self.log(f"migration_load: destinations of {n} wave(s) resharded in {gather_ms:.2f} ms of "
                  f"{(time.perf_counter() - t_start) * 1e3:.2f} ms")
         return target

@@ -12,6 +12,7 @@ against the oracle's closed form of the same global tensors, bit for bit.
 ``opts`` (a dict) varies a run:
 * ``wait_for_release`` / ``return_before_release``: passed to migration_load;
 * ``mode`` / ``wave_bytes``: the hand-off order, passed to migration_save;
+  ``ring=False`` gives every wave hand-off allocations of its own;
 * ``spec``: a ModelSpec replacing the small default model, whose global
   tensors are then index-coded (cheap to build at a larger size);
 * ``gate``: an event both worlds wait for after reporting ready (the new
@@ -144,6 +145,9 @@ def old_rank(rank, world, port, queues, old, new, events, opts=None):
         del glob
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+        if opts.get("ring") is False:
+            from suika_amd import handoff as H
+            H.USE_RING = False
         _force(opts, "old", rank)
         events.put(("ready", rank, None))
         _wait_gate(opts)

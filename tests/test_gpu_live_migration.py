@@ -20,7 +20,8 @@ last case:
 * the destinations wait for the old world's release (``WANT_RELEASED`` /
   ``RELEASED``);
 * the new world returns without waiting for that release;
-* the hand-off forced into many small waves;
+* the hand-off forced into many small waves, through the two-slot ring and
+  with allocations of every wave's own;
 * a larger state while this process holds device memory so that less than
   the state itself is free: the old world picks waves, and the device's
   low-water free memory, as every rank logged it, shows at most two waves
@@ -173,17 +174,20 @@ def test_live_migration_returning_before_release():
         assert res[("saved", r)][-1] == "migration_save: end"
 
 
-def test_live_migration_in_many_waves():
+@pytest.mark.parametrize("ring", [True, False], ids=["ring", "per_wave_allocations"])
+def test_live_migration_in_many_waves(ring):
     """The hand-off forced into waves of 64 KiB: names move a few at a time,
-    every wave a reshard of its own, and the result is exact."""
+    every wave a reshard of its own, and the result is exact -- through the
+    two slots every wave reuses, and with allocations of every wave's own."""
     old, new = Parallel(tp=2, pp=2), Parallel(tp=4)
-    print(f"[gpu live migration] {old} -> {new}, waves of 64 KiB", flush=True)
-    res = _run(old, new, {"mode": "waves", "wave_bytes": 64 << 10})
+    print(f"[gpu live migration] {old} -> {new}, waves of 64 KiB, ring {ring}", flush=True)
+    res = _run(old, new, {"mode": "waves", "wave_bytes": 64 << 10, "ring": ring})
     _check_exact(res, new)
     waves = None
     for r in range(old.world):
         log = res[("saved", r)]
         assert any("in waves of at most" in m for m in log), log
+        assert any("ring of 2 x" in m for m in log) == ring, log
         line = next(m for m in log if "handed off in" in m)
         k = int(re.search(r"in (\d+) wave", line).group(1))
         assert waves in (None, k)
