@@ -21,7 +21,8 @@ last case:
   ``RELEASED``);
 * the new world returns without waiting for that release;
 * the hand-off forced into many small waves, through the two-slot ring and
-  with allocations of every wave's own;
+  with allocations of every wave's own, and into new worlds with pipeline
+  stages (waves that give some new ranks nothing);
 * a larger state while this process holds device memory so that less than
   the state itself is free: the old world picks waves, and the device's
   low-water free memory, as every rank logged it, shows at most two waves
@@ -197,7 +198,22 @@ def test_live_migration_in_many_waves(ring):
         assert any(f"destinations of {waves} wave(s)" in m for m in res[("loaded", r)]["log"])
 
 
-# about 2.2 GB of fp32 parameters and Adam moments over the four old ranks
+@pytest.mark.parametrize("old,new", [(Parallel(tp=4), Parallel(tp=2, pp=2)),
+                                     (Parallel(tp=1, pp=2), Parallel(tp=2, pp=2))],
+                         ids=["tp4_to_tp2pp2", "tp1pp2_to_tp2pp2"])
+def test_live_migration_waves_into_stages(old, new):
+    """Waves into a new world with pipeline stages: a wave whose names all
+    belong to one stage gives the other stage's ranks nothing to reshard,
+    and they still report it consumed; the world grows from 2 to 4 ranks in
+    the second case.  Exact against the oracle."""
+    print(f"[gpu live migration] {old} -> {new}, waves of 32 KiB", flush=True)
+    res = _run(old, new, {"mode": "waves", "wave_bytes": 32 << 10})
+    _check_exact(res, new)
+    for r in range(old.world):
+        assert any("handed off in" in m for m in res[("saved", r)]), res[("saved", r)]
+
+
+# about 2.4 GB of fp32 parameters and Adam moments over the four old ranks
 SQUEEZE_SPEC = ModelSpec("llama", n_layer=12, hidden=1024, n_head=8, ffn=2816, vocab=16000)
 
 
