@@ -688,8 +688,8 @@ class _OldWorld:
         try:
             for k, names in enumerate(waves):
                 part = {n: state[n] for n in names if n in state}
-                # a ring slot is free again: the wave that used it (k - 2)
-                # was reported consumed before wave k - 1's report was awaited
+                # ring slot k % 2 is free again: the wave that used it (k - 2)
+                # was reported consumed in the previous iteration
                 slot = ring[k % 2] if ring else None
                 t0 = time.perf_counter()
                 handoff, err = _attempt(lambda: Handoff(part, self.device, self.rank, slot=slot))
