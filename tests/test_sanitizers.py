@@ -33,8 +33,11 @@ def test_host_code_is_clean_under_asan_and_ubsan():
                ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
                SUIKA_RESHARD_LIB=str(lib), SUIKA_HOST_LIB=str(host))
+    # the two large Qwen2-TEST plan changes run the same host code as the
+    # others at 64x the bytes; the recast case stays
     res = subprocess.run([sys.executable, "-m", "pytest", *FILES, "-q", "-m", "not gpu", "-p", "no:cacheprovider",
-                          "-n", "6"], cwd=ROOT, env=env, capture_output=True, text=True, timeout=1500)
+                          "-k", "not (qwen2_test_tp2_tp1 or qwen2_test_tp1_tp2_d1)", "-n", "6"],
+                         cwd=ROOT, env=env, capture_output=True, text=True, timeout=1500)
     out = res.stdout + res.stderr
     reports = [l for l in out.splitlines() if "runtime error:" in l or "AddressSanitizer" in l]
     assert res.returncode == 0 and not reports, "\n".join(reports[:20]) + "\n" + out[-4000:]
