@@ -202,3 +202,30 @@ def test_download_regions():
     for d, h in pairs:
         assert torch.equal(d.cpu(), h)
     assert _lib.stage_counters().bytes_down - before == 80 << 20
+
+
+def _extension_cases():
+    from tests import cases
+    out = list(cases.scaled_configs().values())
+    pads = cases.padded_vocab_cases()
+    out += [pads[0], pads[-1]]
+    gold = cases.golden_cases()
+    out += [gold["qkv_tp1_tp2_d1"], gold["qkv_tp2_tp1"], gold["vocab_tp2_tp4_d3"]]
+    return out
+
+
+@pytest.mark.parametrize("w", _extension_cases(), ids=lambda w: w.key)
+def test_host_sources_extension_kinds(w):
+    """The staged route with the build's own layouts: zero-padded vocabulary
+    rows (ZERO pieces), head-granular fused QKV, the bf16 recast and the
+    five benchmark plan changes at a small shape, from host-resident shards
+    to HBM and back to the host, exact against the oracle."""
+    srcs, want = _state(w)
+    fake = to_device(srcs, w, "cpu")
+    fields = [(f, "normal") for f in w.src_fields]
+    for device in ("cuda", "cpu"):
+        print(f"[gpu host sources] {w.key} device={device}", flush=True)
+        out = execute_param_transfer(w.ops(), {}, device, fields, rank=w.dst_rank,
+                                     fake_source_state_dicts=fake, recast=w.recast_map)
+        torch.cuda.synchronize()
+        _compare(w.key, out, want, device)
