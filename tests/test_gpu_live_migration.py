@@ -12,7 +12,8 @@ closed form, bit for bit.
 Both of the reference's branches run:
 * a world that shrinks (TP2 -> TP1: 2 old + 1 new processes);
 * one that grows (TP1 -> TP2);
-* one of equal size whose stages change (TP2 x PP2 -> TP4: 4 + 4 processes).
+* one of equal size whose stages change (TP2 x PP2 -> TP4: 4 + 4 processes);
+* one whose old world holds data-parallel replicas (TP2 x DP2 -> TP4).
 
 The small states leave room on the device, so the hand-off is whole and the
 new world allocates its destinations beside the old state.  More runs of the
@@ -131,8 +132,9 @@ def _low_water(log) -> float:
 
 @pytest.mark.parametrize("old,new", [(Parallel(tp=2), Parallel(tp=1)),
                                      (Parallel(tp=1), Parallel(tp=2)),
-                                     (Parallel(tp=2, pp=2), Parallel(tp=4))],
-                         ids=["tp2_to_tp1", "tp1_to_tp2", "tp2pp2_to_tp4"])
+                                     (Parallel(tp=2, pp=2), Parallel(tp=4)),
+                                     (Parallel(tp=2, dp=2), Parallel(tp=4))],
+                         ids=["tp2_to_tp1", "tp1_to_tp2", "tp2pp2_to_tp4", "tp2dp2_to_tp4"])
 def test_live_migration_on_one_gpu(old, new):
     print(f"[gpu live migration] {old} -> {new}", flush=True)
     res = _run(old, new)
@@ -199,13 +201,16 @@ def test_live_migration_in_many_waves(ring):
 
 
 @pytest.mark.parametrize("old,new", [(Parallel(tp=4), Parallel(tp=2, pp=2)),
-                                     (Parallel(tp=1, pp=2), Parallel(tp=2, pp=2))],
-                         ids=["tp4_to_tp2pp2", "tp1pp2_to_tp2pp2"])
+                                     (Parallel(tp=1, pp=2), Parallel(tp=2, pp=2)),
+                                     (Parallel(tp=2, dp=2), Parallel(tp=4))],
+                         ids=["tp4_to_tp2pp2", "tp1pp2_to_tp2pp2", "tp2dp2_to_tp4"])
 def test_live_migration_waves_into_stages(old, new):
     """Waves into a new world with pipeline stages: a wave whose names all
     belong to one stage gives the other stage's ranks nothing to reshard,
     and they still report it consumed; the world grows from 2 to 4 ranks in
-    the second case.  Exact against the oracle."""
+    the second case.  The third case comes from data-parallel replicas: each
+    new rank maps only the replicas the schedule picked for its pieces.
+    Exact against the oracle."""
     print(f"[gpu live migration] {old} -> {new}, waves of 32 KiB", flush=True)
     res = _run(old, new, {"mode": "waves", "wave_bytes": 32 << 10})
     _check_exact(res, new)
