@@ -50,13 +50,16 @@ old rank 0 picks one of two orders from the device's free memory:
 **Waves** (it does not: the device holds less than twice the state).  Names
 are cut into waves of at most a third of the free memory, in the same order
 on every old rank; a name's tensors on every old rank move in one wave, so a
-wave is a self-contained reshard.  For each wave the old ranks pack its
-tensors into hand-off allocations, free them and return their memory (the
-reference's per-tensor free and periodic ``cuda_gc``), and old rank 0 sends
-the wave's records; the new ranks map them, reshard that wave into an arena
-of its own and report it consumed, and the old ranks free its hand-off.  The
-old world packs wave ``k + 1`` while the new world reshards wave ``k``, so the
-device holds the state plus at most two waves.
+wave is a self-contained reshard.  Each old rank allocates two hand-off
+slots once (the ring), each as large as its largest wave needs, when every
+rank's slots fit the room; else each wave gets allocations of its own.  For
+each wave the old ranks pack its tensors into slot ``k mod 2``, free them and
+return their memory (the reference's per-tensor free and periodic
+``cuda_gc``), and only then does old rank 0 send the wave's records; the new
+ranks map the slots (once each), reshard that wave into an arena of its own
+and report it consumed.  The old world packs wave ``k + 1`` while the new
+world reshards wave ``k``, so the device holds the state plus the ring (or
+plus at most two waves without it).
 
 Every step at which one rank may fail ends in an exchange of errors within
 its world, so a failure raises on every rank of that world instead of
