@@ -114,7 +114,7 @@ py::object lookup(PyObject* d, PyObject* key) {
 // Interned attribute names (created once, never released).
 struct Names {
   PyObject *dtype, *shape, *kind_args, *tp_meta, *kind, *rows, *name, *dict;
-  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta;
+  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta, *sr_rows;
   PyObject *chunk, *vocab_pad, *qkv_heads;
   Names() {
     auto in = [](const char* s) { return PyUnicode_InternFromString(s); };
@@ -122,6 +122,7 @@ struct Names {
     kind = in("kind"); rows = in("rows"); name = in("name"); dict = in("__dict__");
     param_name = in("param_name"); src_rank = in("src_rank"); dst_rank = in("dst_rank");
     src_meta = in("src_meta"); dst_meta = in("dst_meta"); dst_shard_meta = in("dst_shard_meta");
+    sr_rows = in("_sr_rows");
     chunk = in("chunk"); vocab_pad = in("vocab_pad"); qkv_heads = in("qkv_heads");
   }
 };
@@ -263,18 +264,22 @@ class FreshTensors {
 //
 // On a share of many small tensors the caching-allocator call behind each
 // fresh destination tensor is a large part of the host's time per tensor.
-// Once a launch group's sources are read (their dtypes fix the bytes), its
-// destination blocks are handed to a helper thread, which allocates them on
+// In the drop-in call's prologue every destination's block is handed to a
+// helper thread, tensor by tensor in launch order, which allocates them on
 // the call's device and current stream -- the allocations at::empty would
-// make -- while the calling thread lowers and plans the group.  The tensors
-// are then built on those blocks: each still has an allocation of its own.
-// A block the helper did not make (an allocation failed, the job was
-// stopped) or whose size is not the planned tensor's is not used; the
-// tensor is allocated on the calling thread instead, which also reports
-// any allocation failure.  Unused blocks are freed before the group's
-// launch, on the calling thread.
+// make -- while the calling thread reads, lowers and plans the launch
+// groups.  A block's size is the tensor's elements (its pieces' total) times
+// the element size its field has in the first sources the prologue reads.
+// The tensors are then built on those blocks, on the calling thread (built
+// on the helper, they cost both threads more than they saved): each still
+// has an allocation of its own.  A block the helper did not make (an
+// allocation failed, the job was stopped) or whose size is not the planned
+// tensor's (another dtype, a padded vocabulary shard) is not used; the
+// tensor is allocated on the calling thread instead, which also reports any
+// allocation failure.  Unused blocks are freed when the call ends, on the
+// calling thread.
 
-// One launch group's blocks: slot i has nbytes[i] bytes (0: no block).
+// The blocks of one job: slot i has nbytes[i] bytes (0: no block).
 class BlockJob {
  public:
   BlockJob(c10::Allocator* alloc, c10::Stream stream, std::vector<size_t> nbytes)
@@ -399,12 +404,66 @@ inline size_t block_slot(size_t nid, int64_t f, bool recast, int64_t nf) {
   return (nid * 2 + (recast ? 1 : 0)) * size_t(nf) + size_t(f);
 }
 
+constexpr size_t kNoBlock = SIZE_MAX;
+
+// The destination blocks of one drop-in call, made on the helper thread in
+// launch order: tensor t (a rank_runs index) is position pos_[t] of the
+// order, its field f (and f's bf16 copy) slot block_slot(pos, f, copy, nf).
+class AheadBlocks {
+ public:
+  // order: tensor indices in launch order; numel / padded: per tensor (rank_runs);
+  // itemsize: bytes per element of each field (0: no block); copies: 1 for a
+  // field with a bf16 copy
+  AheadBlocks(int64_t device_index, const RowTable& order, const RowTable& numel, py::array_t<bool> padded,
+              std::vector<int64_t> itemsize, std::vector<int64_t> copies)
+      : nf_(int64_t(itemsize.size())) {
+    if (order.ndim() != 1 || numel.ndim() != 1 || padded.ndim() != 1 || numel.shape(0) != padded.shape(0) ||
+        copies.size() != itemsize.size())
+      throw py::value_error("ahead blocks: order, numel and padded must be 1-D, one itemsize and copy flag per field");
+    const int64_t n_tensors = numel.shape(0);
+    pos_.assign(size_t(n_tensors), kNoBlock);
+    std::vector<size_t> nbytes(size_t(order.shape(0)) * 2 * size_t(nf_), 0);
+    const bool* pd = padded.data();
+    for (int64_t p = 0; p < order.shape(0); ++p) {
+      const int64_t t = order.data()[p];
+      if (t < 0 || t >= n_tensors || pos_[size_t(t)] != kNoBlock) throw py::value_error("ahead blocks: bad order");
+      pos_[size_t(t)] = size_t(p);
+      const int64_t elems = numel.data()[t];
+      if (pd[t] || elems <= 0) continue;
+      for (int64_t f = 0; f < nf_; ++f) {
+        if (itemsize[size_t(f)] > 0) nbytes[block_slot(size_t(p), f, false, nf_)] = size_t(elems * itemsize[size_t(f)]);
+        if (copies[size_t(f)]) nbytes[block_slot(size_t(p), f, true, nf_)] = size_t(elems) * c10::elementSize(at::kBFloat16);
+      }
+    }
+    const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
+    FreshTensors fresh(device);
+    const c10::Stream current = c10::impl::VirtualGuardImpl(device.type()).getStream(device);
+    job_ = std::make_shared<BlockJob>(fresh.allocator(), current, std::move(nbytes));
+    if (!BlockHelper::submit(job_)) job_.reset();
+  }
+  ~AheadBlocks() { finish(); }
+
+  // Position of tensor t in the job, kNoBlock if none.
+  size_t pos(int64_t t) const { return t >= 0 && size_t(t) < pos_.size() ? pos_[size_t(t)] : kNoBlock; }
+  int64_t fields() const { return nf_; }
+  BlockJob* job() const { return job_.get(); }
+  // Stops the helper on this job and frees the blocks no tensor took.
+  void finish() {
+    if (job_) job_->finish();
+  }
+
+ private:
+  int64_t nf_;
+  std::vector<size_t> pos_;
+  std::shared_ptr<BlockJob> job_;
+};
+
 // Fresh destination tensors for the slot rows (and the zero-element ones).
 // With `job`, a tensor takes the block made ahead for it (slot block_slot of
-// op k's tensor op_nid[k]) when there is one of its size.
+// op k's job position op_pos[k]) when there is one of its size.
 py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list names, py::list fields,
                     py::list recast_names, py::list dtypes, at::Device device, const FreshTensors* made = nullptr,
-                    BlockJob* job = nullptr, const std::vector<size_t>* op_nid = nullptr) {
+                    BlockJob* job = nullptr, const std::vector<size_t>* op_pos = nullptr) {
   const int64_t nf = int64_t(fields.size());
   py::dict out;
   const int64_t n = rows.ndim() == 2 ? rows.shape(0) : 0;
@@ -435,8 +494,9 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
       }
       const at::IntArrayRef sizes(r + 5, size_t(nd));
       c10::DataPtr block;
-      const bool ahead = job && job->take(block_slot((*op_nid)[size_t(k)], f, is_recast != 0, nf),
-                                          FreshTensors::bytes_of(sizes, st), &block);
+      const size_t pos = job ? (*op_pos)[size_t(k)] : kNoBlock;
+      const bool ahead = pos != kNoBlock && job->take(block_slot(pos, f, is_recast != 0, nf),
+                                                      FreshTensors::bytes_of(sizes, st), &block);
       if (job) (ahead ? g_blocks_taken : g_blocks_missed).fetch_add(1, std::memory_order_relaxed);
       at::Tensor t = fresh.make(sizes, st, ahead ? &block : nullptr);
       py::handle name = names[k];
@@ -625,6 +685,24 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
   }
 }
 
+// The encoding a scheduled op carries (make_ops): the sr_meta rows of its
+// source meta and of its destination shard, then its piece (tp index and
+// degree, first and end row; as in sr_op).  The schedule's TransferOp and
+// TensorMeta objects are values: nothing edits them once scheduled, so the
+// rows stay those of the objects the op names.
+constexpr int64_t kEncodingWords = 2 * kMetaWords + 4;
+
+// The encoding attached to `op`, or null for an op built otherwise (by the
+// caller, or the reference's own class).  `hold` keeps it alive.
+const int64_t* op_encoding(PyObject* op, py::object* hold) {
+  PyObject* v = nullptr;
+  if (_PyObject_LookupAttr(op, names_().sr_rows, &v) < 0) throw py::error_already_set();
+  if (!v) return nullptr;
+  *hold = py::reinterpret_steal<py::object>(v);
+  if (!PyBytes_Check(v) || PyBytes_GET_SIZE(v) != Py_ssize_t(kEncodingWords * sizeof(int64_t))) return nullptr;
+  return reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(v));
+}
+
 // A ParamLayout's {rank: {name: TensorMeta}} as an [n, 21] sr_meta table,
 // rank by rank in dict order; `names` maps names to ids (extended in first-
 // seen order) and `objs` receives each row's TensorMeta.
@@ -696,13 +774,25 @@ py::object derived(PyObject* meta_cls, PyObject* shard, PyObject* tp_meta, PyObj
 
 // TransferOps of an sr_op table (sr_schedule's output): source metas and
 // destination shards are the layouts' own objects, pieces derived from the
-// shards.
+// shards.  With the layouts' sr_meta tables (`src_rows`, `dst_rows`: row i
+// encodes src_objs[i] / dst_objs[i]), each op also carries its encoding
+// (`_sr_rows`, see op_encoding), which spares encode_ops the walk over its
+// metas' attributes.
 py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::list dst_objs, py::handle op_cls,
-                  py::handle meta_cls) {
+                  py::handle meta_cls, py::object src_rows, py::object dst_rows) {
   const Names& N = names_();
   if (!PyType_Check(op_cls.ptr()) || !PyType_Check(meta_cls.ptr())) throw py::type_error("classes expected");
   const int64_t n = ops.ndim() == 2 ? ops.shape(0) : 0;
   if (n && ops.shape(1) != 9) throw py::value_error("op rows must have 9 columns");
+  const bool encode = !src_rows.is_none() && !dst_rows.is_none();
+  RowTable srow, drow;
+  if (encode) {
+    srow = src_rows.cast<RowTable>();
+    drow = dst_rows.cast<RowTable>();
+    if (srow.ndim() != 2 || drow.ndim() != 2 || srow.shape(1) != kMetaWords || drow.shape(1) != kMetaWords ||
+        srow.shape(0) != int64_t(src_objs.size()) || drow.shape(0) != int64_t(dst_objs.size()))
+      throw py::value_error("meta tables must have one 21-word row per meta object");
+  }
   py::list out(n);
   const int64_t* r = ops.data();
   for (int64_t i = 0; i < n; ++i, r += 9) {
@@ -731,6 +821,17 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
     set(d, N.src_meta, PyList_GET_ITEM(src_objs.ptr(), s_row));
     set(d, N.dst_meta, piece.ptr());
     set(d, N.dst_shard_meta, shard);
+    if (encode) {
+      int64_t w[kEncodingWords];
+      std::memcpy(w, srow.data() + s_row * kMetaWords, sizeof(int64_t) * kMetaWords);
+      std::memcpy(w + kMetaWords, drow.data() + d_row * kMetaWords, sizeof(int64_t) * kMetaWords);
+      w[2 * kMetaWords] = p_idx;
+      w[2 * kMetaWords + 1] = p_deg;
+      w[2 * kMetaWords + 2] = r0;
+      w[2 * kMetaWords + 3] = r1;
+      py::bytes blob(reinterpret_cast<const char*>(w), sizeof(w));
+      set(d, N.sr_rows, blob.ptr());
+    }
     PyList_SET_ITEM(out.ptr(), i, op.release().ptr());
   }
   return out;
@@ -740,7 +841,9 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
 // `shards` maps each name to its destination shard, `name_ids` to its id.
 // Metas are numbered in first-use order (each object once per name); a piece
 // is encoded relative to its shard: (0, 0) for the shard itself, else its tp
-// index and degree (an unsplit piece of a split shard: (0, 1)) and rows.
+// index and degree (an unsplit piece of a split shard: (0, 1)) and rows.  An
+// op that carries the schedule's encoding (op_encoding) of the shard it
+// names is copied from it: its source meta gets a row of its own.
 py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
   const Names& N = names_();
   const int64_t n = int64_t(ops.size());
@@ -773,6 +876,32 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
       throw py::key_error("no shard for " + py::str(name).cast<std::string>());
     }
     const int64_t nid = as_int(nid_obj);
+    py::object hold;
+    const int64_t* enc = op_encoding(op, &hold);
+    if (enc && attr(op, N.dst_shard_meta).ptr() == shard) {
+      int64_t w[kEncodingWords];
+      std::memcpy(w, enc, sizeof(w));
+      orow[0] = nid;
+      orow[1] = as_int(attr(op, N.src_rank).ptr());
+      orow[2] = as_int(attr(op, N.dst_rank).ptr());
+      const int64_t src_row = int64_t(metas.size() / kMetaWords);
+      metas.insert(metas.end(), w, w + kMetaWords);
+      metas[size_t(src_row * kMetaWords)] = 0;
+      metas[size_t(src_row * kMetaWords + 1)] = nid;
+      orow[3] = src_row;
+      const std::pair<PyObject*, int64_t> key(shard, nid);
+      auto it = meta_of.find(key);
+      if (it == meta_of.end()) {
+        const int64_t row = int64_t(metas.size() / kMetaWords);
+        metas.insert(metas.end(), w + kMetaWords, w + 2 * kMetaWords);
+        metas[size_t(row * kMetaWords)] = 0;
+        metas[size_t(row * kMetaWords + 1)] = nid;
+        it = meta_of.emplace(key, row).first;
+      }
+      orow[4] = it->second;
+      std::copy(w + 2 * kMetaWords, w + kEncodingWords, orow + 5);
+      continue;
+    }
     py::object m = attr(op, N.dst_meta);
     int64_t idx = 0, deg = 0, r0 = -1, r1 = -1;
     if (m.ptr() != shard) {
@@ -827,10 +956,40 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
 
 // Elements of every op's piece (op.dst_meta): a row interval times the
 // other dims, else the global size over the tp degree (TensorMeta.numel of
-// a chunk piece).  Used to balance launch groups.
-int64_t piece_numel(PyObject* op) {
+// a chunk piece).  Used to balance launch groups.  With `padded`, whether
+// the piece belongs to a padded vocabulary shard (whose size is not its
+// pieces' total: it also holds rows no piece covers).
+int64_t piece_numel(PyObject* op, bool* padded = nullptr) {
   const Names& N = names_();
+  py::object hold;
+  if (const int64_t* enc = op_encoding(op, &hold)) {
+    // the schedule's encoding: shard row at kMetaWords (ndim at 3, shape
+    // from 4, tp degree at 14, kind at 15), then the piece
+    int64_t w[kEncodingWords];
+    std::memcpy(w, enc, sizeof(w));
+    const int64_t* shard = w + kMetaWords;
+    const int64_t nd = shard[3], p_deg = w[2 * kMetaWords + 1], r0 = w[2 * kMetaWords + 2],
+                  r1 = w[2 * kMetaWords + 3];
+    if (nd < 0 || nd > 8) throw py::value_error("malformed op encoding");
+    if (padded) *padded = shard[15] == 1;
+    int64_t v = 1;
+    if (r0 >= 0) {
+      v = r1 - r0;
+      for (int64_t d = 1; d < nd; ++d) v *= shard[4 + d];
+    } else {
+      for (int64_t d = 0; d < nd; ++d) v *= shard[4 + d];
+      const int64_t deg = p_deg > 0 ? p_deg : shard[14];
+      if (deg > 0) v /= deg;
+    }
+    return v;
+  }
   py::object m = attr(op, N.dst_meta);
+  if (padded) {
+    py::object kind = kind_of(m.ptr());
+    const int eq = PyObject_RichCompareBool(kind.ptr(), N.vocab_pad, Py_EQ);
+    if (eq < 0) throw py::error_already_set();
+    *padded = eq != 0;
+  }
   py::object shape = attr(m.ptr(), N.shape), tp = tp_meta_of(m.ptr()), rows = rows_of(m.ptr());
   if (!PyTuple_Check(shape.ptr())) throw py::type_error("TensorMeta.shape must be a tuple");
   const Py_ssize_t nd = PyTuple_GET_SIZE(shape.ptr());
@@ -874,7 +1033,9 @@ py::tuple name_runs(py::list ops) {
 
 // The ops of `rank` out of a whole schedule (any sequence), and their
 // name_runs, in one pass over the schedule: (ops, order, starts, elements
-// per tensor, single, {name: tensor index}).
+// per tensor, single, {name: tensor index}, padded per tensor).  A padded
+// tensor (a vocabulary shard with padding rows) has more elements than its
+// pieces' total; every other tensor's size is its pieces' total.
 py::tuple rank_runs(py::object schedule, int64_t rank) {
   const Names& N = names_();
   py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(schedule.ptr(), "ops must be a sequence"));
@@ -883,13 +1044,24 @@ py::tuple rank_runs(py::object schedule, int64_t rank) {
   PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
   py::list ops;
   std::vector<int64_t> numel;
+  std::vector<char> padded_op;
   for (Py_ssize_t k = 0; k < total; ++k) {
     if (as_int(attr(items[k], N.dst_rank).ptr()) != rank) continue;
     if (PyList_Append(ops.ptr(), items[k]) != 0) throw py::error_already_set();
-    numel.push_back(piece_numel(items[k]));
+    bool padded = false;
+    numel.push_back(piece_numel(items[k], &padded));
+    padded_op.push_back(padded ? 1 : 0);
   }
   py::tuple runs = runs_of(ops, numel.data(), Py_ssize_t(numel.size()));
-  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3], runs[4]);
+  const RowTable order = runs[0].cast<RowTable>(), starts = runs[1].cast<RowTable>();
+  const int64_t m = starts.shape(0) - 1;
+  py::array_t<bool> padded({m});
+  bool* pd = padded.mutable_data();
+  for (int64_t t = 0; t < m; ++t) {
+    pd[t] = false;
+    for (int64_t j = starts.data()[t]; j < starts.data()[t + 1]; ++j) pd[t] = pd[t] || padded_op[order.data()[j]];
+  }
+  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3], runs[4], padded);
 }
 
 py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {
@@ -938,9 +1110,10 @@ py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {
   return py::make_tuple(order, starts, total, single, ids);
 }
 
-// The ops of the tensors `picked` (indices into runs_of's tensors, any
-// order, each once): tensor by tensor in index order -- order of first
-// appearance --, each tensor's ops in schedule order.  A launch group.
+// The ops of the tensors `picked` (indices into runs_of's tensors, each
+// once): tensor by tensor in `picked` order, each tensor's ops in schedule
+// order.  A launch group, whose destinations are then allocated in the
+// order the helper thread makes their blocks (AheadBlocks).
 py::list take_ops(py::list ops, const RowTable& order, const RowTable& starts, const RowTable& picked) {
   const int64_t n_ops = int64_t(PyList_GET_SIZE(ops.ptr()));
   if (order.ndim() != 1 || order.shape(0) != n_ops || starts.ndim() != 1 || starts.shape(0) < 1 ||
@@ -948,12 +1121,13 @@ py::list take_ops(py::list ops, const RowTable& order, const RowTable& starts, c
     throw py::value_error("take_ops: order, starts and picked must be 1-D, order one entry per op");
   const int64_t m = starts.shape(0) - 1;
   const int64_t *st = starts.data(), *o = order.data();
-  std::vector<int64_t> sel(picked.data(), picked.data() + picked.shape(0));
-  std::sort(sel.begin(), sel.end());
+  const std::vector<int64_t> sel(picked.data(), picked.data() + picked.shape(0));
+  std::vector<int64_t> sorted(sel);
+  std::sort(sorted.begin(), sorted.end());
   Py_ssize_t total = 0;
-  for (size_t j = 0; j < sel.size(); ++j) {
-    const int64_t i = sel[j];
-    if (i < 0 || i >= m || (j && sel[j - 1] == i) || st[i] < 0 || st[i] > st[i + 1] || st[i + 1] > n_ops)
+  for (size_t j = 0; j < sorted.size(); ++j) {
+    const int64_t i = sorted[j];
+    if (i < 0 || i >= m || (j && sorted[j - 1] == i) || st[i] < 0 || st[i] > st[i + 1] || st[i + 1] > n_ops)
       throw py::value_error("take_ops: bad tensor index or runs");
     total += Py_ssize_t(st[i + 1] - st[i]);
   }
@@ -987,6 +1161,26 @@ py::dict ordered_result(py::list ops, py::dict target, py::list field_order) {
     if (!entry) {
       if (PyErr_Occurred()) throw py::error_already_set();
       throw py::key_error(py::str(name).cast<std::string>());
+    }
+    // an entry whose fields already follow field_order is taken as it is
+    bool in_order = PyDict_CheckExact(entry);
+    {
+      Py_ssize_t pos = 0, f = 0;
+      PyObject *key, *value;
+      while (in_order && PyDict_Next(entry, &pos, &key, &value)) {
+        bool found = false;   // the key among the fields after the previous key's
+        while (!found && f < nf) {
+          PyObject* want = PyList_GET_ITEM(field_order.ptr(), f++);
+          const int eq = want == key ? 1 : PyObject_RichCompareBool(want, key, Py_EQ);
+          if (eq < 0) throw py::error_already_set();
+          found = eq != 0;
+        }
+        in_order = found;
+      }
+    }
+    if (in_order) {
+      if (PyDict_SetItem(out.ptr(), name.ptr(), entry) != 0) throw py::error_already_set();
+      continue;
     }
     py::dict e;
     for (Py_ssize_t f = 0; f < nf; ++f) {
@@ -1250,7 +1444,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
   // tensors in order of first appearance, their ops, the destination rank
   py::dict name_ids;
   py::list names, op_names(n);
-  std::vector<std::vector<PyObject*>> by_name;
+  std::vector<PyObject*> first_op;   // per tensor
   std::vector<size_t> op_nid(n);
   std::vector<int64_t> ranks;
   for (Py_ssize_t k = 0; k < n; ++k) {
@@ -1262,13 +1456,12 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
       nid = size_t(as_int(id));
     } else {
       if (PyErr_Occurred()) throw py::error_already_set();
-      nid = by_name.size();
+      nid = first_op.size();
       py::int_ v(nid);
       if (PyDict_SetItem(name_ids.ptr(), name.ptr(), v.ptr()) != 0) throw py::error_already_set();
       names.append(name);
-      by_name.emplace_back();
+      first_op.push_back(op);
     }
-    by_name[nid].push_back(op);
     op_nid[k] = nid;
     const int64_t r = as_int(attr(op, N.dst_rank).ptr());
     if (std::find(ranks.begin(), ranks.end(), r) == ranks.end()) ranks.push_back(r);
@@ -1281,11 +1474,16 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
     assertion("ops target several ranks [" + list + "]");
   }
   py::dict shards;
-  for (size_t i = 0; i < by_name.size(); ++i) {
-    py::object shard = shard_of(by_name[i][0]);
+  std::vector<std::vector<Py_ssize_t>> members;   // each tensor's ops, when a shard is inferred
+  for (size_t i = 0; i < first_op.size(); ++i) {
+    py::object shard = shard_of(first_op[i]);
     if (shard.ptr() == Py_None) {
+      if (members.empty()) {
+        members.resize(first_op.size());
+        for (Py_ssize_t k = 0; k < n; ++k) members[op_nid[size_t(k)]].push_back(k);
+      }
       py::list group;
-      for (PyObject* op : by_name[i]) group.append(py::handle(op));
+      for (Py_ssize_t k : members[i]) group.append(py::handle(PyList_GET_ITEM(ops.ptr(), k)));
       shard = infer_shard(group);
     }
     shards[names[i]] = shard;
@@ -1295,7 +1493,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
   py::array_t<uint64_t> ptrs = col[2].cast<py::array_t<uint64_t>>();
   // one torch dtype per (tensor, field) across its sources: the library
   // compares element types, which several torch dtypes share
-  std::vector<PyObject*> first(by_name.size() * size_t(nf), nullptr);
+  std::vector<PyObject*> first(first_op.size() * size_t(nf), nullptr);
   {
     py::list dtypes = col[1].cast<py::list>();
     for (Py_ssize_t k = 0; k < n; ++k)
@@ -1308,59 +1506,33 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
                     ": dtype differs between sources");
       }
   }
-  // Fresh destinations: their blocks are made on the helper thread from
-  // here on, while this thread lowers and plans.  `ahead` = (name -> index,
-  // elements per index) gives each tensor's elements (its pieces' total,
-  // which is the tensor's size unless the shard has rows no piece covers).
+  // Fresh destinations: with `ahead` = ({name: tensor index}, AheadBlocks)
+  // their blocks are being made on the helper thread (see AheadBlocks).
   const at::Device device(at::kCUDA, c10::DeviceIndex(device_index));
   std::unique_ptr<FreshTensors> fresh;
-  std::shared_ptr<BlockJob> job;
-  struct Finish {
-    std::shared_ptr<BlockJob>& job;
-    ~Finish() {
-      if (job) job->finish();
-    }
-  } finish_job{job};
+  BlockJob* job = nullptr;
+  std::vector<size_t> op_pos;
   if (gather && dst_part.is_none()) {
     fresh = std::make_unique<FreshTensors>(device);
     if (!ahead.is_none()) {
       py::tuple a = ahead.cast<py::tuple>();
-      if (a.size() != 2 || !PyDict_Check(a[0].ptr())) throw py::value_error("ahead must be (dict, elements)");
+      if (a.size() != 2 || !PyDict_Check(a[0].ptr())) throw py::value_error("ahead must be (dict, AheadBlocks)");
       PyObject* index = a[0].ptr();
-      const RowTable numel = a[1].cast<RowTable>();
-      const int64_t n_numel = numel.ndim() == 1 ? numel.shape(0) : 0;
-      std::vector<size_t> nbytes(by_name.size() * 2 * size_t(nf), 0);
-      for (size_t i = 0; i < by_name.size(); ++i) {
-        // a padded vocabulary shard holds rows no piece covers: its size is
-        // not its pieces' total, and it is allocated on this thread
-        PyObject* shard = PyDict_GetItemWithError(shards.ptr(), names[i].ptr());
-        if (!shard) {
-          if (PyErr_Occurred()) throw py::error_already_set();
-          continue;
+      const AheadBlocks* blocks = a[1].cast<const AheadBlocks*>();
+      if (blocks->job() && blocks->fields() == nf) {
+        std::vector<size_t> pos(first_op.size(), kNoBlock);
+        for (size_t i = 0; i < first_op.size(); ++i) {
+          PyObject* at = PyDict_GetItemWithError(index, names[i].ptr());
+          if (!at) {
+            if (PyErr_Occurred()) throw py::error_already_set();
+            continue;
+          }
+          pos[i] = blocks->pos(as_int(at));
         }
-        py::object kind = kind_of(shard);
-        const int padded = PyObject_RichCompareBool(kind.ptr(), N.vocab_pad, Py_EQ);
-        if (padded < 0) throw py::error_already_set();
-        if (padded) continue;
-        PyObject* at = PyDict_GetItemWithError(index, names[i].ptr());
-        if (!at) {
-          if (PyErr_Occurred()) throw py::error_already_set();
-          continue;
-        }
-        const int64_t id = as_int(at);
-        if (id < 0 || id >= n_numel || numel.data()[id] <= 0) continue;
-        const size_t elems = size_t(numel.data()[id]);
-        for (int64_t f = 0; f < nf; ++f) {
-          PyObject* dt = first[i * size_t(nf) + size_t(f)];
-          if (dt && THPDtype_Check(dt))
-            nbytes[block_slot(i, f, false, nf)] =
-                elems * c10::elementSize(reinterpret_cast<THPDtype*>(dt)->scalar_type);
-          if (recast[size_t(f)]) nbytes[block_slot(i, f, true, nf)] = elems * c10::elementSize(at::kBFloat16);
-        }
+        op_pos.resize(size_t(n));
+        for (Py_ssize_t k = 0; k < n; ++k) op_pos[size_t(k)] = pos[op_nid[size_t(k)]];
+        job = blocks->job();
       }
-      const c10::Stream current = c10::impl::VirtualGuardImpl(device.type()).getStream(device);
-      job = std::make_shared<BlockJob>(fresh->allocator(), current, std::move(nbytes));
-      if (!BlockHelper::submit(job)) job.reset();
     }
   }
   py::tuple enc = encode_ops(ops, shards, name_ids);
@@ -1408,8 +1580,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
     py::array_t<uint64_t> dst_ptrs;
     if (dst_part.is_none()) {
       py::tuple made = alloc_dst(dst_rows, empty_rows, op_names, fields, recast_names, col[1].cast<py::list>(),
-                                 device, fresh.get(), job.get(), &op_nid);
-      if (job) job->finish();   // blocks no tensor took are freed before the launch
+                                 device, fresh.get(), job, &op_pos);
       part = made[0];
       dst_ptrs = made[1].cast<py::array_t<uint64_t>>();
     } else {
@@ -1450,6 +1621,19 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("dtypes"));
   m.def("arena_tensors", &arena_tensors, py::arg("ops"), py::arg("source"), py::arg("order"), py::arg("targets"),
         py::arg("device"));
+  py::class_<AheadBlocks>(m, "AheadBlocks",
+                          "Destination blocks of one drop-in call, made ahead on the helper thread")
+      .def("finish", &AheadBlocks::finish, "stop the helper on these blocks and free those no tensor took");
+  m.def(
+      "start_blocks",
+      [](int64_t device_index, const RowTable& order, const RowTable& numel, py::array_t<bool> padded,
+         std::vector<int64_t> itemsize, std::vector<int64_t> copies) {
+        return std::make_unique<AheadBlocks>(device_index, order, numel, padded, std::move(itemsize),
+                                             std::move(copies));
+      },
+      py::arg("device_index"), py::arg("order"), py::arg("numel"), py::arg("padded"), py::arg("itemsize"),
+      py::arg("copies"),
+      "the destination blocks of tensors `order` (launch order), handed to the helper thread now");
   m.def(
       "blocks_ahead",
       [] { return py::make_tuple(g_blocks_taken.load(), g_blocks_missed.load()); },
@@ -1463,7 +1647,7 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
-        py::arg("op_cls"), py::arg("meta_cls"));
+        py::arg("op_cls"), py::arg("meta_cls"), py::arg("src_rows") = py::none(), py::arg("dst_rows") = py::none());
   m.def("device_views", &device_views, py::arg("base"), py::arg("views"), py::arg("device_index"));
   m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
         py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),

@@ -22,7 +22,6 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
-#include <unordered_map>
 #include <vector>
 
 #include "sr_internal.h"
@@ -164,6 +163,45 @@ struct Scratch {
   std::vector<Box> pads;
 };
 
+// Name id -> dense group index, for at most `n` ids: open addressing in one
+// allocation (a node-based map costs an allocation per name).
+class IdTable {
+ public:
+  explicit IdTable(size_t n) {
+    size_t cap = 16;
+    while (cap < 2 * n) cap *= 2;
+    slots_.assign(cap, Slot{0, -1});
+    mask_ = cap - 1;
+  }
+  // the value stored for `id`, or `value` after storing it
+  int64_t find_or_add(int64_t id, int64_t value) {
+    uint64_t h = uint64_t(id) * 0x9E3779B97F4A7C15ull;
+    for (size_t i = size_t(h >> 32) & mask_;; i = (i + 1) & mask_) {
+      Slot& s = slots_[i];
+      if (s.value < 0) {
+        s = Slot{id, value};
+        return value;
+      }
+      if (s.id == id) return s.value;
+    }
+  }
+
+ private:
+  struct Slot {
+    int64_t id, value;   // value -1: empty
+  };
+  std::vector<Slot> slots_;
+  size_t mask_;
+};
+
+// One tensor's ops: a range of op indices.
+struct Span {
+  const int64_t *b, *e;
+  const int64_t* begin() const { return b; }
+  const int64_t* end() const { return e; }
+  int64_t operator[](size_t i) const { return b[i]; }
+};
+
 // Region moves of one op, source local -> destination local.
 int lower_op(const sr_op& op, const sr_meta* metas, const View& shard, int view, Scratch& w,
              std::vector<Region>* out) {
@@ -265,28 +303,46 @@ int lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops
   for (int64_t k = 0; k < n_ops; ++k) L->peer_v.push_back(ops[k].src_rank);
   std::sort(L->peer_v.begin(), L->peer_v.end());
   L->peer_v.erase(std::unique(L->peer_v.begin(), L->peer_v.end()), L->peer_v.end());
-  // tensors in order of first appearance, each with its ops in schedule order
-  std::unordered_map<int64_t, size_t> group_of;
-  std::vector<std::vector<int64_t>> groups;
-  for (int64_t k = 0; k < n_ops; ++k) {
-    auto it = group_of.emplace(ops[k].name, groups.size());
-    if (it.second) groups.emplace_back();
-    groups[it.first->second].push_back(k);
-  }
-  struct PairHash {
-    size_t operator()(const std::pair<int64_t, int64_t>& p) const {
-      // unsigned: corrupted ranks must not overflow a signed product
-      return std::hash<uint64_t>()(uint64_t(p.first) * 1000003u ^ uint64_t(p.second));
+  // tensors in order of first appearance, each with its ops in schedule
+  // order: group g's ops are member[begin[g] .. begin[g + 1])
+  std::vector<int64_t> group_of(static_cast<size_t>(n_ops)), begin, member(static_cast<size_t>(n_ops));
+  {
+    IdTable ids(static_cast<size_t>(n_ops));
+    for (int64_t k = 0; k < n_ops; ++k) {
+      const int64_t g = ids.find_or_add(ops[k].name, int64_t(begin.size()));
+      if (g == int64_t(begin.size())) begin.push_back(0);
+      group_of[k] = g;
+      ++begin[g];
     }
-  };
-  std::unordered_map<std::pair<int64_t, int64_t>, int32_t, PairHash> src_base;   // (rank, name) -> slot
+    int64_t at = 0;
+    for (int64_t& b : begin) {
+      const int64_t n = b;
+      b = at;
+      at += n;
+    }
+    begin.push_back(at);
+    std::vector<int64_t> fill(begin.begin(), begin.end() - 1);
+    for (int64_t k = 0; k < n_ops; ++k) member[fill[group_of[k]]++] = k;
+  }
+  const int64_t n_groups = int64_t(begin.size()) - 1;
+  int64_t n_recast = 0;
+  for (int64_t f = 0; f < n_fields; ++f) n_recast += recast[f];
+  L->dst_v.reserve(size_t(n_groups * (n_fields + n_recast)));
+  L->dst_key_v.reserve(L->dst_v.capacity());
+  L->src_v.reserve(size_t(n_ops * n_fields));
+  L->src_key_v.reserve(L->src_v.capacity());
+  L->piece_v.reserve(size_t(n_ops * n_fields));
+  // a tensor's source slots by source rank (the ranks of one tensor's ops)
+  std::vector<std::pair<int64_t, int32_t>> src_base;
   std::vector<int64_t> field_dtype(n_fields);
   std::vector<int32_t> dslot(n_fields), dslot2(n_fields);
   std::vector<Region> regions;
   Scratch w;
   char a[160], b[160];
-  for (const std::vector<int64_t>& g : groups) {
+  for (int64_t gi = 0; gi < n_groups; ++gi) {
+    const Span g{member.data() + begin[gi], member.data() + begin[gi + 1]};
     const int64_t k0 = g[0];
+    src_base.clear();
     const sr_meta& sh = metas[ops[k0].dst_shard];
     const View shard = view_of(sh);
     const int64_t name = ops[k0].name;
@@ -361,8 +417,12 @@ int lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops
       const sr_op& op = ops[k];
       const int32_t peer = int32_t(std::lower_bound(L->peer_v.begin(), L->peer_v.end(), op.src_rank) -
                                    L->peer_v.begin());
-      auto ins = src_base.emplace(std::make_pair(op.src_rank, name), int32_t(L->src_v.size()));
-      if (ins.second) {
+      int32_t base = -1;
+      for (const auto& rb : src_base)
+        if (rb.first == op.src_rank) base = rb.second;
+      if (base < 0) {
+        base = int32_t(L->src_v.size());
+        src_base.emplace_back(op.src_rank, base);
         const sr_src_spec& s0 = specs[k * n_fields];
         int64_t sR, sC;
         if (!matrix(s0.shape, s0.ndim, view, &sR, &sC)) return fail(SR_EINVAL, "#%lld: size overflows", ll(name));
@@ -372,7 +432,6 @@ int lower(const sr_meta* metas, int64_t n_metas, const sr_op* ops, int64_t n_ops
           L->src_key_v.push_back(slot_key(k, f, 0, sp.dtype, sp.ndim, sp.shape));
         }
       }
-      const int32_t base = ins.first->second;
       if ((rc = lower_op(op, metas, shard, view, w, &regions)) != SR_OK) return rc;
       for (const Region& r : regions)
         for (int64_t f = 0; f < n_fields; ++f)

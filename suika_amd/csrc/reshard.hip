@@ -808,10 +808,6 @@ PlanView plan_view(const sr_plan* p) {
 
 namespace {
 
-bool mul_overflows(uint64_t a, uint64_t b, uint64_t limit) {
-  return a != 0 && b > limit / a;
-}
-
 int check_tensor(const sr_tensor& t, const char* what, int32_t idx) {
   if (t.reserved != 0) return fail(SR_EINVAL, "%s[%d]: reserved field must be 0", what, idx);
   const int es = dtype_size(t.dtype);
@@ -820,7 +816,8 @@ int check_tensor(const sr_tensor& t, const char* what, int32_t idx) {
     return fail(SR_EINVAL, "%s[%d]: empty tensor [%llu, %llu]", what, idx,
                 (unsigned long long)t.rows, (unsigned long long)t.cols);
   const uint64_t lim = uint64_t(1) << 62;
-  if (mul_overflows(t.rows, t.cols, lim) || mul_overflows(t.rows * t.cols, es, lim))
+  uint64_t n, bytes;
+  if (__builtin_mul_overflow(t.rows, t.cols, &n) || __builtin_mul_overflow(n, uint64_t(es), &bytes) || bytes > lim)
     return fail(SR_EINVAL, "%s[%d]: tensor too large", what, idx);
   return SR_OK;
 }
@@ -1757,8 +1754,10 @@ int sr_plan_create(const sr_tensor* src_tensors, int32_t n_src, const sr_tensor*
       ph.src_name = an;
       ph.dst_name = bn;
     };
-    fill(p->pack, sb, p->peer_bytes, "src_ptrs", "peer_bufs");
-    fill(p->unpack, p->peer_bytes, db, "peer_bufs", "dst_ptrs");
+    if (buffers) {
+      fill(p->pack, sb, p->peer_bytes, "src_ptrs", "peer_bufs");
+      fill(p->unpack, p->peer_bytes, db, "peer_bufs", "dst_ptrs");
+    }
     fill(p->gather, sb, db, "src_ptrs", "dst_ptrs");
   }
   for (Phase* ph : {&p->pack, &p->unpack, &p->gather}) {

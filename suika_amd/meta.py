@@ -433,7 +433,8 @@ def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layou
 
     # TransferOps over the layouts' own metas; a piece is its shard with
     # another tp meta (scale_to_tp) or a row interval (vocab_pad)
-    schedule = _lib.host().make_ops(ops[:n_ops.value], list(names), src_objs, dst_objs, TransferOp, TensorMeta)
+    schedule = _lib.host().make_ops(ops[:n_ops.value], list(names), src_objs, dst_objs, TransferOp, TensorMeta,
+                                    src, dst)
     if log_func is not None:
         for op in schedule:
             if op.src_rank != op.dst_rank:

@@ -144,7 +144,8 @@ def execute_param_transfer(
     """
     assert route in ("direct", "buffers"), f"unknown route {route!r}"
     _lib.lib()   # raises when the HIP library is missing: there is no other path
-    if log_func is None:
+    quiet = log_func is None
+    if quiet:
         log_func = lambda msg: None  # noqa: E731
     if prof is None:
         prof = _NoProf()
@@ -181,23 +182,32 @@ def execute_param_transfer(
             f"[{rank}]: piece from rank {r} needs a cross-GPU exchange, which this one-GPU build "
             "does not implement; pass the peer shards as fake_source_state_dicts")
 
-    # bytes per element over the moved fields, from the first op's sources
-    # (only used to balance the launch groups)
-    elem_bytes = 0
-    if ops and normal:
-        first = source(ops[0].src_rank).get(ops[0].param_name, {})
-        elem_bytes = sum(first[f].element_size() for f in normal if f in first)
+    # bytes per element of each moved field, from the first op's sources
+    first = source(ops[0].src_rank).get(ops[0].param_name, {}) if ops and normal else {}
+    itemsize = [first[f].element_size() if f in first else 0 for f in normal]
+    elem_bytes = sum(itemsize)   # over all moved fields (balances the launch groups)
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
     groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:5])
+    # fresh destinations of the direct route: their allocations are made on
+    # a helper thread from here on, tensor by tensor in launch order, while
+    # this thread plans the groups (each tensor's elements: its pieces';
+    # each field's element size: the first source's)
+    blocks = None
+    if not arena and route == "direct" and device.type == "cuda" and any(itemsize) and \
+            all(first[f].is_cuda for f in normal if f in first):
+        copies = set(recast.values())
+        launch = getattr(groups, "launch_order", None)   # the order the groups take the tensors in
+        if launch is None:
+            launch = np.arange(len(runs[3]), dtype=np.int64)
+        blocks = _lib.host().start_blocks(gpu.index, launch, runs[3], runs[6], itemsize,
+                                          [1 if f in copies else 0 for f in normal])
     # the staged route (sources in host memory, or results for the host)
     # packs on the host and unpacks on the GPU: its plans keep both phases
     stage_options = replace(plan_options, gather_only=False) if plan_options is not None else None
     if route == "direct":   # the plans only ever gather
         plan_options = _GATHER_ONLY if plan_options is None else replace(plan_options, gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
-    # fresh destinations: each group's allocations are made on a helper
-    # thread while the group is planned (each tensor's elements: its pieces')
-    ahead = (runs[5], runs[3]) if arena_views is None else None
+    ahead = (runs[5], blocks) if blocks is not None else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
@@ -345,19 +355,25 @@ def execute_param_transfer(
             # Each group is planned on the host while the GPU runs the
             # previous group's launch.  A source in host memory sends the
             # rest of the transfer through the staged route.
-            done_names: Dict[str, None] = {}
+            done: List[List[TransferOp]] = []
             for group in (() if device.type == "cpu" else groups):
                 try:
                     _device_group(group)
                 except _lib.HostSourceError:
+                    if blocks is not None:
+                        blocks.finish()
+                    done_names = {op.param_name for g in done for op in g}
                     staged([op for op in ops if op.param_name not in done_names] if done_names else ops)
                     break
-                done_names.update(dict.fromkeys(op.param_name for op in group))
+                done.append(group)
             else:
                 if device.type == "cpu":
                     staged(ops)
-        log_func(f"=== reshard plan: {sum(p.n_pieces for p in plans)} pieces in {len(plans)} "
-                 f"launch group(s), {sum(p.info.buffer_bytes for p in plans) / 1e6:.1f} MB of buffers ===")
+            if blocks is not None:
+                blocks.finish()   # blocks no tensor took (another dtype, say) are freed
+        if not quiet:
+            log_func(f"=== reshard plan: {sum(p.n_pieces for p in plans)} pieces in {len(plans)} "
+                     f"launch group(s), {sum(p.info.buffer_bytes for p in plans) / 1e6:.1f} MB of buffers ===")
 
         # The rest of the host work runs while the last launches finish.
         # 1-element sub-fields ride along whole; the first op's source wins,
@@ -388,6 +404,8 @@ def execute_param_transfer(
     finally:
         # destroying a plan waits for its launches: buffers and sources may
         # be released afterwards whatever stream the kernels ran on
+        if blocks is not None:
+            blocks.finish()
         prof.start("execute wait")
         for plan in plans:
             plan.close()
@@ -571,7 +589,9 @@ class _LaunchGroups:
     forms the last group once a next group would hold fewer than
     MIN_GROUP_TENSORS names or less GPU time than its own planning overhead
     (PLAN_NS_PER_GROUP), or at the ``pipeline``-th group.  Within a group
-    the ops keep their schedule order.
+    the tensors stay largest first (``launch_order``, the order in which
+    their destinations are allocated ahead), each tensor's ops in schedule
+    order.
 
     Iterating yields the groups; the time between two requests is taken as
     the planning time of the group handed out first.  ``elem_bytes`` is the
@@ -595,9 +615,15 @@ class _LaunchGroups:
     def _gpu(self, a: int, b: int) -> float:
         return float(self.cum[b - 1] - (self.cum[a - 1] if a else 0.0))
 
+    @property
+    def launch_order(self) -> np.ndarray:
+        """Tensor indices in the order the groups hold them: largest first,
+        or order of first appearance when the transfer is not cut."""
+        if self.pipeline <= 1 or self.n <= 1:
+            return np.arange(self.n, dtype=np.int64)
+        return self.rank
+
     def _take(self, a: int, b: int) -> List[TransferOp]:
-        if a == 0 and b == self.n:
-            return self.ops
         return _lib.host().take_ops(self.ops, self.order, self.starts, self.rank[a:b])
 
     def _next_end(self, start: int, end: int, groups: int) -> int:

@@ -196,10 +196,11 @@ class ReshardPlan:
         drop-in call's direct route.  The destinations are fresh tensors (as
         ``alloc_dst``), or ``dst`` ``{name: {field: tensor}}``, each checked
         against its slot (as ``bind_dst_ptrs``).  With ``ahead`` = ({name:
-        index}, elements per index) -- each tensor's elements --, the fresh
-        tensors' allocations are made on a helper thread while the plan is
-        built.  Returns the plan (its kernels possibly still running:
-        ``close`` waits for them) and the destinations."""
+        tensor index}, blocks) -- blocks from the host extension's
+        ``start_blocks``, which a helper thread is allocating --, the fresh
+        tensors are built on those blocks where their sizes match.  Returns
+        the plan (its kernels possibly still running: ``close`` waits for
+        them) and the destinations."""
         plan, _, part = cls._native(ops, source, fields, device, recast, options, rank, gather=True,
                                     stream=_stream_handle(stream).value or 0, dst=dst, ahead=ahead)
         return plan, part

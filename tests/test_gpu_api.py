@@ -440,13 +440,14 @@ def test_fresh_destinations_are_ordinary_independent_tensors():
 @pytest.mark.parametrize("key", ["gpt125m_tp2_tp4", "qwen7b_tp2_tp4"])
 def test_destination_blocks_made_ahead(key, groups, monkeypatch):
     """The direct route's fresh destinations are allocated on a helper thread
-    while each launch group is planned.  Every tensor whose pieces cover it
-    (all but vocabulary shards, which may be padded, and empty tensors) is
-    built on such a block, sized by that tensor's own source dtype -- here
-    one tensor's exp_avg is float64 among float32 ones -- and bf16 recast
-    copies included; the rest are allocated on the calling thread.  The
-    result matches the oracle, each tensor holds one allocation of its own
-    and no block is left over."""
+    from the call's prologue on, while the launch groups are planned.  Every
+    tensor whose pieces cover it (all but vocabulary shards, which may be
+    padded, and empty tensors) and whose element size is its field's in the
+    first source the prologue reads is built on such a block, bf16 recast
+    copies included; the rest -- here one tensor's exp_avg, float64 among
+    float32 ones -- are allocated on the calling thread.  The result matches
+    the oracle, each tensor holds one allocation of its own and no block is
+    left over."""
     from suika_amd import _lib
     from suika_amd import migration as M
     from tests.harness import round_robin_groups
@@ -482,8 +483,14 @@ def test_destination_blocks_made_ahead(key, groups, monkeypatch):
     tensors = [t for e in out.values() for t in e.values()]
     assert after - before == _blocks_of(tensors)
     assert len({t.untyped_storage().data_ptr() for t in tensors if t.numel()}) == sum(1 for t in tensors if t.numel())
-    own = sum(len(e) for n, e in out.items()
-              if n in vocab or pieces[n] == 0 or pieces[n] != next(iter(e.values())).numel())
+    # the element size each field's blocks are made for: the first source's
+    first_op = next(op for op in ops if op.dst_rank == w.dst_rank)
+    first = fake[first_op.src_rank][first_op.param_name]
+    guess = {f: first[f].element_size() for f in w.src_fields}
+    guess.update({t: 2 for t in w.recast_map})
+    own = sum(1 for n, e in out.items() for f, t in e.items()
+              if n in vocab or pieces[n] == 0 or pieces[n] != t.numel() or t.element_size() != guess[f])
+    assert own >= 1
     assert (taken, missed) == (len(tensors) - own, own), (taken, missed, own)
     assert out[odd]["exp_avg"].dtype == torch.float64
     for name, e in want.items():

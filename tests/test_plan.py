@@ -8,6 +8,8 @@
   coverage check;
 * the benchmark plans have the documented sizes (P, D, pieces).
 """
+from collections import OrderedDict
+
 import numpy as np
 import pytest
 import torch
@@ -310,8 +312,9 @@ def _group_costs(w, groups, elem, tpn):
 def test_pipeline_groups_keep_tensors_whole():
     """Launch groups of execute_param_transfer: every op in exactly one
     group, every op of a tensor in the same group, at most ``pipeline``
-    groups, schedule order kept within a group, the largest tensor in the
-    first group."""
+    groups, within a group the tensors largest first (the order their
+    destinations are allocated in) and each tensor's ops in schedule order,
+    the largest tensor in the first group."""
     from suika_amd import migration
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
@@ -323,17 +326,24 @@ def test_pipeline_groups_keep_tensors_whole():
             groups = migration._pipeline_groups(ops, elem, pipeline, tpn).cut()
             assert sorted(position[id(op)] for g in groups for op in g) == list(range(len(ops)))
             assert 1 <= len(groups) <= pipeline
-            seen = set()
-            for g in groups:
-                names = {op.param_name for op in g}
-                assert not names & seen, "a tensor split across groups"
-                seen |= names
-                assert [position[id(op)] for op in g] == sorted(position[id(op)] for op in g)
-            if pipeline == 1:
-                assert groups == [ops]
             per_name = {}
             for op in ops:
                 per_name[op.param_name] = per_name.get(op.param_name, 0) + op.dst_meta.numel()
+            seen = set()
+            for g in groups:
+                names = list(dict.fromkeys(op.param_name for op in g))
+                assert not set(names) & seen, "a tensor split across groups"
+                seen |= set(names)
+                if len(groups) > 1:
+                    sizes = [per_name[n] for n in names]
+                    assert sizes == sorted(sizes, reverse=True), "tensors not largest first"
+                for n in names:
+                    run = [position[id(op)] for op in g if op.param_name == n]
+                    assert run == sorted(run)
+                    at = [i for i, op in enumerate(g) if op.param_name == n]
+                    assert at == list(range(at[0], at[0] + len(at))), "a tensor's ops not together"
+            if pipeline == 1:
+                assert groups == [ops]
             if len(groups) > 1:
                 assert max(per_name, key=per_name.get) in {op.param_name for op in groups[0]}
     # a tensor whose ops are not consecutive still lands whole in one group
@@ -446,6 +456,51 @@ def test_launch_groups_survive_a_group_planned_within_the_overhead(monkeypatch, 
     assert len(groups) == timed[0] + 2, sizes     # and the one after it takes the rest
 
 
+def test_encoded_ops_match_the_attribute_walk():
+    """The schedule's ops carry their encoding (the sr_meta rows of their
+    source meta and destination shard, and the piece); encode_ops copies it
+    and piece_numels / rank_runs compute from it instead of reading the
+    metas' attributes.  Both give the same tables op by op, on every config
+    and rank, and an op whose shard is not the one the caller names is
+    encoded from its attributes."""
+    import copy
+
+    from suika_amd import _lib
+    from suika_amd.geometry import infer_dst_shard
+    host = _lib.host()
+
+    def decode(ops, shards, ids):
+        metas, rows = host.encode_ops(ops, shards, ids)
+        return [(tuple(r[[0, 1, 2, 5, 6, 7, 8]]), tuple(metas[r[3]]), tuple(metas[r[4]])) for r in rows]
+
+    def walked(ops):
+        out = []
+        for op in ops:
+            c = copy.copy(op)
+            del c.__dict__["_sr_rows"]
+            out.append(c)
+        return out
+
+    for key in CONFIG_ORDER:
+        w = CONFIGS[key]
+        world = schedule_param_transfer(*w.layouts())
+        assert all(len(op._sr_rows) == 46 * 8 for op in world)
+        for r in sorted({op.dst_rank for op in world}):
+            ops = [op for op in world if op.dst_rank == r]
+            ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
+            shards = {op.param_name: op.dst_shard_meta for op in ops}
+            assert decode(ops, shards, ids) == decode(walked(ops), shards, ids), (key, r)
+            assert host.piece_numels(ops).tolist() == host.piece_numels(walked(ops)).tolist(), (key, r)
+            for a, b in zip(host.rank_runs(ops, r)[1:], host.rank_runs(walked(ops), r)[1:]):
+                assert (a == b) if isinstance(a, (bool, dict)) else a.tolist() == b.tolist(), (key, r)
+    # a caller's own shard object (equal, not the op's) takes the walk
+    w = CONFIGS["gpt125m_tp2_tp4"]
+    ops = [op for op in schedule_param_transfer(*w.layouts()) if op.dst_rank == w.dst_rank]
+    ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
+    inferred = {n: infer_dst_shard([op for op in ops if op.param_name == n]) for n in ids}
+    assert decode(ops, inferred, ids) == decode(walked(ops), inferred, ids)
+
+
 def test_rank_runs_and_ordered_result():
     """The one-pass prologue (a rank's ops, their tensor groups in order of
     first appearance and each tensor's elements) against a Python
@@ -459,7 +514,7 @@ def test_rank_runs_and_ordered_result():
         world = schedule_param_transfer(*w.layouts())
         for sched in (world, tuple(world[::-1]), world[5:] + world[:5]):
             for r in sorted({op.dst_rank for op in sched}):
-                ops, order, starts, numel, single, index = host.rank_runs(sched, r)
+                ops, order, starts, numel, single, index, padded = host.rank_runs(sched, r)
                 want_ops = [op for op in sched if op.dst_rank == r]
                 assert ops == want_ops, (key, r)
                 names = list(dict.fromkeys(op.param_name for op in want_ops))
@@ -469,17 +524,24 @@ def test_rank_runs_and_ordered_result():
                 assert numel.tolist() == [sum(want_ops[i].dst_meta.numel() for i in members[n]) for n in names]
                 assert single == all(m == list(range(m[0], m[0] + len(m))) for m in members.values())
                 assert index == {n: i for i, n in enumerate(names)}
+                # a padded vocabulary shard is larger than its pieces' total
+                assert padded.tolist() == [want_ops[members[n][0]].dst_shard_meta.kind == "vocab_pad"
+                                           for n in names]
+                for n in names:
+                    shard = want_ops[members[n][0]].dst_shard_meta
+                    if shard.kind != "vocab_pad":
+                        assert numel[index[n]] == shard.numel(), (key, n)
     assert host.rank_runs([], 0)[0] == []
-    # a launch group's ops: the picked tensors in index order, each one's ops
-    # in schedule order (tensors whose ops are not consecutive included)
+    # a launch group's ops: the picked tensors in picked order, each one's
+    # ops in schedule order (tensors whose ops are not consecutive included)
     sched = CONFIGS["llama7b_tp4pp2_tp2pp2"].ops()
     sched = sched[7:] + sched[:7]
-    ops, order, starts, numel, single, index = host.rank_runs(sched, sched[0].dst_rank)
+    ops, order, starts, numel, single, index, _ = host.rank_runs(sched, sched[0].dst_rank)
     names = list(index)
     rng = np.random.default_rng(5)
     for size in (1, 5, len(names)):
         picked = rng.permutation(len(names))[:size]
-        want = [op for i in sorted(picked) for op in ops if op.param_name == names[i]]
+        want = [op for i in picked for op in ops if op.param_name == names[i]]
         assert host.take_ops(ops, order, starts, picked) == want
     assert host.take_ops(ops, order, starts, np.array([], dtype=np.int64)) == []
     for bad in ([len(names)], [-1], [2, 2]):
@@ -492,6 +554,20 @@ def test_rank_runs_and_ordered_result():
     out = host.ordered_result(ops, target, ["master", "param", "step", "exp_avg"])
     assert list(out) == list(dict.fromkeys(op.param_name for op in ops))
     assert all(list(e) == ["master", "param", "exp_avg"] for e in out.values())
+    # entries already in field order are returned as they are; others
+    # (out of order, an extra field, a dict subclass) are rebuilt in order
+    order = ["master", "param", "step", "exp_avg"]
+    names = list(dict.fromkeys(op.param_name for op in ops))
+    kinds = [{"master": 3, "param": 2, "exp_avg": 1}, {"param": 2, "exp_avg": 1},
+             {"exp_avg": 1, "master": 3}, {"master": 3, "extra": 0, "param": 2},
+             OrderedDict(master=3, param=2)]
+    target = {n: dict(kinds[i % len(kinds)]) if i % len(kinds) < 4 else OrderedDict(kinds[4])
+              for i, n in enumerate(names)}
+    out = host.ordered_result(ops, target, order)
+    for i, n in enumerate(names):
+        src = target[n]
+        assert list(out[n]) == [f for f in order if f in src], n
+        assert (out[n] is src) == (i % len(kinds) in (0, 1)), n
     with pytest.raises(KeyError):
         host.ordered_result(ops, {}, ["param"])
 
