@@ -1181,15 +1181,17 @@ int setup_offsets(sr_plan* p, hipStream_t stream) {
 
 // First use of a phase: its descriptors, tile prefix and pointer table go
 // up in one copy from pinned memory, then one kernel builds the tile table
-// and binds the items to `ptrs`, stream-ordered on `stream` (ev_setup marks
-// completion).
+// and binds the items to `ptrs`, stream-ordered on `stream`.  With
+// `mark`, ev_setup marks completion (for a copy kernel on another stream);
+// else the phase's next copy kernel follows on `stream` and its ev_kernel
+// stands for the bind.
 int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, const std::vector<uint64_t>& ptrs,
-                hipStream_t stream) {
+                hipStream_t stream, bool mark) {
   if (ph.ready) return SR_OK;
   TableCache& cache = table_cache();
   int rc;
-  for (hipEvent_t* ev : {&ph.ev_setup, &ph.ev_kernel})
-    if (!*ev && (rc = cache.get_event(p->device, ev)) != SR_OK) return rc;
+  if (mark && !ph.ev_setup && (rc = cache.get_event(p->device, &ph.ev_setup)) != SR_OK) return rc;
+  if (!ph.ev_kernel && (rc = cache.get_event(p->device, &ph.ev_kernel)) != SR_OK) return rc;
   const uint32_t n = uint32_t(ph.rel.size());
   if (n > 0) {
     const size_t nptr = std::max<size_t>(1, size_t(ph.n_src_base) + ph.n_dst_base);
@@ -1231,8 +1233,12 @@ int setup_phase(sr_plan* p, Phase& ph, bool needs_offsets, const std::vector<uin
                        ph.d_items);
     SR_HIP_TRY(hipGetLastError());
   }
-  SR_HIP_TRY(hipEventRecord(ph.ev_setup, stream));
-  ph.ev_bound = ph.ev_setup;
+  if (mark) {
+    SR_HIP_TRY(hipEventRecord(ph.ev_setup, stream));
+    ph.ev_bound = ph.ev_setup;
+  } else {
+    ph.ev_bound = ph.ev_kernel;   // recorded after the copy kernel, which follows on `stream`
+  }
   ph.bound = ptrs;
   ph.bound_valid = true;
   ph.ready = true;
@@ -1300,7 +1306,7 @@ int run_phase(sr_plan* p, Phase& ph, PhaseKind kind, const std::vector<uint64_t>
         return fail(SR_EHIP, "hipStreamQuery failed: %s", hipGetErrorString(busy));
       if (busy == hipErrorNotReady && (rc = table_cache().setup_stream(p->device, &setup)) != SR_OK) return rc;
     }
-    rc = setup_phase(p, ph, kind != kGather, ptrs, setup);
+    rc = setup_phase(p, ph, kind != kGather, ptrs, setup, setup != stream);
     if (rc != SR_OK) return rc;
     if (setup != stream) SR_HIP_TRY(hipStreamWaitEvent(stream, ph.ev_setup, 0));
   } else if (rebind) {
@@ -1376,7 +1382,7 @@ int check_ptrs(const void* const* ptrs, size_t n, const std::vector<uint32_t>& a
     const uintptr_t a = reinterpret_cast<uintptr_t>(ptrs[i]);
     if (align[i] == 0) continue;   // slot unused by this phase
     if (a == 0) return fail(SR_EINVAL, "%s[%zu] is null", what, i);
-    if (a % align[i] != 0)
+    if (a & (align[i] - 1))   // element sizes: powers of two
       return fail(SR_EALIGN, "%s[%zu] = %p is not %u-byte aligned", what, i, ptrs[i], align[i]);
   }
   return SR_OK;

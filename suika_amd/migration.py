@@ -208,6 +208,10 @@ def execute_param_transfer(
         plan_options = _GATHER_ONLY if plan_options is None else replace(plan_options, gather_only=True)
     arena_views = _arena_views(ops, source, normal, recast, device) if arena else None
     ahead = (runs[5], blocks) if blocks is not None else None
+    # the direct route's launch groups: planned, allocated and gathered in
+    # one native call each
+    gather = ReshardPlan.gatherer(source, normal, device, recast=recast, options=plan_options, rank=rank,
+                                  stream=stream) if route == "direct" and device.type == "cuda" else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []
@@ -303,9 +307,7 @@ def execute_param_transfer(
                 part = {name: arena_views[name] for name in dict.fromkeys(op.param_name for op in group)}
             prof.start("execute gather")
             try:
-                plan, part = ReshardPlan.gather_sources(group, source, normal, device, recast=recast,
-                                                        options=plan_options, rank=rank, stream=stream,
-                                                        dst=part, ahead=ahead)
+                plan, part = gather(group, part, ahead)
             finally:
                 prof.stop("execute gather")
             plans.append(plan)
@@ -610,10 +612,11 @@ class _LaunchGroups:
         gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
         self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
         self.cum = np.cumsum(gpu_ns[self.rank])
+        self._cum = self.cum.tolist()                           # plain floats for the cutter
         self.plan_ns = float(PLAN_NS_PER_TENSOR)                 # per destination tensor
 
     def _gpu(self, a: int, b: int) -> float:
-        return float(self.cum[b - 1] - (self.cum[a - 1] if a else 0.0))
+        return self._cum[b - 1] - (self._cum[a - 1] if a else 0.0)
 
     @property
     def launch_order(self) -> np.ndarray:

@@ -216,17 +216,52 @@ class ReshardPlan:
         self._L = _lib.lib()
         # grouping, shards, tables, source checks, sr_lower and sr_plan_create
         # (and with `gather` the destinations and the launch) in one native call
-        (handle, self._names, self.dst_metas, self._op_names, self.dst_rank, self._dtypes, src_ptrs,
-         self._src_arr, self._dst_arr, self._piece_arr, self.peers, self._src_rows, self._dst_rows,
-         self._empty_rows, self.peer_bytes, info, part) = _lib.host().plan_sources(
+        src_ptrs, part = self._adopt(_lib.host().plan_sources(
             self._ops, source, self.fields, [self._recast_of.get(f) for f in self.fields],
             infer_dst_shard, dev_index, who, opt.tile_bytes, opt.max_blocks, opt.flags,
-            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst, ahead, host_ok)
+            _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, gather, stream, dst, ahead, host_ok))
+        return self, src_ptrs, part
+
+    def _adopt(self, made):
+        """The plan's state from plan_sources' result; returns the source
+        addresses and the destinations."""
+        (handle, self._names, self.dst_metas, self._op_names, self.dst_rank, self._dtypes, src_ptrs,
+         self._src_arr, self._dst_arr, self._piece_arr, self.peers, self._src_rows, self._dst_rows,
+         self._empty_rows, self.peer_bytes, info, part) = made
         self._handle = ctypes.c_void_p(handle)
         self.info = _lib.SrPlanInfo.from_buffer_copy(info)
         self.n_pieces = len(self._piece_arr)
         self._views = self._pieces_view = self._c_src_view = self._c_dst_view = None
-        return self, src_ptrs, part
+        return src_ptrs, part
+
+    @classmethod
+    def gatherer(cls, source: Callable[[int], Mapping], fields: Sequence[str], device: torch.device,
+                 recast: Optional[Mapping[str, str]] = None, options: Optional[PlanOptions] = None,
+                 rank: Optional[int] = None, stream=None):
+        """``gather_sources`` for many groups of ops with the same sources,
+        fields, device, options and stream: what the groups share is checked
+        and converted once.  Returns ``gather(ops, dst=None, ahead=None) ->
+        (plan, destinations)``."""
+        proto = cls.__new__(cls)
+        proto._configure((), fields, recast, options)
+        fields, recast, options, recast_of = proto.fields, proto.recast, proto.options, proto._recast_of
+        recast_names = [recast_of.get(f) for f in fields]
+        dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        who = f"[{rank}]" if rank is not None else ""
+        # the stream: `stream`, else the device's current stream
+        handle = torch._C._cuda_getCurrentRawStream(dev_index) if stream is None else _stream_handle(stream).value
+        args = (infer_dst_shard, dev_index, who, options.tile_bytes, options.max_blocks, options.flags,
+                _lib.SR_TENSOR_DTYPE, _lib.SR_PIECE_DTYPE, True, handle or 0)
+        L, plan_sources = _lib.lib(), _lib.host().plan_sources
+
+        def gather(ops, dst=None, ahead=None):
+            self = cls.__new__(cls)
+            self.fields, self.recast, self.options, self._recast_of, self._L = fields, recast, options, recast_of, L
+            self._handle = ctypes.c_void_p()
+            self._ops = ops
+            _, part = self._adopt(plan_sources(ops, source, fields, recast_names, *args, dst, ahead, False))
+            return self, part
+        return gather
 
     def _configure(self, ops, fields, recast, options) -> None:
         """Fields, recast map and options, validated."""

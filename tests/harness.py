@@ -181,6 +181,7 @@ def poisoned_allocations():
     alloc_dst, alloc_dst_ptrs = ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs
     alloc_buffers, arena_views = ReshardPlan.alloc_buffers, migration._arena_views
     gather_sources = ReshardPlan.__dict__["gather_sources"]
+    gatherer = ReshardPlan.__dict__["gatherer"]
 
     poisoned = {"tensors": 0}
 
@@ -222,15 +223,21 @@ def poisoned_allocations():
         plan.gather_ptrs(src_ptrs, ptrs, stream)
         return plan, part
 
+    def make_gatherer(cls, source, fields, device, recast=None, options=None, rank=None, stream=None):
+        return lambda ops, dst=None, ahead=None: gather(cls, ops, source, fields, device, recast, options, rank,
+                                                        stream, dst, ahead)
+
     ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = dst, dst_ptrs
     ReshardPlan.alloc_buffers, migration._arena_views = buffers, arena
     ReshardPlan.gather_sources = classmethod(gather)
+    ReshardPlan.gatherer = classmethod(make_gatherer)
     try:
         yield poisoned
     finally:
         ReshardPlan.alloc_dst, ReshardPlan.alloc_dst_ptrs = alloc_dst, alloc_dst_ptrs
         ReshardPlan.alloc_buffers, migration._arena_views = alloc_buffers, arena_views
         ReshardPlan.gather_sources = gather_sources
+        ReshardPlan.gatherer = gatherer
 
 
 def gpu_execute(w: Workload, srcs_np, device="cuda", plan_options=None, route="buffers", arena=False):
