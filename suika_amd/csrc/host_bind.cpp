@@ -220,17 +220,37 @@ using RowTable = py::array_t<int64_t, py::array::c_style | py::array::forcecast>
 // at::empty gives (same allocator, current stream, resizable storage), at a
 // fraction of at::empty's per-call cost -- the drop-in call allocates one per
 // destination tensor and field.
+// A dense tensor of `device` as at::empty makes it: its dispatch keys
+// (autograd keys included) and the allocator its storage comes from.  Outside
+// inference mode (whose tensors carry other keys) they are read once per
+// device and kept for the process.
+struct TensorKind {
+  c10::DispatchKeySet keys;
+  c10::Allocator* alloc;
+};
+
+TensorKind tensor_kind(at::Device device) {
+  auto read = [&] {
+    at::Tensor t = at::empty({0}, at::TensorOptions().device(device));
+    TensorKind k{t.key_set(), t.storage().allocator()};
+    if (k.alloc == nullptr) throw std::runtime_error("no allocator for " + device.str());
+    return k;
+  };
+  if (c10::InferenceMode::is_enabled()) return read();
+  static std::mutex mu;
+  static std::vector<std::pair<at::Device, TensorKind>>* kinds = new std::vector<std::pair<at::Device, TensorKind>>();
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& dk : *kinds)
+    if (dk.first == device) return dk.second;
+  const TensorKind k = read();
+  kinds->emplace_back(device, k);
+  return k;
+}
+
 class FreshTensors {
  public:
-  explicit FreshTensors(at::Device device)
-      : guard_(device),
-        // a dense tensor of this device as at::empty makes it: its dispatch keys
-        // (autograd keys included) and the allocator its storage came from
-        tmpl_(at::empty({0}, at::TensorOptions().device(device))),
-        keys_(tmpl_.key_set()),
-        alloc_(tmpl_.storage().allocator()) {
-    if (alloc_ == nullptr) throw std::runtime_error("no allocator for " + device.str());
-  }
+  explicit FreshTensors(at::Device device) : guard_(device), kind_(tensor_kind(device)),
+                                             keys_(kind_.keys), alloc_(kind_.alloc) {}
 
   static size_t bytes_of(at::IntArrayRef sizes, at::ScalarType st) {
     int64_t numel = 1;
@@ -255,7 +275,7 @@ class FreshTensors {
 
  private:
   c10::DeviceGuard guard_;   // the allocator serves the current device
-  at::Tensor tmpl_;
+  TensorKind kind_;
   c10::DispatchKeySet keys_;
   c10::Allocator* alloc_;
 };
@@ -1031,22 +1051,40 @@ py::tuple name_runs(py::list ops) {
   return runs_of(ops, e, n);
 }
 
-// The ops of `rank` out of a whole schedule (any sequence), and their
-// name_runs, in one pass over the schedule: (ops, order, starts, elements
+// The ops of `rank` out of a whole schedule (any sequence; `positions`, when
+// given, says where they are), and their name_runs, in one pass over the
+// schedule: (ops, order, starts, elements
 // per tensor, single, {name: tensor index}, padded per tensor).  A padded
 // tensor (a vocabulary shard with padding rows) has more elements than its
 // pieces' total; every other tensor's size is its pieces' total.
-py::tuple rank_runs(py::object schedule, int64_t rank) {
+py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions) {
   const Names& N = names_();
   py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(schedule.ptr(), "ops must be a sequence"));
   if (!seq) throw py::error_already_set();
   const Py_ssize_t total = PySequence_Fast_GET_SIZE(seq.ptr());
   PyObject** items = PySequence_Fast_ITEMS(seq.ptr());
+  // `positions`: where the schedule holds this rank's ops (ascending), used
+  // when every one of them is in range and targets `rank`; else a scan
+  std::vector<Py_ssize_t> cand;
+  bool indexed = !positions.is_none();
+  if (indexed) {
+    const RowTable pos = positions.cast<RowTable>();
+    indexed = pos.ndim() == 1;
+    for (int64_t i = 0; indexed && i < pos.shape(0); ++i) {
+      const int64_t k = pos.data()[i];
+      indexed = k >= 0 && k < total && (i == 0 || k > pos.data()[i - 1]) &&
+                as_int(attr(items[k], N.dst_rank).ptr()) == rank;
+      cand.push_back(Py_ssize_t(k));
+    }
+  }
+  if (!indexed) cand.clear();
   py::list ops;
   std::vector<int64_t> numel;
   std::vector<char> padded_op;
-  for (Py_ssize_t k = 0; k < total; ++k) {
-    if (as_int(attr(items[k], N.dst_rank).ptr()) != rank) continue;
+  const Py_ssize_t n_cand = indexed ? Py_ssize_t(cand.size()) : total;
+  for (Py_ssize_t c = 0; c < n_cand; ++c) {
+    const Py_ssize_t k = indexed ? cand[size_t(c)] : c;
+    if (!indexed && as_int(attr(items[k], N.dst_rank).ptr()) != rank) continue;
     if (PyList_Append(ops.ptr(), items[k]) != 0) throw py::error_already_set();
     bool padded = false;
     numel.push_back(piece_numel(items[k], &padded));
@@ -1642,7 +1680,7 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
   m.def("piece_numels", &piece_numels, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
-  m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"));
+  m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"), py::arg("positions") = py::none());
   m.def("take_ops", &take_ops, py::arg("ops"), py::arg("order"), py::arg("starts"), py::arg("picked"));
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
   m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));

@@ -32,6 +32,7 @@ import re
 from itertools import chain
 from typing import Any, Callable, Dict, List, Optional, Tuple, Union
 
+import numpy as np
 import torch
 import torch.distributed as dist
 from torch import Tensor
@@ -392,9 +393,51 @@ def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta
     return _lib.host().encode_layout(pl.layout, names, objs)
 
 
+class Schedule(list):
+    """The ops ``schedule_param_transfer`` returns: a list, which also keeps
+    the positions of each destination rank's ops, so that the drop-in call
+    takes a rank's ops without scanning the whole schedule.  Any change to
+    the list drops the positions (the call then scans it)."""
+
+    def __init__(self, ops=(), dst_ranks=None):
+        super().__init__(ops)
+        self._positions: Optional[Dict[int, np.ndarray]] = None
+        if dst_ranks is not None and len(dst_ranks) == len(self):
+            order = np.argsort(dst_ranks, kind="stable")
+            ranks, first = np.unique(dst_ranks[order], return_index=True)
+            bounds = list(first) + [len(order)]
+            self._positions = {int(r): order[bounds[i]:bounds[i + 1]] for i, r in enumerate(ranks)}
+
+    def positions_of(self, rank: int) -> Optional[np.ndarray]:
+        """Positions of ``rank``'s ops in schedule order, or None when the
+        list has changed since it was scheduled."""
+        if self._positions is None:
+            return None
+        return self._positions.get(int(rank), _NO_POSITIONS)
+
+    def _changed(self) -> None:
+        self._positions = None
+
+
+def _dropping_positions(name):
+    method = getattr(list, name)
+
+    def change(self, *args, **kwargs):
+        self._changed()
+        return method(self, *args, **kwargs)
+    change.__name__ = name
+    return change
+
+
+for _name in ("__setitem__", "__delitem__", "__iadd__", "__imul__", "append", "extend", "insert", "pop",
+              "remove", "sort", "reverse", "clear"):
+    setattr(Schedule, _name, _dropping_positions(_name))
+_NO_POSITIONS = np.zeros(0, dtype=np.int64)
+
+
 def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layout: ParamLayout,
                             log_func: Optional[Callable] = None,
-                            minimum_est_peers: Optional[int] = None) -> List[TransferOp]:
+                            minimum_est_peers: Optional[int] = None) -> Schedule:
     """Greedy piece -> source assignment of Suika/migration.py:322-381.
 
     Every target tensor is cut into pieces at the largest source TP degree
@@ -433,8 +476,9 @@ def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layou
 
     # TransferOps over the layouts' own metas; a piece is its shard with
     # another tp meta (scale_to_tp) or a row interval (vocab_pad)
-    schedule = _lib.host().make_ops(ops[:n_ops.value], list(names), src_objs, dst_objs, TransferOp, TensorMeta,
-                                    src, dst)
+    table = ops[:n_ops.value]
+    schedule = Schedule(_lib.host().make_ops(table, list(names), src_objs, dst_objs, TransferOp, TensorMeta,
+                                             src, dst), table[:, 2])   # column 2: dst_rank
     if log_func is not None:
         for op in schedule:
             if op.src_rank != op.dst_rank:

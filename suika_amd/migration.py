@@ -43,7 +43,7 @@ from torch import Tensor
 from torch.nn import Module
 from torch.optim import Optimizer
 
-from .meta import (CHUNK, QKV_HEADS, ParamLayout, TensorMeta, TransferOp,
+from .meta import (CHUNK, QKV_HEADS, ParamLayout, Schedule, TensorMeta, TransferOp,
                    get_named_parameters_and_persistent_buffers, schedule_param_transfer)
 from . import _lib
 from .plan import PlanOptions, ReshardPlan, download
@@ -167,7 +167,8 @@ def execute_param_transfer(
     prof.start("execute prologue")
     # this rank's ops, grouped by tensor with each tensor's elements, in one
     # pass over the schedule
-    runs = _lib.host().rank_runs(transfer_ops, int(rank))
+    runs = _lib.host().rank_runs(transfer_ops, int(rank),
+                                 transfer_ops.positions_of(rank) if type(transfer_ops) is Schedule else None)
     ops = runs[0]
     normal = [f for f, t in expected_sub_fields if not _is_meta_field(t)]
     scalars = [f for f, t in expected_sub_fields if _is_meta_field(t)]

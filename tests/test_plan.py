@@ -501,6 +501,38 @@ def test_encoded_ops_match_the_attribute_walk():
     assert decode(ops, inferred, ids) == decode(walked(ops), inferred, ids)
 
 
+def test_schedule_positions_match_a_scan():
+    """schedule_param_transfer's list keeps each destination rank's op
+    positions; rank_runs given them returns what a scan of the whole
+    schedule returns, falls back to the scan on positions that do not hold
+    the rank's ops, and any change to the list drops the positions."""
+    from suika_amd import _lib
+    from suika_amd.meta import Schedule
+    host = _lib.host()
+
+    def same(a, b):
+        assert a[0] == b[0]
+        for x, y in zip(a[1:], b[1:]):
+            assert (x == y) if isinstance(x, (bool, dict)) else x.tolist() == y.tolist()
+
+    for key in CONFIG_ORDER:
+        sched = schedule_param_transfer(*CONFIGS[key].layouts())
+        assert type(sched) is Schedule
+        for r in sorted({op.dst_rank for op in sched}) + [99]:
+            pos = sched.positions_of(r)
+            assert pos.tolist() == [i for i, op in enumerate(sched) if op.dst_rank == r]
+            same(host.rank_runs(sched, r, pos), host.rank_runs(list(sched), r))
+    r = sched[0].dst_rank
+    others = np.array([i for i, op in enumerate(sched) if op.dst_rank != r][:3], dtype=np.int64)
+    for bad in (others, np.array([len(sched)], dtype=np.int64), sched.positions_of(r)[::-1].copy()):
+        same(host.rank_runs(sched, r, bad), host.rank_runs(list(sched), r))
+    for change in (lambda s: s.append(s[0]), lambda s: s.__setitem__(0, s[1]), lambda s: s.sort(key=id),
+                   lambda s: s.pop(), lambda s: s.__iadd__([s[0]]), lambda s: s.__delitem__(slice(0, 2))):
+        s = schedule_param_transfer(*CONFIGS["gpt125m_tp2_tp4"].layouts())
+        change(s)
+        assert s.positions_of(0) is None
+
+
 def test_rank_runs_and_ordered_result():
     """The one-pass prologue (a rank's ops, their tensor groups in order of
     first appearance and each tensor's elements) against a Python
