@@ -182,7 +182,7 @@ py::tuple collect_sources(py::list ops, py::function source, py::list fields, in
     auto nm = [&]() { return py::str(name).cast<std::string>(); };
     if (!entry) assertion(who + ": param missing in source " + nm());
     for (int64_t f = 0; f < nf; ++f) {
-      py::handle field = fields[f];
+      py::handle field = PyList_GET_ITEM(fields.ptr(), f);
       py::object obj = lookup(entry.ptr(), field.ptr());
       if (!obj) assertion("expected_sub_fields mismatch: " + nm() + " has no " + py::str(field).cast<std::string>());
       if (!THPVariable_Check(obj.ptr()))
@@ -205,8 +205,9 @@ py::tuple collect_sources(py::list ops, py::function source, py::list fields, in
       int64_t* row = sp + (k * nf + f) * kSpecWords;
       row[0] = code;
       row[1] = nd;
-      for (int64_t d = 0; d < nd; ++d) row[2 + d] = t.size(d);
-      dtypes[k * nf + f] = dtype_object(t.scalar_type());
+      const at::IntArrayRef sizes = t.sizes();
+      for (int64_t d = 0; d < nd; ++d) row[2 + d] = sizes[size_t(d)];
+      PyList_SET_ITEM(dtypes.ptr(), k * nf + f, dtype_object(t.scalar_type()).release().ptr());
       pp[k * nf + f] = reinterpret_cast<uint64_t>(t.data_ptr());
     }
   }
@@ -492,6 +493,11 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
   std::unique_ptr<FreshTensors> own;
   if (!made) made = (own = std::make_unique<FreshTensors>(device)).get();
   const FreshTensors& fresh = *made;
+  const Py_ssize_t n_names = PyList_GET_SIZE(names.ptr());
+  if (PyList_GET_SIZE(recast_names.ptr()) != nf || PyList_GET_SIZE(dtypes.ptr()) < n_names * nf)
+    throw py::value_error("one recast name per field and one dtype per (op, field)");
+  int64_t last_k = -1;   // the rows of one tensor come together: its entry is kept
+  PyObject* entry = nullptr;
   for (int pass = 0; pass < 2; ++pass) {
     const auto& tbl = pass == 0 ? rows : empty_rows;
     const int64_t m = tbl.ndim() == 2 ? tbl.shape(0) : 0;
@@ -499,18 +505,18 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
     const int64_t* r = tbl.data();
     for (int64_t i = 0; i < m; ++i, r += kKeyWords) {
       const int64_t k = r[0], f = r[1], is_recast = r[2], nd = r[4];
-      if (k < 0 || k >= int64_t(names.size()) || f < 0 || f >= nf || nd < 0 || nd > 8)
+      if (k < 0 || k >= n_names || f < 0 || f >= nf || nd < 0 || nd > 8)
         throw py::value_error("malformed slot row");
       at::ScalarType st;
-      py::handle field;
+      PyObject* field;
       if (is_recast) {
         st = at::kBFloat16;
-        field = recast_names[f];
+        field = PyList_GET_ITEM(recast_names.ptr(), f);
       } else {
-        py::handle dt = dtypes[k * nf + f];
-        if (!THPDtype_Check(dt.ptr())) throw py::type_error("dtypes must hold torch.dtype objects");
-        st = reinterpret_cast<THPDtype*>(dt.ptr())->scalar_type;
-        field = fields[f];
+        PyObject* dt = PyList_GET_ITEM(dtypes.ptr(), k * nf + f);
+        if (!THPDtype_Check(dt)) throw py::type_error("dtypes must hold torch.dtype objects");
+        st = reinterpret_cast<THPDtype*>(dt)->scalar_type;
+        field = PyList_GET_ITEM(fields.ptr(), f);
       }
       const at::IntArrayRef sizes(r + 5, size_t(nd));
       c10::DataPtr block;
@@ -519,17 +525,20 @@ py::tuple alloc_dst(const RowTable& rows, const RowTable& empty_rows, py::list n
                                                       FreshTensors::bytes_of(sizes, st), &block);
       if (job) (ahead ? g_blocks_taken : g_blocks_missed).fetch_add(1, std::memory_order_relaxed);
       at::Tensor t = fresh.make(sizes, st, ahead ? &block : nullptr);
-      py::handle name = names[k];
-      PyObject* entry = PyDict_GetItemWithError(out.ptr(), name.ptr());
-      if (!entry) {
-        if (PyErr_Occurred()) throw py::error_already_set();
-        py::dict fresh;
-        out[name] = fresh;
-        entry = fresh.ptr();
+      if (k != last_k) {
+        PyObject* name = PyList_GET_ITEM(names.ptr(), k);
+        entry = PyDict_GetItemWithError(out.ptr(), name);
+        if (!entry) {
+          if (PyErr_Occurred()) throw py::error_already_set();
+          py::dict e;
+          if (PyDict_SetItem(out.ptr(), name, e.ptr()) != 0) throw py::error_already_set();
+          entry = e.ptr();   // held by `out`
+        }
+        last_k = k;
       }
-      py::object wrapped = py::reinterpret_steal<py::object>(THPVariable_Wrap(t));
-      if (PyDict_SetItem(entry, field.ptr(), wrapped.ptr()) != 0) throw py::error_already_set();
       if (pass == 0) pp[i] = reinterpret_cast<uint64_t>(t.data_ptr());
+      py::object wrapped = py::reinterpret_steal<py::object>(THPVariable_Wrap(std::move(t)));
+      if (!wrapped || PyDict_SetItem(entry, field, wrapped.ptr()) != 0) throw py::error_already_set();
     }
   }
   return py::make_tuple(out, ptrs);
@@ -707,20 +716,26 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
 
 // The encoding a scheduled op carries (make_ops): the sr_meta rows of its
 // source meta and of its destination shard, then its piece (tp index and
-// degree, first and end row; as in sr_op).  The schedule's TransferOp and
-// TensorMeta objects are values: nothing edits them once scheduled, so the
-// rows stay those of the objects the op names.
+// degree, first and end row; as in sr_op), with the source and piece meta
+// objects it was made from.  TensorMeta objects are values: nothing edits
+// one once scheduled, so the rows stay those of the objects.
 constexpr int64_t kEncodingWords = 2 * kMetaWords + 4;
 
 // The encoding attached to `op`, or null for an op built otherwise (by the
-// caller, or the reference's own class).  `hold` keeps it alive.
+// caller, or the reference's own class) or whose src_meta or dst_meta has
+// been replaced since.  `hold` keeps it alive.
 const int64_t* op_encoding(PyObject* op, py::object* hold) {
+  const Names& N = names_();
   PyObject* v = nullptr;
-  if (_PyObject_LookupAttr(op, names_().sr_rows, &v) < 0) throw py::error_already_set();
+  if (_PyObject_LookupAttr(op, N.sr_rows, &v) < 0) throw py::error_already_set();
   if (!v) return nullptr;
   *hold = py::reinterpret_steal<py::object>(v);
-  if (!PyBytes_Check(v) || PyBytes_GET_SIZE(v) != Py_ssize_t(kEncodingWords * sizeof(int64_t))) return nullptr;
-  return reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(v));
+  if (!PyTuple_Check(v) || PyTuple_GET_SIZE(v) != 3) return nullptr;
+  PyObject* rows = PyTuple_GET_ITEM(v, 0);
+  if (!PyBytes_Check(rows) || PyBytes_GET_SIZE(rows) != Py_ssize_t(kEncodingWords * sizeof(int64_t))) return nullptr;
+  if (attr(op, N.src_meta).ptr() != PyTuple_GET_ITEM(v, 1) || attr(op, N.dst_meta).ptr() != PyTuple_GET_ITEM(v, 2))
+    return nullptr;
+  return reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(rows));
 }
 
 // A ParamLayout's {rank: {name: TensorMeta}} as an [n, 21] sr_meta table,
@@ -850,7 +865,8 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
       w[2 * kMetaWords + 2] = r0;
       w[2 * kMetaWords + 3] = r1;
       py::bytes blob(reinterpret_cast<const char*>(w), sizeof(w));
-      set(d, N.sr_rows, blob.ptr());
+      py::tuple enc = py::make_tuple(blob, py::handle(PyList_GET_ITEM(src_objs.ptr(), s_row)), piece);
+      set(d, N.sr_rows, enc.ptr());
     }
     PyList_SET_ITEM(out.ptr(), i, op.release().ptr());
   }
@@ -1503,7 +1519,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
     op_nid[k] = nid;
     const int64_t r = as_int(attr(op, N.dst_rank).ptr());
     if (std::find(ranks.begin(), ranks.end(), r) == ranks.end()) ranks.push_back(r);
-    op_names[k] = name;
+    PyList_SET_ITEM(op_names.ptr(), k, name.release().ptr());
   }
   if (ranks.size() > 1) {
     std::sort(ranks.begin(), ranks.end());

@@ -484,7 +484,7 @@ def test_encoded_ops_match_the_attribute_walk():
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         world = schedule_param_transfer(*w.layouts())
-        assert all(len(op._sr_rows) == 46 * 8 for op in world)
+        assert all(len(op._sr_rows[0]) == 46 * 8 for op in world)
         for r in sorted({op.dst_rank for op in world}):
             ops = [op for op in world if op.dst_rank == r]
             ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
@@ -499,6 +499,15 @@ def test_encoded_ops_match_the_attribute_walk():
     ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
     inferred = {n: infer_dst_shard([op for op in ops if op.param_name == n]) for n in ids}
     assert decode(ops, inferred, ids) == decode(walked(ops), inferred, ids)
+    # so does an op whose source or piece meta was replaced after scheduling
+    # (here by a meta of another shape, whose rows the encoding does not hold)
+    shards = {op.param_name: op.dst_shard_meta for op in ops}
+    edited = [copy.copy(op) for op in ops]
+    edited[0].src_meta = TensorMeta(name=ops[0].param_name, dtype=torch.float64, shape=(3, 5))
+    edited[1].dst_meta = copy.copy(ops[1].dst_meta)
+    got, want = decode(edited, shards, ids), decode(walked(edited), shards, ids)
+    assert got == want and got[0][1] != decode(ops, shards, ids)[0][1]
+    assert host.piece_numels(edited).tolist() == host.piece_numels(walked(edited)).tolist()
 
 
 def test_schedule_positions_match_a_scan():
