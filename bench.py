@@ -220,9 +220,11 @@ def row_sweep(nbytes: int, steps: int) -> list:
     through sr_gather.  "cat": two [R, C] f32 sources written as the column
     halves of one [R, 2C] destination (the dim -1 merge: strided writes).
     "split": one [R, 2C] source read as two [R, C] destinations (the dim -1
-    split: strided reads).  A row of C f32 is the row width swept; every case
-    reads and writes ``nbytes``.  Two contiguous RECAST cases (the fused
-    fp32 -> bf16 unpack) come first."""
+    split: strided reads).  "slice": one band of C columns read out of an
+    [R, 8C] source (one destination's piece of a dim -1 split eight ways:
+    sparse strided reads over eight times the bytes).  A row of C f32 is the
+    row width swept; every case reads and writes ``nbytes``.  Two contiguous
+    RECAST cases (the fused fp32 -> bf16 unpack) come first."""
     import ctypes
     import torch
     from suika_amd import _lib
@@ -297,6 +299,8 @@ def row_sweep(nbytes: int, steps: int) -> list:
             "flat": ([(r, 2 * c)], [(r, 2 * c)], [(0, 0, r, 2 * c, 0, 0)]),
             "cat": ([(r, c), (r, c)], [(r, 2 * c)], [(0, 0, r, c, 0, 0), (1, 0, r, c, 0, c)]),
             "split": ([(r, 2 * c)], [(r, c), (r, c)], [(0, 0, r, c, 0, 0), (0, 1, r, c, c, 0)]),
+            # the fifth of eight bands of 2R rows: nbytes read, nbytes written
+            "slice": ([(2 * r, 8 * c)], [(2 * r, c)], [(0, 0, 2 * r, c, 4 * c, 0)]),
         }
         for name, (ss, ds, pcs) in cases.items():
             if name == "flat" and width != ROW_SWEEP_BYTES[0]:
