@@ -722,9 +722,9 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
 constexpr int64_t kEncodingWords = 2 * kMetaWords + 4;
 
 // The encoding attached to `op`, or null for an op built otherwise (by the
-// caller, or the reference's own class) or whose src_meta or dst_meta has
-// been replaced since.  `hold` keeps it alive.
-const int64_t* op_encoding(PyObject* op, py::object* hold) {
+// caller, or the reference's own class) or whose dst_meta (and, with
+// `source`, src_meta) has been replaced since.  `hold` keeps it alive.
+const int64_t* op_encoding(PyObject* op, py::object* hold, bool source = true) {
   const Names& N = names_();
   PyObject* v = nullptr;
   if (_PyObject_LookupAttr(op, N.sr_rows, &v) < 0) throw py::error_already_set();
@@ -733,7 +733,8 @@ const int64_t* op_encoding(PyObject* op, py::object* hold) {
   if (!PyTuple_Check(v) || PyTuple_GET_SIZE(v) != 3) return nullptr;
   PyObject* rows = PyTuple_GET_ITEM(v, 0);
   if (!PyBytes_Check(rows) || PyBytes_GET_SIZE(rows) != Py_ssize_t(kEncodingWords * sizeof(int64_t))) return nullptr;
-  if (attr(op, N.src_meta).ptr() != PyTuple_GET_ITEM(v, 1) || attr(op, N.dst_meta).ptr() != PyTuple_GET_ITEM(v, 2))
+  if ((source && attr(op, N.src_meta).ptr() != PyTuple_GET_ITEM(v, 1)) ||
+      attr(op, N.dst_meta).ptr() != PyTuple_GET_ITEM(v, 2))
     return nullptr;
   return reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(rows));
 }
@@ -998,7 +999,7 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
 int64_t piece_numel(PyObject* op, bool* padded = nullptr) {
   const Names& N = names_();
   py::object hold;
-  if (const int64_t* enc = op_encoding(op, &hold)) {
+  if (const int64_t* enc = op_encoding(op, &hold, /*source=*/false)) {   // the piece alone
     // the schedule's encoding: shard row at kMetaWords (ndim at 3, shape
     // from 4, tp degree at 14, kind at 15), then the piece
     int64_t w[kEncodingWords];
@@ -1070,7 +1071,8 @@ py::tuple name_runs(py::list ops) {
 // The ops of `rank` out of a whole schedule (any sequence; `positions`, when
 // given, says where they are), and their name_runs, in one pass over the
 // schedule: (ops, order, starts, elements
-// per tensor, single, {name: tensor index}, padded per tensor).  A padded
+// per tensor, single, {name: tensor index}, padded per tensor, tensor indices
+// largest first, running total of their elements in that order).  A padded
 // tensor (a vocabulary shard with padding rows) has more elements than its
 // pieces' total; every other tensor's size is its pieces' total.
 py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions) {
@@ -1115,7 +1117,24 @@ py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions) {
     pd[t] = false;
     for (int64_t j = starts.data()[t]; j < starts.data()[t + 1]; ++j) pd[t] = pd[t] || padded_op[order.data()[j]];
   }
-  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3], runs[4], padded);
+  // the launch order: tensors largest first (stable), and the running total
+  // of their elements in that order
+  const RowTable totals = runs[2].cast<RowTable>();
+  std::vector<int64_t> idx(static_cast<size_t>(m));
+  for (int64_t t = 0; t < m; ++t) idx[size_t(t)] = t;
+  const int64_t* tot = totals.data();
+  std::stable_sort(idx.begin(), idx.end(), [tot](int64_t a, int64_t b) { return tot[a] > tot[b]; });
+  py::array_t<int64_t> launch({m});
+  std::copy(idx.begin(), idx.end(), launch.mutable_data());
+  py::list cum(m);
+  int64_t acc = 0;
+  for (int64_t i = 0; i < m; ++i) {
+    acc += tot[idx[size_t(i)]];
+    PyObject* v = PyLong_FromLongLong(acc);
+    if (!v) throw py::error_already_set();
+    PyList_SET_ITEM(cum.ptr(), i, v);
+  }
+  return py::make_tuple(ops, runs[0], runs[1], runs[2], runs[3], runs[4], padded, launch, cum);
 }
 
 py::tuple runs_of(py::list ops, const int64_t* e, Py_ssize_t n) {

@@ -30,6 +30,7 @@ intended ``cat`` in ascending piece order.
 """
 from __future__ import annotations
 
+import bisect
 import contextlib
 import gc
 import time
@@ -188,7 +189,7 @@ def execute_param_transfer(
     itemsize = [first[f].element_size() if f in first else 0 for f in normal]
     elem_bytes = sum(itemsize)   # over all moved fields (balances the launch groups)
     n_copies = sum(1 for sf in recast.values() if sf in normal)   # bf16 recast targets
-    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:5])
+    groups = _pipeline_groups(ops, elem_bytes, pipeline, len(normal) + n_copies, runs=runs[1:])
     # fresh destinations of the direct route: their allocations are made on
     # a helper thread from here on, tensor by tensor in launch order, while
     # this thread plans the groups (each tensor's elements: its pieces';
@@ -607,13 +608,23 @@ class _LaunchGroups:
         self.pipeline = int(pipeline)
         self.per_name = max(1, int(tensors_per_name))
         # op indices tensor by tensor, tensors in order of first appearance,
-        # and each tensor's elements (``runs``: already computed for ``ops``)
-        self.order, self.starts, numel = (runs if runs is not None else _lib.host().name_runs(self.ops))[:3]
+        # and each tensor's elements (``runs``: already computed for ``ops``,
+        # from rank_runs with the tensors largest first and the running total
+        # of their elements in that order)
+        r = runs if runs is not None else _lib.host().name_runs(self.ops)
+        self.order, self.starts, numel = r[:3]
         self.n = len(numel)
-        gpu_ns = numel * (2.0 * elem_bytes / GATHER_BYTES_PER_NS)
-        self.rank = np.argsort(-gpu_ns, kind="stable")          # largest first
-        self.cum = np.cumsum(gpu_ns[self.rank])
-        self._cum = self.cum.tolist()                           # plain floats for the cutter
+        scale = 2.0 * elem_bytes / GATHER_BYTES_PER_NS           # GPU ns per element
+        if scale > 0:
+            if len(r) > 7:
+                self.rank, total = r[6], r[7]
+            else:
+                self.rank = np.argsort(-numel, kind="stable")   # largest first
+                total = np.cumsum(numel[self.rank]).tolist()
+            self._cum = [t * scale for t in total]               # GPU ns of the first k tensors
+        else:
+            self.rank = np.arange(self.n, dtype=np.int64)
+            self._cum = [0.0] * self.n
         self.plan_ns = float(PLAN_NS_PER_TENSOR)                 # per destination tensor
 
     def _gpu(self, a: int, b: int) -> float:
@@ -649,7 +660,7 @@ class _LaunchGroups:
         if self.pipeline <= 1 or self.n <= 1:
             yield self.ops
             return
-        end = min(self.n, int(np.searchsorted(self.cum, FIRST_GROUP_NS, side="left")) + 1)
+        end = min(self.n, bisect.bisect_left(self._cum, FIRST_GROUP_NS) + 1)
         start, groups = 0, 1
         while True:
             t0 = _clock_ns()
@@ -668,7 +679,7 @@ class _LaunchGroups:
         """All groups at once, at the prior planning rate (no timing)."""
         if self.pipeline <= 1 or self.n <= 1:
             return [self.ops]
-        bounds = [0, min(self.n, int(np.searchsorted(self.cum, FIRST_GROUP_NS, side="left")) + 1)]
+        bounds = [0, min(self.n, bisect.bisect_left(self._cum, FIRST_GROUP_NS) + 1)]
         while bounds[-1] < self.n:
             bounds.append(self._next_end(bounds[-2], bounds[-1], len(bounds)))
         return [self._take(a, b) for a, b in zip(bounds[:-1], bounds[1:])]

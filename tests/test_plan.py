@@ -492,7 +492,7 @@ def test_encoded_ops_match_the_attribute_walk():
             assert decode(ops, shards, ids) == decode(walked(ops), shards, ids), (key, r)
             assert host.piece_numels(ops).tolist() == host.piece_numels(walked(ops)).tolist(), (key, r)
             for a, b in zip(host.rank_runs(ops, r)[1:], host.rank_runs(walked(ops), r)[1:]):
-                assert (a == b) if isinstance(a, (bool, dict)) else a.tolist() == b.tolist(), (key, r)
+                assert (a == b) if isinstance(a, (bool, dict, list)) else a.tolist() == b.tolist(), (key, r)
     # a caller's own shard object (equal, not the op's) takes the walk
     w = CONFIGS["gpt125m_tp2_tp4"]
     ops = [op for op in schedule_param_transfer(*w.layouts()) if op.dst_rank == w.dst_rank]
@@ -522,7 +522,7 @@ def test_schedule_positions_match_a_scan():
     def same(a, b):
         assert a[0] == b[0]
         for x, y in zip(a[1:], b[1:]):
-            assert (x == y) if isinstance(x, (bool, dict)) else x.tolist() == y.tolist()
+            assert (x == y) if isinstance(x, (bool, dict, list)) else x.tolist() == y.tolist()
 
     for key in CONFIG_ORDER:
         sched = schedule_param_transfer(*CONFIGS[key].layouts())
@@ -555,7 +555,7 @@ def test_rank_runs_and_ordered_result():
         world = schedule_param_transfer(*w.layouts())
         for sched in (world, tuple(world[::-1]), world[5:] + world[:5]):
             for r in sorted({op.dst_rank for op in sched}):
-                ops, order, starts, numel, single, index, padded = host.rank_runs(sched, r)
+                ops, order, starts, numel, single, index, padded, launch, total = host.rank_runs(sched, r)
                 want_ops = [op for op in sched if op.dst_rank == r]
                 assert ops == want_ops, (key, r)
                 names = list(dict.fromkeys(op.param_name for op in want_ops))
@@ -565,6 +565,9 @@ def test_rank_runs_and_ordered_result():
                 assert numel.tolist() == [sum(want_ops[i].dst_meta.numel() for i in members[n]) for n in names]
                 assert single == all(m == list(range(m[0], m[0] + len(m))) for m in members.values())
                 assert index == {n: i for i, n in enumerate(names)}
+                # tensors largest first (ties in index order) and their running total
+                assert launch.tolist() == np.argsort(-numel, kind="stable").tolist()
+                assert total == np.cumsum(numel[launch]).tolist()
                 # a padded vocabulary shard is larger than its pieces' total
                 assert padded.tolist() == [want_ops[members[n][0]].dst_shard_meta.kind == "vocab_pad"
                                            for n in names]
@@ -577,7 +580,7 @@ def test_rank_runs_and_ordered_result():
     # ops in schedule order (tensors whose ops are not consecutive included)
     sched = CONFIGS["llama7b_tp4pp2_tp2pp2"].ops()
     sched = sched[7:] + sched[:7]
-    ops, order, starts, numel, single, index, _ = host.rank_runs(sched, sched[0].dst_rank)
+    ops, order, starts, numel, single, index = host.rank_runs(sched, sched[0].dst_rank)[:6]
     names = list(index)
     rng = np.random.default_rng(5)
     for size in (1, 5, len(names)):
