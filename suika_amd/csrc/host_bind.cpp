@@ -114,7 +114,7 @@ py::object lookup(PyObject* d, PyObject* key) {
 // Interned attribute names (created once, never released).
 struct Names {
   PyObject *dtype, *shape, *kind_args, *tp_meta, *kind, *rows, *name, *dict;
-  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta, *sr_rows;
+  PyObject *param_name, *src_rank, *dst_rank, *src_meta, *dst_meta, *dst_shard_meta, *tables;
   PyObject *chunk, *vocab_pad, *qkv_heads;
   Names() {
     auto in = [](const char* s) { return PyUnicode_InternFromString(s); };
@@ -122,7 +122,7 @@ struct Names {
     kind = in("kind"); rows = in("rows"); name = in("name"); dict = in("__dict__");
     param_name = in("param_name"); src_rank = in("src_rank"); dst_rank = in("dst_rank");
     src_meta = in("src_meta"); dst_meta = in("dst_meta"); dst_shard_meta = in("dst_shard_meta");
-    sr_rows = in("_sr_rows");
+    tables = in("_tables");
     chunk = in("chunk"); vocab_pad = in("vocab_pad"); qkv_heads = in("qkv_heads");
   }
 };
@@ -714,30 +714,124 @@ void meta_row(PyObject* m, int64_t rank, int64_t name_id, int64_t* row) {
   }
 }
 
-// The encoding a scheduled op carries (make_ops): the sr_meta rows of its
-// source meta and of its destination shard, then its piece (tp index and
-// degree, first and end row; as in sr_op), with the source and piece meta
-// objects it was made from.  TensorMeta objects are values: nothing edits
-// one once scheduled, so the rows stay those of the objects.
+// The encoding of a scheduled op: the sr_meta rows of its source meta and of
+// its destination shard, then its piece (tp index and degree, first and end
+// row; as in sr_op).
 constexpr int64_t kEncodingWords = 2 * kMetaWords + 4;
 
-// The encoding attached to `op`, or null for an op built otherwise (by the
-// caller, or the reference's own class) or whose dst_meta (and, with
-// `source`, src_meta) has been replaced since.  `hold` keeps it alive.
-const int64_t* op_encoding(PyObject* op, py::object* hold, bool source = true) {
-  const Names& N = names_();
-  PyObject* v = nullptr;
-  if (_PyObject_LookupAttr(op, N.sr_rows, &v) < 0) throw py::error_already_set();
-  if (!v) return nullptr;
-  *hold = py::reinterpret_steal<py::object>(v);
-  if (!PyTuple_Check(v) || PyTuple_GET_SIZE(v) != 3) return nullptr;
-  PyObject* rows = PyTuple_GET_ITEM(v, 0);
-  if (!PyBytes_Check(rows) || PyBytes_GET_SIZE(rows) != Py_ssize_t(kEncodingWords * sizeof(int64_t))) return nullptr;
-  if ((source && attr(op, N.src_meta).ptr() != PyTuple_GET_ITEM(v, 1)) ||
-      attr(op, N.dst_meta).ptr() != PyTuple_GET_ITEM(v, 2))
-    return nullptr;
-  return reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(rows));
-}
+// The tables a schedule's ops are encoded from: suika_amd.meta.Schedule
+// keeps them as `_tables` = (its sr_op table, the sr_meta tables of both
+// layouts, the layouts' meta objects, each op's piece meta), row k for the
+// op at position k, and drops them when the list changes.  An op is encoded
+// from them while the schedule still holds its tables and the op at the
+// position found for it, and the op still names the scheduled metas; any
+// other op is read from its attributes.  TensorMeta objects are values:
+// nothing edits one in place once scheduled.
+//
+// Positions are found by object identity in a table that rank_runs fills
+// with the ops it takes (note), else with the whole list on first use.
+class Encoded {
+ public:
+  Encoded(py::object schedule, py::object tables) {
+    if (schedule.is_none() || tables.is_none()) return;
+    py::tuple t = tables.cast<py::tuple>();
+    if (t.size() != 6) throw py::value_error("schedule tables: 6 items expected");
+    sched_ = schedule;
+    tables_ = tables;
+    ops_ = t[0].cast<RowTable>();
+    src_ = t[1].cast<RowTable>();
+    dst_ = t[2].cast<RowTable>();
+    src_objs_ = t[3];
+    dst_objs_ = t[4];
+    pieces_ = t[5];
+    if (!PyList_Check(sched_.ptr()) || !PyList_Check(src_objs_.ptr()) || !PyList_Check(dst_objs_.ptr()) ||
+        !PyList_Check(pieces_.ptr()) || ops_.ndim() != 2 || ops_.shape(1) != 9 || src_.ndim() != 2 ||
+        src_.shape(1) != kMetaWords || dst_.ndim() != 2 || dst_.shape(1) != kMetaWords ||
+        ops_.shape(0) != PyList_GET_SIZE(sched_.ptr()) || ops_.shape(0) != PyList_GET_SIZE(pieces_.ptr()) ||
+        src_.shape(0) != PyList_GET_SIZE(src_objs_.ptr()) || dst_.shape(0) != PyList_GET_SIZE(dst_objs_.ptr()))
+      throw py::value_error("schedule tables: inconsistent");
+    valid_ = true;
+  }
+
+  // Whether the schedule still holds these tables (checked once per native
+  // call; a changed schedule has dropped them).
+  bool current() const {
+    if (!valid_) return false;
+    PyObject* v = nullptr;
+    if (_PyObject_LookupAttr(sched_.ptr(), names_().tables, &v) < 0) throw py::error_already_set();
+    Py_XDECREF(v);   // compared by identity only; the schedule holds it
+    return v == tables_.ptr();
+  }
+
+  // `op` is the schedule's op at position k.
+  void note(PyObject* op, int64_t k) const {
+    if (!valid_) return;
+    if ((used_ + 1) * 2 > slots_.size()) grow();
+    const size_t mask = slots_.size() - 1;
+    size_t i = slot_of(op) & mask;
+    while (slots_[i].op && slots_[i].op != op) i = (i + 1) & mask;
+    if (!slots_[i].op) ++used_;
+    slots_[i] = Slot{op, k};
+  }
+
+  // op's encoding into w and its destination shard object, when op is
+  // encoded (see above; `source`: its source meta is checked too).
+  bool get(PyObject* op, int64_t* w, bool source, PyObject** shard = nullptr) const {
+    if (!valid_) return false;
+    if (slots_.empty()) {
+      const Py_ssize_t n = PyList_GET_SIZE(sched_.ptr());
+      for (Py_ssize_t k = 0; k < n; ++k) note(PyList_GET_ITEM(sched_.ptr(), k), k);
+      if (slots_.empty()) return false;
+    }
+    const size_t mask = slots_.size() - 1;
+    size_t i = slot_of(op) & mask;
+    while (slots_[i].op && slots_[i].op != op) i = (i + 1) & mask;
+    if (!slots_[i].op) return false;
+    const int64_t k = slots_[i].at;
+    if (k < 0 || k >= ops_.shape(0) || k >= PyList_GET_SIZE(sched_.ptr()) ||
+        PyList_GET_ITEM(sched_.ptr(), k) != op)
+      return false;
+    const Names& N = names_();
+    const int64_t* r = ops_.data() + k * 9;
+    const int64_t s_row = r[3], d_row = r[4];
+    if (s_row < 0 || s_row >= src_.shape(0) || d_row < 0 || d_row >= dst_.shape(0)) return false;
+    if (source && attr(op, N.src_meta).ptr() != PyList_GET_ITEM(src_objs_.ptr(), s_row)) return false;
+    if (attr(op, N.dst_meta).ptr() != PyList_GET_ITEM(pieces_.ptr(), k)) return false;
+    std::memcpy(w, src_.data() + s_row * kMetaWords, sizeof(int64_t) * kMetaWords);
+    std::memcpy(w + kMetaWords, dst_.data() + d_row * kMetaWords, sizeof(int64_t) * kMetaWords);
+    std::copy(r + 5, r + 9, w + 2 * kMetaWords);
+    if (shard) *shard = PyList_GET_ITEM(dst_objs_.ptr(), d_row);
+    return true;
+  }
+
+ private:
+  struct Slot {
+    PyObject* op;
+    int64_t at;
+  };
+  static size_t slot_of(PyObject* op) {
+    uint64_t x = uint64_t(reinterpret_cast<uintptr_t>(op)) >> 4;
+    x *= 0x9E3779B97F4A7C15ull;
+    return size_t(x ^ (x >> 32));
+  }
+  void grow() const {
+    std::vector<Slot> old(std::max<size_t>(64, slots_.size() * 2), Slot{nullptr, -1});
+    old.swap(slots_);
+    used_ = 0;
+    for (const Slot& s : old)
+      if (s.op) note(s.op, s.at);
+  }
+
+  bool valid_ = false;
+  py::object sched_, tables_, src_objs_, dst_objs_, pieces_;
+  RowTable ops_, src_, dst_;
+  mutable std::vector<Slot> slots_;   // keys are borrowed: the schedule holds every op
+  mutable size_t used_ = 0;
+};
+
+// The encoding to use in one native call: E while its schedule still holds
+// its tables, else none.
+const Encoded* live(const Encoded* E) { return E && E->current() ? E : nullptr; }
 
 // A ParamLayout's {rank: {name: TensorMeta}} as an [n, 21] sr_meta table,
 // rank by rank in dict order; `names` maps names to ids (extended in first-
@@ -810,25 +904,17 @@ py::object derived(PyObject* meta_cls, PyObject* shard, PyObject* tp_meta, PyObj
 
 // TransferOps of an sr_op table (sr_schedule's output): source metas and
 // destination shards are the layouts' own objects, pieces derived from the
-// shards.  With the layouts' sr_meta tables (`src_rows`, `dst_rows`: row i
-// encodes src_objs[i] / dst_objs[i]), each op also carries its encoding
-// (`_sr_rows`, see op_encoding), which spares encode_ops the walk over its
-// metas' attributes.
+// shards.  A `pieces` list receives each op's piece meta: what the
+// schedule's encoding (Encoded) needs besides the tables sr_schedule read.
 py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::list dst_objs, py::handle op_cls,
-                  py::handle meta_cls, py::object src_rows, py::object dst_rows) {
+                  py::handle meta_cls, py::object pieces) {
   const Names& N = names_();
   if (!PyType_Check(op_cls.ptr()) || !PyType_Check(meta_cls.ptr())) throw py::type_error("classes expected");
   const int64_t n = ops.ndim() == 2 ? ops.shape(0) : 0;
   if (n && ops.shape(1) != 9) throw py::value_error("op rows must have 9 columns");
-  const bool encode = !src_rows.is_none() && !dst_rows.is_none();
-  RowTable srow, drow;
-  if (encode) {
-    srow = src_rows.cast<RowTable>();
-    drow = dst_rows.cast<RowTable>();
-    if (srow.ndim() != 2 || drow.ndim() != 2 || srow.shape(1) != kMetaWords || drow.shape(1) != kMetaWords ||
-        srow.shape(0) != int64_t(src_objs.size()) || drow.shape(0) != int64_t(dst_objs.size()))
-      throw py::value_error("meta tables must have one 21-word row per meta object");
-  }
+  const bool encode = !pieces.is_none();
+  if (encode && (!PyList_Check(pieces.ptr()) || PyList_GET_SIZE(pieces.ptr()) != 0))
+    throw py::value_error("pieces must be an empty list");
   py::list out(n);
   const int64_t* r = ops.data();
   for (int64_t i = 0; i < n; ++i, r += 9) {
@@ -857,18 +943,7 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
     set(d, N.src_meta, PyList_GET_ITEM(src_objs.ptr(), s_row));
     set(d, N.dst_meta, piece.ptr());
     set(d, N.dst_shard_meta, shard);
-    if (encode) {
-      int64_t w[kEncodingWords];
-      std::memcpy(w, srow.data() + s_row * kMetaWords, sizeof(int64_t) * kMetaWords);
-      std::memcpy(w + kMetaWords, drow.data() + d_row * kMetaWords, sizeof(int64_t) * kMetaWords);
-      w[2 * kMetaWords] = p_idx;
-      w[2 * kMetaWords + 1] = p_deg;
-      w[2 * kMetaWords + 2] = r0;
-      w[2 * kMetaWords + 3] = r1;
-      py::bytes blob(reinterpret_cast<const char*>(w), sizeof(w));
-      py::tuple enc = py::make_tuple(blob, py::handle(PyList_GET_ITEM(src_objs.ptr(), s_row)), piece);
-      set(d, N.sr_rows, enc.ptr());
-    }
+    if (encode && PyList_Append(pieces.ptr(), piece.ptr()) != 0) throw py::error_already_set();
     PyList_SET_ITEM(out.ptr(), i, op.release().ptr());
   }
   return out;
@@ -879,10 +954,11 @@ py::list make_ops(const RowTable& ops, py::list names, py::list src_objs, py::li
 // Metas are numbered in first-use order (each object once per name); a piece
 // is encoded relative to its shard: (0, 0) for the shard itself, else its tp
 // index and degree (an unsplit piece of a split shard: (0, 1)) and rows.  An
-// op that carries the schedule's encoding (op_encoding) of the shard it
-// names is copied from it: its source meta gets a row of its own.
-py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
+// op encoded by the schedule (Encoded) whose shard is the one `shards` names
+// is copied from its tables: its source meta gets a row of its own.
+py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids, const Encoded* E) {
   const Names& N = names_();
+  E = live(E);
   const int64_t n = int64_t(ops.size());
   py::array_t<int64_t> op_rows({n, int64_t(9)});
   int64_t* orow = op_rows.mutable_data();
@@ -913,11 +989,9 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
       throw py::key_error("no shard for " + py::str(name).cast<std::string>());
     }
     const int64_t nid = as_int(nid_obj);
-    py::object hold;
-    const int64_t* enc = op_encoding(op, &hold);
-    if (enc && attr(op, N.dst_shard_meta).ptr() == shard) {
-      int64_t w[kEncodingWords];
-      std::memcpy(w, enc, sizeof(w));
+    int64_t w[kEncodingWords];
+    PyObject* enc_shard = nullptr;
+    if (E && E->get(op, w, /*source=*/true, &enc_shard) && enc_shard == shard) {
       orow[0] = nid;
       orow[1] = as_int(attr(op, N.src_rank).ptr());
       orow[2] = as_int(attr(op, N.dst_rank).ptr());
@@ -996,14 +1070,12 @@ py::tuple encode_ops(py::list ops, py::dict shards, py::dict name_ids) {
 // a chunk piece).  Used to balance launch groups.  With `padded`, whether
 // the piece belongs to a padded vocabulary shard (whose size is not its
 // pieces' total: it also holds rows no piece covers).
-int64_t piece_numel(PyObject* op, bool* padded = nullptr) {
+int64_t piece_numel(PyObject* op, bool* padded = nullptr, const Encoded* E = nullptr) {
   const Names& N = names_();
-  py::object hold;
-  if (const int64_t* enc = op_encoding(op, &hold, /*source=*/false)) {   // the piece alone
+  int64_t w[kEncodingWords];
+  if (E && E->get(op, w, /*source=*/false)) {   // the piece alone
     // the schedule's encoding: shard row at kMetaWords (ndim at 3, shape
     // from 4, tp degree at 14, kind at 15), then the piece
-    int64_t w[kEncodingWords];
-    std::memcpy(w, enc, sizeof(w));
     const int64_t* shard = w + kMetaWords;
     const int64_t nd = shard[3], p_deg = w[2 * kMetaWords + 1], r0 = w[2 * kMetaWords + 2],
                   r1 = w[2 * kMetaWords + 3];
@@ -1069,14 +1141,16 @@ py::tuple name_runs(py::list ops) {
 }
 
 // The ops of `rank` out of a whole schedule (any sequence; `positions`, when
-// given, says where they are), and their name_runs, in one pass over the
+// given, says where they are; `encoding`, the schedule's Encoded tables), and
+// their name_runs, in one pass over the
 // schedule: (ops, order, starts, elements
 // per tensor, single, {name: tensor index}, padded per tensor, tensor indices
 // largest first, running total of their elements in that order).  A padded
 // tensor (a vocabulary shard with padding rows) has more elements than its
 // pieces' total; every other tensor's size is its pieces' total.
-py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions) {
+py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions, const Encoded* E) {
   const Names& N = names_();
+  E = live(E);
   py::object seq = py::reinterpret_steal<py::object>(PySequence_Fast(schedule.ptr(), "ops must be a sequence"));
   if (!seq) throw py::error_already_set();
   const Py_ssize_t total = PySequence_Fast_GET_SIZE(seq.ptr());
@@ -1104,8 +1178,9 @@ py::tuple rank_runs(py::object schedule, int64_t rank, py::object positions) {
     const Py_ssize_t k = indexed ? cand[size_t(c)] : c;
     if (!indexed && as_int(attr(items[k], N.dst_rank).ptr()) != rank) continue;
     if (PyList_Append(ops.ptr(), items[k]) != 0) throw py::error_already_set();
+    if (E) E->note(items[k], int64_t(k));
     bool padded = false;
-    numel.push_back(piece_numel(items[k], &padded));
+    numel.push_back(piece_numel(items[k], &padded, E));
     padded_op.push_back(padded ? 1 : 0);
   }
   py::tuple runs = runs_of(ops, numel.data(), Py_ssize_t(numel.size()));
@@ -1505,7 +1580,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
                        py::function infer_shard, int64_t device_index, const std::string& who,
                        uint32_t tile_bytes, uint32_t max_blocks, uint32_t flags, py::dtype tensor_dt,
                        py::dtype piece_dt, bool gather, uint64_t stream, py::object dst_part,
-                       py::object ahead, bool host_ok) {
+                       py::object ahead, bool host_ok, const Encoded* encoding) {
   // host addresses are for sr_stage_pack alone: a kernel must never see one
   if (gather && host_ok) throw py::value_error("host-resident sources cannot be gathered on the device");
   const Names& N = names_();
@@ -1608,7 +1683,7 @@ py::tuple plan_sources(py::list ops, py::function source, py::list fields, py::l
       }
     }
   }
-  py::tuple enc = encode_ops(ops, shards, name_ids);
+  py::tuple enc = encode_ops(ops, shards, name_ids, encoding);
   py::array_t<int64_t> metas = enc[0].cast<py::array_t<int64_t>>(), op_rows = enc[1].cast<py::array_t<int64_t>>();
   const int64_t no_recast = 0;
 
@@ -1694,6 +1769,10 @@ PYBIND11_MODULE(_suika_host, m) {
         py::arg("dtypes"));
   m.def("arena_tensors", &arena_tensors, py::arg("ops"), py::arg("source"), py::arg("order"), py::arg("targets"),
         py::arg("device"));
+  py::class_<Encoded>(m, "ScheduleEncoding",
+                      "a schedule and the tables its ops were made from (sr_op table, both layouts' sr_meta "
+                      "tables and meta objects, each op's piece meta)")
+      .def(py::init<py::object, py::object>(), py::arg("schedule"), py::arg("tables"));
   py::class_<AheadBlocks>(m, "AheadBlocks",
                           "Destination blocks of one drop-in call, made ahead on the helper thread")
       .def("finish", &AheadBlocks::finish, "stop the helper on these blocks and free those no tensor took");
@@ -1715,16 +1794,21 @@ PYBIND11_MODULE(_suika_host, m) {
   m.def("encode_layout", &encode_layout, py::arg("layout"), py::arg("names"), py::arg("objs"));
   m.def("piece_numels", &piece_numels, py::arg("ops"));
   m.def("name_runs", &name_runs, py::arg("ops"));
-  m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"), py::arg("positions") = py::none());
+  m.def("rank_runs", &rank_runs, py::arg("schedule"), py::arg("rank"), py::arg("positions") = py::none(),
+        py::arg("encoding") = static_cast<const Encoded*>(nullptr));
   m.def("take_ops", &take_ops, py::arg("ops"), py::arg("order"), py::arg("starts"), py::arg("picked"));
   m.def("ordered_result", &ordered_result, py::arg("ops"), py::arg("target"), py::arg("field_order"));
-  m.def("encode_ops", &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"));
+  m.def(
+      "encode_ops",
+      &encode_ops, py::arg("ops"), py::arg("shards"), py::arg("name_ids"),
+      py::arg("encoding") = static_cast<const Encoded*>(nullptr));
   m.def("make_ops", &make_ops, py::arg("ops"), py::arg("names"), py::arg("src_objs"), py::arg("dst_objs"),
-        py::arg("op_cls"), py::arg("meta_cls"), py::arg("src_rows") = py::none(), py::arg("dst_rows") = py::none());
+        py::arg("op_cls"), py::arg("meta_cls"), py::arg("pieces") = py::none());
   m.def("device_views", &device_views, py::arg("base"), py::arg("views"), py::arg("device_index"));
   m.def("plan_sources", &plan_sources, py::arg("ops"), py::arg("source"), py::arg("fields"),
         py::arg("recast_names"), py::arg("infer_shard"), py::arg("device_index"), py::arg("who"),
         py::arg("tile_bytes"), py::arg("max_blocks"), py::arg("flags"), py::arg("tensor_dtype"),
         py::arg("piece_dtype"), py::arg("gather") = false, py::arg("stream") = 0, py::arg("dst_part") = py::none(),
-        py::arg("ahead") = py::none(), py::arg("host_ok") = false);
+        py::arg("ahead") = py::none(), py::arg("host_ok") = false,
+        py::arg("encoding") = static_cast<const Encoded*>(nullptr));
 }

@@ -395,28 +395,43 @@ def _encode_layout(pl: ParamLayout, names: Dict[str, int], objs: List[TensorMeta
 
 class Schedule(list):
     """The ops ``schedule_param_transfer`` returns: a list, which also keeps
-    the positions of each destination rank's ops, so that the drop-in call
-    takes a rank's ops without scanning the whole schedule.  Any change to
-    the list drops the positions (the call then scans it)."""
+    each op's destination rank as an array, so that the drop-in call takes a
+    rank's ops without reading every op's attributes, and the tables its ops
+    were made from (the sr_op table, both layouts' sr_meta tables and meta
+    objects, each op's piece meta), so that the call encodes them without
+    walking their metas' attributes.  Any change to the list drops both (the
+    call then scans it and walks the metas)."""
 
-    def __init__(self, ops=(), dst_ranks=None):
+    def __init__(self, ops=(), dst_ranks=None, tables=None):
         super().__init__(ops)
-        self._positions: Optional[Dict[int, np.ndarray]] = None
-        if dst_ranks is not None and len(dst_ranks) == len(self):
-            order = np.argsort(dst_ranks, kind="stable")
-            ranks, first = np.unique(dst_ranks[order], return_index=True)
-            bounds = list(first) + [len(order)]
-            self._positions = {int(r): order[bounds[i]:bounds[i + 1]] for i, r in enumerate(ranks)}
+        n = len(self)
+        self._dst_ranks = dst_ranks if dst_ranks is not None and len(dst_ranks) == n else None
+        self._positions: Dict[int, np.ndarray] = {}
+        self._tables = tables if tables is not None and len(tables[0]) == n else None
 
     def positions_of(self, rank: int) -> Optional[np.ndarray]:
         """Positions of ``rank``'s ops in schedule order, or None when the
         list has changed since it was scheduled."""
-        if self._positions is None:
+        if self._dst_ranks is None:
             return None
-        return self._positions.get(int(rank), _NO_POSITIONS)
+        rank = int(rank)
+        found = self._positions.get(rank)
+        if found is None:
+            found = self._positions[rank] = np.flatnonzero(self._dst_ranks == rank)
+        return found
+
+    def encoding(self):
+        """The host extension's view of the tables (a ScheduleEncoding), or
+        None when the list has changed since it was scheduled."""
+        if self._tables is None:
+            return None
+        from . import _lib
+        return _lib.host().ScheduleEncoding(self, self._tables)
 
     def _changed(self) -> None:
-        self._positions = None
+        self._dst_ranks = None
+        self._positions = {}
+        self._tables = None
 
 
 def _dropping_positions(name):
@@ -432,7 +447,6 @@ def _dropping_positions(name):
 for _name in ("__setitem__", "__delitem__", "__iadd__", "__imul__", "append", "extend", "insert", "pop",
               "remove", "sort", "reverse", "clear"):
     setattr(Schedule, _name, _dropping_positions(_name))
-_NO_POSITIONS = np.zeros(0, dtype=np.int64)
 
 
 def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layout: ParamLayout,
@@ -477,8 +491,10 @@ def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layou
     # TransferOps over the layouts' own metas; a piece is its shard with
     # another tp meta (scale_to_tp) or a row interval (vocab_pad)
     table = ops[:n_ops.value]
-    schedule = Schedule(_lib.host().make_ops(table, list(names), src_objs, dst_objs, TransferOp, TensorMeta,
-                                             src, dst), table[:, 2])   # column 2: dst_rank
+    pieces: List[TensorMeta] = []
+    schedule = Schedule(_lib.host().make_ops(table, list(names), src_objs, dst_objs, TransferOp, TensorMeta, pieces),
+                        table[:, 2],   # column 2: dst_rank
+                        (table, src, dst, src_objs, dst_objs, pieces))
     if log_func is not None:
         for op in schedule:
             if op.src_rank != op.dst_rank:

@@ -168,8 +168,10 @@ def execute_param_transfer(
     prof.start("execute prologue")
     # this rank's ops, grouped by tensor with each tensor's elements, in one
     # pass over the schedule
-    runs = _lib.host().rank_runs(transfer_ops, int(rank),
-                                 transfer_ops.positions_of(rank) if type(transfer_ops) is Schedule else None)
+    scheduled = type(transfer_ops) is Schedule   # its rank positions and encoding tables ride along
+    encoding = transfer_ops.encoding() if scheduled else None
+    runs = _lib.host().rank_runs(transfer_ops, int(rank), transfer_ops.positions_of(rank) if scheduled else None,
+                                 encoding)
     ops = runs[0]
     normal = [f for f, t in expected_sub_fields if not _is_meta_field(t)]
     scalars = [f for f, t in expected_sub_fields if _is_meta_field(t)]
@@ -213,7 +215,8 @@ def execute_param_transfer(
     # the direct route's launch groups: planned, allocated and gathered in
     # one native call each
     gather = ReshardPlan.gatherer(source, normal, device, recast=recast, options=plan_options, rank=rank,
-                                  stream=stream) if route == "direct" and device.type == "cuda" else None
+                                  stream=stream, encoding=encoding) \
+        if route == "direct" and device.type == "cuda" else None
     target: StateDict = {}
     plans: List[ReshardPlan] = []
     buffers: List[List[Tensor]] = []

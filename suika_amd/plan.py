@@ -237,11 +237,12 @@ class ReshardPlan:
     @classmethod
     def gatherer(cls, source: Callable[[int], Mapping], fields: Sequence[str], device: torch.device,
                  recast: Optional[Mapping[str, str]] = None, options: Optional[PlanOptions] = None,
-                 rank: Optional[int] = None, stream=None):
+                 rank: Optional[int] = None, stream=None, encoding=None):
         """``gather_sources`` for many groups of ops with the same sources,
         fields, device, options and stream: what the groups share is checked
-        and converted once.  Returns ``gather(ops, dst=None, ahead=None) ->
-        (plan, destinations)``."""
+        and converted once.  ``encoding`` (the schedule's ``encoding()``)
+        encodes the ops of that schedule from its tables.  Returns
+        ``gather(ops, dst=None, ahead=None) -> (plan, destinations)``."""
         proto = cls.__new__(cls)
         proto._configure((), fields, recast, options)
         fields, recast, options, recast_of = proto.fields, proto.recast, proto.options, proto._recast_of
@@ -259,7 +260,7 @@ class ReshardPlan:
             self.fields, self.recast, self.options, self._recast_of, self._L = fields, recast, options, recast_of, L
             self._handle = ctypes.c_void_p()
             self._ops = ops
-            _, part = self._adopt(plan_sources(ops, source, fields, recast_names, *args, dst, ahead, False))
+            _, part = self._adopt(plan_sources(ops, source, fields, recast_names, *args, dst, ahead, False, encoding))
             return self, part
         return gather
 

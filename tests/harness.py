@@ -223,7 +223,8 @@ def poisoned_allocations():
         plan.gather_ptrs(src_ptrs, ptrs, stream)
         return plan, part
 
-    def make_gatherer(cls, source, fields, device, recast=None, options=None, rank=None, stream=None):
+    def make_gatherer(cls, source, fields, device, recast=None, options=None, rank=None, stream=None,
+                      encoding=None):
         return lambda ops, dst=None, ahead=None: gather(cls, ops, source, fields, device, recast, options, rank,
                                                         stream, dst, ahead)
 

@@ -457,57 +457,78 @@ def test_launch_groups_survive_a_group_planned_within_the_overhead(monkeypatch, 
 
 
 def test_encoded_ops_match_the_attribute_walk():
-    """The schedule's ops carry their encoding (the sr_meta rows of their
-    source meta and destination shard, and the piece); encode_ops copies it
-    and piece_numels / rank_runs compute from it instead of reading the
-    metas' attributes.  Both give the same tables op by op, on every config
-    and rank, and an op whose shard is not the one the caller names is
-    encoded from its attributes."""
+    """The schedule keeps the tables its ops were made from (sr_op table,
+    both layouts' sr_meta rows and meta objects, each op's piece); with the
+    schedule's encoding, encode_ops copies an op's rows and rank_runs
+    computes its piece's size from them instead of reading the metas'
+    attributes.  Both give the same tables op by op, on every config and
+    rank, whether or not rank_runs found the positions first.  An op the
+    encoding does not describe any more -- whose source or piece meta was
+    replaced, an op of another schedule, one whose shard is not the one the
+    caller names, any op once the list changed -- is read from its
+    attributes."""
     import copy
 
     from suika_amd import _lib
     from suika_amd.geometry import infer_dst_shard
     host = _lib.host()
 
-    def decode(ops, shards, ids):
-        metas, rows = host.encode_ops(ops, shards, ids)
+    def decode(ops, shards, ids, enc=None):
+        metas, rows = host.encode_ops(ops, shards, ids, enc)
         return [(tuple(r[[0, 1, 2, 5, 6, 7, 8]]), tuple(metas[r[3]]), tuple(metas[r[4]])) for r in rows]
 
-    def walked(ops):
-        out = []
-        for op in ops:
-            c = copy.copy(op)
-            del c.__dict__["_sr_rows"]
-            out.append(c)
-        return out
+    def same_runs(a, b):
+        for x, y in zip(a, b):
+            assert (x == y) if isinstance(x, (bool, dict, list)) else x.tolist() == y.tolist()
 
     for key in CONFIG_ORDER:
         w = CONFIGS[key]
         world = schedule_param_transfer(*w.layouts())
-        assert all(len(op._sr_rows[0]) == 46 * 8 for op in world)
         for r in sorted({op.dst_rank for op in world}):
             ops = [op for op in world if op.dst_rank == r]
             ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
             shards = {op.param_name: op.dst_shard_meta for op in ops}
-            assert decode(ops, shards, ids) == decode(walked(ops), shards, ids), (key, r)
-            assert host.piece_numels(ops).tolist() == host.piece_numels(walked(ops)).tolist(), (key, r)
-            for a, b in zip(host.rank_runs(ops, r)[1:], host.rank_runs(walked(ops), r)[1:]):
-                assert (a == b) if isinstance(a, (bool, dict, list)) else a.tolist() == b.tolist(), (key, r)
-    # a caller's own shard object (equal, not the op's) takes the walk
+            walked = decode(ops, shards, ids)
+            assert decode(ops, shards, ids, world.encoding()) == walked, (key, r)   # positions found on use
+            enc = world.encoding()
+            same_runs(host.rank_runs(world, r, world.positions_of(r), enc)[1:], host.rank_runs(list(world), r)[1:])
+            assert decode(ops, shards, ids, enc) == walked, (key, r)   # positions rank_runs found
     w = CONFIGS["gpt125m_tp2_tp4"]
-    ops = [op for op in schedule_param_transfer(*w.layouts()) if op.dst_rank == w.dst_rank]
+    world = schedule_param_transfer(*w.layouts())
+    enc = world.encoding()
+    ops = [op for op in world if op.dst_rank == w.dst_rank]
     ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
-    inferred = {n: infer_dst_shard([op for op in ops if op.param_name == n]) for n in ids}
-    assert decode(ops, inferred, ids) == decode(walked(ops), inferred, ids)
-    # so does an op whose source or piece meta was replaced after scheduling
-    # (here by a meta of another shape, whose rows the encoding does not hold)
     shards = {op.param_name: op.dst_shard_meta for op in ops}
-    edited = [copy.copy(op) for op in ops]
-    edited[0].src_meta = TensorMeta(name=ops[0].param_name, dtype=torch.float64, shape=(3, 5))
-    edited[1].dst_meta = copy.copy(ops[1].dst_meta)
-    got, want = decode(edited, shards, ids), decode(walked(edited), shards, ids)
-    assert got == want and got[0][1] != decode(ops, shards, ids)[0][1]
-    assert host.piece_numels(edited).tolist() == host.piece_numels(walked(edited)).tolist()
+    before = decode(ops, shards, ids, enc)
+    # a caller's own shard object (equal, not the op's) takes the walk
+    inferred = {n: infer_dst_shard([op for op in ops if op.param_name == n]) for n in ids}
+    assert decode(ops, inferred, ids, enc) == decode(ops, inferred, ids)
+    # ops of another schedule of the same layouts, with this schedule's encoding
+    other = [op for op in schedule_param_transfer(*w.layouts()) if op.dst_rank == w.dst_rank]
+    assert decode(other, {op.param_name: op.dst_shard_meta for op in other}, ids, enc) == before
+    # a source meta of another shape, and a copied piece meta, put in place
+    ops[0].src_meta = TensorMeta(name=ops[0].param_name, dtype=torch.float64, shape=(3, 5))
+    ops[1].dst_meta = copy.copy(ops[1].dst_meta)
+    got = decode(ops, shards, ids, enc)
+    assert got == decode(ops, shards, ids) and got[0][1] != before[0][1]
+    same_runs(host.rank_runs(world, w.dst_rank, world.positions_of(w.dst_rank), enc)[1:],
+              host.rank_runs(list(world), w.dst_rank)[1:])
+    # the tables are what is read (a doctored source element size shows), and
+    # only while the schedule holds them: a changed list drops them, also for
+    # an encoding made before the change
+    world = schedule_param_transfer(*w.layouts())
+    ops = [op for op in world if op.dst_rank == w.dst_rank]
+    shards = {op.param_name: op.dst_shard_meta for op in ops}
+    before = decode(ops, shards, ids)
+    table, src, *rest = world._tables
+    world._tables = (table, src.copy(), *rest)
+    world._tables[1][:, 2] += 1    # column 2: element size
+    enc = world.encoding()
+    doctored = decode(ops, shards, ids, enc)
+    assert [m[2] for _, m, _ in doctored] == [m[2] + 1 for _, m, _ in before]
+    world.append(world[0])
+    assert decode(ops, shards, ids, enc) == before
+    assert world.encoding() is None and world.positions_of(w.dst_rank) is None
 
 
 def test_schedule_positions_match_a_scan():
