@@ -531,6 +531,40 @@ def test_encoded_ops_match_the_attribute_walk():
     assert world.encoding() is None and world.positions_of(w.dst_rank) is None
 
 
+def test_copied_and_pickled_schedules_encode_like_the_walk():
+    """A schedule copied (copy.copy, copy.deepcopy) or pickled and loaded is
+    a list of its own: whatever it keeps of the tables, rank_runs and
+    encode_ops give what reading the ops' attributes gives, and a change to
+    the copy leaves the original's tables in place."""
+    import copy
+    import pickle
+
+    from suika_amd import _lib
+    from suika_amd.meta import Schedule
+    host = _lib.host()
+    w = CONFIGS["llama7b_tp4pp2_tp2pp2"]
+    world = schedule_param_transfer(*w.layouts())
+    r = w.dst_rank
+
+    def tables(s):
+        enc = s.encoding() if type(s) is Schedule else None
+        runs = host.rank_runs(s, r, s.positions_of(r) if type(s) is Schedule else None, enc)
+        ops = runs[0]
+        ids = {n: i for i, n in enumerate(dict.fromkeys(op.param_name for op in ops))}
+        shards = {op.param_name: op.dst_shard_meta for op in ops}
+        metas, rows = host.encode_ops(ops, shards, ids, enc)
+        return ([tuple(x.tolist()) if hasattr(x, "tolist") else x for x in runs[1:5]],
+                [(tuple(q[[0, 1, 2, 5, 6, 7, 8]]), tuple(metas[q[3]]), tuple(metas[q[4]])) for q in rows])
+
+    want = tables(list(world))
+    for other in (copy.copy(world), copy.deepcopy(world), pickle.loads(pickle.dumps(world))):
+        assert type(other) is Schedule and list(map(type, other)) == list(map(type, world))
+        assert tables(other) == want
+        other.append(other[0])
+        assert tables(other[:-1]) == want
+    assert world.encoding() is not None and tables(world) == want
+
+
 def test_schedule_positions_match_a_scan():
     """schedule_param_transfer's list keeps each destination rank's op
     positions; rank_runs given them returns what a scan of the whole
