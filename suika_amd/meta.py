@@ -434,7 +434,7 @@ class Schedule(list):
         self._tables = None
 
 
-def _dropping_positions(name):
+def _dropping_tables(name):
     method = getattr(list, name)
 
     def change(self, *args, **kwargs):
@@ -446,7 +446,7 @@ def _dropping_positions(name):
 
 for _name in ("__setitem__", "__delitem__", "__iadd__", "__imul__", "append", "extend", "insert", "pop",
               "remove", "sort", "reverse", "clear"):
-    setattr(Schedule, _name, _dropping_positions(_name))
+    setattr(Schedule, _name, _dropping_tables(_name))
 
 
 def schedule_param_transfer(source_param_layout: ParamLayout, target_param_layout: ParamLayout,
