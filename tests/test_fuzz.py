@@ -129,3 +129,32 @@ def test_fuzz_gpu_fused_direct(seed, monkeypatch):
     for name, ent in want.items():
         for f, a in ent.items():
             np.testing.assert_array_equal(got[name][f], a, err_msg=f"{w.key}: {name}/{f}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", GPU_SEEDS[1::3])
+def test_fuzz_gpu_host_sources(seed):
+    """The staged route on random layouts: every source shard in host
+    memory (the reference's checkpoint_load passes them so), the pieces'
+    bytes packed by host threads and unpacked on the GPU, the result on the
+    GPU or, every other case, back in host memory (``device="cpu"``);
+    device-side destinations and buffers start as POISON bytes."""
+    from suika_amd import execute_param_transfer
+    from tests.harness import poisoned_allocations, t2np, to_device
+    w = random_case(seed)
+    device = "cpu" if seed % 2 else "cuda"
+    print(f"[gpu fuzz host sources -> {device}] {w}", flush=True)
+    glob = index_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    fake = to_device(srcs, w, "cpu")
+    with poisoned_allocations():
+        out = execute_param_transfer(w.ops(), {}, torch.device(device), [(f, "normal") for f in w.src_fields],
+                                     rank=w.dst_rank, fake_source_state_dicts=fake, recast=w.recast_map)
+    torch.cuda.synchronize()
+    assert set(out) == set(want)
+    for name, ent in want.items():
+        for f, a in ent.items():
+            t = out[name][f]
+            assert t.device.type == device, f"{w.key}: {name}/{f} on {t.device}"
+            np.testing.assert_array_equal(t2np(t), a, err_msg=f"{w.key}: {name}/{f}")
