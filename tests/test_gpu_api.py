@@ -555,3 +555,28 @@ def test_prepare_then_reshard():
     for name, e in want.items():
         for f, a in e.items():
             np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{name}/{f}")
+
+
+@pytest.mark.parametrize("w", cases.all_small_cases(), ids=lambda w: w.key)
+def test_whole_schedule_and_plain_list_agree(w):
+    """The drop-in call given the world's whole schedule (this rank's ops
+    taken at the schedule's positions, encoded from its tables) and given
+    the same ops as a plain list (every op's attributes read) returns the
+    oracle's state both times."""
+    from suika_amd import schedule_param_transfer
+    from suika_amd.meta import Schedule
+    print(f"[gpu api] whole schedule vs list {w.key}", flush=True)
+    world = schedule_param_transfer(*w.layouts())
+    assert type(world) is Schedule and world.encoding() is not None
+    glob = global_state(w, _names(w))
+    srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
+    want = oracle_dest(w, srcs)
+    for ops in (world, list(world)):
+        out = execute_param_transfer(ops, {}, torch.device("cuda"), [(f, "normal") for f in w.src_fields],
+                                     rank=w.dst_rank, fake_source_state_dicts=to_device(srcs, w, "cuda"),
+                                     recast=w.recast_map)
+        torch.cuda.synchronize()
+        assert set(out) == set(want), (w.key, type(ops))
+        for name, e in want.items():
+            for f, a in e.items():
+                np.testing.assert_array_equal(t2np(out[name][f]), a, err_msg=f"{w.key} {type(ops)}: {name}/{f}")
