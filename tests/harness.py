@@ -403,14 +403,16 @@ def dirty_allocator_cache(device="cuda", total=256 << 20):
     del held
 
 
-def dirty_cache_execute(w: Workload, srcs_np, device="cuda", plan_options=None):
+def dirty_cache_execute(w: Workload, srcs_np, device="cuda", plan_options=None, ops=None):
     """The drop-in call's default path (route "direct", fresh destinations:
     one native call per launch group) on the GPU, after dirtying the
-    allocator cache."""
+    allocator cache.  ``ops``: the schedule to pass (default: this rank's
+    ops as a plain list)."""
     from suika_amd import execute_param_transfer
     fake = to_device(srcs_np, w, device)
     dirty_allocator_cache(device)
-    out = execute_param_transfer(w.ops(), {}, torch.device(device), [(f, "normal") for f in w.src_fields],
+    out = execute_param_transfer(w.ops() if ops is None else ops, {}, torch.device(device),
+                                 [(f, "normal") for f in w.src_fields],
                                  rank=w.dst_rank, fake_source_state_dicts=fake, recast=w.recast_map,
                                  plan_options=plan_options)
     torch.cuda.synchronize()

@@ -114,8 +114,10 @@ def test_fuzz_gpu_fused_direct(seed, monkeypatch):
     """The drop-in call's default path -- one native call per launch group,
     fresh destinations built on the helper thread's blocks -- on random
     layouts, after dirtying the allocator cache; every other case in three
-    round-robin launch groups."""
+    round-robin launch groups, and half of them (of both kinds) given the
+    world's whole schedule (its positions and encoding tables)."""
     from suika_amd import migration as M
+    from suika_amd import schedule_param_transfer
     from tests.harness import dirty_cache_execute, round_robin_groups
     if seed % 2:
         monkeypatch.setattr(M, "_pipeline_groups", round_robin_groups(3))
@@ -124,7 +126,8 @@ def test_fuzz_gpu_fused_direct(seed, monkeypatch):
     glob = index_state(w, _names(w))
     srcs = source_shards(w, sorted(w.layouts()[0].layout), glob)
     want = oracle_dest(w, srcs)
-    got = dirty_cache_execute(w, srcs)
+    world = schedule_param_transfer(*w.layouts()) if seed % 4 in (0, 3) else None
+    got = dirty_cache_execute(w, srcs, ops=world)
     assert set(got) == set(want)
     for name, ent in want.items():
         for f, a in ent.items():
